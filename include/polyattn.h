@@ -1,0 +1,155 @@
+/*
+ * polyattn.h -- C ABI of libpolyattn.so, the MI355X (gfx950) poly-attention core.
+ *
+ * The library computes "attention passes" (one level of the poly-attention chain) and
+ * single-token decode steps over the poly KV cache.  It never allocates device memory:
+ * every buffer, including scratch workspaces, belongs to the caller.  All calls are
+ * asynchronous on the given HIP stream, stateless and re-entrant.
+ *
+ * Reference interfaces replaced (lucidrains/poly-attention 0.3.6):
+ *   pa_attn_pass_fwd   one level of reference_poly_attention / NPolyAttention scores+aggregation
+ *                      (poly_attention/poly_attention.py:48-116, n_poly_attention.py:233-313);
+ *                      the Triton launch it stands in for is _poly_flash_fwd_kernel
+ *                      (flash_poly_attention.py:12-154, launched at :347 and :365).
+ *   pa_attn_pass_bwd   the backward of one level (flash_poly_attention.py:156-316, launched at
+ *                      :409 and :429 inside PolyFlashAttention.backward :386-446).
+ *   pa_poly_decode     the cached single-token step of Order2PolyAttention.forward
+ *                      (poly_attention.py:283-287, 331-338, 360-363) and of
+ *                      NPolyAttention.forward (n_poly_attention.py:196-313, 332-340).
+ *
+ * Semantics of one pass (per batch b, pass head h, query row i, key j):
+ *   s_ij  = scale * <q[b, h/rq, i], k[b, h/rk, j]>           rq = heads / q.heads, etc.
+ *   s_ij  = softclamp * tanh(s_ij / softclamp)              when softclamp > 0
+ *   s_ij  = -FLT_MAX  when (causal && j > i) || !key_mask[b, j] || !query_mask[b, i]
+ *   s_ij += bias[b, h/rb, j]                                 when bias is given
+ *   v_j   = round_to_dtype(v[b, h/rv, j] * vmul[b, h/rm, j]) when vmul is given, else v
+ *   out_i = sum_j softmax_j(s_ij) v_j,   lse_i = logsumexp_j(s_ij)   (lse in fp32)
+ * The finite -FLT_MAX fill is the reference's (poly_attention.py:68): a row whose entries
+ * are all masked is the uniform average over the keys whose score is exactly -FLT_MAX
+ * (lse = -FLT_MAX); a row whose entries are all -inf (a masked entry plus a -FLT_MAX
+ * bias) yields NaN (lse = -inf), as torch.softmax does.
+ */
+#ifndef POLYATTN_H
+#define POLYATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PA_ABI_VERSION 1
+#define PA_MAX_ORDER 8
+
+/* status codes (0 = success, negative = failure) */
+#define PA_OK            0
+#define PA_EINVAL       -1   /* bad shape, stride, head count or pointer */
+#define PA_EUNSUPPORTED -2   /* valid request this build does not implement */
+#define PA_EHIP         -3   /* a HIP runtime call failed (pa_last_hip_error) */
+#define PA_EWORKSPACE   -4   /* workspace missing or too small */
+
+/* element types */
+#define PA_F32  0
+#define PA_F16  1
+#define PA_BF16 2
+
+/* pa_pass.flags */
+#define PA_FLAG_MAY_DEGENERATE 1   /* masks or -FLT_MAX biases may leave rows fully masked */
+/* pa_pass_grad.accumulate bits: add into the gradient buffer instead of overwriting it */
+#define PA_ACC_DQ    1
+#define PA_ACC_DK    2
+#define PA_ACC_DV    4
+#define PA_ACC_DVMUL 8
+#define PA_ACC_DBIAS 16
+
+/* A strided view of a [batch, heads, n, dim] tensor (or [batch, heads, n] for lse / bias).
+ * Strides are in elements; the innermost (dim) stride is 1. ptr == NULL means "absent". */
+typedef struct pa_view {
+    void*   ptr;
+    int64_t sb, sh, sn;
+    int32_t heads;   /* head count of this tensor; it divides the pass head count */
+    int32_t dtype;   /* PA_F32 / PA_F16 / PA_BF16 */
+} pa_view;
+
+/* A [batch, n] keep-mask of bytes (nonzero = keep). ptr == NULL means "no mask". */
+typedef struct pa_mask {
+    const uint8_t* ptr;
+    int64_t sb, sn;
+} pa_mask;
+
+/* One attention pass (one level of the poly chain). */
+typedef struct pa_pass {
+    int32_t batch, heads, nq, nk, dim;
+    float   scale;        /* usually dim ** -0.5 */
+    float   softclamp;    /* <= 0: off */
+    int32_t causal;       /* mask j > i (top-left aligned, the reference's triu(1)) */
+    int32_t flags;        /* PA_FLAG_* */
+    pa_view q, k, v;      /* q: [B, hq, nq, dim]; k, v: [B, hk, nk, dim]; same dtype */
+    pa_view vmul;         /* optional element-wise value multiplier, same dtype as v */
+    pa_view bias;         /* optional per-key bias [B, hb, nk] (f32, f16 or bf16) */
+    pa_mask key_mask;     /* optional [B, nk] */
+    pa_mask query_mask;   /* optional [B, nq] */
+    pa_view out;          /* [B, heads, nq, dim], dtype of q */
+    pa_view lse;          /* [B, heads, nq], PA_F32 */
+} pa_pass;
+
+/* Backward of one pass.  In the backward the key-side tensors (k, v, vmul, bias) must share
+ * one head count hk; their gradients are summed over the heads/hk query heads of a group. */
+typedef struct pa_pass_grad {
+    pa_pass fwd;          /* forward description, with out and lse as written by the forward */
+    pa_view dout;         /* [B, heads, nq, dim] */
+    pa_view dlse;         /* optional fp32 [B, heads, nq]: gradient reaching lse */
+    pa_view dq, dk, dv;   /* dq like q; dk, dv like k, v */
+    pa_view dvmul;        /* required iff fwd.vmul is given */
+    pa_view dbias;        /* optional fp32 [B, hk, nk] */
+    int32_t accumulate;   /* PA_ACC_* bits */
+    void*   workspace;
+    size_t  workspace_bytes;
+} pa_pass_grad;
+
+/* One level of a cached single-token decode step (see pa_poly_decode). */
+typedef struct pa_decode_level {
+    pa_view q;            /* [B, hq, 1, dim]: the new token's query for this level */
+    pa_view k;            /* [B, kv_heads, n, dim]: keys, the new token at position n-1 */
+    pa_view v;            /* [B, hv, n, dim]: values (the msg cache for the final level) */
+    pa_view vmul;         /* middle levels: the msg cache of the deeper level */
+    pa_view bias;         /* every level but the deepest: the lse cache of the deeper level */
+    pa_view out;          /* [B, heads, 1, dim]: the msg cache slot n-1, or the final output */
+    pa_view lse;          /* [B, heads, 1]: the lse cache slot n-1 (optional for the final level) */
+    int32_t heads;        /* head count of this level (kv_heads or the query head count) */
+} pa_decode_level;
+
+/* A single-token decode step of an order-`order` poly attention over a cache of n positions
+ * (the new token already written at position n-1 of every q/k/v cache).  levels[0] is the
+ * deepest level (scores q_order . q_{order+1}), levels[order-1] the final level (q1 . q2).
+ * Level t's value at the new position is: levels[0]: v[n-1]; middle levels:
+ * round(v[n-1] * msg_{t-1}); final level: msg_{t-1}, with bias lse_{t-1}, where msg_{t-1}
+ * and lse_{t-1} are the step results of level t-1 (also written to its out/lse slots). */
+typedef struct pa_decode {
+    int32_t batch, kv_heads, n, dim, order;
+    float   scale, softclamp;
+    int32_t chunk;        /* keys per split-K chunk, 0 = automatic */
+    pa_decode_level levels[PA_MAX_ORDER];
+    void*   workspace;
+    size_t  workspace_bytes;
+} pa_decode;
+
+int         pa_abi_version(void);
+const char* pa_strerror(int status);
+int         pa_last_hip_error(void);   /* hipError_t of the last PA_EHIP on this thread */
+/* sizeof of the ABI structs, for binding checks: 0 pa_view, 1 pa_mask, 2 pa_pass,
+ * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode; 0 for other values */
+size_t      pa_struct_size(int which);
+
+int    pa_attn_pass_fwd(const pa_pass* p, void* stream);
+size_t pa_attn_pass_bwd_workspace(const pa_pass_grad* g);
+int    pa_attn_pass_bwd(const pa_pass_grad* g, void* stream);
+size_t pa_poly_decode_workspace(const pa_decode* d);
+int    pa_poly_decode(const pa_decode* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POLYATTN_H */

@@ -1,0 +1,224 @@
+// pa_abi.hip -- the extern "C" entry points of libpolyattn.so: argument validation and
+// kernel dispatch.  Declarations and semantics: include/polyattn.h.
+#include "pa_common.h"
+#include "pa_launch.h"
+
+using namespace pa;
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+bool valid_dtype(int d) { return d == PA_F32 || d == PA_F16 || d == PA_BF16; }
+
+// A view that is either absent (allowed when !required) or well-formed for a pass with
+// `pass_heads` heads.  want_dtype < 0 accepts any element type.
+int check_view(const pa_view& v, int pass_heads, bool required, int want_dtype) {
+    if (!v.ptr) return required ? PA_EINVAL : PA_OK;
+    if (v.heads <= 0 || pass_heads % v.heads != 0) return PA_EINVAL;
+    if (!valid_dtype(v.dtype)) return PA_EINVAL;
+    if (want_dtype >= 0 && v.dtype != want_dtype) return PA_EINVAL;
+    return PA_OK;
+}
+
+DView to_dview(const pa_view& v, int pass_heads) {
+    DView d;
+    d.p = static_cast<char*>(v.ptr);
+    d.sb = v.sb;
+    d.sh = v.sh;
+    d.sn = v.sn;
+    d.hdiv = (v.ptr && v.heads > 0) ? pass_heads / v.heads : 1;
+    d.dtype = v.dtype;
+    return d;
+}
+
+DMask to_dmask(const pa_mask& m) {
+    DMask d;
+    d.p = m.ptr;
+    d.sb = m.sb;
+    d.sn = m.sn;
+    return d;
+}
+
+#define PA_TRY(expr)                   \
+    do {                               \
+        int _st = (expr);              \
+        if (_st != PA_OK) return _st;  \
+    } while (0)
+
+int validate_pass(const pa_pass* p) {
+    if (!p) return PA_EINVAL;
+    if (p->batch < 1 || p->heads < 1 || p->nq < 1 || p->nk < 1) return PA_EINVAL;
+    if (p->dim < 1 || p->dim > 256) return PA_EUNSUPPORTED;
+    const int T = p->q.dtype;
+    if (!valid_dtype(T)) return PA_EINVAL;
+    PA_TRY(check_view(p->q, p->heads, true, T));
+    PA_TRY(check_view(p->k, p->heads, true, T));
+    PA_TRY(check_view(p->v, p->heads, true, T));
+    PA_TRY(check_view(p->vmul, p->heads, false, T));
+    PA_TRY(check_view(p->bias, p->heads, false, -1));
+    PA_TRY(check_view(p->out, p->heads, true, T));
+    PA_TRY(check_view(p->lse, p->heads, true, PA_F32));
+    if (p->out.heads != p->heads || p->lse.heads != p->heads) return PA_EINVAL;
+    return PA_OK;
+}
+
+PassDev to_passdev(const pa_pass* p) {
+    PassDev P;
+    P.batch = p->batch;
+    P.heads = p->heads;
+    P.nq = p->nq;
+    P.nk = p->nk;
+    P.dim = p->dim;
+    P.scale = p->scale;
+    P.softclamp = p->softclamp;
+    P.causal = p->causal;
+    P.flags = p->flags;
+    P.q = to_dview(p->q, p->heads);
+    P.k = to_dview(p->k, p->heads);
+    P.v = to_dview(p->v, p->heads);
+    P.vmul = to_dview(p->vmul, p->heads);
+    P.bias = to_dview(p->bias, p->heads);
+    P.out = to_dview(p->out, p->heads);
+    P.lse = to_dview(p->lse, p->heads);
+    P.km = to_dmask(p->key_mask);
+    P.qm = to_dmask(p->query_mask);
+    return P;
+}
+
+int finish_launch() {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        g_last_hip_error = static_cast<int>(e);
+        return PA_EHIP;
+    }
+    return PA_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t bwd_ws_bytes(const pa_pass& f) {
+    const size_t rows = (size_t)f.batch * f.heads * f.nq;
+    return 3 * align256(rows * sizeof(float));
+}
+
+}  // namespace
+
+extern "C" {
+
+int pa_abi_version(void) { return PA_ABI_VERSION; }
+
+const char* pa_strerror(int status) {
+    switch (status) {
+        case PA_OK: return "success";
+        case PA_EINVAL: return "invalid argument (shape, stride, head count, dtype or pointer)";
+        case PA_EUNSUPPORTED: return "unsupported by this build of libpolyattn";
+        case PA_EHIP: return "HIP runtime error";
+        case PA_EWORKSPACE: return "workspace missing or too small";
+        default: return "unknown libpolyattn status";
+    }
+}
+
+int pa_last_hip_error(void) { return g_last_hip_error; }
+
+size_t pa_struct_size(int which) {
+    switch (which) {
+        case 0: return sizeof(pa_view);
+        case 1: return sizeof(pa_mask);
+        case 2: return sizeof(pa_pass);
+        case 3: return sizeof(pa_pass_grad);
+        case 4: return sizeof(pa_decode_level);
+        case 5: return sizeof(pa_decode);
+        default: return 0;
+    }
+}
+
+int pa_attn_pass_fwd(const pa_pass* p, void* stream) {
+    PA_TRY(validate_pass(p));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const PassDev P = to_passdev(p);
+    const int T = p->q.dtype;
+    if (mfma_fwd_supported(P, T)) {
+        launch_mfma_fwd(P, T, s);
+        const bool may_degenerate = (p->flags & PA_FLAG_MAY_DEGENERATE) || p->key_mask.ptr ||
+                                    p->query_mask.ptr;
+        if (may_degenerate) launch_simt_fixup(P, T, s);
+    } else {
+        launch_simt_fwd(P, T, s);
+    }
+    return finish_launch();
+}
+
+size_t pa_attn_pass_bwd_workspace(const pa_pass_grad* g) {
+    if (!g) return 0;
+    return bwd_ws_bytes(g->fwd);
+}
+
+int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
+    if (!g) return PA_EINVAL;
+    const pa_pass* p = &g->fwd;
+    PA_TRY(validate_pass(p));
+    const int T = p->q.dtype;
+    const int H = p->heads;
+    const int hk = p->k.heads;
+    // backward: queries at the pass head count, key-side tensors at one head count
+    if (p->q.heads != H) return PA_EUNSUPPORTED;
+    if (p->v.heads != hk) return PA_EUNSUPPORTED;
+    if (p->vmul.ptr && p->vmul.heads != hk) return PA_EUNSUPPORTED;
+    if (p->bias.ptr && p->bias.heads != hk) return PA_EUNSUPPORTED;
+    PA_TRY(check_view(g->dout, H, true, T));
+    PA_TRY(check_view(g->dlse, H, false, PA_F32));
+    PA_TRY(check_view(g->dq, H, true, T));
+    PA_TRY(check_view(g->dk, H, true, T));
+    PA_TRY(check_view(g->dv, H, true, T));
+    PA_TRY(check_view(g->dvmul, H, p->vmul.ptr != nullptr, T));
+    PA_TRY(check_view(g->dbias, H, false, PA_F32));
+    if (g->dout.heads != H || g->dq.heads != H || g->dk.heads != hk || g->dv.heads != hk)
+        return PA_EINVAL;
+    if (g->dvmul.ptr && g->dvmul.heads != hk) return PA_EINVAL;
+    if (g->dbias.ptr && g->dbias.heads != hk) return PA_EINVAL;
+    if (g->dlse.ptr && g->dlse.heads != H) return PA_EINVAL;
+    const size_t need = bwd_ws_bytes(*p);
+    if (!g->workspace || g->workspace_bytes < need) return PA_EWORKSPACE;
+
+    GradDev G;
+    G.f = to_passdev(p);
+    G.dout = to_dview(g->dout, H);
+    G.dlse = to_dview(g->dlse, H);
+    G.dq = to_dview(g->dq, H);
+    G.dk = to_dview(g->dk, H);
+    G.dv = to_dview(g->dv, H);
+    G.dvmul = to_dview(g->dvmul, H);
+    G.dbias = to_dview(g->dbias, H);
+    G.accumulate = g->accumulate;
+    G.hk = hk;
+    const size_t rows = (size_t)p->batch * H * p->nq;
+    char* ws = static_cast<char*>(g->workspace);
+    G.ws_D = reinterpret_cast<float*>(ws);
+    G.ws_lse = reinterpret_cast<float*>(ws + align256(rows * sizeof(float)));
+    G.ws_invc = reinterpret_cast<float*>(ws + 2 * align256(rows * sizeof(float)));
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    launch_simt_bwd(G, T, s, /*pre=*/true, false, false);
+    if (mfma_bwd_supported(G, T)) {
+        launch_mfma_bwd(G, T, s);
+    } else {
+        launch_simt_bwd(G, T, s, false, /*dq=*/true, /*dkv=*/true);
+    }
+    return finish_launch();
+}
+
+size_t pa_poly_decode_workspace(const pa_decode* d) {
+    if (!d) return 0;
+    int chunk = 0, nchunks = 0;
+    return decode_workspace_bytes(d, &chunk, &nchunks);
+}
+
+int pa_poly_decode(const pa_decode* d, void* stream) {
+    if (!d) return PA_EINVAL;
+    const int st = launch_decode(d, static_cast<hipStream_t>(stream));
+    if (st != PA_OK) return st;
+    return finish_launch();
+}
+
+}  // extern "C"

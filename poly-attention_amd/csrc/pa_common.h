@@ -1,0 +1,103 @@
+// pa_common.h -- device-side helpers shared by the libpolyattn kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <float.h>
+#include <math.h>
+
+#include "polyattn.h"
+
+namespace pa {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// A score at or below this is "masked" in the reference's finite-fill sense
+// (-finfo.max, poly_attention.py:68); normal scores and lse values are far above it.
+constexpr float kMaskedThreshold = -1.0e30f;
+
+// ---------------------------------------------------------------------------------------
+// element conversions (bf16 / f16 rounding is round-to-nearest-even, as torch's casts)
+template <typename T> __device__ __forceinline__ float to_f(T x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
+template <typename T> __device__ __forceinline__ float round_to(float x) { return (float)(T)x; }
+
+__device__ __forceinline__ float load_any(const void* p, int dtype, int64_t off) {
+    if (dtype == PA_F32) return ((const float*)p)[off];
+    if (dtype == PA_F16) return (float)((const f16*)p)[off];
+    return (float)((const bf16*)p)[off];
+}
+__device__ __forceinline__ void store_any(void* p, int dtype, int64_t off, float v) {
+    if (dtype == PA_F32) ((float*)p)[off] = v;
+    else if (dtype == PA_F16) ((f16*)p)[off] = (f16)v;
+    else ((bf16*)p)[off] = (bf16)v;
+}
+
+// ---------------------------------------------------------------------------------------
+// A view as the kernels see it: hdiv = (pass head count) / (this tensor's head count).
+struct DView {
+    char* p;
+    int64_t sb, sh, sn;
+    int32_t hdiv;
+    int32_t dtype;
+    __host__ __device__ __forceinline__ bool ok() const { return p != nullptr; }
+    __device__ __forceinline__ int64_t idx(int b, int h, int64_t n) const {
+        return (int64_t)b * sb + (int64_t)(h / hdiv) * sh + n * sn;
+    }
+    template <typename T> __device__ __forceinline__ const T* row(int b, int h, int64_t n) const {
+        return reinterpret_cast<const T*>(p) + idx(b, h, n);
+    }
+    template <typename T> __device__ __forceinline__ T* wrow(int b, int h, int64_t n) const {
+        return reinterpret_cast<T*>(p) + idx(b, h, n);
+    }
+    __device__ __forceinline__ float scalar(int b, int h, int64_t n) const {
+        return load_any(p, dtype, idx(b, h, n));
+    }
+};
+
+struct DMask {
+    const uint8_t* p;
+    int64_t sb, sn;
+    __device__ __forceinline__ bool keep(int b, int64_t n) const {
+        return p == nullptr || p[(int64_t)b * sb + n * sn] != 0;
+    }
+};
+
+// All the geometry of one pass, as passed to every pass kernel (by value).
+struct PassDev {
+    int32_t batch, heads, nq, nk, dim;
+    float scale, softclamp;
+    int32_t causal, flags;
+    DView q, k, v, vmul, bias, out, lse;
+    DMask km, qm;
+};
+
+struct GradDev {
+    PassDev f;
+    DView dout, dlse, dq, dk, dv, dvmul, dbias;
+    int32_t accumulate;
+    int32_t hk;            // key-side head count (k, v, vmul, bias share it)
+    float* ws_D;           // [B, heads, nq]  rowsum(dO * O) - dlse
+    float* ws_lse;         // [B, heads, nq]  lse for normal rows, +inf for degenerate rows
+    float* ws_invc;        // [B, heads, nq]  1 / (#class-1 keys) for degenerate rows, else 0
+};
+
+// class of a bias value in the finite-fill arithmetic: 0 normal, 1 = -FLT_MAX, 2 = -inf
+__device__ __forceinline__ int bias_class(float x) {
+    return x == -INFINITY ? 2 : (x <= kMaskedThreshold ? 1 : 0);
+}
+
+__device__ __forceinline__ float softclamp_f(float x, float c) {
+    return c > 0.f ? c * tanhf(x / c) : x;
+}
+// d softclamp(x) / dx expressed through y = softclamp(x)
+__device__ __forceinline__ float softclamp_grad(float y, float c) {
+    if (c <= 0.f) return 1.f;
+    float t = y / c;
+    return 1.f - t * t;
+}
+
+}  // namespace pa

@@ -1,0 +1,480 @@
+// pa_decode.hip -- single-token decode over the poly KV cache.
+//
+// A decode step of an order-n poly attention reads every cached tensor once; it is HBM
+// bound.  Phase 1 (k_dec_partial) splits the cached positions 0..n-2 of every level into
+// chunks and computes, per (level, batch, head, chunk), the online-softmax partial
+// (m, l, sum p v) with coalesced 16-byte loads; the K row of a position is read once and
+// shared by the query heads of its KV group.  Phase 2 (k_dec_combine) runs one workgroup
+// per (batch, KV group): level by level (deepest first) it merges the chunk partials,
+// adds the new position n-1 -- whose value and bias are the step results of the deeper
+// level -- and writes the level's msg / lse cache slot (or the final output).
+#include "pa_common.h"
+#include "pa_launch.h"
+
+namespace pa {
+
+struct DecLevelDev {
+    DView q, k, v, vmul, bias, out, lse;  // hdiv relative to the level head count
+    int32_t heads;                        // level head count
+    int32_t rep;                          // level heads per KV group
+    int32_t out_rep, lse_rep;             // view heads per level head (replicated writes)
+    float* ws;                            // partial records [B][heads][nchunks][rec]
+};
+
+struct DecodeDev {
+    int32_t batch, kv_heads, n, dim, order, chunk, nchunks, rec, lpr;
+    float scale, softclamp;
+    DecLevelDev L[PA_MAX_ORDER];
+};
+
+constexpr int kDecThreads = 256;
+constexpr int kDecHB = 4;      // heads per register batch in the partial kernel
+constexpr int kDecUnroll = 4;  // positions in flight per key group
+constexpr int kDecMaxHeadsPerGroup = 64;
+constexpr int kDecMaxGroupElems = 8192;  // level heads per KV group * head dim
+
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> { typedef uint4 type; static constexpr int n = 8; };
+template <> struct Vec16<f16> { typedef uint4 type; static constexpr int n = 8; };
+template <> struct Vec16<float> { typedef uint4 type; static constexpr int n = 4; };
+
+template <typename T>
+__device__ __forceinline__ void load16(const T* p, float* out) {
+    constexpr int E = Vec16<T>::n;
+    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int i = 0; i < E; ++i) out[i] = to_f(e[i]);
+}
+
+// merge (m2, l2, a2) into (m, l, a); m in the log2 domain, -inf when empty
+template <int E>
+__device__ __forceinline__ void merge_state(float& m, float& l, float* a, float m2, float l2,
+                                            const float* a2) {
+    const float mn = fmaxf(m, m2);
+    if (mn == -INFINITY) return;
+    const float c1 = exp2f(m - mn), c2 = exp2f(m2 - mn);
+    l = l * c1 + l2 * c2;
+#pragma unroll
+    for (int i = 0; i < E; ++i) a[i] = a[i] * c1 + a2[i] * c2;
+    m = mn;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kDecThreads) void k_dec_partial(DecodeDev D) {
+    constexpr int E = Vec16<T>::n;
+    const int c = blockIdx.x, bg = blockIdx.y, t = blockIdx.z;
+    const int b = bg / D.kv_heads, g = bg % D.kv_heads;
+    const DecLevelDev& L = D.L[t];
+    const int lpr = D.lpr;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & (lpr - 1);
+    const int kg = threadIdx.x / lpr;
+    const int KG = kDecThreads / lpr;
+    const int d0 = sub * E;
+    const bool dok = d0 < D.dim;
+    const int j_begin = c * D.chunk;
+    const int j_end = min(j_begin + D.chunk, D.n - 1);
+    const bool has_bias = L.bias.ok(), has_vmul = L.vmul.ok();
+
+    __shared__ float s_red[kDecThreads / 64][kDecHB][2];
+    __shared__ float s_acc[kDecThreads / 64][kDecHB][256];
+
+    for (int hb0 = 0; hb0 < L.rep; hb0 += kDecHB) {
+        const int nh = min(kDecHB, L.rep - hb0);
+        float qv[kDecHB][E], acc[kDecHB][E], m[kDecHB], l[kDecHB];
+#pragma unroll
+        for (int hh = 0; hh < kDecHB; ++hh) {
+            const int h = g * L.rep + hb0 + hh;
+            if (hh < nh && dok) load16<T>(L.q.row<T>(b, h, 0) + d0, qv[hh]);
+            else
+#pragma unroll
+                for (int e = 0; e < E; ++e) qv[hh][e] = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[hh][e] = 0.f;
+            m[hh] = -INFINITY;
+            l[hh] = 0.f;
+        }
+        const int h0 = g * L.rep + hb0;
+        for (int jb = j_begin + kg; jb < j_end; jb += KG * kDecUnroll) {
+            float kf[kDecUnroll][E];
+#pragma unroll
+            for (int u = 0; u < kDecUnroll; ++u) {
+                const int j = jb + u * KG;
+                if (j < j_end && dok) load16<T>(L.k.row<T>(b, h0, j) + d0, kf[u]);
+                else
+#pragma unroll
+                    for (int e = 0; e < E; ++e) kf[u][e] = 0.f;
+            }
+#pragma unroll
+            for (int hh = 0; hh < kDecHB; ++hh) {
+                if (hh >= nh) break;
+                const int h = h0 + hh;
+                float vf[kDecUnroll][E], sc[kDecUnroll];
+#pragma unroll
+                for (int u = 0; u < kDecUnroll; ++u) {
+                    const int j = jb + u * KG;
+                    float s = 0.f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) s += qv[hh][e] * kf[u][e];
+                    sc[u] = s;
+                    if (j < j_end && dok) {
+                        load16<T>(L.v.row<T>(b, h, j) + d0, vf[u]);
+                        if (has_vmul) {
+                            float mf[E];
+                            load16<T>(L.vmul.row<T>(b, h, j) + d0, mf);
+#pragma unroll
+                            for (int e = 0; e < E; ++e) vf[u][e] = round_to<T>(vf[u][e] * mf[e]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < E; ++e) vf[u][e] = 0.f;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kDecUnroll; ++u) {
+                    float s = sc[u];
+                    for (int off = lpr >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off);
+                    const int j = jb + u * KG;
+                    if (j >= j_end) continue;
+                    float bj = has_bias ? L.bias.scalar(b, h, j) : 0.f;
+                    if (bias_class(bj) != 0) continue;  // -FLT_MAX / -inf keys: weight 0
+                    const float tt = (softclamp_f(s * D.scale, D.softclamp) + bj) * kLog2e;
+                    if (tt > m[hh]) {
+                        const float cc = exp2f(m[hh] - tt);
+                        l[hh] *= cc;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) acc[hh][e] *= cc;
+                        m[hh] = tt;
+                    }
+                    const float p = exp2f(tt - m[hh]);
+                    l[hh] += p;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) acc[hh][e] += p * vf[u][e];
+                }
+            }
+        }
+        // merge key groups inside the wave (lanes with equal `sub`)
+        for (int off = lpr; off < 64; off <<= 1) {
+#pragma unroll
+            for (int hh = 0; hh < kDecHB; ++hh) {
+                const float m2 = __shfl_xor(m[hh], off);
+                const float l2 = __shfl_xor(l[hh], off);
+                float a2[E];
+#pragma unroll
+                for (int e = 0; e < E; ++e) a2[e] = __shfl_xor(acc[hh][e], off);
+                merge_state<E>(m[hh], l[hh], acc[hh], m2, l2, a2);
+            }
+        }
+        // merge the waves through LDS
+        if (lane < lpr) {
+#pragma unroll
+            for (int hh = 0; hh < kDecHB; ++hh) {
+                if (lane == 0) {
+                    s_red[wave][hh][0] = m[hh];
+                    s_red[wave][hh][1] = l[hh];
+                }
+#pragma unroll
+                for (int e = 0; e < E; ++e)
+                    if (d0 + e < 256) s_acc[wave][hh][d0 + e] = acc[hh][e];
+            }
+        }
+        __syncthreads();
+        for (int x = threadIdx.x; x < nh * D.dim; x += kDecThreads) {
+            const int hh = x / D.dim, d = x % D.dim;
+            float mm = -INFINITY, ll = 0.f, aa = 0.f;
+            for (int w = 0; w < kDecThreads / 64; ++w) {
+                const float m2 = s_red[w][hh][0];
+                const float mn = fmaxf(mm, m2);
+                if (mn == -INFINITY) continue;
+                const float c1 = exp2f(mm - mn), c2 = exp2f(m2 - mn);
+                ll = ll * c1 + s_red[w][hh][1] * c2;
+                aa = aa * c1 + s_acc[w][hh][d] * c2;
+                mm = mn;
+            }
+            const int h = h0 + hh;
+            float* rec = L.ws + (((int64_t)b * L.heads + h) * D.nchunks + c) * D.rec;
+            rec[2 + d] = aa;
+            if (d == 0) {
+                rec[0] = mm;
+                rec[1] = ll;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// One workgroup per (batch, KV group): chain the levels, deepest first.
+template <typename T>
+__global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
+    const int b = blockIdx.x / D.kv_heads, g = blockIdx.x % D.kv_heads;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int kWaves = kDecThreads / 64;
+    // step results of the previous (deeper) level, per level head of this group:
+    // [head][dim] flattened, heads-per-group * dim <= kDecMaxGroupElems (checked on the host)
+    __shared__ float s_msg[kDecMaxGroupElems];
+    __shared__ float s_lse[kDecMaxHeadsPerGroup];
+    __shared__ float s_msg2[kDecMaxGroupElems];
+    __shared__ float s_lse2[kDecMaxHeadsPerGroup];
+    int prev_rep = 1;
+    const int dim = D.dim;
+    const int nold = D.n - 1;
+
+    for (int t = 0; t < D.order; ++t) {
+        const DecLevelDev& L = D.L[t];
+        const bool deepest = (t == 0), final_level = (t == D.order - 1);
+        for (int hh = wave; hh < L.rep; hh += kWaves) {
+            const int h = g * L.rep + hh;
+            // index of this head's deeper-level result (deeper level has prev_rep heads/group)
+            const int ph = (hh * prev_rep) / L.rep;
+            // 1. merge the chunk partials
+            float mm = -INFINITY;
+            const float* recs = L.ws + ((int64_t)b * L.heads + h) * D.nchunks * D.rec;
+            for (int c = lane; c < D.nchunks; c += 64) mm = fmaxf(mm, recs[(int64_t)c * D.rec]);
+            for (int off = 32; off > 0; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
+            float ll = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+            if (mm != -INFINITY) {
+                for (int c = 0; c < D.nchunks; ++c) {
+                    const float* rc = recs + (int64_t)c * D.rec;
+                    const float mc = rc[0];
+                    if (mc == -INFINITY) continue;
+                    const float w = exp2f(mc - mm);
+                    ll += rc[1] * w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int d = lane + 64 * e;
+                        if (d < dim) acc[e] += rc[2 + d] * w;
+                    }
+                }
+            }
+            // 2. the new position n-1
+            float part = 0.f, vnew[4];
+            const T* qrow = L.q.row<T>(b, h, 0);
+            const T* krow = L.k.row<T>(b, h, nold);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = lane + 64 * e;
+                vnew[e] = 0.f;
+                if (d < dim) {
+                    part += to_f(qrow[d]) * to_f(krow[d]);
+                    if (deepest) vnew[e] = to_f(L.v.row<T>(b, h, nold)[d]);
+                    else if (final_level) vnew[e] = s_msg[ph * dim + d];
+                    else vnew[e] = round_to<T>(to_f(L.v.row<T>(b, h, nold)[d]) * s_msg[ph * dim + d]);
+                }
+            }
+            for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+            const float bnew = deepest ? 0.f : s_lse[ph];
+            const bool new_ok = bias_class(bnew) == 0;
+            if (new_ok) {
+                const float tt = (softclamp_f(part * D.scale, D.softclamp) + bnew) * kLog2e;
+                const float mn = fmaxf(mm, tt);
+                const float c1 = exp2f(mm - mn), c2 = exp2f(tt - mn);
+                ll = ll * c1 + c2;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = acc[e] * c1 + vnew[e] * c2;
+                mm = mn;
+            }
+            float lse_v, inv;
+            if (ll > 0.f) {
+                lse_v = (mm + log2f(ll)) * kLn2;
+                inv = 1.f / ll;
+            } else {
+                // every position masked: uniform average over the -FLT_MAX-biased positions
+                float c1 = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = 0.f;
+                for (int j = 0; j < D.n; ++j) {
+                    const float bj = (j == nold) ? bnew : (L.bias.ok() ? L.bias.scalar(b, h, j) : 0.f);
+                    if (bias_class(bj) != 1) continue;
+                    c1 += 1.f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int d = lane + 64 * e;
+                        if (d >= dim) continue;
+                        float v;
+                        if (j == nold) v = vnew[e];
+                        else {
+                            v = to_f(L.v.row<T>(b, h, j)[d]);
+                            if (L.vmul.ok()) v = round_to<T>(v * to_f(L.vmul.row<T>(b, h, j)[d]));
+                        }
+                        acc[e] += v;
+                    }
+                }
+                lse_v = c1 > 0.f ? -FLT_MAX : -INFINITY;
+                inv = c1 > 0.f ? 1.f / c1 : NAN;
+            }
+            // 3. write the step result (replicated over the view heads) and keep it in LDS
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = lane + 64 * e;
+                if (d >= dim) continue;
+                const float o = acc[e] * inv;
+                for (int r = 0; r < L.out_rep; ++r)
+                    L.out.wrow<T>(b, h * L.out_rep + r, 0)[d] = from_f<T>(o);
+                s_msg2[hh * dim + d] = round_to<T>(o);
+            }
+            if (lane == 0) {
+                float stored = lse_v;
+                if (L.lse.ok()) {
+                    for (int r = 0; r < L.lse_rep; ++r)
+                        store_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep + r, 0), lse_v);
+                    stored = load_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep, 0));
+                }
+                s_lse2[hh] = stored;  // the value the next level's cached bias will hold
+            }
+        }
+        __syncthreads();
+        for (int x = threadIdx.x; x < L.rep * dim; x += kDecThreads)
+            s_msg[x] = s_msg2[x];
+        for (int x = threadIdx.x; x < L.rep; x += kDecThreads) s_lse[x] = s_lse2[x];
+        __syncthreads();
+        prev_rep = L.rep;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+
+static int elem_size(int dtype) { return dtype == PA_F32 ? 4 : 2; }
+
+static int pick_chunks(const pa_decode* d, int* chunk_out) {
+    const int nold = d->n - 1;
+    if (nold <= 0) {
+        *chunk_out = 1;
+        return 0;
+    }
+    int chunk = d->chunk;
+    if (chunk <= 0) {
+        const long units = (long)d->batch * d->kv_heads * d->order;
+        long want = (2048 + units - 1) / units;  // aim for >= 2048 workgroups
+        if (want < 1) want = 1;
+        chunk = (int)((nold + want - 1) / want);
+        if (chunk < 256) chunk = 256;
+    }
+    *chunk_out = chunk;
+    return (nold + chunk - 1) / chunk;
+}
+
+static int level_heads(const pa_decode_level& L) {
+    int h = L.heads;
+    return h;
+}
+
+size_t decode_workspace_bytes(const pa_decode* d, int* chunk_out, int* nchunks_out) {
+    const int nchunks = pick_chunks(d, chunk_out);
+    *nchunks_out = nchunks;
+    const int rec = (d->dim + 2 + 3) & ~3;
+    size_t total = 0;
+    for (int t = 0; t < d->order && t < PA_MAX_ORDER; ++t) {
+        const size_t sz = (size_t)d->batch * level_heads(d->levels[t]) * nchunks * rec * 4;
+        total += (sz + 255) & ~size_t(255);
+    }
+    return total;
+}
+
+static bool aligned16(const pa_view& v) {
+    const int es = elem_size(v.dtype);
+    const int E = 16 / es;
+    return ((uintptr_t)v.ptr % 16 == 0) && v.sb % E == 0 && v.sh % E == 0 && v.sn % E == 0;
+}
+
+int launch_decode(const pa_decode* d, hipStream_t s) {
+    if (d->order < 2 || d->order > PA_MAX_ORDER) return PA_EINVAL;
+    if (d->batch < 1 || d->kv_heads < 1 || d->n < 1 || d->dim < 1) return PA_EINVAL;
+    for (int t = 0; t < d->order; ++t)
+        if (!d->levels[t].q.ptr || !d->levels[t].k.ptr || !d->levels[t].v.ptr) return PA_EINVAL;
+    if (d->dim > 256) return PA_EUNSUPPORTED;
+    const int T = d->levels[0].q.dtype;
+    if (T != PA_F32 && T != PA_F16 && T != PA_BF16) return PA_EINVAL;
+    const int E = 16 / elem_size(T);
+    if (d->dim % E != 0) return PA_EUNSUPPORTED;
+    int lpr = 1;
+    while (lpr * E < d->dim) lpr <<= 1;
+    if (lpr > 64) return PA_EUNSUPPORTED;
+
+    DecodeDev D;
+    D.batch = d->batch;
+    D.kv_heads = d->kv_heads;
+    D.n = d->n;
+    D.dim = d->dim;
+    D.order = d->order;
+    D.scale = d->scale;
+    D.softclamp = d->softclamp;
+    D.lpr = lpr;
+    D.rec = (d->dim + 2 + 3) & ~3;
+    int chunk = 1;
+    D.nchunks = pick_chunks(d, &chunk);
+    D.chunk = chunk;
+    const size_t need = decode_workspace_bytes(d, &chunk, &D.nchunks);
+    if (D.nchunks > 0 && (!d->workspace || d->workspace_bytes < need)) return PA_EWORKSPACE;
+
+    char* ws = static_cast<char*>(d->workspace);
+    size_t off = 0;
+    for (int t = 0; t < d->order; ++t) {
+        const pa_decode_level& l = d->levels[t];
+        const int H = l.heads;
+        if (H < 1 || H % d->kv_heads != 0) return PA_EINVAL;
+        if (H / d->kv_heads > kDecMaxHeadsPerGroup) return PA_EUNSUPPORTED;
+        if ((H / d->kv_heads) * d->dim > kDecMaxGroupElems) return PA_EUNSUPPORTED;
+        auto chk = [&](const pa_view& v, bool required, int dt) -> bool {
+            if (!v.ptr) return !required;
+            if (v.heads < 1) return false;
+            if (dt >= 0 && v.dtype != dt) return false;
+            return true;
+        };
+        const bool deepest = t == 0, final_level = t == d->order - 1;
+        if (!chk(l.q, true, T) || !chk(l.k, true, T) || !chk(l.v, true, T)) return PA_EINVAL;
+        if (!chk(l.vmul, !deepest && !final_level, T)) return PA_EINVAL;
+        if (!chk(l.bias, !deepest, -1) || !chk(l.out, true, T) || !chk(l.lse, !final_level, -1))
+            return PA_EINVAL;
+        // tensors read with the level's head index: their head count divides H
+        const pa_view* reads[5] = {&l.q, &l.k, &l.v, &l.vmul, &l.bias};
+        for (const pa_view* v : reads)
+            if (v->ptr && H % v->heads != 0) return PA_EINVAL;
+        if (l.k.heads != d->kv_heads) return PA_EINVAL;
+        if (l.out.heads % H != 0 || (l.lse.ptr && l.lse.heads % H != 0)) return PA_EINVAL;
+        const pa_view* vecs[4] = {&l.q, &l.k, &l.v, &l.vmul};
+        for (const pa_view* v : vecs)
+            if (v->ptr && !aligned16(*v)) return PA_EUNSUPPORTED;
+        if (t > 0 && d->levels[t - 1].heads > H) return PA_EUNSUPPORTED;
+
+        DecLevelDev& L = D.L[t];
+        auto mk = [&](const pa_view& v) {
+            DView x;
+            x.p = static_cast<char*>(v.ptr);
+            x.sb = v.sb;
+            x.sh = v.sh;
+            x.sn = v.sn;
+            x.hdiv = (v.ptr && v.heads > 0 && v.heads <= H) ? H / v.heads : 1;
+            x.dtype = v.dtype;
+            return x;
+        };
+        L.q = mk(l.q);
+        L.k = mk(l.k);
+        L.v = mk(l.v);
+        L.vmul = mk(l.vmul);
+        L.bias = mk(l.bias);
+        L.out = mk(l.out);
+        L.out.hdiv = 1;
+        L.lse = mk(l.lse);
+        L.lse.hdiv = 1;
+        L.heads = H;
+        L.rep = H / d->kv_heads;
+        L.out_rep = l.out.heads / H;
+        L.lse_rep = l.lse.ptr ? l.lse.heads / H : 1;
+        L.ws = reinterpret_cast<float*>(ws + off);
+        off += (((size_t)d->batch * H * D.nchunks * D.rec * 4) + 255) & ~size_t(255);
+    }
+    if (D.nchunks > 0) {
+        dim3 grid(D.nchunks, d->batch * d->kv_heads, d->order);
+        if (T == PA_F32) hipLaunchKernelGGL((k_dec_partial<float>), grid, dim3(kDecThreads), 0, s, D);
+        else if (T == PA_F16) hipLaunchKernelGGL((k_dec_partial<f16>), grid, dim3(kDecThreads), 0, s, D);
+        else hipLaunchKernelGGL((k_dec_partial<bf16>), grid, dim3(kDecThreads), 0, s, D);
+    }
+    dim3 cgrid(d->batch * d->kv_heads);
+    if (T == PA_F32) hipLaunchKernelGGL((k_dec_combine<float>), cgrid, dim3(kDecThreads), 0, s, D);
+    else if (T == PA_F16) hipLaunchKernelGGL((k_dec_combine<f16>), cgrid, dim3(kDecThreads), 0, s, D);
+    else hipLaunchKernelGGL((k_dec_combine<bf16>), cgrid, dim3(kDecThreads), 0, s, D);
+    return PA_OK;
+}
+
+}  // namespace pa

@@ -1,0 +1,24 @@
+// pa_launch.h -- host-side launchers of the libpolyattn kernels (internal to the library).
+#pragma once
+
+#include "pa_common.h"
+
+namespace pa {
+
+// generic (one lane per row) kernels: every dtype, head dim <= 256, every mask feature
+void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s);
+void launch_simt_fixup(const PassDev& P, int dtype, hipStream_t s);
+void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool dq, bool dkv);
+
+// MFMA kernels (bf16 / f16, head dim 64 or 128); return false when they do not cover P
+bool mfma_fwd_supported(const PassDev& P, int dtype);
+void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s);
+bool mfma_bwd_supported(const GradDev& G, int dtype);
+void launch_mfma_bwd(const GradDev& G, int dtype, hipStream_t s);
+
+// decode
+struct DecodeDev;
+size_t decode_workspace_bytes(const pa_decode* d, int* chunk_out, int* nchunks_out);
+int launch_decode(const pa_decode* d, hipStream_t s);
+
+}  // namespace pa

@@ -1,0 +1,212 @@
+"""ctypes binding of libpolyattn.so (declared in include/polyattn.h).
+
+The structures below mirror the C structs field for field; ``pa_struct_size`` lets the
+tests check the layouts against the compiled library.  Loading never touches the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolyattn.so"
+
+PA_ABI_VERSION = 1
+PA_MAX_ORDER = 8
+
+PA_OK = 0
+PA_EINVAL = -1
+PA_EUNSUPPORTED = -2
+PA_EHIP = -3
+PA_EWORKSPACE = -4
+
+PA_F32, PA_F16, PA_BF16 = 0, 1, 2
+PA_FLAG_MAY_DEGENERATE = 1
+PA_ACC_DQ, PA_ACC_DK, PA_ACC_DV, PA_ACC_DVMUL, PA_ACC_DBIAS = 1, 2, 4, 8, 16
+
+DTYPE_CODE = {torch.float32: PA_F32, torch.float16: PA_F16, torch.bfloat16: PA_BF16}
+
+# every symbol include/polyattn.h declares
+EXPORTED_SYMBOLS = (
+    "pa_abi_version",
+    "pa_strerror",
+    "pa_last_hip_error",
+    "pa_struct_size",
+    "pa_attn_pass_fwd",
+    "pa_attn_pass_bwd_workspace",
+    "pa_attn_pass_bwd",
+    "pa_poly_decode_workspace",
+    "pa_poly_decode",
+)
+
+
+class PaView(ctypes.Structure):
+    _fields_ = [
+        ("ptr", c_void_p),
+        ("sb", c_int64),
+        ("sh", c_int64),
+        ("sn", c_int64),
+        ("heads", c_int32),
+        ("dtype", c_int32),
+    ]
+
+
+class PaMask(ctypes.Structure):
+    _fields_ = [("ptr", c_void_p), ("sb", c_int64), ("sn", c_int64)]
+
+
+class PaPass(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int32),
+        ("heads", c_int32),
+        ("nq", c_int32),
+        ("nk", c_int32),
+        ("dim", c_int32),
+        ("scale", c_float),
+        ("softclamp", c_float),
+        ("causal", c_int32),
+        ("flags", c_int32),
+        ("q", PaView),
+        ("k", PaView),
+        ("v", PaView),
+        ("vmul", PaView),
+        ("bias", PaView),
+        ("key_mask", PaMask),
+        ("query_mask", PaMask),
+        ("out", PaView),
+        ("lse", PaView),
+    ]
+
+
+class PaPassGrad(ctypes.Structure):
+    _fields_ = [
+        ("fwd", PaPass),
+        ("dout", PaView),
+        ("dlse", PaView),
+        ("dq", PaView),
+        ("dk", PaView),
+        ("dv", PaView),
+        ("dvmul", PaView),
+        ("dbias", PaView),
+        ("accumulate", c_int32),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
+class PaDecodeLevel(ctypes.Structure):
+    _fields_ = [
+        ("q", PaView),
+        ("k", PaView),
+        ("v", PaView),
+        ("vmul", PaView),
+        ("bias", PaView),
+        ("out", PaView),
+        ("lse", PaView),
+        ("heads", c_int32),
+    ]
+
+
+class PaDecode(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int32),
+        ("kv_heads", c_int32),
+        ("n", c_int32),
+        ("dim", c_int32),
+        ("order", c_int32),
+        ("scale", c_float),
+        ("softclamp", c_float),
+        ("chunk", c_int32),
+        ("levels", PaDecodeLevel * PA_MAX_ORDER),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
+STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode)
+
+
+class PolyAttnError(RuntimeError):
+    """A libpolyattn call returned a failure status."""
+
+    def __init__(self, status: int, what: str, lib=None):
+        msg = f"{what}: libpolyattn status {status}"
+        if lib is not None:
+            msg += f" ({lib.pa_strerror(status).decode()})"
+            if status == PA_EHIP:
+                msg += f", hipError {lib.pa_last_hip_error()}"
+        super().__init__(msg)
+        self.status = status
+
+
+_LIB = None
+_LOAD_ERROR: Exception | None = None
+
+
+def _configure(lib) -> None:
+    lib.pa_abi_version.restype = c_int
+    lib.pa_strerror.restype = ctypes.c_char_p
+    lib.pa_strerror.argtypes = [c_int]
+    lib.pa_last_hip_error.restype = c_int
+    lib.pa_struct_size.restype = c_size_t
+    lib.pa_struct_size.argtypes = [c_int]
+    lib.pa_attn_pass_fwd.restype = c_int
+    lib.pa_attn_pass_fwd.argtypes = [ctypes.POINTER(PaPass), c_void_p]
+    lib.pa_attn_pass_bwd_workspace.restype = c_size_t
+    lib.pa_attn_pass_bwd_workspace.argtypes = [ctypes.POINTER(PaPassGrad)]
+    lib.pa_attn_pass_bwd.restype = c_int
+    lib.pa_attn_pass_bwd.argtypes = [ctypes.POINTER(PaPassGrad), c_void_p]
+    lib.pa_poly_decode_workspace.restype = c_size_t
+    lib.pa_poly_decode_workspace.argtypes = [ctypes.POINTER(PaDecode)]
+    lib.pa_poly_decode.restype = c_int
+    lib.pa_poly_decode.argtypes = [ctypes.POINTER(PaDecode), c_void_p]
+
+
+def load(path: str | os.PathLike | None = None):
+    """Load libpolyattn.so (once); raises when it is missing or its ABI does not match."""
+    global _LIB, _LOAD_ERROR
+    if _LIB is not None:
+        return _LIB
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(
+            f"{p} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+            "or `python poly-attention_amd/poly_attention/_build.py`"
+        )
+    lib = ctypes.CDLL(str(p))
+    _configure(lib)
+    ver = lib.pa_abi_version()
+    if ver != PA_ABI_VERSION:
+        raise RuntimeError(f"libpolyattn ABI {ver} != expected {PA_ABI_VERSION}")
+    for i, st in enumerate(STRUCTS):
+        if lib.pa_struct_size(i) != ctypes.sizeof(st):
+            raise RuntimeError(
+                f"libpolyattn struct {st.__name__}: C size {lib.pa_struct_size(i)} "
+                f"!= ctypes size {ctypes.sizeof(st)}"
+            )
+    _LIB = lib
+    return lib
+
+
+def available() -> bool:
+    """True when libpolyattn.so loads (does not initialise the GPU)."""
+    global _LOAD_ERROR
+    try:
+        load()
+        return True
+    except Exception as e:  # noqa: BLE001 - reported through load_error()
+        _LOAD_ERROR = e
+        return False
+
+
+def load_error() -> Exception | None:
+    return _LOAD_ERROR
+
+
+def check(status: int, what: str) -> None:
+    if status != PA_OK:
+        raise PolyAttnError(status, what, _LIB)

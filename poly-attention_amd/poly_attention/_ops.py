@@ -1,0 +1,361 @@
+"""Host side of the HIP poly-attention path: tensors -> ABI structs -> libpolyattn.
+
+* ``polyattn::pass_fwd`` / ``polyattn::pass_bwd`` -- one attention pass (one level of the
+  poly chain) as torch custom ops with fake (meta) kernels and autograd, so torch.compile
+  and autocast see an opaque, differentiable op.  They are registered for CUDA (HIP)
+  devices only: there is no CPU implementation, the product path fails loudly without the
+  library.
+* ``poly_chain`` -- the order-n forward of poly_attention.py:48-116 / n_poly_attention.py:
+  233-313 as a right-to-left sequence of passes (each level's lse is the next level's key
+  bias, each level's output its value, multiplied by that level's v in the middle levels).
+* ``poly_decode_step`` -- the cached single-token step through ``pa_poly_decode``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import (
+    DTYPE_CODE,
+    PA_FLAG_MAY_DEGENERATE,
+    PaDecode,
+    PaMask,
+    PaPass,
+    PaPassGrad,
+    PaView,
+)
+
+# ---------------------------------------------------------------------------------------
+# marshalling
+
+
+def _inner_contig(t: Tensor) -> Tensor:
+    return t if t.stride(-1) == 1 or t.shape[-1] == 1 else t.contiguous()
+
+
+def _view(t: Optional[Tensor]) -> PaView:
+    v = PaView()
+    if t is None:
+        return v
+    assert t.dim() in (3, 4), "expected a [batch, heads, n(, dim)] tensor"
+    if t.dim() == 4:
+        assert t.stride(-1) == 1 or t.shape[-1] == 1, "feature stride must be 1"
+    v.ptr = t.data_ptr()
+    v.sb, v.sh, v.sn = t.stride(0), t.stride(1), t.stride(2)
+    v.heads = t.shape[1]
+    v.dtype = DTYPE_CODE[t.dtype]
+    return v
+
+
+def _mask(m: Optional[Tensor]) -> PaMask:
+    pm = PaMask()
+    if m is None:
+        return pm
+    assert m.dtype == torch.uint8 and m.dim() == 2
+    pm.ptr = m.data_ptr()
+    pm.sb, pm.sn = m.stride(0), m.stride(1)
+    return pm
+
+
+def _mask_u8(m: Optional[Tensor]) -> Optional[Tensor]:
+    if m is None:
+        return None
+    return m.to(torch.uint8)
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _pass_struct(q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal, softclamp, scale,
+                 may_degenerate) -> PaPass:
+    p = PaPass()
+    p.batch, p.heads, p.nq, p.dim = q.shape[0], out.shape[1], q.shape[2], q.shape[3]
+    p.nk = k.shape[2]
+    p.scale = float(scale)
+    p.softclamp = float(softclamp) if softclamp else 0.0
+    p.causal = int(bool(causal))
+    p.flags = PA_FLAG_MAY_DEGENERATE if may_degenerate else 0
+    p.q, p.k, p.v = _view(q), _view(k), _view(v)
+    p.vmul, p.bias = _view(vmul), _view(bias)
+    p.key_mask, p.query_mask = _mask(key_mask), _mask(query_mask)
+    p.out, p.lse = _view(out), _view(lse)
+    return p
+
+
+def _pass_heads(q, k, v, vmul, bias) -> int:
+    return max(t.shape[1] for t in (q, k, v, vmul, bias) if t is not None)
+
+
+def _check_pass_inputs(q, k, v, vmul, bias, key_mask, query_mask):
+    assert q.dim() == k.dim() == v.dim() == 4, "q, k, v must be [batch, heads, n, dim]"
+    assert q.dtype == k.dtype == v.dtype, "q, k, v must share one dtype"
+    assert q.dtype in DTYPE_CODE, f"unsupported dtype {q.dtype}"
+    assert k.shape[2] == v.shape[2], "k and v must have the same length"
+    assert q.shape[-1] == k.shape[-1] == v.shape[-1], "q, k, v must share the head dim"
+    if vmul is not None:
+        assert vmul.dtype == v.dtype and vmul.shape[2] == v.shape[2]
+    if bias is not None:
+        assert bias.dim() == 3 and bias.shape[2] == k.shape[2]
+    if key_mask is not None:
+        assert key_mask.shape == (k.shape[0], k.shape[2])
+    if query_mask is not None:
+        assert query_mask.shape == (q.shape[0], q.shape[2])
+
+
+# ---------------------------------------------------------------------------------------
+# one pass: raw calls
+
+
+def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale,
+                 may_degenerate) -> tuple[Tensor, Tensor]:
+    lib = _lib.load()
+    q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
+    vmul = _inner_contig(vmul) if vmul is not None else None
+    _check_pass_inputs(q, k, v, vmul, bias, key_mask, query_mask)
+    km, qm = _mask_u8(key_mask), _mask_u8(query_mask)
+    B, _, nq, d = q.shape
+    H = _pass_heads(q, k, v, vmul, bias)
+    out = torch.empty(B, H, nq, d, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, H, nq, dtype=torch.float32, device=q.device)
+    p = _pass_struct(q, k, v, vmul, bias, km, qm, out, lse, causal, softclamp, scale,
+                     may_degenerate or km is not None or qm is not None)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.pa_attn_pass_fwd(ctypes.byref(p), _stream(q)), "pa_attn_pass_fwd")
+    return out, lse
+
+
+def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal,
+                 softclamp, scale, may_degenerate):
+    lib = _lib.load()
+    q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
+    vmul = _inner_contig(vmul) if vmul is not None else None
+    dout = _inner_contig(dout).to(q.dtype)
+    km, qm = _mask_u8(key_mask), _mask_u8(query_mask)
+    H = out.shape[1]
+    if q.shape[1] != H:
+        # queries shared by several pass heads: the backward wants them per pass head (the
+        # caller sums the per-head dq back)
+        q = q.repeat_interleave(H // q.shape[1], dim=1)
+    hk = k.shape[1]
+    key_side = [t for t in (v, vmul, bias) if t is not None]
+    assert all(t.shape[1] == hk for t in key_side), \
+        "backward: k, v, vmul and bias must share one head count"
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    dvmul = torch.empty(vmul.shape, dtype=v.dtype, device=v.device) if vmul is not None else None
+    dbias = (torch.empty(bias.shape, dtype=torch.float32, device=q.device)
+             if bias is not None else None)
+    dlse32 = dlse.float() if dlse is not None else None
+    g = PaPassGrad()
+    g.fwd = _pass_struct(q, k, v, vmul, bias, km, qm, out, lse, causal, softclamp, scale,
+                         may_degenerate or km is not None or qm is not None)
+    g.dout, g.dlse = _view(dout), _view(dlse32)
+    g.dq, g.dk, g.dv = _view(dq), _view(dk), _view(dv)
+    g.dvmul, g.dbias = _view(dvmul), _view(dbias)
+    g.accumulate = 0
+    ws_bytes = lib.pa_attn_pass_bwd_workspace(ctypes.byref(g))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    g.workspace, g.workspace_bytes = ws.data_ptr(), ws_bytes
+    with torch.cuda.device(q.device):
+        _lib.check(lib.pa_attn_pass_bwd(ctypes.byref(g), _stream(q)), "pa_attn_pass_bwd")
+    if dbias is not None and bias is not None and dbias.dtype != bias.dtype:
+        dbias = dbias.to(bias.dtype)
+    return dq, dk, dv, dvmul, dbias
+
+
+# ---------------------------------------------------------------------------------------
+# custom ops
+
+
+@torch.library.custom_op("polyattn::pass_fwd", mutates_args=(), device_types="cuda")
+def pass_fwd_op(q: Tensor, k: Tensor, v: Tensor, vmul: Optional[Tensor], bias: Optional[Tensor],
+                key_mask: Optional[Tensor], query_mask: Optional[Tensor], causal: bool,
+                softclamp: float, scale: float, may_degenerate: bool) -> tuple[Tensor, Tensor]:
+    return pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale,
+                        may_degenerate)
+
+
+@pass_fwd_op.register_fake
+def _(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale, may_degenerate):
+    B, _, nq, d = q.shape
+    H = _pass_heads(q, k, v, vmul, bias)
+    return (q.new_empty(B, H, nq, d), q.new_empty(B, H, nq, dtype=torch.float32))
+
+
+@torch.library.custom_op("polyattn::pass_bwd", mutates_args=(), device_types="cuda")
+def pass_bwd_op(dout: Tensor, dlse: Optional[Tensor], q: Tensor, k: Tensor, v: Tensor,
+                vmul: Optional[Tensor], bias: Optional[Tensor], key_mask: Optional[Tensor],
+                query_mask: Optional[Tensor], out: Tensor, lse: Tensor, causal: bool,
+                softclamp: float, scale: float,
+                may_degenerate: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    dq, dk, dv, dvmul, dbias = pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask,
+                                            query_mask, out, lse, causal, softclamp, scale,
+                                            may_degenerate)
+    if dvmul is None:
+        dvmul = q.new_empty(0)
+    if dbias is None:
+        dbias = q.new_empty(0)
+    return dq, dk, dv, dvmul, dbias
+
+
+@pass_bwd_op.register_fake
+def _(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal, softclamp, scale,
+      may_degenerate):
+    H = out.shape[1]
+    dq = q.new_empty(q.shape[0], H, *q.shape[2:]) if q.shape[1] != H else q.new_empty(q.shape)
+    dvmul = vmul.new_empty(vmul.shape) if vmul is not None else q.new_empty(0)
+    dbias = bias.new_empty(bias.shape) if bias is not None else q.new_empty(0)
+    return dq, k.new_empty(k.shape), v.new_empty(v.shape), dvmul, dbias
+
+
+def _pass_setup(ctx, inputs, output):
+    q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale, may_degenerate = inputs
+    out, lse = output
+    ctx.save_for_backward(q, k, v, vmul, bias, key_mask, query_mask, out, lse)
+    ctx.causal, ctx.softclamp, ctx.scale = causal, softclamp, scale
+    ctx.may_degenerate = may_degenerate
+    ctx.has_vmul, ctx.has_bias = vmul is not None, bias is not None
+    ctx.set_materialize_grads(False)
+
+
+def _pass_backward(ctx, dout, dlse):
+    q, k, v, vmul, bias, key_mask, query_mask, out, lse = ctx.saved_tensors
+    if dout is None:
+        dout = torch.zeros_like(out)
+    dq, dk, dv, dvmul, dbias = pass_bwd_op(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask,
+                                           out, lse, ctx.causal, ctx.softclamp, ctx.scale,
+                                           ctx.may_degenerate)
+    if dq.shape[1] != q.shape[1]:  # queries were shared across pass heads: sum their grads
+        dq = dq.unflatten(1, (q.shape[1], -1)).sum(2)
+    return (dq, dk, dv, dvmul if ctx.has_vmul else None, dbias if ctx.has_bias else None,
+            None, None, None, None, None, None)
+
+
+torch.library.register_autograd("polyattn::pass_fwd", _pass_backward, setup_context=_pass_setup)
+
+
+def attn_pass(q: Tensor, k: Tensor, v: Tensor, vmul: Optional[Tensor] = None,
+              bias: Optional[Tensor] = None, key_mask: Optional[Tensor] = None,
+              query_mask: Optional[Tensor] = None, causal: bool = False,
+              softclamp: Optional[float] = None, scale: Optional[float] = None,
+              may_degenerate: bool = False) -> tuple[Tensor, Tensor]:
+    """One differentiable attention pass on the GPU: returns (out, lse[fp32])."""
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    return pass_fwd_op(q, k, v, vmul, bias, key_mask, query_mask, bool(causal),
+                       float(softclamp or 0.0), float(scale), bool(may_degenerate))
+
+
+# ---------------------------------------------------------------------------------------
+# the order-n chain
+
+
+def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence[Tensor], *,
+               causal: bool, softclamp: Optional[float], scale: float,
+               query_mask: Optional[Tensor] = None,
+               key_masks: Optional[Sequence[Optional[Tensor]]] = None,
+               may_degenerate: bool = False):
+    """Order-n poly attention through HIP passes.
+
+    q_left[l] . q_right[l] are the scores of level l (l = 0 is q1 . q2); vs are the values
+    v_3 .. v_{n+1}.  Returns (out, lses, msgs) with lses / msgs ordered deepest level first
+    (the reference's cache order, n_poly_attention.py:268-305).
+    """
+    n = len(q_left)
+    assert len(q_right) == n and len(vs) == n - 1 and n >= 2
+    key_masks = list(key_masks) if key_masks is not None else [None] * n
+    may_degenerate = may_degenerate or query_mask is not None or any(
+        m is not None for m in key_masks)
+    lses, msgs = [], []
+    msg_next = lse_next = None
+    out = None
+    for lvl in range(n - 1, -1, -1):
+        if lvl == n - 1:
+            v, vmul, bias = vs[-1], None, None
+        elif lvl == 0:
+            v, vmul, bias = msg_next, None, lse_next
+        else:
+            v, vmul, bias = vs[lvl - 1], msg_next, lse_next
+        o, lse = attn_pass(q_left[lvl], q_right[lvl], v, vmul, bias,
+                           key_mask=key_masks[lvl],
+                           query_mask=query_mask if lvl == 0 else None,
+                           causal=causal, softclamp=softclamp, scale=scale,
+                           may_degenerate=may_degenerate)
+        if lvl > 0:
+            msgs.append(o)
+            lses.append(lse)
+            msg_next, lse_next = o, lse
+        else:
+            out = o
+    return out, lses, msgs
+
+
+# ---------------------------------------------------------------------------------------
+# decode
+
+
+def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
+                     v_caches: Sequence[Tensor], msg_caches: Sequence[Tensor],
+                     lse_caches: Sequence[Tensor], *, kv_heads: int, heads: int,
+                     softclamp: Optional[float], scale: float, chunk: int = 0) -> Tensor:
+    """One cached decode step through pa_poly_decode (no autograd).
+
+    Level l (l = 0: q1 . q2) has query q_new[l] [B, h, 1, d] and keys k_caches[l]
+    [B, kv_heads, n, d] whose position n-1 already holds the new token.  v_caches are the
+    value caches v_3 .. v_{n+1}; msg_caches / lse_caches (deepest first, the reference's
+    order) hold n positions whose slot n-1 this call fills.  Returns the output [B, heads, 1, d].
+    """
+    lib = _lib.load()
+    order = len(q_new)
+    assert len(k_caches) == order and len(v_caches) == order - 1
+    assert len(msg_caches) == order - 1 and len(lse_caches) == order - 1
+    B, _, n, d = k_caches[0].shape
+    dt = q_new[0].dtype
+    out = torch.empty(B, heads, 1, d, dtype=dt, device=q_new[0].device)
+    D = PaDecode()
+    D.batch, D.kv_heads, D.n, D.dim, D.order = B, kv_heads, n, d, order
+    D.scale = float(scale)
+    D.softclamp = float(softclamp) if softclamp else 0.0
+    D.chunk = int(chunk)
+    keep = []
+    # pa_decode level t = chain level lvl = order - 1 - t (chain level lvl scores
+    # q_{lvl+1} . q_{lvl+2}); the msg / lse caches list the deepest level first, so level
+    # lvl >= 1 writes cache index order-1-lvl and level lvl <= order-2 reads index order-2-lvl
+    for t in range(order):
+        lvl = order - 1 - t
+        L = D.levels[t]
+        q = _inner_contig(q_new[lvl])
+        keep.append(q)
+        L.q, L.k = _view(q), _view(k_caches[lvl])
+        if t == 0:
+            L.v = _view(v_caches[-1])
+            heads_t = max(q.shape[1], v_caches[-1].shape[1])
+        else:
+            src = order - 2 - lvl
+            if lvl == 0:
+                L.v = _view(msg_caches[src])
+                heads_t = heads
+            else:
+                L.v = _view(v_caches[lvl - 1])
+                L.vmul = _view(msg_caches[src])
+                heads_t = max(q.shape[1], msg_caches[src].shape[1], lse_caches[src].shape[1])
+            L.bias = _view(lse_caches[src])
+        if lvl == 0:
+            L.out = _view(out)
+        else:
+            dst = order - 1 - lvl
+            L.out = _view(msg_caches[dst].narrow(2, n - 1, 1))
+            L.lse = _view(lse_caches[dst].narrow(2, n - 1, 1))
+        L.heads = heads_t
+    ws_bytes = lib.pa_poly_decode_workspace(ctypes.byref(D))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=out.device)
+    D.workspace, D.workspace_bytes = ws.data_ptr(), ws_bytes
+    with torch.cuda.device(out.device):
+        _lib.check(lib.pa_poly_decode(ctypes.byref(D), _stream(out)), "pa_poly_decode")
+    return out

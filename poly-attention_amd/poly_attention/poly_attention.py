@@ -1,0 +1,384 @@
+"""Order-2 poly attention (Chakrabarti et al., https://arxiv.org/abs/2602.02422).
+
+Drop-in for ``poly_attention/poly_attention.py`` of lucidrains/poly-attention 0.3.6: same
+``reference_poly_attention`` function, same ``Order2PolyAttention`` constructor, forward
+signature, parameter names / creation order and KV-cache tuple.  On GPU tensors the
+attention core runs in the HIP kernels of libpolyattn (fused forward and backward passes,
+split-K decode); ``reference_poly_attention`` is the reference's eager formulation and
+serves CPU tensors and ``use_flash_kernel=False``.
+"""
+
+from __future__ import annotations
+
+from functools import partial
+
+import torch
+from torch import Tensor, einsum, nn
+from torch.nn import Module, RMSNorm
+
+from einops.layers.torch import Rearrange
+
+from . import _cache, _lib
+from ._helpers import (
+    add_key_bias,
+    cast_tuple,
+    default,
+    divisible_by,
+    exists,
+    first,
+    maybe,
+    repeat_kv,
+    safe_cat,
+    softclamp,
+    where_keys,
+    where_queries,
+)
+from .rotary import RotaryEmbedding, apply_rotary_emb
+
+LinearNoBias = partial(nn.Linear, bias=False)
+
+
+def fused_available() -> bool:
+    """The HIP path's plugin switch: libpolyattn.so loads (poly_attention.py:17-20)."""
+    return _lib.available()
+
+
+# attention
+
+
+def reference_poly_attention(q1, q2_pass1, q2_pass2, q3, v3, mask=None, context_mask=None,
+                             softclamp_value=None, causal=False, cache=None):
+    """Eager order-2 poly attention, as poly_attention.py:48-116.
+
+    Pass 1 (q2 attends to q3) gives lse23 and msg; pass 2 (q1 attends to q2) adds lse23 as a
+    key bias and aggregates msg.  Masked scores take the finite value -finfo.max.
+    Returns (out, lse23_step, msg_step).
+    """
+    scale = q1.shape[-1] ** -0.5
+    has_cache = exists(cache)
+    context_mask1, context_mask2 = context_mask if exists(context_mask) else (None, None)
+
+    sim23 = einsum("b h i d, b h j d -> b h i j", q2_pass1, q3) * scale
+    if exists(softclamp_value):
+        sim23 = softclamp(sim23, softclamp_value)
+    mask_value = -torch.finfo(sim23.dtype).max
+    if causal and not has_cache:
+        i, j = sim23.shape[-2:]
+        causal_mask = torch.ones((i, j), device=sim23.device, dtype=torch.bool).triu(1)
+        sim23 = sim23.masked_fill(causal_mask, mask_value)
+    if exists(context_mask2):
+        sim23 = where_keys(context_mask2, sim23, mask_value)
+
+    lse23_step = sim23.logsumexp(dim=-1)
+    attn23 = sim23.softmax(dim=-1)
+    msg_step = einsum("b h i j, b h j d -> b h i d", attn23, v3)
+
+    _, _, _, clse23, cmsg = cache if has_cache else (None, None, None, None, None)
+    lse23 = safe_cat((clse23, lse23_step), dim=-1)
+    msg = safe_cat((cmsg, msg_step), dim=-2)
+
+    sim12 = einsum("b h i d, b h j d -> b h i j", q1, q2_pass2) * scale
+    if exists(softclamp_value):
+        sim12 = softclamp(sim12, softclamp_value)
+    if causal and not has_cache:
+        i, j = sim12.shape[-2:]
+        causal_mask = torch.ones((i, j), device=sim12.device, dtype=torch.bool).triu(1)
+        sim12 = sim12.masked_fill(causal_mask, mask_value)
+    if exists(context_mask1):
+        sim12 = where_keys(context_mask1, sim12, mask_value)
+    if exists(mask):
+        sim12 = where_queries(mask, sim12, mask_value)
+
+    sim12 = add_key_bias(lse23.to(sim12.dtype), sim12)
+    attn12 = sim12.softmax(dim=-1)
+    out = einsum("b h i j, b h j d -> b h i d", attn12, msg.to(attn12.dtype))
+    return out, lse23_step, msg_step
+
+
+def _compute_dtype(*ts: Tensor) -> torch.dtype:
+    if torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    dt = ts[0].dtype
+    for t in ts[1:]:
+        dt = torch.promote_types(dt, t.dtype)
+    return dt
+
+
+# poly attention
+
+
+class Order2PolyAttention(Module):
+    """Order-2 poly attention module (poly_attention.py:120-365)."""
+
+    def __init__(self, dim, heads=8, kv_heads=None, dim_head=64, causal=False, shared_kv=False,
+                 softclamp_value=None, use_rotary_embed=False, prenorm=False,
+                 separate_context_norms=False, multiply_root_value=False,
+                 use_root_value_as_attn_gate=False, attn_gate=False, use_flash_kernel=None):
+        super().__init__()
+        self.norm = RMSNorm(dim) if prenorm else nn.Identity()
+
+        self.context_norms = None
+        if separate_context_norms and prenorm:
+            self.context_norms = nn.ModuleList([RMSNorm(dim), RMSNorm(dim)])
+
+        # use_flash_kernel: None = the HIP path whenever libpolyattn loads and the tensors are
+        # on the GPU; True = demand it; False = always eager
+        self._flash_requested = use_flash_kernel
+        self.use_flash_kernel = default(use_flash_kernel, fused_available())
+        assert not (self.use_flash_kernel and not fused_available()), \
+            "fused poly attention is not available"
+
+        self.scale = dim_head ** -0.5
+
+        kv_heads = default(kv_heads, heads)
+        assert divisible_by(heads, kv_heads), "heads must be divisible by kv_heads"
+
+        self.heads = heads
+        self.kv_heads = kv_heads
+
+        dim_inner = dim_head * heads
+        dim_inner_kv = dim_head * kv_heads
+
+        self.causal = causal
+        self.shared_kv = shared_kv
+        self.softclamp_value = softclamp_value
+        self.multiply_root_value = multiply_root_value
+        self.use_root_value_as_attn_gate = use_root_value_as_attn_gate
+        self.attn_gate = attn_gate
+
+        self.is_gqa = heads != kv_heads
+
+        assert not (use_root_value_as_attn_gate and (self.is_gqa or self.shared_kv)), \
+            "cannot use root value as attention gate if using GQA or shared KV"
+
+        q_split = 2 if attn_gate else 1
+        self.split_q = Rearrange("b n (split h d) -> split b h n d", split=q_split, h=self.heads)
+
+        self.has_root_v = multiply_root_value and not shared_kv
+        kv1_split = 2 if self.has_root_v else 1
+        self.split_kv1 = Rearrange("b n (split h d) -> split b h n d", split=kv1_split,
+                                   h=self.kv_heads)
+
+        kv_split = 1 if self.shared_kv else 2
+        self.split_kv = Rearrange("b n (split h d) -> split b h n d", split=kv_split,
+                                  h=self.kv_heads)
+
+        self.merge_heads = Rearrange("b h n d -> b n (h d)")
+
+        if self.is_gqa:
+            self.num_rep = heads // kv_heads
+
+        self.to_q = LinearNoBias(dim, dim_inner * q_split)
+
+        kv_mult = 1 if shared_kv else 2
+        self.to_kvs = nn.ModuleList([
+            LinearNoBias(dim, dim_inner_kv * kv1_split),
+            LinearNoBias(dim, dim_inner_kv * kv_mult),
+        ])
+
+        self.q_norms = nn.ModuleList([RMSNorm(dim_head), RMSNorm(dim_head), RMSNorm(dim_head)])
+
+        self.rotary_emb = RotaryEmbedding(dim_head) if use_rotary_embed else None
+
+        self.to_out = nn.Linear(dim_inner, dim)
+
+    # -------------------------------------------------------------------------------------
+
+    def _use_fused(self, t: Tensor) -> bool:
+        if not self.use_flash_kernel or not t.is_cuda:
+            return False
+        _lib.load()  # a GPU tensor with the fused path requested: a missing library is fatal
+        return True
+
+    def forward(self, x, context: Tensor | tuple[Tensor, ...] | None = None, mask=None,
+                context_mask: Tensor | tuple[Tensor | None, ...] | None = None,
+                rotary_pos_emb=None, cache=None, return_cache=False):
+        seq_len, device = x.shape[-2], x.device
+
+        has_cache = exists(cache)
+        if has_cache:
+            assert seq_len == 1, "sequence length must be 1 when using kv cache"
+
+        orig_x = x
+        x = self.norm(x)
+
+        q_and_maybe_gates = self.split_q(self.to_q(x))
+        if self.attn_gate:
+            q1, gates = q_and_maybe_gates
+        else:
+            q1 = first(q_and_maybe_gates)
+
+        # contexts
+
+        has_context = exists(context)
+        context = default(context, orig_x)
+        context = cast_tuple(context, 2)
+        assert len(context) == 2
+
+        if self.multiply_root_value:
+            assert first(context).shape[-2] == seq_len, (
+                "first context sequence length (context[0]) must match base sequence x when "
+                "multiply_root_value is True")
+
+        explicit_context_mask = exists(context_mask)
+        if exists(context_mask):
+            context_mask = cast_tuple(context_mask, 2)
+            assert len(context_mask) == 2
+        elif not has_context and exists(mask):
+            context_mask = (mask, mask)
+        else:
+            context_mask = (None, None)
+
+        if exists(self.context_norms):
+            ctx1, ctx2 = (norm(c) for c, norm in zip(context, self.context_norms))
+        else:
+            ctx1, ctx2 = context if has_context else (x, x)
+
+        # kvs
+
+        kv1 = self.split_kv1(first(self.to_kvs)(ctx1))
+        kv2 = self.split_kv(self.to_kvs[1](ctx2))
+
+        if self.shared_kv:
+            qs = (q1, first(kv1), first(kv2))
+            v2, v3 = first(kv1), first(kv2)
+        else:
+            q2 = first(kv1)
+            v2 = kv1[1] if self.has_root_v else None
+            q3, v3 = kv2
+            qs = (q1, q2, q3)
+
+        qs = tuple(norm(q) for norm, q in zip(self.q_norms, qs))
+
+        if exists(rotary_pos_emb):
+            qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)
+
+        q1, q2, q3 = qs
+
+        # dispatch: the HIP kernels take every case on the GPU (masks, contexts, GQA, caches);
+        # an explicitly requested fused kernel still refuses an explicit context_mask, as the
+        # reference does (poly_attention.py:310)
+        if self._flash_requested is True and explicit_context_mask:
+            assert not any(exists(m) for m in context_mask), \
+                "context_mask is not supported in flash poly attention"
+
+        if self._use_fused(q1):
+            out, new_cache = self._fused_core(q1, q2, q3, v3, mask, context_mask, rotary_pos_emb,
+                                              cache, return_cache)
+            v2 = repeat_kv(v2, self.num_rep) if self.is_gqa else v2
+        else:
+            out, new_cache, v2 = self._eager_core(q1, q2, q3, v2, v3, mask, context_mask,
+                                                  rotary_pos_emb, cache, return_cache)
+
+        # elementwise multiply root values
+
+        if self.multiply_root_value:
+            if self.use_root_value_as_attn_gate:
+                v2 = v2.sigmoid()
+            out = v2 * out
+
+        if self.attn_gate:
+            out = out * gates.sigmoid()
+
+        out = self.to_out(self.merge_heads(out))
+
+        if not return_cache:
+            return out
+        return out, new_cache
+
+    # -------------------------------------------------------------------------------------
+
+    def _eager_core(self, q1, q2, q3, v2, v3, mask, context_mask, rotary_pos_emb, cache,
+                    return_cache):
+        """poly_attention.py:283-365 (eager path)."""
+        has_cache = exists(cache)
+        cq2, cq3, cv3, clse23, cmsg = cache if has_cache else (None, None, None, None, None)
+
+        q2_cache = safe_cat((cq2, q2), dim=-2)
+        q3_cache = safe_cat((cq3, q3), dim=-2)
+        v3_cache = safe_cat((cv3, v3), dim=-2)
+
+        if self.is_gqa:
+            match_kv = maybe(lambda t: repeat_kv(t, self.num_rep))
+            q2, q3, v2, v3 = map(match_kv, (q2, q3, v2, v3))
+            q2_full, q3_full, v3_full = map(match_kv, (q2_cache, q3_cache, v3_cache))
+        else:
+            q2_full, q3_full, v3_full = q2_cache, q3_cache, v3_cache
+
+        q2_left = q2
+        q2_right = q2_full
+
+        if not exists(rotary_pos_emb) and exists(self.rotary_emb):
+            q1, q2_right = self.rotary_emb.rotate_queries_with_cached_keys(q1, q2_right)
+            q2_left, q3_full = self.rotary_emb.rotate_queries_with_cached_keys(q2_left, q3_full)
+
+        out, lse23_step, msg_step = reference_poly_attention(
+            q1, q2_left, q2_right, q3_full, v3_full, mask=mask, context_mask=context_mask,
+            softclamp_value=self.softclamp_value, causal=self.causal, cache=cache)
+
+        new_cache = None
+        if return_cache:
+            lse23_full = safe_cat((clse23, lse23_step), dim=-1)
+            msg_full = safe_cat((cmsg, msg_step), dim=-2)
+            new_cache = (q2_cache, q3_cache, v3_cache, lse23_full, msg_full)
+        return out, new_cache, v2
+
+    def _fused_core(self, q1, q2, q3, v3, mask, context_mask, rotary_pos_emb, cache,
+                    return_cache):
+        """The attention core on the HIP kernels; q2 / q3 / v3 stay at kv_heads."""
+        from . import _ops
+
+        rep = self.num_rep if self.is_gqa else 1
+        dt = _compute_dtype(q1, q2, q3, v3)
+        q1, q2, q3, v3 = (t.to(dt) for t in (q1, q2, q3, v3))
+        module_rotary = not exists(rotary_pos_emb) and exists(self.rotary_emb)
+
+        if not exists(cache):
+            q1r, q2r_right, q2r_left, q3r = q1, q2, q2, q3
+            if module_rotary:
+                q1r, q2r_right = self.rotary_emb.rotate_queries_with_cached_keys(q1, q2)
+                q2r_left, q3r = self.rotary_emb.rotate_queries_with_cached_keys(q2, q3)
+            out, lses, msgs = _ops.poly_chain(
+                [q1r, q2r_left], [q2r_right, q3r], [v3], causal=self.causal,
+                softclamp=self.softclamp_value, scale=self.scale, query_mask=mask,
+                key_masks=list(context_mask))
+            new_cache = None
+            if return_cache:
+                lse23 = repeat_kv(lses[0][:, :, :, None], rep)[..., 0]
+                msg = repeat_kv(msgs[0], rep)
+                new_cache = (_cache.adopt(q2, -2), _cache.adopt(q3, -2), _cache.adopt(v3, -2),
+                             _cache.adopt(lse23, -1), _cache.adopt(msg, -2))
+            return out, new_cache
+
+        # cached single-token step (poly_attention.py:283-287, 331-338, 360-365)
+        cq2, cq3, cv3, clse23, cmsg = cache
+        q2_cache = _cache.append(cq2, q2.to(cq2.dtype), -2)
+        q3_cache = _cache.append(cq3, q3.to(cq3.dtype), -2)
+        v3_cache = _cache.append(cv3, v3.to(cv3.dtype), -2)
+        q1r, q2_left, q2_right, q3_full = q1, q2, q2_cache, q3_cache
+        if module_rotary:
+            q1r, q2_right = self.rotary_emb.rotate_queries_with_cached_keys(q1, q2_cache)
+            q2_left, q3_full = self.rotary_emb.rotate_queries_with_cached_keys(q2, q3_cache)
+
+        needs_grad = torch.is_grad_enabled() and any(
+            t.requires_grad for t in (q1, q2, q3, v3, cq2, cq3, cv3, clse23, cmsg))
+        if needs_grad:
+            # differentiable step: the two passes as autograd ops (the reference's math)
+            msg_step, lse_step = _ops.attn_pass(q2_left, q3_full, v3_cache,
+                                                softclamp=self.softclamp_value,
+                                                scale=self.scale)
+            lse_step_h = repeat_kv(lse_step[:, :, :, None], rep)[..., 0]
+            lse23_full = torch.cat((clse23, lse_step_h.to(clse23.dtype)), dim=-1)
+            msg_full = torch.cat((cmsg, repeat_kv(msg_step, rep).to(cmsg.dtype)), dim=-2)
+            out, _ = _ops.attn_pass(q1r, repeat_kv(q2_right, rep), msg_full, bias=lse23_full,
+                                    softclamp=self.softclamp_value, scale=self.scale,
+                                    may_degenerate=True)
+            return out, (q2_cache, q3_cache, v3_cache, lse23_full, msg_full)
+
+        lse23_full = _cache.reserve(clse23, clse23[:, :, :1], -1)
+        msg_full = _cache.reserve(cmsg, cmsg[:, :, :1], -2)
+        out = _ops.poly_decode_step(
+            [q1r, q2_left], [q2_right, q3_full], [v3_cache], [msg_full], [lse23_full],
+            kv_heads=self.kv_heads, heads=self.heads, softclamp=self.softclamp_value,
+            scale=self.scale)
+        return out, (q2_cache, q3_cache, v3_cache, lse23_full, msg_full)

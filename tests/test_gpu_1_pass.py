@@ -1,0 +1,134 @@
+"""GPU parity of single attention passes (libpolyattn through its C ABI) vs the CPU oracle.
+
+Tolerances (the north star's): fp32 -- max-abs error <= 1e-4; bf16 / f16 -- max-abs error
+<= 2e-2 against the fp32 oracle evaluated on the same low-precision-rounded inputs.  Both are
+applied as max-abs error / max(1, max|reference|): outputs and gradients of order 1 are held
+to the absolute bound, larger ones (gradients grow with the sequence length, products of two
+N(0,1) values feed the middle levels) to the same bound relative to their magnitude.
+"""
+
+import pytest
+import torch
+
+import oracle.poly_oracle as O
+
+pytestmark = pytest.mark.gpu
+param = pytest.mark.parametrize
+
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda")
+
+
+def randn(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+def max_err(a, b):
+    return (a.float().cpu() - b.float().cpu()).abs().max().item()
+
+
+def assert_close(got, ref, tol, what):
+    ref = ref.float().cpu()
+    err = max_err(got, ref)
+    denom = max(1.0, ref.abs().max().item())
+    assert err / denom <= tol, f"{what}: max-abs err {err:.3e} (ref max {ref.abs().max():.3e})"
+
+
+def run_pass(q, k, v, vmul=None, bias=None, key_mask=None, query_mask=None, causal=False,
+             softclamp=None, grads=True, seed=99):
+    """Run the HIP pass (autograd custom op) and the oracle on the same inputs."""
+    from poly_attention import _ops
+
+    d = dev()
+    inputs = [q, k, v, vmul, bias]
+    g_in = [t.detach().to(d).requires_grad_(grads) if t is not None else None for t in inputs]
+    o_in = [t.detach().float().clone().requires_grad_(grads) if t is not None else None
+            for t in inputs]
+    km = key_mask.to(d) if key_mask is not None else None
+    qm = query_mask.to(d) if query_mask is not None else None
+    out, lse = _ops.attn_pass(*g_in, key_mask=km, query_mask=qm, causal=causal,
+                              softclamp=softclamp)
+    ref_out, ref_lse = O.attn_pass(*o_in, key_mask=key_mask, query_mask=query_mask,
+                                   causal=causal, softclamp_value=softclamp)
+    res = dict(out=(out, ref_out), lse=(lse, ref_lse))
+    if grads:
+        do = randn(ref_out.shape, q.dtype, seed)
+        dl = randn(ref_lse.shape, torch.float32, seed + 1)
+        torch.autograd.backward((out, lse), (do.to(d), dl.to(d)))
+        torch.autograd.backward((ref_out, ref_lse), (do.float(), dl))
+        for name, a, b in zip(("dq", "dk", "dv", "dvmul", "dbias"), g_in, o_in):
+            if a is not None:
+                res[name] = (a.grad, b.grad)
+    torch.cuda.synchronize()
+    return res
+
+
+def check(res, dtype):
+    tol = TOL[dtype]
+    for name, (got, ref) in res.items():
+        if name == "lse":
+            got = got.float().cpu()
+            ok = ref > -1e30
+            assert_close(got[ok], ref[ok], max(tol, 1e-4), name)
+            assert bool((got[~ok] <= -1e30).all()), "fully-masked rows must keep lse = -finfo.max"
+            continue
+        assert_close(got, ref, tol, name)
+
+
+@param("dtype", (torch.float32, torch.bfloat16, torch.float16))
+@param("n", (31, 32, 127, 128))
+@param("causal", (False, True))
+@param("softclamp", (None, 20.0))
+def test_pass_basic(dtype, n, causal, softclamp):
+    """The reference's fused-op test grid (tests:213-240): N in {31,32,127,128}, d = 64."""
+    shape = (2, 4, n, 64)
+    q, k, v = (randn(shape, dtype, s) for s in (1, 2, 3))
+    check(run_pass(q, k, v, causal=causal, softclamp=softclamp), dtype)
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("d", (16, 32, 128))
+def test_pass_head_dims(dtype, d):
+    q, k, v = (randn((1, 2, 40, d), dtype, s) for s in (4, 5, 6))
+    check(run_pass(q, k, v, causal=True), dtype)
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("causal", (False, True))
+def test_pass_gqa_bias_vmul(dtype, causal):
+    """A middle level of the chain: queries at 8 heads over 2 KV heads, key bias (the deeper
+    level's lse) and a value multiplier (the deeper level's msg)."""
+    q = randn((2, 8, 50, 64), dtype, 7)
+    k, v, vmul = (randn((2, 2, 50, 64), dtype, s) for s in (8, 9, 10))
+    bias = randn((2, 2, 50), torch.float32, 11, scale=2.0)
+    check(run_pass(q, k, v, vmul=vmul, bias=bias, causal=causal), dtype)
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("causal", (False, True))
+def test_pass_masks_and_degenerate_rows(dtype, causal):
+    """Key / query masks with fully-masked rows (uniform over -finfo.max entries)."""
+    q, k, v = (randn((2, 2, 24, 32), dtype, s) for s in (12, 13, 14))
+    km = torch.ones(2, 24, dtype=torch.bool)
+    km[:, 17:] = False
+    km[1, 0] = False
+    qm = torch.ones(2, 24, dtype=torch.bool)
+    qm[0, 20:] = False
+    bias = randn((2, 2, 24), torch.float32, 15)
+    bias[1, 1, 5] = -torch.finfo(torch.float32).max
+    check(run_pass(q, k, v, bias=bias, key_mask=km, query_mask=qm, causal=causal), dtype)
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+def test_pass_cross_lengths(dtype):
+    """Different query and key lengths (contexts), causal with a top-left aligned mask."""
+    q = randn((2, 4, 20, 64), dtype, 16)
+    k, v = (randn((2, 4, 33, 64), dtype, s) for s in (17, 18))
+    check(run_pass(q, k, v, causal=True), dtype)
+    check(run_pass(q, k, v, causal=False), dtype)

@@ -1,0 +1,211 @@
+"""GPU parity of the drop-in modules and ops (HIP path) vs the CPU oracle.
+
+Same tolerances as test_gpu_1_pass.py: fp32 max-abs <= 1e-4; bf16 max-abs <= 2e-2 against
+the fp32 oracle on the same bf16-rounded inputs and weights, both as max-abs error /
+max(1, max|reference|).
+"""
+
+import math
+
+import pytest
+import torch
+
+import oracle.poly_oracle as O
+
+pytestmark = pytest.mark.gpu
+param = pytest.mark.parametrize
+
+
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda")
+
+
+def assert_close(got, ref, tol, what, grad=False):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    err = (got - ref).abs().max().item()
+    denom = max(1.0, ref.abs().max().item())
+    assert err / denom <= tol, f"{what}: max-abs err {err:.3e}"
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("causal", (False, True))
+@param("softclamp_value", (None, 20.0))
+@param("seq_len", (31, 32, 127, 128))
+def test_flash_poly_attention(dtype, causal, softclamp_value, seq_len):
+    """The reference's fused-op test (tests/test_poly_attention.py:213-240), fwd + 4 grads."""
+    from poly_attention.flash_poly_attention import flash_poly_attention
+
+    d = dev()
+    torch.manual_seed(42)
+    tensors = [torch.randn(2, 4, seq_len, 64).to(dtype) for _ in range(4)]
+    g_t = [t.to(d).requires_grad_() for t in tensors]
+    o_t = [t.float().requires_grad_() for t in tensors]
+    q1, q2, q3, v3 = o_t
+    out_ref, _, _ = O.reference_poly_attention(q1, q2, q2, q3, v3, softclamp_value=softclamp_value,
+                                               causal=causal)
+    dout = torch.randn_like(out_ref).to(dtype)
+    out_ref.backward(dout.float())
+    out = flash_poly_attention(*g_t, softclamp_value=softclamp_value, is_causal=causal)
+    out.backward(dout.to(d))
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert_close(out, out_ref, tol, "out")
+    for i, (a, b) in enumerate(zip(g_t, o_t)):
+        assert_close(a.grad, b.grad, tol, f"grad {i}", grad=True)
+
+
+def test_flash_poly_attention_context_mask_disallowed():  # reference tests:541-558
+    from poly_attention.flash_poly_attention import flash_poly_attention
+
+    d = dev()
+    q = torch.randn(2, 4, 16, 32, device=d)
+    cm = (torch.ones(2, 16, dtype=torch.bool), torch.ones(2, 16, dtype=torch.bool))
+    with pytest.raises(AssertionError, match="context_mask is not supported"):
+        flash_poly_attention(q, q, q, q, context_mask=cm)
+
+
+ORDER2_CFGS = [
+    dict(heads=4, dim_head=64, causal=False),
+    dict(heads=4, dim_head=64, causal=True, softclamp_value=20.0),
+    dict(heads=8, kv_heads=2, dim_head=64, causal=True),
+    dict(heads=4, dim_head=32, causal=True, multiply_root_value=True, attn_gate=True,
+         use_rotary_embed=True, prenorm=True),
+    dict(heads=4, kv_heads=1, dim_head=64, causal=False, shared_kv=True),
+]
+
+
+@param("cfg", ORDER2_CFGS)
+@param("masked", (False, True))
+@param("seq_len", (31, 64))
+def test_order2_module_e2e(cfg, masked, seq_len):
+    """Module-level fwd + dx vs the oracle (reference tests:242-273 and :291-341)."""
+    from poly_attention import Order2PolyAttention
+
+    d = dev()
+    torch.manual_seed(42)
+    m = Order2PolyAttention(dim=64, use_flash_kernel=True, **cfg).to(d)
+    x = torch.randn(2, seq_len, 64)
+    mask = None
+    if masked:
+        mask = torch.ones(2, seq_len, dtype=torch.bool)
+        mask[:, seq_len // 2:] = False
+    xg = x.to(d).requires_grad_()
+    out = m(xg, mask=mask.to(d) if masked else None)
+    params = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    xo = x.clone().requires_grad_()
+    ref = O.order2_forward(params, cfg, xo, mask=mask)
+    dout = torch.randn_like(ref)
+    out.backward(dout.to(d))
+    ref.backward(dout)
+    assert_close(out, ref, 1e-4, "out")
+    assert_close(xg.grad, xo.grad, 1e-4, "dx", grad=True)
+
+
+@param("order", (2, 3, 4))
+@param("kv_heads", (2, 4))
+@param("causal", (False, True))
+def test_npoly_module_e2e(order, kv_heads, causal):
+    from poly_attention import NPolyAttention
+
+    d = dev()
+    torch.manual_seed(7)
+    cfg = dict(heads=4, kv_heads=kv_heads, dim_head=64, causal=causal, order=order)
+    m = NPolyAttention(dim=64, **cfg).to(d)
+    x = torch.randn(2, 40, 64)
+    xg = x.to(d).requires_grad_()
+    out = m(xg)
+    params = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    xo = x.clone().requires_grad_()
+    ref = O.npoly_forward(params, cfg, xo)
+    dout = torch.randn_like(ref)
+    out.backward(dout.to(d))
+    ref.backward(dout)
+    assert_close(out, ref, 1e-4, "out")
+    assert_close(xg.grad, xo.grad, 1e-4, "dx", grad=True)
+
+
+def test_contexts_and_context_masks_e2e():
+    """Variable context lengths with context masks (reference tests:426-514) on the GPU."""
+    from poly_attention import Order2PolyAttention
+
+    d = dev()
+    torch.manual_seed(3)
+    cfg = dict(heads=4, dim_head=64)
+    m = Order2PolyAttention(dim=64, **cfg).to(d)
+    x, c1, c2 = torch.randn(2, 16, 64), torch.randn(2, 20, 64), torch.randn(2, 24, 64)
+    mx = torch.ones(2, 16, dtype=torch.bool)
+    mx[:, 12:] = False
+    m1 = torch.ones(2, 20, dtype=torch.bool)
+    m1[:, 15:] = False
+    m2 = torch.ones(2, 24, dtype=torch.bool)
+    m2[:, 18:] = False
+    out = m(x.to(d), context=(c1.to(d), c2.to(d)), mask=mx.to(d),
+            context_mask=(m1.to(d), m2.to(d)))
+    params = {k: v.cpu() for k, v in m.state_dict().items()}
+    ref = O.order2_forward(params, cfg, x, context=(c1, c2), mask=mx, context_mask=(m1, m2))
+    assert_close(out.detach(), ref, 1e-4, "out")
+
+
+@param("order", (2, 3))
+@param("kv_heads", (2, 4))
+@param("use_rotary_embed", (False, True))
+def test_kv_cache_stepwise_equals_parallel(order, kv_heads, use_rotary_embed):
+    """Prefill with return_cache, then single-token steps through the decode kernel; the
+    concatenated outputs equal the oracle's parallel causal forward (reference tests:103-179)."""
+    from poly_attention import NPolyAttention, Order2PolyAttention
+
+    d = dev()
+    torch.manual_seed(11)
+    cfg = dict(heads=4, kv_heads=kv_heads, dim_head=64, causal=True,
+               use_rotary_embed=use_rotary_embed)
+    if order == 2:
+        m = Order2PolyAttention(dim=64, **cfg).to(d)
+        fwd = O.order2_forward
+    else:
+        m = NPolyAttention(dim=64, order=order, **cfg).to(d)
+        fwd = O.npoly_forward
+        cfg = dict(cfg, order=order)
+    x = torch.randn(2, 12, 64)
+    params = {k: v.cpu() for k, v in m.state_dict().items()}
+    ref = fwd(params, cfg, x)
+    with torch.no_grad():
+        out0, cache = m(x[:, :5].to(d), return_cache=True)
+        outs = [out0]
+        for i in range(5, 12):
+            o, cache = m(x[:, i:i + 1].to(d), cache=cache, return_cache=True)
+            outs.append(o)
+    assert_close(torch.cat(outs, dim=1), ref, 1e-4, "stepwise")
+
+
+def test_decode_kernel_gqa_synthetic_cache():
+    """Config-5 shape class (GQA 8/2 heads, d=128) at a small cache, with a synthetic cache
+    (q/k/v/msg ~ N(0,1), lse = log(j+1) + N(0,1)) against the oracle's cached branch."""
+    from poly_attention import _ops
+
+    d = dev()
+    g = torch.Generator().manual_seed(5)
+    B, H, G, n, dh = 2, 8, 2, 300, 128
+    r = H // G
+    for dtype in (torch.float32, torch.bfloat16):
+        q2c, q3c, v3c = (torch.randn(B, G, n, dh, generator=g).to(dtype) for _ in range(3))
+        msg = torch.randn(B, H, n, dh, generator=g).to(dtype)
+        lse = (torch.log(torch.arange(1, n + 1).float()) + torch.randn(B, H, n, generator=g))
+        q1 = torch.randn(B, H, 1, dh, generator=g).to(dtype)
+        q2n = q2c[:, :, -1:].clone()
+        # oracle: the reference's cached step with the cache of the first n-1 positions
+        f = lambda t: O.repeat_kv(t.float(), r)  # noqa: E731
+        cache = (None, None, None, lse[:, :, :-1], msg[:, :, :-1].float())
+        ref, lse_step, msg_step = O.reference_poly_attention(
+            q1.float(), f(q2n), f(q2c), f(q3c), f(v3c), cache=cache)
+        msg_d, lse_d = msg.to(d).clone(), lse.to(d).clone()
+        out = _ops.poly_decode_step([q1.to(d), q2n.to(d)], [q2c.to(d), q3c.to(d)], [v3c.to(d)],
+                                    [msg_d], [lse_d], kv_heads=G, heads=H, softclamp=None,
+                                    scale=dh ** -0.5)
+        torch.cuda.synchronize()
+        tol = 1e-4 if dtype == torch.float32 else 2e-2
+        assert_close(out, ref, tol, f"out {dtype}")
+        assert_close(msg_d[:, :, -1:], msg_step, tol, f"msg slot {dtype}")
+        assert_close(lse_d[:, :, -1], lse_step[:, :, 0], max(tol, 1e-4), f"lse slot {dtype}")
+        # untouched cache positions
+        assert torch.equal(msg_d[:, :, :-1].cpu(), msg[:, :, :-1])

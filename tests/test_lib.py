@@ -1,0 +1,110 @@
+"""libpolyattn.so: it loads, exports every symbol include/polyattn.h declares, its struct
+layouts match the ctypes mirror, and invalid arguments are rejected before any launch (so
+these run without a GPU)."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from poly_attention import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    text = (ROOT / "include" / "polyattn.h").read_text()
+    return sorted(set(re.findall(r"\b(pa_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_loads_and_version():
+    lib = _lib.load()
+    assert lib.pa_abi_version() == _lib.PA_ABI_VERSION
+
+
+def test_exports_every_declared_symbol():
+    declared = declared_functions()
+    assert set(declared) == set(_lib.EXPORTED_SYMBOLS), declared
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+
+
+def test_struct_layouts_match():
+    lib = _lib.load()
+    for i, st in enumerate(_lib.STRUCTS):
+        assert lib.pa_struct_size(i) == ctypes.sizeof(st), st.__name__
+    assert lib.pa_struct_size(99) == 0
+
+
+def test_strerror():
+    lib = _lib.load()
+    for code in (0, -1, -2, -3, -4, -99):
+        assert isinstance(lib.pa_strerror(code), bytes)
+
+
+def _valid_pass():
+    p = _lib.PaPass()
+    p.batch, p.heads, p.nq, p.nk, p.dim = 1, 4, 8, 8, 64
+    p.scale, p.softclamp, p.causal = 0.125, 0.0, 1
+    fake = 0x1000  # never dereferenced: every case below fails validation first
+    for name in ("q", "k", "v", "out"):
+        v = getattr(p, name)
+        v.ptr, v.sb, v.sh, v.sn, v.heads, v.dtype = fake, 2048, 512, 64, 4, _lib.PA_BF16
+    p.lse.ptr, p.lse.sb, p.lse.sh, p.lse.sn, p.lse.heads = fake, 32, 8, 1, 4
+    p.lse.dtype = _lib.PA_F32
+    return p
+
+
+@pytest.mark.parametrize("breakage", [
+    "null", "batch0", "dim_too_big", "heads_not_divisible", "dtype_mismatch", "lse_dtype",
+    "missing_k", "out_heads",
+])
+def test_pass_fwd_rejects_invalid_arguments(breakage):
+    lib = _lib.load()
+    if breakage == "null":
+        assert lib.pa_attn_pass_fwd(None, None) == _lib.PA_EINVAL
+        return
+    p = _valid_pass()
+    want = _lib.PA_EINVAL
+    if breakage == "batch0":
+        p.batch = 0
+    elif breakage == "dim_too_big":
+        p.dim = 512
+        want = _lib.PA_EUNSUPPORTED
+    elif breakage == "heads_not_divisible":
+        p.k.heads = 3
+    elif breakage == "dtype_mismatch":
+        p.v.dtype = _lib.PA_F16
+    elif breakage == "lse_dtype":
+        p.lse.dtype = _lib.PA_BF16
+    elif breakage == "missing_k":
+        p.k.ptr = None
+    elif breakage == "out_heads":
+        p.out.heads = 2
+    assert lib.pa_attn_pass_fwd(ctypes.byref(p), None) == want
+
+
+def test_pass_bwd_rejects_missing_workspace():
+    lib = _lib.load()
+    g = _lib.PaPassGrad()
+    g.fwd = _valid_pass()
+    for name in ("dout", "dq", "dk", "dv"):
+        setattr(g, name, getattr(g.fwd, "q"))
+    assert lib.pa_attn_pass_bwd_workspace(ctypes.byref(g)) > 0
+    g.workspace, g.workspace_bytes = None, 0
+    assert lib.pa_attn_pass_bwd(ctypes.byref(g), None) == _lib.PA_EWORKSPACE
+
+
+def test_decode_rejects_invalid_order():
+    lib = _lib.load()
+    d = _lib.PaDecode()
+    d.order = 1
+    assert lib.pa_poly_decode(ctypes.byref(d), None) == _lib.PA_EINVAL
+    d.order = 2
+    d.batch = d.kv_heads = d.n = d.dim = 1
+    assert lib.pa_poly_decode(ctypes.byref(d), None) == _lib.PA_EINVAL  # no level tensors

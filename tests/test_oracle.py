@@ -1,0 +1,163 @@
+"""Pins of the CPU oracle (oracle/poly_oracle.py) against closed forms and library routines.
+
+Each check is chosen so that a plausible slip in the oracle (a dropped bias, a transposed
+operand, a wrong causal offset, a missing value product) fails it:
+  * brute force: the order-2 / order-3 / order-n poly score as one softmax over key paths,
+  * torch's scaled_dot_product_attention (a library routine) with a float bias for each pass,
+  * torch.autograd.gradcheck in float64,
+  * an independent float64 derivation of the reference's finite-fill masked rows,
+  * rotation properties of RoPE (parity of its pair layout is unpinned: the package it comes
+    from, rotary-embedding-torch, is absent here).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle.poly_oracle as O
+
+param = pytest.mark.parametrize
+
+
+def rnd(*shape, seed=0, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=dtype)
+
+
+@param("causal", (False, True))
+@param("softclamp", (None, 2.0))
+@param("n", (1, 5, 9))
+def test_order2_matches_pair_softmax(causal, softclamp, n):
+    q1, q2, q3, v3 = (rnd(2, 3, n, 8, seed=s) for s in range(4))
+    out, _, _ = O.reference_poly_attention(q1, q2, q2, q3, v3, causal=causal,
+                                           softclamp_value=softclamp)
+    ref = O.brute_order2(q1, q2, q3, v3, causal=causal, softclamp_value=softclamp)
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-10, atol=1e-10)
+
+
+def test_order2_brute_force_detects_dropped_bias():
+    # planting a mistake in the oracle (no lse bias in pass 2) must break the pin
+    q1, q2, q3, v3 = (rnd(1, 2, 6, 8, seed=10 + s) for s in range(4))
+    ref = O.brute_order2(q1, q2, q3, v3)
+    s = 8 ** -0.5
+    msg = torch.softmax(q2 @ q3.transpose(-1, -2) * s, -1) @ v3
+    wrong = torch.softmax(q1 @ q2.transpose(-1, -2) * s, -1) @ msg
+    assert not np.allclose(wrong.numpy(), ref, atol=1e-6)
+
+
+@param("causal", (False, True))
+def test_passes_match_sdpa(causal):
+    q1, q2, q3, v3 = (rnd(2, 2, 7, 16, seed=20 + s) for s in range(4))
+    out, lse23, msg = O.reference_poly_attention(q1, q2, q2, q3, v3, causal=causal)
+    n = q1.shape[2]
+    cm = torch.ones(n, n, dtype=torch.bool).tril() if causal else None
+    msg_ref = F.scaled_dot_product_attention(q2, q3, v3, attn_mask=cm)
+    s = 16 ** -0.5
+    sim = q2 @ q3.transpose(-1, -2) * s
+    if causal:
+        sim = sim.masked_fill(~cm, -math.inf)
+    torch.testing.assert_close(msg, msg_ref, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(lse23, torch.logsumexp(sim, -1), rtol=1e-10, atol=1e-10)
+    bias = lse23[:, :, None, :].expand(-1, -1, n, -1)
+    if causal:
+        bias = bias.masked_fill(~cm, -math.inf)
+    out_ref = F.scaled_dot_product_attention(q1, q2, msg, attn_mask=bias)
+    torch.testing.assert_close(out, out_ref, rtol=1e-10, atol=1e-10)
+
+
+@param("causal", (False, True))
+def test_order3_matches_path_sum(causal):
+    qs = [rnd(1, 2, 5, 8, seed=30 + s) for s in range(4)]
+    v3, v4 = rnd(1, 2, 5, 8, seed=40), rnd(1, 2, 5, 8, seed=41)
+    out, lses, msgs = O.n_poly_core(qs[:3], qs[1:], [v3, v4], causal=causal)
+    ref = O.brute_order3(*qs, v3, v4, causal=causal)
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-10, atol=1e-10)
+    assert len(lses) == len(msgs) == 2
+
+
+@param("order", (2, 3, 4))
+@param("causal", (False, True))
+def test_order_n_matches_recursive_path_sum(order, causal):
+    n = 4
+    qs = [rnd(1, 1, n, 4, seed=50 + s) for s in range(order + 1)]
+    vs = [rnd(1, 1, n, 4, seed=60 + s) for s in range(order - 1)]
+    out, _, _ = O.n_poly_core(qs[:-1], qs[1:], vs, causal=causal)
+    ref = O.brute_order_n(qs, vs, causal=causal)
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-10, atol=1e-10)
+
+
+@param("causal", (False, True))
+def test_order2_core_equals_n_core(causal):
+    q1, q2, q3, v3 = (rnd(2, 2, 6, 8, seed=70 + s) for s in range(4))
+    a, lse_a, msg_a = O.reference_poly_attention(q1, q2, q2, q3, v3, causal=causal)
+    b, lses, msgs = O.n_poly_core([q1, q2], [q2, q3], [v3], causal=causal)
+    torch.testing.assert_close(a, b, rtol=0, atol=1e-12)
+    torch.testing.assert_close(lse_a, lses[0], rtol=0, atol=1e-12)
+
+
+def test_order2_gradcheck():
+    q1, q2, q3, v3 = (rnd(1, 2, 5, 4, seed=80 + s).requires_grad_() for s in range(4))
+
+    def f(a, b, c, d):
+        return O.reference_poly_attention(a, b, b, c, d, causal=True, softclamp_value=3.0)[0]
+
+    assert torch.autograd.gradcheck(f, (q1, q2, q3, v3))
+
+
+@param("causal", (False, True))
+def test_masked_rows_follow_finite_fill_classes(causal):
+    """Fully-masked query rows are the uniform average over -finfo.max entries."""
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(2, 2, 8, 16, generator=g) for _ in range(3))
+    km = torch.ones(2, 8, dtype=torch.bool)
+    km[:, 5:] = False
+    km[1, 0] = False  # row 0 of batch 1 loses its only causal key
+    qm = torch.ones(2, 8, dtype=torch.bool)
+    qm[0, 6:] = False
+    bias = torch.randn(2, 2, 8, generator=g)
+    bias[1, 0, 3] = -torch.finfo(torch.float32).max  # a class-1 bias entry
+    out, lse = O.attn_pass(q, k, v, bias=bias, key_mask=km, query_mask=qm, causal=causal)
+    ref_out, ref_lse = O.masked_pass_classes(q, k, v, bias=bias, key_mask=km, query_mask=qm,
+                                             causal=causal)
+    np.testing.assert_allclose(out.numpy(), ref_out, rtol=1e-5, atol=1e-5)
+    ok = np.isfinite(ref_lse) & (ref_lse > -1e30)
+    np.testing.assert_allclose(lse.numpy()[ok], ref_lse[ok], rtol=1e-5, atol=1e-5)
+    assert np.all(lse.numpy()[~ok] <= -1e30)
+
+
+def test_padding_invariance_of_key_masks():
+    """tests/test_poly_attention.py:516-539 in oracle form: padded+masked == unpadded."""
+    q1 = rnd(2, 2, 6, 8, seed=90, dtype=torch.float32)
+    q2u, q3u, v3u = (rnd(2, 2, n, 8, seed=91 + i, dtype=torch.float32)
+                     for i, n in enumerate((5, 7, 7)))
+    pad = lambda t, n: torch.cat((t, torch.zeros(2, 2, n, 8)), dim=2)  # noqa: E731
+    q2p, q3p, v3p = pad(q2u, 3), pad(q3u, 4), pad(v3u, 4)
+    m1 = torch.zeros(2, 8, dtype=torch.bool)
+    m1[:, :5] = True
+    m2 = torch.zeros(2, 11, dtype=torch.bool)
+    m2[:, :7] = True
+    a, _, _ = O.reference_poly_attention(q1, q2u, q2u, q3u, v3u)
+    b, _, _ = O.reference_poly_attention(q1, q2p, q2p, q3p, v3p, context_mask=(m1, m2))
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+
+
+def test_rotary_properties():
+    d = 16
+    q, k = rnd(1, 1, 9, d, seed=100, dtype=torch.float32), rnd(1, 1, 9, d, seed=101, dtype=torch.float32)
+    qr, kr = O.rotate_queries_with_cached_keys(d, q, k)
+    # rotations preserve norms
+    torch.testing.assert_close(qr.norm(dim=-1), q.norm(dim=-1), rtol=1e-5, atol=1e-5)
+    # scores depend only on relative positions: shift both by 3
+    f = O.rotary_freqs(d, torch.arange(12))
+    a = O.apply_rotary(f[:9], q) @ O.apply_rotary(f[:9], k).transpose(-1, -2)
+    b = O.apply_rotary(f[3:12], q) @ O.apply_rotary(f[3:12], k).transpose(-1, -2)
+    torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-4)
+    # position 0 is the identity; the first pair at position 1 turns by 1 radian
+    torch.testing.assert_close(qr[..., 0, :], q[..., 0, :])
+    x = torch.zeros(1, 1, 2, d)
+    x[..., 1, 0] = 1.0
+    y = O.apply_rotary(O.rotary_freqs(d, torch.arange(2)), x)
+    torch.testing.assert_close(y[0, 0, 1, :2], torch.tensor([math.cos(1.0), math.sin(1.0)]))
