@@ -1,0 +1,333 @@
+#!/usr/bin/env python
+"""bench.py -- the poly-attention hot path on one MI355X.
+
+Workload: order-2 causal poly attention, B=4, N=4096, heads=16,
+dim_head=64, bf16.  The inputs of the timed op are the module's own q1/q2/q3/v3: a
+PolyAttention(dim=1024, heads=16, dim_head=64, causal=True) with random-init bf16 weights
+(seed 0) applied to x ~ N(0,1) [4, 4096, 1024] (seed 1), i.e. the projections and q/k
+RMSNorms of the reference module.  One step = the fused core forward (both passes) +
+backward (all four input gradients) for upstream grad ~ N(0,1) (seed 2).
+
+Printed: ONE JSON line with the headline metric (core TFLOP/s over the algorithmic flops of
+the step), the live per-kernel roofline of the dominant kernel (HIP events on its launch
+stream), the CPU oracle baseline timed on this host, the full module step time, and the
+config-5 GQA decode step (GB/s against 8 TB/s).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "poly-attention_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+METRIC = "poly-attn fwd+bwd TFLOP/s (%MFMA peak) N=4096 h16 d64 bf16; decode GB/s"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 (published)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (published)
+
+B, N, DIM, H, DH = 4, 4096, 1024, 16, 64
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------------------
+# algorithmic work
+
+
+def core_flops_fwd(b, h, nq, nk, d, causal):
+    """4 * Nq * Nk * d per (batch, head) and attention level; causal x 1/2."""
+    return 4.0 * nq * nk * d * b * h * (0.5 if causal else 1.0)
+
+
+def step_flops():
+    # two levels (pass 1 at kv_heads = 16, pass 2 at 16 heads), forward 4 N^2 d, backward 10 N^2 d
+    fwd = 2 * core_flops_fwd(B, H, N, N, DH, True)
+    return fwd, fwd * 10.0 / 4.0
+
+
+# per kernel family: (bound, peak, work per launch for this workload, unit)
+def kernel_work(name):
+    per_level_fwd = core_flops_fwd(B, H, N, N, DH, True)
+    table = {
+        "mfma_fwd": ("mfma", PEAK_BF16_TFLOPS, per_level_fwd, "TFLOP/s"),
+        # dK/dV kernel: S, dP, dV, dK = 4 GEMMs; dQ kernel: S, dP, dQ = 3 GEMMs
+        "mfma_bwd_dkv": ("mfma", PEAK_BF16_TFLOPS, per_level_fwd * 2.0, "TFLOP/s"),
+        "mfma_bwd_dq": ("mfma", PEAK_BF16_TFLOPS, per_level_fwd * 1.5, "TFLOP/s"),
+        "simt_bwd_dkv": ("mfma", PEAK_FP32_TFLOPS, per_level_fwd * 2.0, "TFLOP/s"),
+        "simt_bwd_dq": ("mfma", PEAK_FP32_TFLOPS, per_level_fwd * 1.5, "TFLOP/s"),
+        # preprocess: reads O and dO (bf16) and lse, writes three fp32 rows (bytes)
+        "bwd_pre": ("hbm", PEAK_HBM_GBS, B * H * N * (2 * DH * 2 + 4 + 12), "GB/s"),
+    }
+    return table.get(name)
+
+
+def achieved_rate(work, avg_ms, unit):
+    return work / (avg_ms / 1e3) / (1e12 if unit == "TFLOP/s" else 1e9)
+
+
+# ---------------------------------------------------------------------------------------
+# config 2: fused fwd + bwd
+
+
+def make_config2(dev):
+    from poly_attention import PolyAttention
+
+    torch.manual_seed(0)
+    m = PolyAttention(dim=DIM, heads=H, dim_head=DH, causal=True).to(dev, torch.bfloat16)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    x = torch.randn(B, N, DIM, generator=g).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        q1 = m.split_q(m.to_q(x))[0]
+        q2 = m.split_kv1(m.to_kvs[0](x))[0]
+        q3, v3 = m.split_kv(m.to_kvs[1](x))
+        q1, q2, q3 = (norm(q) for norm, q in zip(m.q_norms, (q1, q2, q3)))
+    qs = [t.contiguous().requires_grad_() for t in (q1, q2, q3, v3)]
+    g2 = torch.Generator(device="cpu").manual_seed(2)
+    dout = torch.randn(B, H, N, DH, generator=g2).to(dev, torch.bfloat16)
+    dx = torch.randn(B, N, DIM, generator=g2).to(dev, torch.bfloat16)
+    return m, x, qs, dout, dx
+
+
+def core_step(qs, dout):
+    from poly_attention.flash_poly_attention import flash_poly_attention
+
+    for t in qs:
+        t.grad = None
+    out = flash_poly_attention(*qs, is_causal=True)
+    out.backward(dout)
+
+
+def module_step(m, x, dx):
+    m.zero_grad(set_to_none=True)
+    xr = x.detach().requires_grad_()
+    out = m(xr)
+    out.backward(dx)
+
+
+def time_steps(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+# ---------------------------------------------------------------------------------------
+# config 5: GQA decode step
+
+
+def decode_bench(dev, steps, warmup):
+    from poly_attention import _lib, _ops
+
+    Bd, Hq, G, n_old, d = 32, 32, 8, 8192, 128
+    n = n_old + 1
+    g = torch.Generator(device="cpu").manual_seed(3)
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=g, dtype=torch.float32).to(dev, torch.bfloat16)
+
+    q2c, q3c, v3c = rnd(Bd, G, n, d), rnd(Bd, G, n, d), rnd(Bd, G, n, d)
+    msg = rnd(Bd, Hq, n, d)
+    lse = (torch.log(torch.arange(1, n + 1, dtype=torch.float32))
+           + torch.randn(Bd, Hq, n, generator=g)).to(dev)
+    q1 = rnd(Bd, Hq, 1, d)
+    q2n = q2c[:, :, -1:].contiguous()
+
+    def step():
+        _ops.poly_decode_step([q1, q2n], [q2c, q3c], [v3c], [msg], [lse], kv_heads=G, heads=Hq,
+                              softclamp=None, scale=d ** -0.5)
+
+    ms = time_steps(step, steps, warmup)
+    # every cached tensor read once in its stored dtype (order 2: q2, q3, v3 at kv heads;
+    # msg (bf16) and lse (fp32) at query heads)
+    bytes_step = Bd * n * ((2 * 2 - 1) * G * d * 2 + (2 - 1) * Hq * (d * 2 + 4))
+    with _lib.KernelProfile() as prof:
+        for _ in range(steps):
+            step()
+    part = prof.times.get("dec_partial", (0, 0.0))
+    part_bytes = Bd * n_old * (3 * G * d * 2 + Hq * (d * 2 + 4))
+    part_ms = part[1] / max(part[0], 1)
+    del q2c, q3c, v3c, msg, lse
+    torch.cuda.empty_cache()
+    return {
+        "workload": "order-2 GQA decode step, Hq=32 Hkv=8 d=128 B=32, 8192 cached + 1 new, bf16 cache, fp32 lse",
+        "ms_per_step": round(ms, 4),
+        "GB_per_s": round(bytes_step / ms / 1e6, 1),
+        "frac_hbm_peak": round(bytes_step / ms / 1e6 / PEAK_HBM_GBS, 4),
+        "bytes_per_step": bytes_step,
+        "tokens_per_s": round(Bd / (ms / 1e3), 1),
+        "kernel": {"name": "dec_partial", "avg_ms": round(part_ms, 4),
+                   "GB_per_s": round(part_bytes / part_ms / 1e6, 1) if part_ms else None},
+    }
+
+
+# ---------------------------------------------------------------------------------------
+# CPU baseline: the oracle (the reference's eager math) on this host's cores
+
+
+def cpu_baseline(max_seconds=20.0):
+    import oracle.poly_oracle as O
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    hs = 2
+    g = torch.Generator().manual_seed(4)
+    ts = [torch.randn(1, hs, N, DH, generator=g).requires_grad_() for _ in range(4)]
+    dout = torch.randn(1, hs, N, DH, generator=g)
+
+    def step():
+        for t in ts:
+            t.grad = None
+        out, _, _ = O.reference_poly_attention(ts[0], ts[1], ts[1], ts[2], ts[3], causal=True)
+        out.backward(dout)
+
+    step()  # warm-up
+    times = []
+    t_end = time.perf_counter() + max_seconds
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 10):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    fwd, bwd = step_flops()
+    flops_sample = (fwd + bwd) / (B * H) * hs
+    cpu_name = platform.processor() or ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                cpu_name = line.split(":", 1)[1].strip()
+    except Exception:  # noqa: BLE001
+        pass
+    return {
+        "value": round(flops_sample / med / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle reference_poly_attention fp32 causal fwd+bwd, B=1 heads={hs} N={N} d={DH} "
+                  f"(1/{B * H // hs} of the step), median of {len(times)} after 1 warm-up, "
+                  f"{med * 1e3:.0f} ms each; cpu: {cpu_name}",
+        "ms_per_step_scaled": round(med * (B * H / hs) * 1e3, 1),
+    }
+
+
+# ---------------------------------------------------------------------------------------
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-module", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box of this build has a single MI355X; "
+              f"--gpus {args.gpus} is not supported (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs a single process on one GPU", file=sys.stderr)
+        sys.exit(2)
+
+    from poly_attention import _lib
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    _lib.load()
+    dev = torch.device("cuda:0")
+
+    m, x, qs, dout, dx = make_config2(dev)
+    log(f"[bench] config 2 ready on {torch.cuda.get_device_name(0)}; timing {args.steps} steps")
+    ms = time_steps(lambda: core_step(qs, dout), args.steps, args.warmup)
+    fwd_f, bwd_f = step_flops()
+    tflops = (fwd_f + bwd_f) / (ms / 1e3) / 1e12
+    log(f"[bench] core fwd+bwd {ms:.3f} ms/step, {tflops:.1f} TFLOP/s")
+
+    # live per-kernel timing of the same workload (events on the launch stream)
+    with _lib.KernelProfile() as prof:
+        for _ in range(args.steps):
+            core_step(qs, dout)
+    kernels = {k: {"launches": n, "avg_ms": round(t / n, 4)} for k, (n, t) in prof.times.items()}
+    dominant = max(prof.times.items(), key=lambda kv: kv[1][1])[0]
+    n_l, tot = prof.times[dominant]
+    bound, peak, work, unit = kernel_work(dominant)
+    avg_ms = tot / n_l
+    achieved = achieved_rate(work, avg_ms, unit)
+    roofline = {"bound": bound, "kernel": dominant, "achieved": round(achieved, 2),
+                "peak": peak, "unit": unit, "frac": round(achieved / peak, 4), "traffic": None,
+                "avg_ms": round(avg_ms, 4)}
+    log(f"[bench] kernels: {kernels}")
+
+    module_ms = None
+    if not args.no_module:
+        module_ms = time_steps(lambda: module_step(m, x, dx), max(3, args.steps // 2), 2)
+        log(f"[bench] module fwd+bwd {module_ms:.3f} ms/step")
+    del qs, dout
+    torch.cuda.empty_cache()
+
+    decode = None
+    if not args.no_decode:
+        decode = decode_bench(dev, args.steps, args.warmup)
+        log(f"[bench] decode {decode}")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline()
+        log(f"[bench] cpu {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: x~N(0,1), random-init projections (seed 0), upstream grad~N(0,1)",
+        "config": {
+            "workload": "order-2 causal poly-attention core fwd+bwd (flash_poly_attention) on the "
+                        "q1/q2/q3/v3 of PolyAttention(dim=1024, heads=16, dim_head=64, causal) "
+                        "applied to x [4, 4096, 1024] bf16 (BASELINE configs[1])",
+            "batch": B, "seq_len": N, "heads": H, "dim_head": DH, "order": 2, "causal": True,
+        },
+        "frac_mfma_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "tokens_per_s": round(B * N / (ms / 1e3), 1),
+        "flops_per_step": fwd_f + bwd_f,
+        "roofline": roofline,
+        "kernels": kernels,
+        "module_ms_per_step": round(module_ms, 4) if module_ms else None,
+        "cpu_baseline": cpu,
+        "decode": decode,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -142,6 +142,18 @@ int         pa_last_hip_error(void);   /* hipError_t of the last PA_EHIP on this
  * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode; 0 for other values */
 size_t      pa_struct_size(int which);
 
+/* Kernel timing (no counterpart in the reference: a measurement facility for benchmarks).
+ * Between pa_profile_start and pa_profile_stop every kernel this library launches (from any
+ * thread of the process) is bracketed by HIP events on its own stream; pa_profile_stop waits
+ * for those events and returns per-kernel launch counts and summed durations. */
+typedef struct pa_kernel_time {
+    const char* name;      /* static string naming the kernel family */
+    int64_t     launches;
+    double      total_ms;
+} pa_kernel_time;
+int pa_profile_start(void);
+int pa_profile_stop(pa_kernel_time* out, int capacity, int* count);
+
 int    pa_attn_pass_fwd(const pa_pass* p, void* stream);
 size_t pa_attn_pass_bwd_workspace(const pa_pass_grad* g);
 int    pa_attn_pass_bwd(const pa_pass_grad* g, void* stream);

@@ -1,7 +1,43 @@
 // pa_abi.hip -- the extern "C" entry points of libpolyattn.so: argument validation and
 // kernel dispatch.  Declarations and semantics: include/polyattn.h.
+#include <atomic>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
 #include "pa_common.h"
 #include "pa_launch.h"
+
+namespace pa {
+
+// Process-wide: torch runs a backward pass on its own autograd thread, so the recording
+// state cannot be thread-local.
+struct ProfRec {
+    const char* name;
+    hipEvent_t start, stop;
+};
+static std::atomic<bool> g_prof_on{false};
+static std::mutex g_prof_mu;
+static std::vector<ProfRec> g_prof;
+
+ProfScope::ProfScope(const char* name, hipStream_t s) : active(false), idx(0), stream(s) {
+    if (!g_prof_on.load(std::memory_order_relaxed)) return;
+    ProfRec r{name, nullptr, nullptr};
+    if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return;
+    hipEventRecord(r.start, s);
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    idx = g_prof.size();
+    g_prof.push_back(r);
+    active = true;
+}
+
+ProfScope::~ProfScope() {
+    if (!active) return;
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    hipEventRecord(g_prof[idx].stop, stream);
+}
+
+}  // namespace pa
 
 using namespace pa;
 
@@ -131,6 +167,47 @@ size_t pa_struct_size(int which) {
         case 5: return sizeof(pa_decode);
         default: return 0;
     }
+}
+
+int pa_profile_start(void) {
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    for (ProfRec& r : g_prof) {
+        hipEventDestroy(r.start);
+        hipEventDestroy(r.stop);
+    }
+    g_prof.clear();
+    g_prof_on = true;
+    return PA_OK;
+}
+
+int pa_profile_stop(pa_kernel_time* out, int capacity, int* count) {
+    g_prof_on = false;
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    int n = 0;
+    int status = PA_OK;
+    for (ProfRec& r : g_prof) {
+        float ms = 0.f;
+        if (hipEventSynchronize(r.stop) != hipSuccess ||
+            hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) {
+            status = PA_EHIP;
+        }
+        int k = 0;
+        while (k < n && std::strcmp(out[k].name, r.name) != 0) ++k;
+        if (k == n) {
+            if (n >= capacity) continue;
+            out[n].name = r.name;
+            out[n].launches = 0;
+            out[n].total_ms = 0.0;
+            ++n;
+        }
+        out[k].launches += 1;
+        out[k].total_ms += ms;
+        hipEventDestroy(r.start);
+        hipEventDestroy(r.stop);
+    }
+    g_prof.clear();
+    if (count) *count = n;
+    return status;
 }
 
 int pa_attn_pass_fwd(const pa_pass* p, void* stream) {

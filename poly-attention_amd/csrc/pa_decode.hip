@@ -466,11 +466,13 @@ int launch_decode(const pa_decode* d, hipStream_t s) {
     }
     if (D.nchunks > 0) {
         dim3 grid(D.nchunks, d->batch * d->kv_heads, d->order);
+        ProfScope ps("dec_partial", s);
         if (T == PA_F32) hipLaunchKernelGGL((k_dec_partial<float>), grid, dim3(kDecThreads), 0, s, D);
         else if (T == PA_F16) hipLaunchKernelGGL((k_dec_partial<f16>), grid, dim3(kDecThreads), 0, s, D);
         else hipLaunchKernelGGL((k_dec_partial<bf16>), grid, dim3(kDecThreads), 0, s, D);
     }
     dim3 cgrid(d->batch * d->kv_heads);
+    ProfScope ps("dec_combine", s);
     if (T == PA_F32) hipLaunchKernelGGL((k_dec_combine<float>), cgrid, dim3(kDecThreads), 0, s, D);
     else if (T == PA_F16) hipLaunchKernelGGL((k_dec_combine<f16>), cgrid, dim3(kDecThreads), 0, s, D);
     else hipLaunchKernelGGL((k_dec_combine<bf16>), cgrid, dim3(kDecThreads), 0, s, D);

@@ -5,6 +5,16 @@
 
 namespace pa {
 
+// Brackets one kernel launch with HIP events on its stream while pa_profile_start is active
+// on this thread (pa_abi.hip); otherwise it costs one thread-local flag test.
+struct ProfScope {
+    ProfScope(const char* name, hipStream_t s);
+    ~ProfScope();
+    bool active;
+    size_t idx;
+    hipStream_t stream;
+};
+
 // generic (one lane per row) kernels: every dtype, head dim <= 256, every mask feature
 void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s);
 void launch_simt_fixup(const PassDev& P, int dtype, hipStream_t s);

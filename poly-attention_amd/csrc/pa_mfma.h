@@ -1,0 +1,113 @@
+// pa_mfma.h -- MFMA fragment helpers shared by the gfx950 attention kernels.
+//
+// All kernels use v_mfma_f32_32x32x16_{bf16,f16}: A is 32 x 16 (lane l holds row l % 32,
+// k elements 8*(l/32) .. +7), B is 16 x 32 (lane l holds column l % 32, the same k
+// elements), and the 32 x 32 fp32 accumulator gives lane l the column n = l % 32 and the
+// rows m(i) = 8*(i/4) + 4*(l/32) + (i%4) for its 16 registers i.
+//
+// "Transposed-operand" trick used throughout: an accumulator block C (rows m(i) of a lane's
+// column) can be fed back as the B operand of a second product over the same row index by
+// splitting its 16 registers into two groups of 8 (t = 0, 1); group t then carries the row
+// indices 16t + 8*(e/4) + 4*(l/32) + (e%4), e = 0..7, and the matching A operand is read from
+// a transposed LDS copy as two 4-element runs at rows 16t + 4*(l/32) and 16t + 8 + 4*(l/32).
+#pragma once
+
+#include "pa_common.h"
+
+namespace pa {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+template <typename T> struct Mma;
+template <> struct Mma<bf16> {
+    typedef bf16x8_t frag;
+    static __device__ __forceinline__ f32x16_t run(frag a, frag b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Mma<f16> {
+    typedef f16x8_t frag;
+    static __device__ __forceinline__ f32x16_t run(frag a, frag b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+__device__ __forceinline__ f32x16_t zero16() {
+    f32x16_t z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.f;
+    return z;
+}
+
+// two floats -> two T (round to nearest even) packed in one 32-bit word (lo = first)
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    const T a = (T)lo, b = (T)hi;
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// accumulator registers 8t .. 8t+7 (times `scale`) as a B-operand fragment
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag acc_to_frag(const f32x16_t& c, int t) {
+    u32x4_t r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = pack2<T>(c[8 * t + 2 * k], c[8 * t + 2 * k + 1]);
+    return __builtin_bit_cast(typename Mma<T>::frag, r);
+}
+
+// element-wise product of 8 values rounded to T (the reference multiplies in T)
+template <typename T>
+__device__ __forceinline__ u32x4_t mul_round8(u32x4_t v, u32x4_t m) {
+    const T* pv = reinterpret_cast<const T*>(&v);
+    const T* pm = reinterpret_cast<const T*>(&m);
+    u32x4_t r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        r[k] = pack2<T>((float)pv[2 * k] * (float)pm[2 * k],
+                        (float)pv[2 * k + 1] * (float)pm[2 * k + 1]);
+    return r;
+}
+
+// A-operand fragment read as two 4-element runs of a transposed LDS row (see header note)
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag lds_runs(const T* row) {
+    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
+    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 8);
+    const u32x4_t v = {lo[0], lo[1], hi[0], hi[1]};
+    return __builtin_bit_cast(typename Mma<T>::frag, v);
+}
+
+// 16-byte fragment load (LDS or global)
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag ld_frag(const T* p) {
+    return __builtin_bit_cast(typename Mma<T>::frag, *reinterpret_cast<const u32x4_t*>(p));
+}
+
+// Store a 4-row x 8-column block held as four 16-byte rows (w[r] = row r) transposed:
+// dst[(c0 + j) * stride + r] for j = 0..7, r = 0..3, as eight 8-byte stores.
+__device__ __forceinline__ void store_block_transposed(const u32x4_t* w, uint16_t* dst,
+                                                       int stride) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const uint32_t w0 = w[0][m], w1 = w[1][m], w2 = w[2][m], w3 = w[3][m];
+        u32x2_t even, odd;
+        even[0] = (w0 & 0xffffu) | (w1 << 16);
+        even[1] = (w2 & 0xffffu) | (w3 << 16);
+        odd[0] = (w0 >> 16) | (w1 & 0xffff0000u);
+        odd[1] = (w2 >> 16) | (w3 & 0xffff0000u);
+        *reinterpret_cast<u32x2_t*>(dst + (2 * m) * stride) = even;
+        *reinterpret_cast<u32x2_t*>(dst + (2 * m + 1) * stride) = odd;
+    }
+}
+
+static inline bool aligned_rows_host(const DView& v, int elems) {
+    return ((uintptr_t)v.p % 16 == 0) && v.sb % elems == 0 && v.sh % elems == 0 &&
+           v.sn % elems == 0;
+}
+
+}  // namespace pa

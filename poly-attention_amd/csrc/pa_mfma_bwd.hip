@@ -1,0 +1,531 @@
+// pa_mfma_bwd.hip -- MFMA backward of one attention pass (bf16 / f16, head dim 64 or 128).
+//
+// After k_bwd_pre has written per row lse and D = rowsum(dO * O) - dlse:
+//   k_mfma_bwd_dkv (key-major, no atomics): a workgroup owns 128 keys of one key head
+//     (4 waves x 32 keys, K and V kept in registers as B operands) and sweeps the query
+//     tiles of every query head of its group: S = Q K^T and dP = dO V^T give, per lane,
+//     16 queries of the lane's key; P = exp2(S*scale*log2e + bias - lse*log2e) and
+//     dS = P (dP - D) feed dV^T += dO^T P and dK^T += Q^T dS through transposed LDS copies of
+//     Q and dO, and the key bias gradient is the column sum of dS.
+//   k_mfma_bwd_dq (query-major, no atomics): a workgroup owns 128 queries (4 waves x 32) and
+//     sweeps the key tiles: S^T = K Q^T, dP^T = V dO^T, dS^T, then dQ^T += K^T dS^T.
+// Both recompute P from the saved lse; they do not handle fully-masked rows (the host sends
+// masked passes to the generic kernels).
+#include "pa_common.h"
+#include "pa_launch.h"
+#include "pa_mfma.h"
+
+namespace pa {
+
+constexpr int kBwdThreads = 256;
+
+// ---------------------------------------------------------------------------------------
+// dK / dV / dbias
+
+constexpr int kKvBK = 128;  // keys per workgroup
+constexpr int kKvBQ = 64;   // queries per tile
+
+template <int D>
+struct KvTile {
+    static constexpr int RS = D + 8;        // row-major stride (elements)
+    static constexpr int TS = kKvBQ + 4;    // transposed stride (elements)
+    static constexpr int BLOCKS = (kKvBQ / 4) * (D / 8);  // 4-row x 8-column blocks per tensor
+    static constexpr int NB = (2 * BLOCKS + kBwdThreads - 1) / kBwdThreads;
+};
+
+template <int D>
+struct KvStage {
+    u32x4_t w[KvTile<D>::NB][4];
+    float lse, dsum;
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void kv_load(const GradDev& G, int b, int h, int q0, KvStage<D>& st) {
+    using TL = KvTile<D>;
+    const PassDev& P = G.f;
+    const int tid = threadIdx.x;
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int c = 0; c < TL::NB; ++c) {
+        const int task = tid + c * kBwdThreads;
+        if (task < 2 * TL::BLOCKS) {
+            const int tensor = task / TL::BLOCKS, blk = task % TL::BLOCKS;
+            const int rg = blk / (D / 8), cc = blk % (D / 8);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int q = q0 + rg * 4 + r;
+                if (q < P.nq) {
+                    const T* src = tensor == 0 ? P.q.row<T>(b, h, q) : G.dout.row<T>(b, h, q);
+                    st.w[c][r] = *reinterpret_cast<const u32x4_t*>(src + cc * 8);
+                } else {
+                    st.w[c][r] = zero;
+                }
+            }
+        }
+    }
+    if (tid < kKvBQ) {
+        const int q = q0 + tid;
+        const int64_t row = ((int64_t)b * P.heads + h) * P.nq + q;
+        st.lse = q < P.nq ? G.ws_lse[row] * kLog2e : INFINITY;
+        st.dsum = q < P.nq ? G.ws_D[row] : 0.f;
+    }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void kv_store(const KvStage<D>& st, T* sQ, T* sO, T* sQt, T* sOt,
+                                         float* sL, float* sD) {
+    using TL = KvTile<D>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < TL::NB; ++c) {
+        const int task = tid + c * kBwdThreads;
+        if (task < 2 * TL::BLOCKS) {
+            const int tensor = task / TL::BLOCKS, blk = task % TL::BLOCKS;
+            const int rg = blk / (D / 8), cc = blk % (D / 8);
+            T* rows = tensor == 0 ? sQ : sO;
+            T* trans = tensor == 0 ? sQt : sOt;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<u32x4_t*>(rows + (rg * 4 + r) * TL::RS + cc * 8) = st.w[c][r];
+            store_block_transposed(st.w[c], reinterpret_cast<uint16_t*>(trans + (cc * 8) * TL::TS + rg * 4),
+                                   TL::TS);
+        }
+    }
+    if (tid < kKvBQ) {
+        sL[tid] = st.lse;
+        sD[tid] = st.dsum;
+    }
+}
+
+template <typename T, int D, bool CAUSAL, bool SOFTCLAMP, bool HAS_VMUL, bool HAS_BIAS>
+__global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(GradDev G) {
+    using TL = KvTile<D>;
+    using M = Mma<T>;
+    typedef typename M::frag frag;
+    const PassDev& P = G.f;
+    __shared__ __attribute__((aligned(16))) T sQ[kKvBQ * TL::RS];
+    __shared__ __attribute__((aligned(16))) T sO[kKvBQ * TL::RS];
+    __shared__ __attribute__((aligned(16))) T sQt[D * TL::TS];
+    __shared__ __attribute__((aligned(16))) T sOt[D * TL::TS];
+    __shared__ __attribute__((aligned(16))) float sL[kKvBQ];
+    __shared__ __attribute__((aligned(16))) float sD[kKvBQ];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hh = lane >> 5, kcol = lane & 31;
+    const int kblk = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int rep = P.heads / G.hk;
+    const int h0 = kh * rep;
+    const int kw0 = kblk * kKvBK + w * 32;  // first key of this wave
+    const int key = kw0 + kcol;
+    const bool key_ok = key < P.nk;
+
+    // K and effective V of the lane's key as B operands (elements c*16 + 8*hh .. +7)
+    frag kf[D / 16], vf[D / 16];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        u32x4_t kr = {0u, 0u, 0u, 0u}, vr = {0u, 0u, 0u, 0u};
+        if (key_ok) {
+            kr = *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h0, key) + c * 16 + 8 * hh);
+            vr = *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h0, key) + c * 16 + 8 * hh);
+            if (HAS_VMUL)
+                vr = mul_round8<T>(vr, *reinterpret_cast<const u32x4_t*>(P.vmul.row<T>(b, h0, key) + c * 16 + 8 * hh));
+        }
+        kf[c] = __builtin_bit_cast(frag, kr);
+        vf[c] = __builtin_bit_cast(frag, vr);
+    }
+    float bias_l2 = key_ok ? 0.f : -INFINITY;
+    if (HAS_BIAS && key_ok) {
+        const float x = P.bias.scalar(b, h0, key);
+        bias_l2 = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
+    }
+    const float sl2 = P.scale * kLog2e;
+    const float cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
+    const float crec = SOFTCLAMP ? 1.f / P.softclamp : 0.f;
+
+    f32x16_t dk[D / 32], dv[D / 32];
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+        dk[x] = zero16();
+        dv[x] = zero16();
+    }
+    float dbias = 0.f;
+
+    const int q_start = CAUSAL ? (kblk * kKvBK / kKvBQ) * kKvBQ : 0;
+    const int ntiles = P.nq > q_start ? (P.nq - q_start + kKvBQ - 1) / kKvBQ : 0;
+    KvStage<D> st;
+    for (int h = h0; h < h0 + rep; ++h) {
+        if (ntiles > 0) kv_load<T, D>(G, b, h, q_start, st);
+        for (int t = 0; t < ntiles; ++t) {
+            const int q0 = q_start + t * kKvBQ;
+            kv_store<T, D>(st, sQ, sO, sQt, sOt, sL, sD);
+            __syncthreads();
+            if (t + 1 < ntiles) kv_load<T, D>(G, b, h, q0 + kKvBQ, st);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                const int qbase = q0 + qb * 32;
+                if (CAUSAL && qbase + 31 < kw0) continue;  // every query precedes every key
+                f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+                for (int c = 0; c < D / 16; ++c) {
+                    const int off = (qb * 32 + kcol) * TL::RS + c * 16 + 8 * hh;
+                    s = M::run(ld_frag<T>(sQ + off), kf[c], s);
+                    dp = M::run(ld_frag<T>(sO + off), vf[c], dp);
+                }
+                const bool diag = CAUSAL && (qbase < kw0 + 31);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int ql = qb * 32 + 8 * g + 4 * hh;
+                    const float4 Lv = *reinterpret_cast<const float4*>(sL + ql);
+                    const float4 Dv = *reinterpret_cast<const float4*>(sD + ql);
+                    const float L[4] = {Lv.x, Lv.y, Lv.z, Lv.w};
+                    const float Dd[4] = {Dv.x, Dv.y, Dv.z, Dv.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = 4 * g + r;
+                        float y = 0.f, x;
+                        if (SOFTCLAMP) {
+                            y = tanhf(s[i] * cinv);  // softclamp(s*scale) / c
+                            x = y * (P.softclamp * kLog2e) + bias_l2 - L[r];
+                        } else {
+                            x = s[i] * sl2 + bias_l2 - L[r];
+                        }
+                        float pv = exp2f(x);
+                        if (diag && (q0 + ql + r < key)) pv = 0.f;
+                        float dsv = pv * (dp[i] - Dd[r]);
+                        dbias += dsv;
+                        if (SOFTCLAMP) dsv *= (1.f - y * y);
+                        s[i] = pv;
+                        dp[i] = dsv;
+                    }
+                }
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2) {
+                    const frag pf = acc_to_frag<T>(s, t2);
+                    const frag df = acc_to_frag<T>(dp, t2);
+#pragma unroll
+                    for (int x = 0; x < D / 32; ++x) {
+                        const int toff = (x * 32 + kcol) * TL::TS + qb * 32 + 16 * t2 + 4 * hh;
+                        dv[x] = M::run(lds_runs<T>(sOt + toff), pf, dv[x]);
+                        dk[x] = M::run(lds_runs<T>(sQt + toff), df, dk[x]);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    dbias += __shfl_xor(dbias, 32);
+    if (!key_ok) return;
+    (void)crec;
+    // dK = scale * dK^T^T ; registers: d = x*32 + 8g + 4hh + r
+    T* dkrow = G.dk.wrow<T>(b, h0, key);
+    T* dvrow = G.dv.wrow<T>(b, h0, key);
+    const bool acc_k = (G.accumulate & PA_ACC_DK) != 0;
+    const bool acc_v = (G.accumulate & PA_ACC_DV) != 0;
+    const bool acc_m = (G.accumulate & PA_ACC_DVMUL) != 0;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = x * 32 + 8 * g + 4 * hh;
+            float kv[4], vv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                kv[r] = dk[x][4 * g + r] * P.scale;
+                vv[r] = dv[x][4 * g + r];
+            }
+            if (acc_k)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) kv[r] += to_f(dkrow[d + r]);
+            u32x2_t pk;
+            pk[0] = pack2<T>(kv[0], kv[1]);
+            pk[1] = pack2<T>(kv[2], kv[3]);
+            *reinterpret_cast<u32x2_t*>(dkrow + d) = pk;
+            if (HAS_VMUL) {
+                const T* mrow = P.vmul.row<T>(b, h0, key);
+                const T* vrow = P.v.row<T>(b, h0, key);
+                T* dmrow = G.dvmul.wrow<T>(b, h0, key);
+                float gv[4], gm[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    gv[r] = vv[r] * to_f(mrow[d + r]) + (acc_v ? to_f(dvrow[d + r]) : 0.f);
+                    gm[r] = vv[r] * to_f(vrow[d + r]) + (acc_m ? to_f(dmrow[d + r]) : 0.f);
+                }
+                pk[0] = pack2<T>(gv[0], gv[1]);
+                pk[1] = pack2<T>(gv[2], gv[3]);
+                *reinterpret_cast<u32x2_t*>(dvrow + d) = pk;
+                pk[0] = pack2<T>(gm[0], gm[1]);
+                pk[1] = pack2<T>(gm[2], gm[3]);
+                *reinterpret_cast<u32x2_t*>(dmrow + d) = pk;
+            } else {
+                if (acc_v)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) vv[r] += to_f(dvrow[d + r]);
+                pk[0] = pack2<T>(vv[0], vv[1]);
+                pk[1] = pack2<T>(vv[2], vv[3]);
+                *reinterpret_cast<u32x2_t*>(dvrow + d) = pk;
+            }
+        }
+    }
+    if (hh == 0 && G.dbias.ok()) {
+        float* o = G.dbias.wrow<float>(b, h0, key);
+        *o = dbias + ((G.accumulate & PA_ACC_DBIAS) ? *o : 0.f);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// dQ
+
+constexpr int kDqBM = 128;  // queries per workgroup
+constexpr int kDqBN = 64;   // keys per tile
+
+template <int D>
+struct DqTile {
+    static constexpr int RS = D + 8;
+    static constexpr int TS = kDqBN + 4;
+    static constexpr int BLOCKS = (kDqBN / 4) * (D / 8);
+    static constexpr int NB = (2 * BLOCKS + kBwdThreads - 1) / kBwdThreads;
+};
+
+template <int D>
+struct DqStage {
+    u32x4_t w[DqTile<D>::NB][4];
+    float bias;
+};
+
+template <typename T, int D, bool HAS_VMUL, bool HAS_BIAS>
+__device__ __forceinline__ void dq_load(const PassDev& P, int b, int h, int j0, DqStage<D>& st) {
+    using TL = DqTile<D>;
+    const int tid = threadIdx.x;
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int c = 0; c < TL::NB; ++c) {
+        const int task = tid + c * kBwdThreads;
+        if (task < 2 * TL::BLOCKS) {
+            const int tensor = task / TL::BLOCKS, blk = task % TL::BLOCKS;
+            const int rg = blk / (D / 8), cc = blk % (D / 8);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int j = j0 + rg * 4 + r;
+                if (j < P.nk) {
+                    if (tensor == 0) {
+                        st.w[c][r] = *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h, j) + cc * 8);
+                    } else {
+                        u32x4_t v = *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h, j) + cc * 8);
+                        if (HAS_VMUL)
+                            v = mul_round8<T>(v, *reinterpret_cast<const u32x4_t*>(P.vmul.row<T>(b, h, j) + cc * 8));
+                        st.w[c][r] = v;
+                    }
+                } else {
+                    st.w[c][r] = zero;
+                }
+            }
+        }
+    }
+    if (tid < kDqBN) {
+        const int j = j0 + tid;
+        float bv = -INFINITY;
+        if (j < P.nk) {
+            bv = 0.f;
+            if (HAS_BIAS) {
+                const float x = P.bias.scalar(b, h, j);
+                bv = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
+            }
+        }
+        st.bias = bv;
+    }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void dq_store(const DqStage<D>& st, T* sK, T* sV, T* sKt, float* sB) {
+    using TL = DqTile<D>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < TL::NB; ++c) {
+        const int task = tid + c * kBwdThreads;
+        if (task < 2 * TL::BLOCKS) {
+            const int tensor = task / TL::BLOCKS, blk = task % TL::BLOCKS;
+            const int rg = blk / (D / 8), cc = blk % (D / 8);
+            T* rows = tensor == 0 ? sK : sV;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<u32x4_t*>(rows + (rg * 4 + r) * TL::RS + cc * 8) = st.w[c][r];
+            if (tensor == 0)
+                store_block_transposed(st.w[c], reinterpret_cast<uint16_t*>(sKt + (cc * 8) * TL::TS + rg * 4),
+                                       TL::TS);
+        }
+    }
+    if (tid < kDqBN) sB[tid] = st.bias;
+}
+
+template <typename T, int D, bool CAUSAL, bool SOFTCLAMP, bool HAS_VMUL, bool HAS_BIAS>
+__global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(GradDev G) {
+    using TL = DqTile<D>;
+    using M = Mma<T>;
+    typedef typename M::frag frag;
+    const PassDev& P = G.f;
+    __shared__ __attribute__((aligned(16))) T sK[kDqBN * TL::RS];
+    __shared__ __attribute__((aligned(16))) T sV[kDqBN * TL::RS];
+    __shared__ __attribute__((aligned(16))) T sKt[D * TL::TS];
+    __shared__ __attribute__((aligned(16))) float sB[kDqBN];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hh = lane >> 5, kcol = lane & 31;
+    const int qblk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int qw0 = qblk * kDqBM + w * 32;
+    const int qi = qw0 + kcol;
+    const bool q_ok = qi < P.nq;
+
+    frag qf[D / 16], of[D / 16];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        u32x4_t qr = {0u, 0u, 0u, 0u}, orr = {0u, 0u, 0u, 0u};
+        if (q_ok) {
+            qr = *reinterpret_cast<const u32x4_t*>(P.q.row<T>(b, h, qi) + c * 16 + 8 * hh);
+            orr = *reinterpret_cast<const u32x4_t*>(G.dout.row<T>(b, h, qi) + c * 16 + 8 * hh);
+        }
+        qf[c] = __builtin_bit_cast(frag, qr);
+        of[c] = __builtin_bit_cast(frag, orr);
+    }
+    const int64_t row = ((int64_t)b * P.heads + h) * P.nq + (q_ok ? qi : 0);
+    const float lse_l2 = q_ok ? G.ws_lse[row] * kLog2e : INFINITY;
+    const float dpi = q_ok ? G.ws_D[row] : 0.f;
+    const float sl2 = P.scale * kLog2e;
+    const float cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
+
+    f32x16_t dq[D / 32];
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) dq[x] = zero16();
+
+    const int kend = CAUSAL ? min(P.nk, qblk * kDqBM + kDqBM) : P.nk;
+    const int ntiles = (kend + kDqBN - 1) / kDqBN;
+    DqStage<D> st;
+    dq_load<T, D, HAS_VMUL, HAS_BIAS>(P, b, h, 0, st);
+    for (int t = 0; t < ntiles; ++t) {
+        const int j0 = t * kDqBN;
+        dq_store<T, D>(st, sK, sV, sKt, sB);
+        __syncthreads();
+        if (t + 1 < ntiles) dq_load<T, D, HAS_VMUL, HAS_BIAS>(P, b, h, j0 + kDqBN, st);
+        if (!(CAUSAL && j0 > qw0 + 31)) {
+            const bool diag = CAUSAL && (j0 + kDqBN - 1 > qw0);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+                for (int c = 0; c < D / 16; ++c) {
+                    const int off = (kb * 32 + kcol) * TL::RS + c * 16 + 8 * hh;
+                    s = M::run(ld_frag<T>(sK + off), qf[c], s);
+                    dp = M::run(ld_frag<T>(sV + off), of[c], dp);
+                }
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int kr = kb * 32 + 8 * g + 4 * hh;
+                    const float4 bb = *reinterpret_cast<const float4*>(sB + kr);
+                    const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = 4 * g + r;
+                        float y = 0.f, x;
+                        if (SOFTCLAMP) {
+                            y = tanhf(s[i] * cinv);
+                            x = y * (P.softclamp * kLog2e) + bv[r] - lse_l2;
+                        } else {
+                            x = s[i] * sl2 + bv[r] - lse_l2;
+                        }
+                        float pv = exp2f(x);
+                        if (diag && (j0 + kr + r > qi)) pv = 0.f;
+                        float dsv = pv * (dp[i] - dpi);
+                        if (SOFTCLAMP) dsv *= (1.f - y * y);
+                        s[i] = dsv;
+                    }
+                }
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2) {
+                    const frag df = acc_to_frag<T>(s, t2);
+#pragma unroll
+                    for (int x = 0; x < D / 32; ++x) {
+                        const int toff = (x * 32 + kcol) * TL::TS + kb * 32 + 16 * t2 + 4 * hh;
+                        dq[x] = M::run(lds_runs<T>(sKt + toff), df, dq[x]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (!q_ok) return;
+    T* dqrow = G.dq.wrow<T>(b, h, qi);
+    const bool acc = (G.accumulate & PA_ACC_DQ) != 0;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = x * 32 + 8 * g + 4 * hh;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = dq[x][4 * g + r] * P.scale + (acc ? to_f(dqrow[d + r]) : 0.f);
+            u32x2_t pk;
+            pk[0] = pack2<T>(v[0], v[1]);
+            pk[1] = pack2<T>(v[2], v[3]);
+            *reinterpret_cast<u32x2_t*>(dqrow + d) = pk;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+
+bool mfma_bwd_supported(const GradDev& G, int dtype) {
+    const PassDev& P = G.f;
+    if (dtype != PA_BF16 && dtype != PA_F16) return false;
+    if (P.dim != 64 && P.dim != 128) return false;
+    if (P.km.p || P.qm.p || (P.flags & PA_FLAG_MAY_DEGENERATE)) return false;
+    const DView* loads[] = {&P.q, &P.k, &P.v, &G.dout};
+    for (const DView* v : loads)
+        if (!aligned_rows_host(*v, 8)) return false;
+    if (P.vmul.ok() && !aligned_rows_host(P.vmul, 8)) return false;
+    const DView* stores[] = {&G.dq, &G.dk, &G.dv};
+    for (const DView* v : stores)
+        if (!aligned_rows_host(*v, 4)) return false;
+    if (P.vmul.ok() && !aligned_rows_host(G.dvmul, 4)) return false;
+    return true;
+}
+
+template <typename T, int D, bool C, bool S, bool V, bool B>
+static void launch_bwd_t(const GradDev& G, hipStream_t s) {
+    const PassDev& P = G.f;
+    {
+        dim3 grid((P.nk + kKvBK - 1) / kKvBK, G.hk, P.batch);
+        ProfScope ps("mfma_bwd_dkv", s);
+        hipLaunchKernelGGL((k_mfma_bwd_dkv<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
+    }
+    {
+        dim3 grid((P.nq + kDqBM - 1) / kDqBM, P.heads, P.batch);
+        ProfScope ps("mfma_bwd_dq", s);
+        hipLaunchKernelGGL((k_mfma_bwd_dq<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
+    }
+}
+
+template <typename T, int D, bool C, bool S>
+static void launch_bwd_vb(const GradDev& G, hipStream_t s) {
+    const bool v = G.f.vmul.ok(), b = G.f.bias.ok();
+    if (v) b ? launch_bwd_t<T, D, C, S, true, true>(G, s) : launch_bwd_t<T, D, C, S, true, false>(G, s);
+    else b ? launch_bwd_t<T, D, C, S, false, true>(G, s) : launch_bwd_t<T, D, C, S, false, false>(G, s);
+}
+
+template <typename T, int D>
+static void launch_bwd_d(const GradDev& G, hipStream_t s) {
+    const bool c = G.f.causal != 0, sc = G.f.softclamp > 0.f;
+    if (c) sc ? launch_bwd_vb<T, D, true, true>(G, s) : launch_bwd_vb<T, D, true, false>(G, s);
+    else sc ? launch_bwd_vb<T, D, false, true>(G, s) : launch_bwd_vb<T, D, false, false>(G, s);
+}
+
+void launch_mfma_bwd(const GradDev& G, int dtype, hipStream_t s) {
+    if (dtype == PA_BF16) {
+        if (G.f.dim == 64) launch_bwd_d<bf16, 64>(G, s);
+        else launch_bwd_d<bf16, 128>(G, s);
+    } else {
+        if (G.f.dim == 64) launch_bwd_d<f16, 64>(G, s);
+        else launch_bwd_d<f16, 128>(G, s);
+    }
+}
+
+}  // namespace pa

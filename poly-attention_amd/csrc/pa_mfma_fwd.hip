@@ -14,46 +14,9 @@
 // reference's finite-fill semantics to them.
 #include "pa_common.h"
 #include "pa_launch.h"
+#include "pa_mfma.h"
 
 namespace pa {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-
-template <typename T> struct Mma;
-template <> struct Mma<bf16> {
-    typedef bf16x8_t frag;
-    static __device__ __forceinline__ f32x16_t run(frag a, frag b, f32x16_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-    }
-};
-template <> struct Mma<f16> {
-    typedef f16x8_t frag;
-    static __device__ __forceinline__ f32x16_t run(frag a, frag b, f32x16_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
-};
-
-template <typename T>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    const T a = (T)lo, b = (T)hi;
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-}
-
-template <typename T>
-__device__ __forceinline__ u32x4_t mul_round8(u32x4_t v, u32x4_t m) {
-    // element-wise v * m of 8 values, rounded to T (the reference multiplies in T)
-    const T* pv = reinterpret_cast<const T*>(&v);
-    const T* pm = reinterpret_cast<const T*>(&m);
-    u32x4_t r;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        r[k] = pack2<T>((float)pv[2 * k] * (float)pm[2 * k], (float)pv[2 * k + 1] * (float)pm[2 * k + 1]);
-    return r;
-}
 
 constexpr int kFwdBM = 128;  // query rows per workgroup
 constexpr int kFwdBN = 64;   // keys per tile
@@ -163,7 +126,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
     typedef typename M::frag frag;
     __shared__ __attribute__((aligned(16))) T sK[2][kFwdBN * TL::KS];
     __shared__ __attribute__((aligned(16))) T sVt[2][D * TL::VS];
-    __shared__ float sB[2][kFwdBN];
+    __shared__ __attribute__((aligned(16))) float sB[2][kFwdBN];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -302,22 +265,19 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
 
 // ---------------------------------------------------------------------------------------
 
-static bool aligned_rows(const DView& v, int elems) {
-    return ((uintptr_t)v.p % 16 == 0) && v.sb % elems == 0 && v.sh % elems == 0 && v.sn % elems == 0;
-}
-
 bool mfma_fwd_supported(const PassDev& P, int dtype) {
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
     if (P.dim != 64 && P.dim != 128) return false;
-    if (!aligned_rows(P.q, 8) || !aligned_rows(P.k, 8) || !aligned_rows(P.v, 8)) return false;
-    if (P.vmul.ok() && !aligned_rows(P.vmul, 8)) return false;
-    if (!aligned_rows(P.out, 4)) return false;
+    if (!aligned_rows_host(P.q, 8) || !aligned_rows_host(P.k, 8) || !aligned_rows_host(P.v, 8)) return false;
+    if (P.vmul.ok() && !aligned_rows_host(P.vmul, 8)) return false;
+    if (!aligned_rows_host(P.out, 4)) return false;
     return true;
 }
 
 template <typename T, int D, bool C, bool S, bool V>
 static void launch_t(const PassDev& P, hipStream_t s) {
     dim3 grid((P.nq + kFwdBM - 1) / kFwdBM, P.heads, P.batch);
+    ProfScope ps("mfma_fwd", s);
     hipLaunchKernelGGL((k_mfma_fwd<T, D, C, S, V>), grid, dim3(kFwdThreads), 0, s, P);
 }
 
@@ -342,9 +302,5 @@ void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s) {
         else launch_d<f16, 128>(P, s);
     }
 }
-
-// backward: MFMA kernels not built yet
-bool mfma_bwd_supported(const GradDev&, int) { return false; }
-void launch_mfma_bwd(const GradDev&, int, hipStream_t) {}
 
 }  // namespace pa

@@ -384,21 +384,30 @@ __global__ __launch_bounds__(kSimtRows) void k_simt_bwd_dkv(GradDev G) {
 template <typename T, int D>
 static void launch_simt_fwd_t(const PassDev& P, hipStream_t s) {
     dim3 grid((P.nq + kSimtRows - 1) / kSimtRows, P.heads, P.batch);
+    ProfScope ps("simt_fwd", s);
     hipLaunchKernelGGL((k_simt_fwd<T, D>), grid, dim3(kSimtRows), 0, s, P);
 }
 template <typename T, int D>
 static void launch_simt_fixup_t(const PassDev& P, hipStream_t s) {
     dim3 grid((P.nq + kSimtRows - 1) / kSimtRows, P.heads, P.batch);
+    ProfScope ps("simt_fixup", s);
     hipLaunchKernelGGL((k_simt_fixup<T, D>), grid, dim3(kSimtRows), 0, s, P);
 }
 template <typename T, int D>
 static void launch_simt_bwd_t(const GradDev& G, hipStream_t s, bool pre, bool dq, bool dkv) {
     const PassDev& P = G.f;
     dim3 qgrid((P.nq + kSimtRows - 1) / kSimtRows, P.heads, P.batch);
-    if (pre) hipLaunchKernelGGL((k_bwd_pre<T, D>), qgrid, dim3(kSimtRows), 0, s, G);
-    if (dq) hipLaunchKernelGGL((k_simt_bwd_dq<T, D>), qgrid, dim3(kSimtRows), 0, s, G);
+    if (pre) {
+        ProfScope ps("bwd_pre", s);
+        hipLaunchKernelGGL((k_bwd_pre<T, D>), qgrid, dim3(kSimtRows), 0, s, G);
+    }
+    if (dq) {
+        ProfScope ps("simt_bwd_dq", s);
+        hipLaunchKernelGGL((k_simt_bwd_dq<T, D>), qgrid, dim3(kSimtRows), 0, s, G);
+    }
     if (dkv) {
         dim3 kgrid((P.nk + kSimtRows - 1) / kSimtRows, G.hk, P.batch);
+        ProfScope ps("simt_bwd_dkv", s);
         hipLaunchKernelGGL((k_simt_bwd_dkv<T, D>), kgrid, dim3(kSimtRows), 0, s, G);
     }
 }

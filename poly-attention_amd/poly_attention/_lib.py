@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "pa_strerror",
     "pa_last_hip_error",
     "pa_struct_size",
+    "pa_profile_start",
+    "pa_profile_stop",
     "pa_attn_pass_fwd",
     "pa_attn_pass_bwd_workspace",
     "pa_attn_pass_bwd",
@@ -127,6 +129,10 @@ class PaDecode(ctypes.Structure):
     ]
 
 
+class PaKernelTime(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("launches", c_int64), ("total_ms", ctypes.c_double)]
+
+
 STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode)
 
 
@@ -154,6 +160,9 @@ def _configure(lib) -> None:
     lib.pa_last_hip_error.restype = c_int
     lib.pa_struct_size.restype = c_size_t
     lib.pa_struct_size.argtypes = [c_int]
+    lib.pa_profile_start.restype = c_int
+    lib.pa_profile_stop.restype = c_int
+    lib.pa_profile_stop.argtypes = [ctypes.POINTER(PaKernelTime), c_int, ctypes.POINTER(c_int)]
     lib.pa_attn_pass_fwd.restype = c_int
     lib.pa_attn_pass_fwd.argtypes = [ctypes.POINTER(PaPass), c_void_p]
     lib.pa_attn_pass_bwd_workspace.restype = c_size_t
@@ -210,3 +219,23 @@ def load_error() -> Exception | None:
 def check(status: int, what: str) -> None:
     if status != PA_OK:
         raise PolyAttnError(status, what, _LIB)
+
+
+class KernelProfile:
+    """Context manager timing every libpolyattn kernel launched inside it (HIP events on the
+    launch stream).  After exit, ``times`` maps kernel family -> (launches, total_ms)."""
+
+    def __init__(self):
+        self.times: dict[str, tuple[int, float]] = {}
+
+    def __enter__(self):
+        check(load().pa_profile_start(), "pa_profile_start")
+        return self
+
+    def __exit__(self, *exc):
+        buf = (PaKernelTime * 64)()
+        n = c_int(0)
+        check(load().pa_profile_stop(buf, 64, ctypes.byref(n)), "pa_profile_stop")
+        self.times = {buf[i].name.decode(): (buf[i].launches, buf[i].total_ms)
+                      for i in range(n.value)}
+        return False
