@@ -105,6 +105,19 @@ __device__ __forceinline__ void store_block_transposed(const u32x4_t* w, uint16_
     }
 }
 
+// bare v_exp_f32 (2^x; results below 2^-126 flush to 0, which softmax weights tolerate)
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Map the
+// hardware id to a logical id so that every XCD runs a contiguous range of logical ids --
+// consecutive logical ids share a head, so its K/V stay in that XCD's L2.
+constexpr int kNumXcd = 8;
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+    const int per = nblocks / kNumXcd, rem = nblocks % kNumXcd;
+    const int x = bid % kNumXcd, slot = bid / kNumXcd;
+    return (x < rem) ? x * (per + 1) + slot : rem * (per + 1) + (x - rem) * per + slot;
+}
+
 static inline bool aligned_rows_host(const DView& v, int elems) {
     return ((uintptr_t)v.p % 16 == 0) && v.sb % elems == 0 && v.sh % elems == 0 &&
            v.sn % elems == 0;

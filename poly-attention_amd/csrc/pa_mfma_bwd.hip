@@ -39,10 +39,35 @@ struct KvStage {
     float lse, dsum;
 };
 
-template <typename T, int D>
-__device__ __forceinline__ void kv_load(const GradDev& G, int b, int h, int q0, KvStage<D>& st) {
-    using TL = KvTile<D>;
+// Per (batch, query head) pointers of the query-side tiles.
+template <typename T>
+struct QuerySide {
+    const T* q;
+    const T* dout;
+    int64_t qsn, osn;
+    const float* lse;
+    const float* dsum;
+    int32_t nq;
+};
+
+template <typename T>
+__device__ __forceinline__ QuerySide<T> query_side(const GradDev& G, int b, int h) {
     const PassDev& P = G.f;
+    QuerySide<T> s;
+    s.q = P.q.row<T>(b, h, 0);
+    s.dout = G.dout.row<T>(b, h, 0);
+    s.qsn = P.q.sn;
+    s.osn = G.dout.sn;
+    const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
+    s.lse = G.ws_lse + row0;
+    s.dsum = G.ws_D + row0;
+    s.nq = P.nq;
+    return s;
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void kv_load(const QuerySide<T>& qs, int q0, KvStage<D>& st) {
+    using TL = KvTile<D>;
     const int tid = threadIdx.x;
     const u32x4_t zero = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -54,20 +79,19 @@ __device__ __forceinline__ void kv_load(const GradDev& G, int b, int h, int q0, 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int q = q0 + rg * 4 + r;
-                if (q < P.nq) {
-                    const T* src = tensor == 0 ? P.q.row<T>(b, h, q) : G.dout.row<T>(b, h, q);
-                    st.w[c][r] = *reinterpret_cast<const u32x4_t*>(src + cc * 8);
-                } else {
-                    st.w[c][r] = zero;
+                u32x4_t x = zero;
+                if (q < qs.nq) {
+                    const T* src = tensor == 0 ? qs.q + q * qs.qsn : qs.dout + q * qs.osn;
+                    x = *reinterpret_cast<const u32x4_t*>(src + cc * 8);
                 }
+                st.w[c][r] = x;
             }
         }
     }
     if (tid < kKvBQ) {
         const int q = q0 + tid;
-        const int64_t row = ((int64_t)b * P.heads + h) * P.nq + q;
-        st.lse = q < P.nq ? G.ws_lse[row] * kLog2e : INFINITY;
-        st.dsum = q < P.nq ? G.ws_D[row] : 0.f;
+        st.lse = q < qs.nq ? qs.lse[q] * kLog2e : INFINITY;
+        st.dsum = q < qs.nq ? qs.dsum[q] : 0.f;
     }
 }
 
@@ -112,7 +136,10 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int hh = lane >> 5, kcol = lane & 31;
-    const int kblk = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int nkb = (P.nk + kKvBK - 1) / kKvBK;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int kblk = lid % nkb;  // causal: the first key blocks carry the most work
+    const int kh = (lid / nkb) % G.hk, b = (lid / nkb) / G.hk;
     const int rep = P.heads / G.hk;
     const int h0 = kh * rep;
     const int kw0 = kblk * kKvBK + w * 32;  // first key of this wave
@@ -154,12 +181,13 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
     const int ntiles = P.nq > q_start ? (P.nq - q_start + kKvBQ - 1) / kKvBQ : 0;
     KvStage<D> st;
     for (int h = h0; h < h0 + rep; ++h) {
-        if (ntiles > 0) kv_load<T, D>(G, b, h, q_start, st);
+        const QuerySide<T> qs = query_side<T>(G, b, h);
+        if (ntiles > 0) kv_load<T, D>(qs, q_start, st);
         for (int t = 0; t < ntiles; ++t) {
             const int q0 = q_start + t * kKvBQ;
             kv_store<T, D>(st, sQ, sO, sQt, sOt, sL, sD);
             __syncthreads();
-            if (t + 1 < ntiles) kv_load<T, D>(G, b, h, q0 + kKvBQ, st);
+            if (t + 1 < ntiles) kv_load<T, D>(qs, q0 + kKvBQ, st);
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
                 const int qbase = q0 + qb * 32;
@@ -189,7 +217,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
                         } else {
                             x = s[i] * sl2 + bias_l2 - L[r];
                         }
-                        float pv = exp2f(x);
+                        float pv = fast_exp2(x);
                         if (diag && (q0 + ql + r < key)) pv = 0.f;
                         float dsv = pv * (dp[i] - Dd[r]);
                         dbias += dsv;
@@ -287,6 +315,35 @@ struct DqTile {
     static constexpr int NB = (2 * BLOCKS + kBwdThreads - 1) / kBwdThreads;
 };
 
+// Per (batch, key head) pointers of the key-side tiles.
+template <typename T>
+struct KeyRows {
+    const T* k;
+    const T* v;
+    const T* vm;
+    int64_t ksn, vsn, msn;
+    const char* bias;
+    int64_t bsn;
+    int32_t bdt;
+    int32_t nk;
+};
+
+template <typename T>
+__device__ __forceinline__ KeyRows<T> key_rows(const PassDev& P, int b, int h) {
+    KeyRows<T> s;
+    s.k = P.k.row<T>(b, h, 0);
+    s.v = P.v.row<T>(b, h, 0);
+    s.vm = P.vmul.ok() ? P.vmul.row<T>(b, h, 0) : nullptr;
+    s.ksn = P.k.sn;
+    s.vsn = P.v.sn;
+    s.msn = P.vmul.sn;
+    s.bias = P.bias.ok() ? P.bias.p + P.bias.idx(b, h, 0) * (P.bias.dtype == PA_F32 ? 4 : 2) : nullptr;
+    s.bsn = P.bias.sn;
+    s.bdt = P.bias.dtype;
+    s.nk = P.nk;
+    return s;
+}
+
 template <int D>
 struct DqStage {
     u32x4_t w[DqTile<D>::NB][4];
@@ -294,7 +351,7 @@ struct DqStage {
 };
 
 template <typename T, int D, bool HAS_VMUL, bool HAS_BIAS>
-__device__ __forceinline__ void dq_load(const PassDev& P, int b, int h, int j0, DqStage<D>& st) {
+__device__ __forceinline__ void dq_load(const KeyRows<T>& ks, int j0, DqStage<D>& st) {
     using TL = DqTile<D>;
     const int tid = threadIdx.x;
     const u32x4_t zero = {0u, 0u, 0u, 0u};
@@ -307,28 +364,27 @@ __device__ __forceinline__ void dq_load(const PassDev& P, int b, int h, int j0, 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int j = j0 + rg * 4 + r;
-                if (j < P.nk) {
+                u32x4_t x = zero;
+                if (j < ks.nk) {
                     if (tensor == 0) {
-                        st.w[c][r] = *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h, j) + cc * 8);
+                        x = *reinterpret_cast<const u32x4_t*>(ks.k + j * ks.ksn + cc * 8);
                     } else {
-                        u32x4_t v = *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h, j) + cc * 8);
+                        x = *reinterpret_cast<const u32x4_t*>(ks.v + j * ks.vsn + cc * 8);
                         if (HAS_VMUL)
-                            v = mul_round8<T>(v, *reinterpret_cast<const u32x4_t*>(P.vmul.row<T>(b, h, j) + cc * 8));
-                        st.w[c][r] = v;
+                            x = mul_round8<T>(x, *reinterpret_cast<const u32x4_t*>(ks.vm + j * ks.msn + cc * 8));
                     }
-                } else {
-                    st.w[c][r] = zero;
                 }
+                st.w[c][r] = x;
             }
         }
     }
     if (tid < kDqBN) {
         const int j = j0 + tid;
         float bv = -INFINITY;
-        if (j < P.nk) {
+        if (j < ks.nk) {
             bv = 0.f;
             if (HAS_BIAS) {
-                const float x = P.bias.scalar(b, h, j);
+                const float x = load_any(ks.bias, ks.bdt, j * ks.bsn);
                 bv = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
             }
         }
@@ -371,7 +427,10 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int hh = lane >> 5, kcol = lane & 31;
-    const int qblk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int nqb = (P.nq + kDqBM - 1) / kDqBM;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int qblk = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;  // heaviest first
+    const int h = (lid / nqb) % P.heads, b = (lid / nqb) / P.heads;
     const int qw0 = qblk * kDqBM + w * 32;
     const int qi = qw0 + kcol;
     const bool q_ok = qi < P.nq;
@@ -399,13 +458,14 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
 
     const int kend = CAUSAL ? min(P.nk, qblk * kDqBM + kDqBM) : P.nk;
     const int ntiles = (kend + kDqBN - 1) / kDqBN;
+    const KeyRows<T> ks = key_rows<T>(P, b, h);
     DqStage<D> st;
-    dq_load<T, D, HAS_VMUL, HAS_BIAS>(P, b, h, 0, st);
+    dq_load<T, D, HAS_VMUL, HAS_BIAS>(ks, 0, st);
     for (int t = 0; t < ntiles; ++t) {
         const int j0 = t * kDqBN;
         dq_store<T, D>(st, sK, sV, sKt, sB);
         __syncthreads();
-        if (t + 1 < ntiles) dq_load<T, D, HAS_VMUL, HAS_BIAS>(P, b, h, j0 + kDqBN, st);
+        if (t + 1 < ntiles) dq_load<T, D, HAS_VMUL, HAS_BIAS>(ks, j0 + kDqBN, st);
         if (!(CAUSAL && j0 > qw0 + 31)) {
             const bool diag = CAUSAL && (j0 + kDqBN - 1 > qw0);
 #pragma unroll
@@ -432,7 +492,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
                         } else {
                             x = s[i] * sl2 + bv[r] - lse_l2;
                         }
-                        float pv = exp2f(x);
+                        float pv = fast_exp2(x);
                         if (diag && (j0 + kr + r > qi)) pv = 0.f;
                         float dsv = pv * (dp[i] - dpi);
                         if (SOFTCLAMP) dsv *= (1.f - y * y);
@@ -493,12 +553,12 @@ template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_bwd_t(const GradDev& G, hipStream_t s) {
     const PassDev& P = G.f;
     {
-        dim3 grid((P.nk + kKvBK - 1) / kKvBK, G.hk, P.batch);
+        dim3 grid(((P.nk + kKvBK - 1) / kKvBK) * G.hk * P.batch);
         ProfScope ps("mfma_bwd_dkv", s);
         hipLaunchKernelGGL((k_mfma_bwd_dkv<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
     }
     {
-        dim3 grid((P.nq + kDqBM - 1) / kDqBM, P.heads, P.batch);
+        dim3 grid(((P.nq + kDqBM - 1) / kDqBM) * P.heads * P.batch);
         ProfScope ps("mfma_bwd_dq", s);
         hipLaunchKernelGGL((k_mfma_bwd_dq<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
     }

@@ -6,9 +6,12 @@
 // q = l % 32 and 16 key rows, so the online-softmax state (running max m, sum l and the
 // rescale of the output) is a per-lane scalar.  The probabilities, rounded to the input
 // type, stay in registers as the B operand of O^T += V^T . P^T (keys permuted consistently
-// between the two operands), V being staged transposed in LDS.  K / V tiles are double
-// buffered: the global loads of tile t+1 are in flight while tile t is computed.
-// The exponentials run in the log2 domain with scale*log2(e) folded into one multiply.
+// between the two operands, see pa_mfma.h), V being staged transposed in LDS.  K / V tiles
+// are double buffered: the global loads of tile t+1 are in flight while tile t is computed.
+// Exponentials run in the log2 domain (bare v_exp_f32) with scale*log2(e) folded into one
+// FMA; without a key bias the running max is taken on the raw scores.  The output rescale
+// is skipped when no lane's running max moved.  Workgroups are mapped XCD-aware (pa_mfma.h)
+// and causal query blocks run heaviest first.
 //
 // Rows whose every key is masked are left with lse = NaN for k_simt_fixup, which applies the
 // reference's finite-fill semantics to them.
@@ -22,62 +25,89 @@ constexpr int kFwdBM = 128;  // query rows per workgroup
 constexpr int kFwdBN = 64;   // keys per tile
 constexpr int kFwdThreads = 256;
 
-template <typename T, int D>
+template <int D>
 struct FwdTile {
-    static constexpr int KS = D + 8;          // K row stride in LDS (elements)
-    static constexpr int VS = kFwdBN + 4;     // V^T row stride in LDS (elements)
-    static constexpr int KCH = kFwdBN * D / 8 / kFwdThreads;  // 16-B K chunks per thread
-    static constexpr int VTASKS = (kFwdBN / 4) * (D / 8);    // 4-key x 8-dim V blocks
-    static constexpr int VT = (VTASKS + kFwdThreads - 1) / kFwdThreads;
+    static constexpr int KS = D + 8;       // K row stride in LDS (elements)
+    static constexpr int VS = kFwdBN + 4;  // V^T row stride in LDS (elements)
+    static constexpr int BLOCKS = (kFwdBN / 4) * (D / 8);  // 4-key x 8-dim blocks per tensor
+    static constexpr int NB = (2 * BLOCKS + kFwdThreads - 1) / kFwdThreads;
 };
 
+// Per-workgroup key-side pointers (batch and head resolved once).
+template <typename T>
+struct KeySide {
+    const T* k;
+    const T* v;
+    const T* vm;
+    int64_t ksn, vsn, msn;
+    const char* bias;
+    int64_t bsn;
+    int32_t bdt;
+    const uint8_t* km;
+    int64_t kmsn;
+    int32_t nk;
+};
+
+template <typename T>
+__device__ __forceinline__ KeySide<T> key_side(const PassDev& P, int b, int h) {
+    KeySide<T> s;
+    s.k = P.k.row<T>(b, h, 0);
+    s.v = P.v.row<T>(b, h, 0);
+    s.vm = P.vmul.ok() ? P.vmul.row<T>(b, h, 0) : nullptr;
+    s.ksn = P.k.sn;
+    s.vsn = P.v.sn;
+    s.msn = P.vmul.sn;
+    s.bias = P.bias.ok() ? P.bias.p + P.bias.idx(b, h, 0) * (P.bias.dtype == PA_F32 ? 4 : 2) : nullptr;
+    s.bsn = P.bias.sn;
+    s.bdt = P.bias.dtype;
+    s.km = P.km.p ? P.km.p + (int64_t)b * P.km.sb : nullptr;
+    s.kmsn = P.km.sn;
+    s.nk = P.nk;
+    return s;
+}
+
 // Registers holding one tile's global loads between issue and LDS store.
-template <typename T, int D>
+template <int D>
 struct FwdStage {
-    u32x4_t k[FwdTile<T, D>::KCH];
-    u32x4_t v[FwdTile<T, D>::VT][4];
+    u32x4_t w[FwdTile<D>::NB][4];
     float bias;
 };
 
-template <typename T, int D, bool HAS_VMUL>
-__device__ __forceinline__ void fwd_load_tile(const PassDev& P, int b, int h, int j0,
-                                              FwdStage<T, D>& st) {
-    using TL = FwdTile<T, D>;
+template <typename T, int D, bool HAS_VMUL, bool HAS_BIAS>
+__device__ __forceinline__ void fwd_load_tile(const KeySide<T>& ks, int j0, FwdStage<D>& st) {
+    using TL = FwdTile<D>;
     const int tid = threadIdx.x;
     const u32x4_t zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int c = 0; c < TL::KCH; ++c) {
-        const int e = tid + c * kFwdThreads;
-        const int row = e / (D / 8), ch = e % (D / 8);
-        const int j = j0 + row;
-        st.k[c] = (j < P.nk) ? *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h, j) + ch * 8) : zero;
-    }
-#pragma unroll
-    for (int c = 0; c < TL::VT; ++c) {
+    for (int c = 0; c < TL::NB; ++c) {
         const int task = tid + c * kFwdThreads;
-        const int dc = task % (D / 8), kg = task / (D / 8);
-        if (task < TL::VTASKS) {
+        if (task < 2 * TL::BLOCKS) {
+            const int tensor = task / TL::BLOCKS, blk = task % TL::BLOCKS;
+            const int rg = blk / (D / 8), cc = blk % (D / 8);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int j = j0 + kg * 4 + r;
-                if (j < P.nk) {
-                    u32x4_t v = *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h, j) + dc * 8);
-                    if (HAS_VMUL)
-                        v = mul_round8<T>(v, *reinterpret_cast<const u32x4_t*>(P.vmul.row<T>(b, h, j) + dc * 8));
-                    st.v[c][r] = v;
-                } else {
-                    st.v[c][r] = zero;
+                const int j = j0 + rg * 4 + r;
+                u32x4_t x = zero;
+                if (j < ks.nk) {
+                    if (tensor == 0) {
+                        x = *reinterpret_cast<const u32x4_t*>(ks.k + j * ks.ksn + cc * 8);
+                    } else {
+                        x = *reinterpret_cast<const u32x4_t*>(ks.v + j * ks.vsn + cc * 8);
+                        if (HAS_VMUL)
+                            x = mul_round8<T>(x, *reinterpret_cast<const u32x4_t*>(ks.vm + j * ks.msn + cc * 8));
+                    }
                 }
+                st.w[c][r] = x;
             }
         }
     }
-    if (tid < kFwdBN) {
+    if (HAS_BIAS && tid < kFwdBN) {
         const int j = j0 + tid;
         float bv = -INFINITY;
-        if (j < P.nk && P.km.keep(b, j)) {
+        if (j < ks.nk && (!ks.km || ks.km[j * ks.kmsn])) {
             bv = 0.f;
-            if (P.bias.ok()) {
-                const float x = P.bias.scalar(b, h, j);
+            if (ks.bias) {
+                const float x = load_any(ks.bias, ks.bdt, j * ks.bsn);
                 bv = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
             }
         }
@@ -85,162 +115,155 @@ __device__ __forceinline__ void fwd_load_tile(const PassDev& P, int b, int h, in
     }
 }
 
-template <typename T, int D>
-__device__ __forceinline__ void fwd_store_tile(const FwdStage<T, D>& st, T* sK, T* sVt, float* sB) {
-    using TL = FwdTile<T, D>;
+template <typename T, int D, bool HAS_BIAS>
+__device__ __forceinline__ void fwd_store_tile(const FwdStage<D>& st, T* sK, T* sVt, float* sB) {
+    using TL = FwdTile<D>;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int c = 0; c < TL::KCH; ++c) {
-        const int e = tid + c * kFwdThreads;
-        const int row = e / (D / 8), ch = e % (D / 8);
-        *reinterpret_cast<u32x4_t*>(sK + row * TL::KS + ch * 8) = st.k[c];
-    }
-#pragma unroll
-    for (int c = 0; c < TL::VT; ++c) {
+    for (int c = 0; c < TL::NB; ++c) {
         const int task = tid + c * kFwdThreads;
-        const int dc = task % (D / 8), kg = task / (D / 8);
-        if (task < TL::VTASKS) {
-            // transpose a 4-key x 8-dim block: V^T[d][k0..k0+3] for the 8 dims
+        if (task < 2 * TL::BLOCKS) {
+            const int tensor = task / TL::BLOCKS, blk = task % TL::BLOCKS;
+            const int rg = blk / (D / 8), cc = blk % (D / 8);
+            if (tensor == 0) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const uint32_t w0 = st.v[c][0][m], w1 = st.v[c][1][m];
-                const uint32_t w2 = st.v[c][2][m], w3 = st.v[c][3][m];
-                u32x2_t even, odd;
-                even[0] = (w0 & 0xffffu) | (w1 << 16);
-                even[1] = (w2 & 0xffffu) | (w3 << 16);
-                odd[0] = (w0 >> 16) | (w1 & 0xffff0000u);
-                odd[1] = (w2 >> 16) | (w3 & 0xffff0000u);
-                const int d = dc * 8 + 2 * m;
-                *reinterpret_cast<u32x2_t*>(sVt + d * TL::VS + kg * 4) = even;
-                *reinterpret_cast<u32x2_t*>(sVt + (d + 1) * TL::VS + kg * 4) = odd;
+                for (int r = 0; r < 4; ++r)
+                    *reinterpret_cast<u32x4_t*>(sK + (rg * 4 + r) * TL::KS + cc * 8) = st.w[c][r];
+            } else {
+                store_block_transposed(st.w[c], reinterpret_cast<uint16_t*>(sVt + (cc * 8) * TL::VS + rg * 4),
+                                       TL::VS);
             }
         }
     }
-    if (tid < kFwdBN) sB[tid] = st.bias;
+    if (HAS_BIAS && tid < kFwdBN) sB[tid] = st.bias;
 }
 
-template <typename T, int D, bool CAUSAL, bool SOFTCLAMP, bool HAS_VMUL>
+template <typename T, int D, bool CAUSAL, bool SOFTCLAMP, bool HAS_VMUL, bool HAS_BIAS>
 __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassDev P) {
-    using TL = FwdTile<T, D>;
+    using TL = FwdTile<D>;
     using M = Mma<T>;
     typedef typename M::frag frag;
+    constexpr bool PLAIN = !HAS_BIAS && !SOFTCLAMP;  // max taken on raw scores
     __shared__ __attribute__((aligned(16))) T sK[2][kFwdBN * TL::KS];
     __shared__ __attribute__((aligned(16))) T sVt[2][D * TL::VS];
     __shared__ __attribute__((aligned(16))) float sB[2][kFwdBN];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int hh = lane >> 5, kcol = lane & 31;
+    const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int qb = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;
+    const int bh = lid / nqb;
+    const int h = bh % P.heads, b = bh / P.heads;
     const int q0 = qb * kFwdBM + w * 32;
-    const int qi = q0 + (lane & 31);
-    const int hh = lane >> 5;
-    const int kcol = lane & 31;
+    const int qi = q0 + kcol;
 
     // Q^T operand fragments: lane (q, hh) holds Q[q][c*16 + 8*hh .. +7]
     frag qf[D / 16];
+    {
+        const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-        u32x4_t raw = {0u, 0u, 0u, 0u};
-        if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(P.q.row<T>(b, h, qi) + c * 16 + 8 * hh);
-        qf[c] = __builtin_bit_cast(frag, raw);
+        for (int c = 0; c < D / 16; ++c) {
+            u32x4_t raw = {0u, 0u, 0u, 0u};
+            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
+            qf[c] = __builtin_bit_cast(frag, raw);
+        }
     }
     f32x16_t o[D / 32];
 #pragma unroll
-    for (int x = 0; x < D / 32; ++x)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[x][i] = 0.f;
+    for (int x = 0; x < D / 32; ++x) o[x] = zero16();
     float m = -INFINITY, l = 0.f;
     const float sl2 = P.scale * kLog2e;
     const float cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
     const float cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
 
+    const KeySide<T> ks = key_side<T>(P, b, h);
     const int kend = CAUSAL ? min(P.nk, qb * kFwdBM + kFwdBM) : P.nk;
     const int ntiles = (kend + kFwdBN - 1) / kFwdBN;
 
-    FwdStage<T, D> st;
-    fwd_load_tile<T, D, HAS_VMUL>(P, b, h, 0, st);
-    fwd_store_tile<T, D>(st, sK[0], sVt[0], sB[0]);
+    FwdStage<D> st;
+    fwd_load_tile<T, D, HAS_VMUL, HAS_BIAS>(ks, 0, st);
+    fwd_store_tile<T, D, HAS_BIAS>(st, sK[0], sVt[0], sB[0]);
     __syncthreads();
 
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
         const int j0 = t * kFwdBN;
-        if (t + 1 < ntiles) fwd_load_tile<T, D, HAS_VMUL>(P, b, h, j0 + kFwdBN, st);
+        if (t + 1 < ntiles) fwd_load_tile<T, D, HAS_VMUL, HAS_BIAS>(ks, j0 + kFwdBN, st);
         if (!(CAUSAL && j0 > q0 + 31)) {
             const T* K = sK[buf];
             const T* Vt = sVt[buf];
-            const float* Bs = sB[buf];
             f32x16_t s[2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
+                s[kb] = zero16();
 #pragma unroll
-                for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
-#pragma unroll
-                for (int c = 0; c < D / 16; ++c) {
-                    const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(
-                        K + (kb * 32 + kcol) * TL::KS + c * 16 + 8 * hh);
-                    s[kb] = M::run(__builtin_bit_cast(frag, raw), qf[c], s[kb]);
-                }
+                for (int c = 0; c < D / 16; ++c)
+                    s[kb] = M::run(ld_frag<T>(K + (kb * 32 + kcol) * TL::KS + c * 16 + 8 * hh), qf[c], s[kb]);
             }
-            // scores in the log2 domain, bias / masks, running max
-            const bool diag = CAUSAL && (j0 + kFwdBN - 1 > q0);
+            // scores (log2 domain unless PLAIN), masks, running max
+            const bool edge = (CAUSAL && j0 + kFwdBN - 1 > q0) || (!HAS_BIAS && j0 + kFwdBN > P.nk);
             float mx = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int kr = kb * 32 + 8 * g + 4 * hh;  // first of 4 consecutive keys
-                    const float4 bb = *reinterpret_cast<const float4*>(Bs + kr);
-                    const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
+                    const int kr = kb * 32 + 8 * g + 4 * hh;
+                    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+                    if (HAS_BIAS) {
+                        const float4 bb = *reinterpret_cast<const float4*>(sB[buf] + kr);
+                        bv[0] = bb.x;
+                        bv[1] = bb.y;
+                        bv[2] = bb.z;
+                        bv[3] = bb.w;
+                    }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = 4 * g + r;
-                        float x;
-                        if (SOFTCLAMP) x = cl2 * tanhf(s[kb][i] * cinv) + bv[r];
-                        else x = s[kb][i] * sl2 + bv[r];
-                        if (diag && (j0 + kr + r > qi)) x = -INFINITY;
+                        float x = s[kb][i];
+                        if (!PLAIN) x = (SOFTCLAMP ? cl2 * tanhf(x * cinv) : x * sl2) + bv[r];
+                        if (edge) {
+                            const int key = j0 + kr + r;
+                            if ((CAUSAL && key > qi) || key >= P.nk) x = -INFINITY;
+                        }
                         s[kb][i] = x;
                         mx = fmaxf(mx, x);
                     }
                 }
             }
             mx = fmaxf(mx, __shfl_xor(mx, 32));
+            if (PLAIN) mx *= sl2;
             const float m_new = fmaxf(m, mx);
-            const float alpha = (m == m_new) ? 1.f : exp2f(m - m_new);
-            const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;
-            m = m_new;
-            l *= alpha;
+            if (__any(m_new > m)) {
+                const float alpha = (m_new > m) ? fast_exp2(m - m_new) : 1.f;
+                l *= alpha;
 #pragma unroll
-            for (int x = 0; x < D / 32; ++x)
+                for (int x = 0; x < D / 32; ++x)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) o[x][i] *= alpha;
+                    for (int i = 0; i < 16; ++i) o[x][i] *= alpha;
+                m = m_new;
+            }
+            const float m_sub = (m == -INFINITY) ? 0.f : m;
             // P^T operands and O^T += V^T . P^T
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float p = PLAIN ? fast_exp2(fmaf(s[kb][i], sl2, -m_sub)) : fast_exp2(s[kb][i] - m_sub);
+                    s[kb][i] = p;
+                    l += p;
+                }
+#pragma unroll
                 for (int t2 = 0; t2 < 2; ++t2) {
-                    float p[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        p[e] = exp2f(s[kb][8 * t2 + e] - m_sub);
-                        l += p[e];
-                    }
-                    u32x4_t praw;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) praw[k] = pack2<T>(p[2 * k], p[2 * k + 1]);
-                    const frag pb = __builtin_bit_cast(frag, praw);
+                    const frag pb = acc_to_frag<T>(s[kb], t2);
                     const int kbase = kb * 32 + 16 * t2 + 4 * hh;
 #pragma unroll
-                    for (int x = 0; x < D / 32; ++x) {
-                        const T* vrow = Vt + (x * 32 + kcol) * TL::VS + kbase;
-                        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
-                        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 8);
-                        const u32x4_t vraw = {lo[0], lo[1], hi[0], hi[1]};
-                        o[x] = M::run(__builtin_bit_cast(frag, vraw), pb, o[x]);
-                    }
+                    for (int x = 0; x < D / 32; ++x)
+                        o[x] = M::run(lds_runs<T>(Vt + (x * 32 + kcol) * TL::VS + kbase), pb, o[x]);
                 }
             }
         }
-        if (t + 1 < ntiles) fwd_store_tile<T, D>(st, sK[buf ^ 1], sVt[buf ^ 1], sB[buf ^ 1]);
+        if (t + 1 < ntiles) fwd_store_tile<T, D, HAS_BIAS>(st, sK[buf ^ 1], sVt[buf ^ 1], sB[buf ^ 1]);
         __syncthreads();
     }
 
@@ -274,23 +297,26 @@ bool mfma_fwd_supported(const PassDev& P, int dtype) {
     return true;
 }
 
-template <typename T, int D, bool C, bool S, bool V>
+template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_t(const PassDev& P, hipStream_t s) {
-    dim3 grid((P.nq + kFwdBM - 1) / kFwdBM, P.heads, P.batch);
+    const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
+    dim3 grid(nqb * P.heads * P.batch);
     ProfScope ps("mfma_fwd", s);
-    hipLaunchKernelGGL((k_mfma_fwd<T, D, C, S, V>), grid, dim3(kFwdThreads), 0, s, P);
+    hipLaunchKernelGGL((k_mfma_fwd<T, D, C, S, V, B>), grid, dim3(kFwdThreads), 0, s, P);
+}
+
+template <typename T, int D, bool C, bool S>
+static void launch_vb(const PassDev& P, hipStream_t s) {
+    const bool v = P.vmul.ok(), b = P.bias.ok() || P.km.p;
+    if (v) b ? launch_t<T, D, C, S, true, true>(P, s) : launch_t<T, D, C, S, true, false>(P, s);
+    else b ? launch_t<T, D, C, S, false, true>(P, s) : launch_t<T, D, C, S, false, false>(P, s);
 }
 
 template <typename T, int D>
 static void launch_d(const PassDev& P, hipStream_t s) {
-    const bool c = P.causal != 0, sc = P.softclamp > 0.f, v = P.vmul.ok();
-    if (c) {
-        if (sc) v ? launch_t<T, D, true, true, true>(P, s) : launch_t<T, D, true, true, false>(P, s);
-        else v ? launch_t<T, D, true, false, true>(P, s) : launch_t<T, D, true, false, false>(P, s);
-    } else {
-        if (sc) v ? launch_t<T, D, false, true, true>(P, s) : launch_t<T, D, false, true, false>(P, s);
-        else v ? launch_t<T, D, false, false, true>(P, s) : launch_t<T, D, false, false, false>(P, s);
-    }
+    const bool c = P.causal != 0, sc = P.softclamp > 0.f;
+    if (c) sc ? launch_vb<T, D, true, true>(P, s) : launch_vb<T, D, true, false>(P, s);
+    else sc ? launch_vb<T, D, false, true>(P, s) : launch_vb<T, D, false, false>(P, s);
 }
 
 void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s) {

@@ -196,6 +196,53 @@ __global__ __launch_bounds__(kSimtRows) void k_bwd_pre(GradDev G) {
     G.ws_invc[r] = invc;
 }
 
+// The same preprocess for 16-bit types with head dims that are multiples of 8: LPR lanes
+// per row read 16 bytes each (a wave covers 64/LPR whole rows per load), then reduce.
+template <typename T, int LPR>
+__global__ __launch_bounds__(256) void k_bwd_pre_vec(GradDev G) {
+    const PassDev& P = G.f;
+    constexpr int kRows = 256 / LPR;
+    const int64_t total = (int64_t)P.batch * P.heads * P.nq;
+    const int64_t r = (int64_t)blockIdx.x * kRows + threadIdx.x / LPR;
+    const int sub = threadIdx.x % LPR;
+    if (r >= total) return;  // whole LPR-lane groups leave together
+    const int i = (int)(r % P.nq);
+    const int h = (int)((r / P.nq) % P.heads), b = (int)(r / ((int64_t)P.nq * P.heads));
+    const int d0 = sub * 8;
+    float dsum = 0.f;
+    if (d0 < P.dim) {
+        const uint4 ov = *reinterpret_cast<const uint4*>(P.out.row<T>(b, h, i) + d0);
+        const uint4 gv = *reinterpret_cast<const uint4*>(G.dout.row<T>(b, h, i) + d0);
+        const T* oe = reinterpret_cast<const T*>(&ov);
+        const T* ge = reinterpret_cast<const T*>(&gv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dsum += to_f(oe[e]) * to_f(ge[e]);
+    }
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off);
+    if (sub != 0) return;
+    const float dl = G.dlse.ok() ? *G.dlse.row<float>(b, h, i) : 0.f;
+    const float l = *P.lse.row<float>(b, h, i);
+    float lseb = l, invc = 0.f;
+    if (l > kMaskedThreshold) {
+        dsum -= dl;
+    } else {  // fully-masked row (rare): count its class-1 entries
+        const bool qok = P.qm.keep(b, i);
+        float c1 = 0.f;
+        for (int j = 0; j < P.nk; ++j) {
+            const bool own_masked = !qok || (P.causal && j > i) || !P.km.keep(b, j);
+            const float bj = P.bias.ok() ? P.bias.scalar(b, h, j) : 0.f;
+            if ((own_masked ? 1 : 0) + bias_class(bj) == 1) c1 += 1.f;
+        }
+        lseb = INFINITY;
+        invc = c1 > 0.f ? 1.f / c1 : 0.f;
+        dsum = c1 > 0.f ? dsum - c1 * dl : 0.f;
+    }
+    G.ws_D[r] = dsum;
+    G.ws_lse[r] = lseb;
+    G.ws_invc[r] = invc;
+}
+
 // probability of entry (i, j) given the row's (lse, 1/c1) and the entry's mask state
 __device__ __forceinline__ float entry_prob(bool normal, bool own_ok, int bcls, float y_plus_bias,
                                             float lseb, float invc) {
@@ -399,7 +446,26 @@ static void launch_simt_bwd_t(const GradDev& G, hipStream_t s, bool pre, bool dq
     dim3 qgrid((P.nq + kSimtRows - 1) / kSimtRows, P.heads, P.batch);
     if (pre) {
         ProfScope ps("bwd_pre", s);
-        hipLaunchKernelGGL((k_bwd_pre<T, D>), qgrid, dim3(kSimtRows), 0, s, G);
+        auto al16 = [](const DView& v) {
+            return (uintptr_t)v.p % 16 == 0 && v.sb % 8 == 0 && v.sh % 8 == 0 && v.sn % 8 == 0;
+        };
+        const bool vec = sizeof(T) == 2 && P.dim % 8 == 0 && al16(P.out) && al16(G.dout);
+        if (vec) {
+            int lpr = 1;
+            while (lpr * 8 < P.dim) lpr <<= 1;
+            const int64_t total = (int64_t)P.batch * P.heads * P.nq;
+            const unsigned blocks = (unsigned)((total * lpr + 255) / 256);
+            switch (lpr) {
+                case 1: hipLaunchKernelGGL((k_bwd_pre_vec<T, 1>), dim3(blocks), dim3(256), 0, s, G); break;
+                case 2: hipLaunchKernelGGL((k_bwd_pre_vec<T, 2>), dim3(blocks), dim3(256), 0, s, G); break;
+                case 4: hipLaunchKernelGGL((k_bwd_pre_vec<T, 4>), dim3(blocks), dim3(256), 0, s, G); break;
+                case 8: hipLaunchKernelGGL((k_bwd_pre_vec<T, 8>), dim3(blocks), dim3(256), 0, s, G); break;
+                case 16: hipLaunchKernelGGL((k_bwd_pre_vec<T, 16>), dim3(blocks), dim3(256), 0, s, G); break;
+                default: hipLaunchKernelGGL((k_bwd_pre_vec<T, 32>), dim3(blocks), dim3(256), 0, s, G); break;
+            }
+        } else {
+            hipLaunchKernelGGL((k_bwd_pre<T, D>), qgrid, dim3(kSimtRows), 0, s, G);
+        }
     }
     if (dq) {
         ProfScope ps("simt_bwd_dq", s);
