@@ -28,8 +28,9 @@ struct DecodeDev {
 };
 
 constexpr int kDecThreads = 256;
-constexpr int kDecHB = 4;      // heads per register batch in the partial kernel
-constexpr int kDecUnroll = 4;  // positions in flight per key group
+constexpr int kDecHB = 8;      // level heads scored per pass over a chunk's K rows
+constexpr int kDecU = 8;       // rows in flight per row group
+constexpr int kDecScoreElems = 8192;  // LDS floats for one chunk's scores (heads x positions)
 constexpr int kDecMaxHeadsPerGroup = 64;
 constexpr int kDecMaxGroupElems = 8192;  // level heads per KV group * head dim
 
@@ -60,145 +61,182 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float* a, float 
     m = mn;
 }
 
-template <typename T>
+// Sum over the LPR lanes of a row group (LPR <= 16 stays inside a 16-lane DPP row).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                                 0xF, 0xF, false));
+}
+template <int LPR>
+__device__ __forceinline__ float group_sum(float x) {
+    if (LPR >= 2) x += dpp_f<0xB1>(x);   // quad_perm [1,0,3,2]
+    if (LPR >= 4) x += dpp_f<0x4E>(x);   // quad_perm [2,3,0,1]
+    if (LPR >= 8) x += dpp_f<0x141>(x);  // row_half_mirror
+    if (LPR >= 16) x += dpp_f<0x140>(x); // row_mirror
+    if (LPR >= 32) x += __shfl_xor(x, 16);
+    if (LPR >= 64) x += __shfl_xor(x, 32);
+    return x;
+}
+
+// One workgroup per (chunk of cached positions, batch, KV group, level):
+//   1. the chunk's key biases (the deeper level's lse, log2 domain) are staged in LDS, then
+//      each row group of LPR lanes reads whole K rows (16 bytes per lane, kDecU rows in
+//      flight) and adds the score of every level head of the group;
+//   2. per head: max, p = 2^(s - max) in place, and the sum, over the chunk;
+//   3. per head: the values (times vmul for middle levels) are streamed with one FMA per
+//      element, reduced over the row groups and written as the chunk record (m, l, sum p v).
+template <typename T, int LPR>
 __global__ __launch_bounds__(kDecThreads) void k_dec_partial(DecodeDev D) {
     constexpr int E = Vec16<T>::n;
+    constexpr int KG = kDecThreads / LPR;
+    __shared__ float s_sc[kDecScoreElems];
+    __shared__ float s_ml[kDecMaxHeadsPerGroup][2];
+    __shared__ float s_acc[kDecThreads / 64][256];
+
     const int c = blockIdx.x, bg = blockIdx.y, t = blockIdx.z;
     const int b = bg / D.kv_heads, g = bg % D.kv_heads;
     const DecLevelDev& L = D.L[t];
-    const int lpr = D.lpr;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane & (lpr - 1);
-    const int kg = threadIdx.x / lpr;
-    const int KG = kDecThreads / lpr;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = tid % LPR, kg = tid / LPR;
     const int d0 = sub * E;
     const bool dok = d0 < D.dim;
-    const int j_begin = c * D.chunk;
-    const int j_end = min(j_begin + D.chunk, D.n - 1);
-    const bool has_bias = L.bias.ok(), has_vmul = L.vmul.ok();
+    const int C = D.chunk;
+    const int j_begin = c * C;
+    const int cnt = min(C, D.n - 1 - j_begin);
+    const int rep = L.rep, h0 = g * rep;
+    const float cinv = D.softclamp > 0.f ? D.scale / D.softclamp : 0.f;
+    const float cl2 = D.softclamp * kLog2e;
+    const float sl2 = D.scale * kLog2e;
 
-    __shared__ float s_red[kDecThreads / 64][kDecHB][2];
-    __shared__ float s_acc[kDecThreads / 64][kDecHB][256];
+    // 1a. biases
+    for (int x = tid; x < rep * cnt; x += kDecThreads) {
+        const int hh = x / cnt, jl = x % cnt;
+        float bv = 0.f;
+        if (L.bias.ok()) {
+            const float bj = L.bias.scalar(b, h0 + hh, j_begin + jl);
+            bv = bias_class(bj) == 0 ? bj * kLog2e : -INFINITY;
+        }
+        s_sc[hh * C + jl] = bv;
+    }
+    __syncthreads();
 
-    for (int hb0 = 0; hb0 < L.rep; hb0 += kDecHB) {
-        const int nh = min(kDecHB, L.rep - hb0);
-        float qv[kDecHB][E], acc[kDecHB][E], m[kDecHB], l[kDecHB];
+    // 1b. scores, heads in batches of kDecHB (K re-read per batch when rep > kDecHB)
+    const T* kbase = L.k.row<T>(b, h0, 0) + d0;
+    const int64_t ksn = L.k.sn;
+    for (int hb0 = 0; hb0 < rep; hb0 += kDecHB) {
+        float qv[kDecHB][E];
 #pragma unroll
         for (int hh = 0; hh < kDecHB; ++hh) {
-            const int h = g * L.rep + hb0 + hh;
-            if (hh < nh && dok) load16<T>(L.q.row<T>(b, h, 0) + d0, qv[hh]);
+            if (hb0 + hh < rep && dok) load16<T>(L.q.row<T>(b, h0 + hb0 + hh, 0) + d0, qv[hh]);
             else
 #pragma unroll
                 for (int e = 0; e < E; ++e) qv[hh][e] = 0.f;
-#pragma unroll
-            for (int e = 0; e < E; ++e) acc[hh][e] = 0.f;
-            m[hh] = -INFINITY;
-            l[hh] = 0.f;
         }
-        const int h0 = g * L.rep + hb0;
-        for (int jb = j_begin + kg; jb < j_end; jb += KG * kDecUnroll) {
-            float kf[kDecUnroll][E];
+        for (int jl0 = kg; jl0 < cnt; jl0 += KG * kDecU) {
+            float kf[kDecU][E];
 #pragma unroll
-            for (int u = 0; u < kDecUnroll; ++u) {
-                const int j = jb + u * KG;
-                if (j < j_end && dok) load16<T>(L.k.row<T>(b, h0, j) + d0, kf[u]);
+            for (int u = 0; u < kDecU; ++u) {
+                const int jl = jl0 + u * KG;
+                if (jl < cnt && dok) load16<T>(kbase + (j_begin + jl) * ksn, kf[u]);
                 else
 #pragma unroll
                     for (int e = 0; e < E; ++e) kf[u][e] = 0.f;
             }
 #pragma unroll
             for (int hh = 0; hh < kDecHB; ++hh) {
-                if (hh >= nh) break;
-                const int h = h0 + hh;
-                float vf[kDecUnroll][E], sc[kDecUnroll];
+                if (hb0 + hh >= rep) break;
 #pragma unroll
-                for (int u = 0; u < kDecUnroll; ++u) {
-                    const int j = jb + u * KG;
-                    float s = 0.f;
+                for (int u = 0; u < kDecU; ++u) {
+                    float part = 0.f;
 #pragma unroll
-                    for (int e = 0; e < E; ++e) s += qv[hh][e] * kf[u][e];
-                    sc[u] = s;
-                    if (j < j_end && dok) {
-                        load16<T>(L.v.row<T>(b, h, j) + d0, vf[u]);
-                        if (has_vmul) {
-                            float mf[E];
-                            load16<T>(L.vmul.row<T>(b, h, j) + d0, mf);
-#pragma unroll
-                            for (int e = 0; e < E; ++e) vf[u][e] = round_to<T>(vf[u][e] * mf[e]);
-                        }
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < E; ++e) vf[u][e] = 0.f;
+                    for (int e = 0; e < E; ++e) part += qv[hh][e] * kf[u][e];
+                    const float dot = group_sum<LPR>(part);
+                    const int jl = jl0 + u * KG;
+                    if (sub == 0 && jl < cnt) {
+                        const float x = D.softclamp > 0.f ? cl2 * tanhf(dot * cinv) : dot * sl2;
+                        s_sc[(hb0 + hh) * C + jl] += x;
                     }
                 }
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. per-head max, exponentials and sum
+    for (int hh = wave; hh < rep; hh += kDecThreads / 64) {
+        float* sc = s_sc + hh * C;
+        float mx = -INFINITY;
+        for (int jl = lane; jl < cnt; jl += 64) mx = fmaxf(mx, sc[jl]);
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        const float msub = mx == -INFINITY ? 0.f : mx;
+        float sum = 0.f;
+        for (int jl = lane; jl < cnt; jl += 64) {
+            const float p = __builtin_amdgcn_exp2f(sc[jl] - msub);
+            sc[jl] = p;
+            sum += p;
+        }
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+        if (lane == 0) {
+            s_ml[hh][0] = mx;
+            s_ml[hh][1] = sum;
+        }
+    }
+    __syncthreads();
+
+    // 3. values
+    const bool has_vmul = L.vmul.ok();
+    for (int hh = 0; hh < rep; ++hh) {
+        const int h = h0 + hh;
+        const T* vbase = L.v.row<T>(b, h, 0) + d0;
+        const T* mbase = has_vmul ? L.vmul.row<T>(b, h, 0) + d0 : nullptr;
+        const int64_t vsn = L.v.sn, msn = L.vmul.sn;
+        const float* p = s_sc + hh * C;
+        float acc[E];
 #pragma unroll
-                for (int u = 0; u < kDecUnroll; ++u) {
-                    float s = sc[u];
-                    for (int off = lpr >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off);
-                    const int j = jb + u * KG;
-                    if (j >= j_end) continue;
-                    float bj = has_bias ? L.bias.scalar(b, h, j) : 0.f;
-                    if (bias_class(bj) != 0) continue;  // -FLT_MAX / -inf keys: weight 0
-                    const float tt = (softclamp_f(s * D.scale, D.softclamp) + bj) * kLog2e;
-                    if (tt > m[hh]) {
-                        const float cc = exp2f(m[hh] - tt);
-                        l[hh] *= cc;
+        for (int e = 0; e < E; ++e) acc[e] = 0.f;
+        for (int jl0 = kg; jl0 < cnt; jl0 += KG * kDecU) {
+            float vf[kDecU][E];
 #pragma unroll
-                        for (int e = 0; e < E; ++e) acc[hh][e] *= cc;
-                        m[hh] = tt;
+            for (int u = 0; u < kDecU; ++u) {
+                const int jl = jl0 + u * KG;
+                if (jl < cnt && dok) {
+                    load16<T>(vbase + (j_begin + jl) * vsn, vf[u]);
+                    if (has_vmul) {
+                        float mf[E];
+                        load16<T>(mbase + (j_begin + jl) * msn, mf);
+#pragma unroll
+                        for (int e = 0; e < E; ++e) vf[u][e] = round_to<T>(vf[u][e] * mf[e]);
                     }
-                    const float p = exp2f(tt - m[hh]);
-                    l[hh] += p;
+                } else {
 #pragma unroll
-                    for (int e = 0; e < E; ++e) acc[hh][e] += p * vf[u][e];
+                    for (int e = 0; e < E; ++e) vf[u][e] = 0.f;
                 }
             }
-        }
-        // merge key groups inside the wave (lanes with equal `sub`)
-        for (int off = lpr; off < 64; off <<= 1) {
 #pragma unroll
-            for (int hh = 0; hh < kDecHB; ++hh) {
-                const float m2 = __shfl_xor(m[hh], off);
-                const float l2 = __shfl_xor(l[hh], off);
-                float a2[E];
+            for (int u = 0; u < kDecU; ++u) {
+                const int jl = jl0 + u * KG;
+                const float pj = jl < cnt ? p[jl] : 0.f;
 #pragma unroll
-                for (int e = 0; e < E; ++e) a2[e] = __shfl_xor(acc[hh][e], off);
-                merge_state<E>(m[hh], l[hh], acc[hh], m2, l2, a2);
+                for (int e = 0; e < E; ++e) acc[e] += pj * vf[u][e];
             }
         }
-        // merge the waves through LDS
-        if (lane < lpr) {
+        for (int off = LPR; off < 64; off <<= 1)
 #pragma unroll
-            for (int hh = 0; hh < kDecHB; ++hh) {
-                if (lane == 0) {
-                    s_red[wave][hh][0] = m[hh];
-                    s_red[wave][hh][1] = l[hh];
-                }
+            for (int e = 0; e < E; ++e) acc[e] += __shfl_xor(acc[e], off);
+        if (lane < LPR && dok)
 #pragma unroll
-                for (int e = 0; e < E; ++e)
-                    if (d0 + e < 256) s_acc[wave][hh][d0 + e] = acc[hh][e];
-            }
-        }
+            for (int e = 0; e < E; ++e) s_acc[wave][d0 + e] = acc[e];
         __syncthreads();
-        for (int x = threadIdx.x; x < nh * D.dim; x += kDecThreads) {
-            const int hh = x / D.dim, d = x % D.dim;
-            float mm = -INFINITY, ll = 0.f, aa = 0.f;
-            for (int w = 0; w < kDecThreads / 64; ++w) {
-                const float m2 = s_red[w][hh][0];
-                const float mn = fmaxf(mm, m2);
-                if (mn == -INFINITY) continue;
-                const float c1 = exp2f(mm - mn), c2 = exp2f(m2 - mn);
-                ll = ll * c1 + s_red[w][hh][1] * c2;
-                aa = aa * c1 + s_acc[w][hh][d] * c2;
-                mm = mn;
-            }
-            const int h = h0 + hh;
-            float* rec = L.ws + (((int64_t)b * L.heads + h) * D.nchunks + c) * D.rec;
-            rec[2 + d] = aa;
-            if (d == 0) {
-                rec[0] = mm;
-                rec[1] = ll;
-            }
+        float* rec = L.ws + (((int64_t)b * L.heads + h) * D.nchunks + c) * D.rec;
+        for (int x = tid; x < D.dim; x += kDecThreads) {
+            float a = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < kDecThreads / 64; ++w2) a += s_acc[w2][x];
+            rec[2 + x] = a;
+        }
+        if (tid == 0) {
+            rec[0] = s_ml[hh][0];
+            rec[1] = s_ml[hh][1];
         }
         __syncthreads();
     }
@@ -342,16 +380,40 @@ static int pick_chunks(const pa_decode* d, int* chunk_out) {
         *chunk_out = 1;
         return 0;
     }
+    // the scores of one chunk (level heads per KV group x positions) live in LDS
+    int max_rep = 1;
+    for (int t = 0; t < d->order && t < PA_MAX_ORDER; ++t)
+        if (d->kv_heads > 0 && d->levels[t].heads / d->kv_heads > max_rep)
+            max_rep = d->levels[t].heads / d->kv_heads;
+    int cap = kDecScoreElems / max_rep;
+    if (cap > 1024) cap = 1024;
+    cap = cap / 64 * 64;
+    if (cap < 64) cap = 64;
     int chunk = d->chunk;
     if (chunk <= 0) {
         const long units = (long)d->batch * d->kv_heads * d->order;
         long want = (2048 + units - 1) / units;  // aim for >= 2048 workgroups
         if (want < 1) want = 1;
         chunk = (int)((nold + want - 1) / want);
-        if (chunk < 256) chunk = 256;
+        chunk = (chunk + 63) / 64 * 64;
     }
+    if (chunk > cap) chunk = cap;
+    if (chunk < 64) chunk = 64;
     *chunk_out = chunk;
     return (nold + chunk - 1) / chunk;
+}
+
+template <typename T>
+static void launch_partial_t(const DecodeDev& D, dim3 grid, hipStream_t s) {
+    switch (D.lpr) {
+        case 1: hipLaunchKernelGGL((k_dec_partial<T, 1>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 2: hipLaunchKernelGGL((k_dec_partial<T, 2>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 4: hipLaunchKernelGGL((k_dec_partial<T, 4>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 8: hipLaunchKernelGGL((k_dec_partial<T, 8>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 16: hipLaunchKernelGGL((k_dec_partial<T, 16>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 32: hipLaunchKernelGGL((k_dec_partial<T, 32>), grid, dim3(kDecThreads), 0, s, D); break;
+        default: hipLaunchKernelGGL((k_dec_partial<T, 64>), grid, dim3(kDecThreads), 0, s, D); break;
+    }
 }
 
 static int level_heads(const pa_decode_level& L) {
@@ -467,9 +529,9 @@ int launch_decode(const pa_decode* d, hipStream_t s) {
     if (D.nchunks > 0) {
         dim3 grid(D.nchunks, d->batch * d->kv_heads, d->order);
         ProfScope ps("dec_partial", s);
-        if (T == PA_F32) hipLaunchKernelGGL((k_dec_partial<float>), grid, dim3(kDecThreads), 0, s, D);
-        else if (T == PA_F16) hipLaunchKernelGGL((k_dec_partial<f16>), grid, dim3(kDecThreads), 0, s, D);
-        else hipLaunchKernelGGL((k_dec_partial<bf16>), grid, dim3(kDecThreads), 0, s, D);
+        if (T == PA_F32) launch_partial_t<float>(D, grid, s);
+        else if (T == PA_F16) launch_partial_t<f16>(D, grid, s);
+        else launch_partial_t<bf16>(D, grid, s);
     }
     dim3 cgrid(d->batch * d->kv_heads);
     ProfScope ps("dec_combine", s);
