@@ -2,8 +2,8 @@
 //
 // A decode step of an order-n poly attention reads every cached tensor once; it is HBM
 // bound.  Phase 1 (k_dec_partial) splits the cached positions 0..n-2 of every level into
-// chunks and computes, per (level, batch, head, chunk), the online-softmax partial
-// (m, l, sum p v) with coalesced 16-byte loads; the K row of a position is read once and
+// chunks and computes, per (level, batch, head, chunk), the softmax partial (m, l, sum p v)
+// with coalesced, non-temporal 16-byte loads; the K row of a position is read once and
 // shared by the query heads of its KV group.  Phase 2 (k_dec_combine) runs one workgroup
 // per (batch, KV group): level by level (deepest first) it merges the chunk partials,
 // adds the new position n-1 -- whose value and bias are the step results of the deeper
@@ -28,9 +28,9 @@ struct DecodeDev {
 };
 
 constexpr int kDecThreads = 256;
-constexpr int kDecHB = 8;      // level heads scored per pass over a chunk's K rows
+constexpr int kDecHB = 4;      // level heads scored per pass over a chunk's K rows
 constexpr int kDecU = 8;       // rows in flight per row group
-constexpr int kDecScoreElems = 8192;  // LDS floats for one chunk's scores (heads x positions)
+constexpr int kDecScoreElems = 4096;  // LDS floats for one chunk's scores (heads x positions)
 constexpr int kDecMaxHeadsPerGroup = 64;
 constexpr int kDecMaxGroupElems = 8192;  // level heads per KV group * head dim
 
@@ -39,10 +39,12 @@ template <> struct Vec16<bf16> { typedef uint4 type; static constexpr int n = 8;
 template <> struct Vec16<f16> { typedef uint4 type; static constexpr int n = 8; };
 template <> struct Vec16<float> { typedef uint4 type; static constexpr int n = 4; };
 
+// 16-byte streaming load: the cache is read once per step, so it bypasses cache retention
 template <typename T>
 __device__ __forceinline__ void load16(const T* p, float* out) {
     constexpr int E = Vec16<T>::n;
-    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     const T* e = reinterpret_cast<const T*>(&raw);
 #pragma unroll
     for (int i = 0; i < E; ++i) out[i] = to_f(e[i]);
