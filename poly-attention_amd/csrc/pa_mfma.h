@@ -43,13 +43,18 @@ __device__ __forceinline__ f32x16_t zero16() {
     return z;
 }
 
-// two floats -> two T (round to nearest even) packed in one 32-bit word (lo = first)
+// two floats -> two T (round to nearest even) packed in one 32-bit word (lo = first);
+// one v_cvt_pk_{bf16,f16}_f32
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    const T a = (T)lo, b = (T)hi;
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef T t2 __attribute__((ext_vector_type(2)));
+    const f2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, t2));
 }
+
+// the wave index as a scalar value, so conditions built from it compile to scalar branches
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // accumulator registers 8t .. 8t+7 (times `scale`) as a B-operand fragment
 template <typename T>

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
     __shared__ __attribute__((aligned(16))) float sL[kKvBQ];
     __shared__ __attribute__((aligned(16))) float sD[kKvBQ];
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int hh = lane >> 5, kcol = lane & 31;
     const int nkb = (P.nk + kKvBK - 1) / kKvBK;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -199,30 +199,42 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
                     s = M::run(ld_frag<T>(sQ + off), kf[c], s);
                     dp = M::run(ld_frag<T>(sO + off), vf[c], dp);
                 }
-                const bool diag = CAUSAL && (qbase < kw0 + 31);
+                // P: register i holds query qbase + 8*(i/4) + 4*hh + (i%4) of the lane's key
+                float yv[16];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int ql = qb * 32 + 8 * g + 4 * hh;
-                    const float4 Lv = *reinterpret_cast<const float4*>(sL + ql);
-                    const float4 Dv = *reinterpret_cast<const float4*>(sD + ql);
+                    const float4 Lv = *reinterpret_cast<const float4*>(sL + qb * 32 + 8 * g + 4 * hh);
                     const float L[4] = {Lv.x, Lv.y, Lv.z, Lv.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = 4 * g + r;
+                        float x;
+                        if (SOFTCLAMP) {
+                            yv[i] = tanhf(s[i] * cinv);  // softclamp(s*scale) / c
+                            x = yv[i] * (P.softclamp * kLog2e) + bias_l2 - L[r];
+                        } else {
+                            x = fmaf(s[i], sl2, bias_l2 - L[r]);
+                        }
+                        s[i] = fast_exp2(x);
+                    }
+                }
+                if (CAUSAL && qbase < kw0 + 31) {  // queries before the lane's key: P = 0
+                    const int lim = key - qbase - 4 * hh;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (8 * (i / 4) + (i % 4) < lim) s[i] = 0.f;
+                }
+                // dS = P (dP - D); the key bias gradient is its column sum
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 Dv = *reinterpret_cast<const float4*>(sD + qb * 32 + 8 * g + 4 * hh);
                     const float Dd[4] = {Dv.x, Dv.y, Dv.z, Dv.w};
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = 4 * g + r;
-                        float y = 0.f, x;
-                        if (SOFTCLAMP) {
-                            y = tanhf(s[i] * cinv);  // softclamp(s*scale) / c
-                            x = y * (P.softclamp * kLog2e) + bias_l2 - L[r];
-                        } else {
-                            x = s[i] * sl2 + bias_l2 - L[r];
-                        }
-                        float pv = fast_exp2(x);
-                        if (diag && (q0 + ql + r < key)) pv = 0.f;
-                        float dsv = pv * (dp[i] - Dd[r]);
+                        float dsv = s[i] * (dp[i] - Dd[r]);
                         dbias += dsv;
-                        if (SOFTCLAMP) dsv *= (1.f - y * y);
-                        s[i] = pv;
+                        if (SOFTCLAMP) dsv *= (1.f - yv[i] * yv[i]);
                         dp[i] = dsv;
                     }
                 }
@@ -425,7 +437,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
     __shared__ __attribute__((aligned(16))) T sKt[D * TL::TS];
     __shared__ __attribute__((aligned(16))) float sB[kDqBN];
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int hh = lane >> 5, kcol = lane & 31;
     const int nqb = (P.nq + kDqBM - 1) / kDqBM;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -477,27 +489,36 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
                     s = M::run(ld_frag<T>(sK + off), qf[c], s);
                     dp = M::run(ld_frag<T>(sV + off), of[c], dp);
                 }
+                // P^T: register i holds key j0 + kb*32 + 8*(i/4) + 4*hh + (i%4) of the lane's query
+                float yv[16];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int kr = kb * 32 + 8 * g + 4 * hh;
-                    const float4 bb = *reinterpret_cast<const float4*>(sB + kr);
+                    const float4 bb = *reinterpret_cast<const float4*>(sB + kb * 32 + 8 * g + 4 * hh);
                     const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = 4 * g + r;
-                        float y = 0.f, x;
+                        float x;
                         if (SOFTCLAMP) {
-                            y = tanhf(s[i] * cinv);
-                            x = y * (P.softclamp * kLog2e) + bv[r] - lse_l2;
+                            yv[i] = tanhf(s[i] * cinv);
+                            x = yv[i] * (P.softclamp * kLog2e) + bv[r] - lse_l2;
                         } else {
-                            x = s[i] * sl2 + bv[r] - lse_l2;
+                            x = fmaf(s[i], sl2, bv[r] - lse_l2);
                         }
-                        float pv = fast_exp2(x);
-                        if (diag && (j0 + kr + r > qi)) pv = 0.f;
-                        float dsv = pv * (dp[i] - dpi);
-                        if (SOFTCLAMP) dsv *= (1.f - y * y);
-                        s[i] = dsv;
+                        s[i] = fast_exp2(x);
                     }
+                }
+                if (diag) {  // keys after the lane's query: P = 0
+                    const int lim = qi - j0 - kb * 32 - 4 * hh;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (8 * (i / 4) + (i % 4) > lim) s[i] = 0.f;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float dsv = s[i] * (dp[i] - dpi);
+                    if (SOFTCLAMP) dsv *= (1.f - yv[i] * yv[i]);
+                    s[i] = dsv;
                 }
 #pragma unroll
                 for (int t2 = 0; t2 < 2; ++t2) {

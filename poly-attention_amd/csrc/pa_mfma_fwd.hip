@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
     __shared__ __attribute__((aligned(16))) T sVt[2][D * TL::VS];
     __shared__ __attribute__((aligned(16))) float sB[2][kFwdBN];
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int hh = lane >> 5, kcol = lane & 31;
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -201,36 +201,45 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
                 for (int c = 0; c < D / 16; ++c)
                     s[kb] = M::run(ld_frag<T>(K + (kb * 32 + kcol) * TL::KS + c * 16 + 8 * hh), qf[c], s[kb]);
             }
-            // scores (log2 domain unless PLAIN), masks, running max
-            const bool edge = (CAUSAL && j0 + kFwdBN - 1 > q0) || (!HAS_BIAS && j0 + kFwdBN > P.nk);
-            float mx = -INFINITY;
+            // scores in the log2 domain (raw when PLAIN) plus the key bias
+            if (!PLAIN) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int kr = kb * 32 + 8 * g + 4 * hh;
-                    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-                    if (HAS_BIAS) {
-                        const float4 bb = *reinterpret_cast<const float4*>(sB[buf] + kr);
-                        bv[0] = bb.x;
-                        bv[1] = bb.y;
-                        bv[2] = bb.z;
-                        bv[3] = bb.w;
-                    }
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int i = 4 * g + r;
-                        float x = s[kb][i];
-                        if (!PLAIN) x = (SOFTCLAMP ? cl2 * tanhf(x * cinv) : x * sl2) + bv[r];
-                        if (edge) {
-                            const int key = j0 + kr + r;
-                            if ((CAUSAL && key > qi) || key >= P.nk) x = -INFINITY;
+                    for (int g = 0; g < 4; ++g) {
+                        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+                        if (HAS_BIAS) {
+                            const float4 bb = *reinterpret_cast<const float4*>(sB[buf] + kb * 32 + 8 * g + 4 * hh);
+                            bv[0] = bb.x;
+                            bv[1] = bb.y;
+                            bv[2] = bb.z;
+                            bv[3] = bb.w;
                         }
-                        s[kb][i] = x;
-                        mx = fmaxf(mx, x);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float x = s[kb][4 * g + r];
+                            s[kb][4 * g + r] = (SOFTCLAMP ? cl2 * tanhf(x * cinv) : x * sl2) + bv[r];
+                        }
                     }
                 }
             }
+            // causal diagonal / past-the-end tiles: register i of block kb holds key
+            // j0 + kb*32 + 8*(i/4) + 4*hh + (i%4), valid while that offset stays <= lim
+            if ((CAUSAL && j0 + kFwdBN - 1 > q0) || (!HAS_BIAS && j0 + kFwdBN > P.nk)) {
+                int lim = HAS_BIAS ? (1 << 30) : P.nk - 1 - j0;
+                if (CAUSAL) lim = min(lim, qi - j0);
+                lim -= 4 * hh;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (kb * 32 + 8 * (i / 4) + (i % 4) > lim) s[kb][i] = -INFINITY;
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             if (PLAIN) mx *= sl2;
             const float m_new = fmaxf(m, mx);
