@@ -24,7 +24,7 @@ ProfScope::ProfScope(const char* name, hipStream_t s) : active(false), idx(0), s
     if (!g_prof_on.load(std::memory_order_relaxed)) return;
     ProfRec r{name, nullptr, nullptr};
     if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return;
-    hipEventRecord(r.start, s);
+    (void)hipEventRecord(r.start, s);
     std::lock_guard<std::mutex> lock(g_prof_mu);
     idx = g_prof.size();
     g_prof.push_back(r);
@@ -34,7 +34,7 @@ ProfScope::ProfScope(const char* name, hipStream_t s) : active(false), idx(0), s
 ProfScope::~ProfScope() {
     if (!active) return;
     std::lock_guard<std::mutex> lock(g_prof_mu);
-    hipEventRecord(g_prof[idx].stop, stream);
+    (void)hipEventRecord(g_prof[idx].stop, stream);
 }
 
 }  // namespace pa
@@ -172,8 +172,8 @@ size_t pa_struct_size(int which) {
 int pa_profile_start(void) {
     std::lock_guard<std::mutex> lock(g_prof_mu);
     for (ProfRec& r : g_prof) {
-        hipEventDestroy(r.start);
-        hipEventDestroy(r.stop);
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
     }
     g_prof.clear();
     g_prof_on = true;
@@ -202,8 +202,8 @@ int pa_profile_stop(pa_kernel_time* out, int capacity, int* count) {
         }
         out[k].launches += 1;
         out[k].total_ms += ms;
-        hipEventDestroy(r.start);
-        hipEventDestroy(r.stop);
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
     }
     g_prof.clear();
     if (count) *count = n;

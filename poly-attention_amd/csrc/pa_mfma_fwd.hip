@@ -21,15 +21,20 @@
 
 namespace pa {
 
+#ifndef PA_FWD_KB64
+#define PA_FWD_KB64 2
+#endif
+
 constexpr int kFwdBM = 128;  // query rows per workgroup
-constexpr int kFwdBN = 64;   // keys per tile
 constexpr int kFwdThreads = 256;
 
-template <int D>
+// Key tile of BN = 32 * KB keys: KB accumulator blocks per wave and tile.
+template <int D, int KB>
 struct FwdTile {
-    static constexpr int KS = D + 8;       // K row stride in LDS (elements)
-    static constexpr int VS = kFwdBN + 4;  // V^T row stride in LDS (elements)
-    static constexpr int BLOCKS = (kFwdBN / 4) * (D / 8);  // 4-key x 8-dim blocks per tensor
+    static constexpr int BN = 32 * KB;
+    static constexpr int KS = D + 8;   // K row stride in LDS (elements)
+    static constexpr int VS = BN + 4;  // V^T row stride in LDS (elements)
+    static constexpr int BLOCKS = (BN / 4) * (D / 8);  // 4-key x 8-dim blocks per tensor
     static constexpr int NB = (2 * BLOCKS + kFwdThreads - 1) / kFwdThreads;
 };
 
@@ -67,15 +72,15 @@ __device__ __forceinline__ KeySide<T> key_side(const PassDev& P, int b, int h) {
 }
 
 // Registers holding one tile's global loads between issue and LDS store.
-template <int D>
+template <int D, int KB>
 struct FwdStage {
-    u32x4_t w[FwdTile<D>::NB][4];
+    u32x4_t w[FwdTile<D, KB>::NB][4];
     float bias;
 };
 
-template <typename T, int D, bool HAS_VMUL, bool HAS_BIAS>
-__device__ __forceinline__ void fwd_load_tile(const KeySide<T>& ks, int j0, FwdStage<D>& st) {
-    using TL = FwdTile<D>;
+template <typename T, int D, int KB, bool HAS_VMUL, bool HAS_BIAS>
+__device__ __forceinline__ void fwd_load_tile(const KeySide<T>& ks, int j0, FwdStage<D, KB>& st) {
+    using TL = FwdTile<D, KB>;
     const int tid = threadIdx.x;
     const u32x4_t zero = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -101,7 +106,7 @@ __device__ __forceinline__ void fwd_load_tile(const KeySide<T>& ks, int j0, FwdS
             }
         }
     }
-    if (HAS_BIAS && tid < kFwdBN) {
+    if (HAS_BIAS && tid < TL::BN) {
         const int j = j0 + tid;
         float bv = -INFINITY;
         if (j < ks.nk && (!ks.km || ks.km[j * ks.kmsn])) {
@@ -115,9 +120,9 @@ __device__ __forceinline__ void fwd_load_tile(const KeySide<T>& ks, int j0, FwdS
     }
 }
 
-template <typename T, int D, bool HAS_BIAS>
-__device__ __forceinline__ void fwd_store_tile(const FwdStage<D>& st, T* sK, T* sVt, float* sB) {
-    using TL = FwdTile<D>;
+template <typename T, int D, int KB, bool HAS_BIAS>
+__device__ __forceinline__ void fwd_store_tile(const FwdStage<D, KB>& st, T* sK, T* sVt, float* sB) {
+    using TL = FwdTile<D, KB>;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int c = 0; c < TL::NB; ++c) {
@@ -135,18 +140,19 @@ __device__ __forceinline__ void fwd_store_tile(const FwdStage<D>& st, T* sK, T* 
             }
         }
     }
-    if (HAS_BIAS && tid < kFwdBN) sB[tid] = st.bias;
+    if (HAS_BIAS && tid < TL::BN) sB[tid] = st.bias;
 }
 
-template <typename T, int D, bool CAUSAL, bool SOFTCLAMP, bool HAS_VMUL, bool HAS_BIAS>
+template <typename T, int D, int KB, bool CAUSAL, bool SOFTCLAMP, bool HAS_VMUL, bool HAS_BIAS>
 __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassDev P) {
-    using TL = FwdTile<D>;
+    using TL = FwdTile<D, KB>;
+    constexpr int BN = TL::BN;
     using M = Mma<T>;
     typedef typename M::frag frag;
     constexpr bool PLAIN = !HAS_BIAS && !SOFTCLAMP;  // max taken on raw scores
-    __shared__ __attribute__((aligned(16))) T sK[2][kFwdBN * TL::KS];
+    __shared__ __attribute__((aligned(16))) T sK[2][BN * TL::KS];
     __shared__ __attribute__((aligned(16))) T sVt[2][D * TL::VS];
-    __shared__ __attribute__((aligned(16))) float sB[2][kFwdBN];
+    __shared__ __attribute__((aligned(16))) float sB[2][BN];
 
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int hh = lane >> 5, kcol = lane & 31;
@@ -179,23 +185,23 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
 
     const KeySide<T> ks = key_side<T>(P, b, h);
     const int kend = CAUSAL ? min(P.nk, qb * kFwdBM + kFwdBM) : P.nk;
-    const int ntiles = (kend + kFwdBN - 1) / kFwdBN;
+    const int ntiles = (kend + BN - 1) / BN;
 
-    FwdStage<D> st;
-    fwd_load_tile<T, D, HAS_VMUL, HAS_BIAS>(ks, 0, st);
-    fwd_store_tile<T, D, HAS_BIAS>(st, sK[0], sVt[0], sB[0]);
+    FwdStage<D, KB> st;
+    fwd_load_tile<T, D, KB, HAS_VMUL, HAS_BIAS>(ks, 0, st);
+    fwd_store_tile<T, D, KB, HAS_BIAS>(st, sK[0], sVt[0], sB[0]);
     __syncthreads();
 
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
-        const int j0 = t * kFwdBN;
-        if (t + 1 < ntiles) fwd_load_tile<T, D, HAS_VMUL, HAS_BIAS>(ks, j0 + kFwdBN, st);
+        const int j0 = t * BN;
+        if (t + 1 < ntiles) fwd_load_tile<T, D, KB, HAS_VMUL, HAS_BIAS>(ks, j0 + BN, st);
         if (!(CAUSAL && j0 > q0 + 31)) {
             const T* K = sK[buf];
             const T* Vt = sVt[buf];
-            f32x16_t s[2];
+            f32x16_t s[KB];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < KB; ++kb) {
                 s[kb] = zero16();
 #pragma unroll
                 for (int c = 0; c < D / 16; ++c)
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
             // scores in the log2 domain (raw when PLAIN) plus the key bias
             if (!PLAIN) {
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         float bv[4] = {0.f, 0.f, 0.f, 0.f};
@@ -225,22 +231,22 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
             }
             // causal diagonal / past-the-end tiles: register i of block kb holds key
             // j0 + kb*32 + 8*(i/4) + 4*hh + (i%4), valid while that offset stays <= lim
-            if ((CAUSAL && j0 + kFwdBN - 1 > q0) || (!HAS_BIAS && j0 + kFwdBN > P.nk)) {
+            if ((CAUSAL && j0 + BN - 1 > q0) || (!HAS_BIAS && j0 + BN > P.nk)) {
                 int lim = HAS_BIAS ? (1 << 30) : P.nk - 1 - j0;
                 if (CAUSAL) lim = min(lim, qi - j0);
                 lim -= 4 * hh;
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
                     for (int i = 0; i < 16; ++i)
                         if (kb * 32 + 8 * (i / 4) + (i % 4) > lim) s[kb][i] = -INFINITY;
             }
             float mx = -INFINITY;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = xhalf_max(mx);
             if (PLAIN) mx *= sl2;
             const float m_new = fmaxf(m, mx);
             if (__any(m_new > m)) {
@@ -255,7 +261,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
             const float m_sub = (m == -INFINITY) ? 0.f : m;
             // P^T operands and O^T += V^T . P^T
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const float p = PLAIN ? fast_exp2(fmaf(s[kb][i], sl2, -m_sub)) : fast_exp2(s[kb][i] - m_sub);
@@ -272,11 +278,11 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
                 }
             }
         }
-        if (t + 1 < ntiles) fwd_store_tile<T, D, HAS_BIAS>(st, sK[buf ^ 1], sVt[buf ^ 1], sB[buf ^ 1]);
+        if (t + 1 < ntiles) fwd_store_tile<T, D, KB, HAS_BIAS>(st, sK[buf ^ 1], sVt[buf ^ 1], sB[buf ^ 1]);
         __syncthreads();
     }
 
-    l += __shfl_xor(l, 32);
+    l = xhalf_sum(l);
     if (qi >= P.nq) return;
     const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
     const float inv = degenerate ? 0.f : 1.f / l;
@@ -297,6 +303,11 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
 
 // ---------------------------------------------------------------------------------------
 
+// 32-key blocks per key tile: 128-key tiles at head dim 64 (without softclamp, whose tanh
+// temporaries would spill), 64-key tiles otherwise
+template <int D, bool SOFTCLAMP>
+constexpr int kFwdKB = (D == 64 && !SOFTCLAMP) ? PA_FWD_KB64 : 2;
+
 bool mfma_fwd_supported(const PassDev& P, int dtype) {
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
     if (P.dim != 64 && P.dim != 128) return false;
@@ -308,10 +319,11 @@ bool mfma_fwd_supported(const PassDev& P, int dtype) {
 
 template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_t(const PassDev& P, hipStream_t s) {
+    constexpr int KB = kFwdKB<D, S>;
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     dim3 grid(nqb * P.heads * P.batch);
     ProfScope ps("mfma_fwd", s);
-    hipLaunchKernelGGL((k_mfma_fwd<T, D, C, S, V, B>), grid, dim3(kFwdThreads), 0, s, P);
+    hipLaunchKernelGGL((k_mfma_fwd<T, D, KB, C, S, V, B>), grid, dim3(kFwdThreads), 0, s, P);
 }
 
 template <typename T, int D, bool C, bool S>
