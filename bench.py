@@ -76,6 +76,23 @@ def kernel_work(name):
     return table.get(name)
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "pmc_hbm_traffic_config2_config5.md")
+
+
+def measured_traffic(family):
+    """HBM bytes per launch of a kernel family from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a plain copy in the same runs), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 7 and cells[0] == family:
+                    return int(float(cells[6]))
+    except OSError:
+        pass
+    return None
+
+
 def achieved_rate(work, avg_ms, unit):
     return work / (avg_ms / 1e3) / (1e12 if unit == "TFLOP/s" else 1e9)
 
@@ -177,7 +194,8 @@ def decode_bench(dev, steps, warmup):
         "bytes_per_step": bytes_step,
         "tokens_per_s": round(Bd / (ms / 1e3), 1),
         "kernel": {"name": "dec_partial", "avg_ms": round(part_ms, 4),
-                   "GB_per_s": round(part_bytes / part_ms / 1e6, 1) if part_ms else None},
+                   "GB_per_s": round(part_bytes / part_ms / 1e6, 1) if part_ms else None,
+                   "algorithmic_bytes": part_bytes, "traffic": measured_traffic("dec_partial")},
     }
 
 
@@ -280,8 +298,8 @@ def main():
     avg_ms = tot / n_l
     achieved = achieved_rate(work, avg_ms, unit)
     roofline = {"bound": bound, "kernel": dominant, "achieved": round(achieved, 2),
-                "peak": peak, "unit": unit, "frac": round(achieved / peak, 4), "traffic": None,
-                "avg_ms": round(avg_ms, 4)}
+                "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+                "traffic": measured_traffic(dominant), "avg_ms": round(avg_ms, 4)}
     log(f"[bench] kernels: {kernels}")
 
     module_ms = None

@@ -64,6 +64,10 @@ __device__ __forceinline__ float xhalf_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Marks a rarely taken uniform branch body: the side-effecting (empty) asm keeps the compiler
+// from flattening the branch into unconditionally executed selects.
+__device__ __forceinline__ void keep_branch() { asm volatile("" ::: "memory"); }
+
 // the wave index as a scalar value, so conditions built from it compile to scalar branches
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -74,6 +78,21 @@ __device__ __forceinline__ typename Mma<T>::frag acc_to_frag(const f32x16_t& c, 
 #pragma unroll
     for (int k = 0; k < 4; ++k) r[k] = pack2<T>(c[8 * t + 2 * k], c[8 * t + 2 * k + 1]);
     return __builtin_bit_cast(typename Mma<T>::frag, r);
+}
+
+// acc + lo + hi of a packed pair of T (one v_dot2c_f32_{bf16,f16} against (1, 1))
+template <typename T> __device__ __forceinline__ float sum_pair(uint32_t w, float acc);
+template <>
+__device__ __forceinline__ float sum_pair<bf16>(uint32_t w, float acc) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, w), __builtin_bit_cast(v2, 0x3F803F80u),
+                                           acc, false);
+}
+template <>
+__device__ __forceinline__ float sum_pair<f16>(uint32_t w, float acc) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, w), __builtin_bit_cast(v2, 0x3C003C00u), acc,
+                                  false);
 }
 
 // element-wise product of 8 values rounded to T (the reference multiplies in T)
@@ -119,6 +138,81 @@ __device__ __forceinline__ void store_block_transposed(const u32x4_t* w, uint16_
         *reinterpret_cast<u32x2_t*>(dst + (2 * m) * stride) = even;
         *reinterpret_cast<u32x2_t*>(dst + (2 * m + 1) * stride) = odd;
     }
+}
+
+// ---------------------------------------------------------------------------------------
+// Direct global -> LDS loads (buffer_load_dwordx4 ... lds) and transposing LDS reads.
+//
+// The loads are issued through inline assembly, so the compiler neither sees them nor
+// inserts waits for them: kernels that use them count their outstanding vector-memory
+// operations themselves (wait_vmcnt) and order LDS with lds_barrier.  The assembly sets M0
+// (the LDS destination); no compiler-generated code in these kernels uses M0.
+
+typedef int32_t srd_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// raw buffer descriptor over [base, base + bytes): offsets >= bytes read as zeros
+__device__ __forceinline__ srd_t make_srd(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    srd_t r;
+    r[0] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)(a >> 32) & 0xffff);  // stride 0
+    r[2] = __builtin_amdgcn_readfirstlane((int32_t)bytes);
+    r[3] = 0x00020000;  // 32-bit data format
+    return r;
+}
+
+// byte address of a __shared__ object in LDS
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>((const lds_void*)p);
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// Each active lane loads 16 bytes at byte offset `voff` of the buffer; lane i's bytes land at
+// LDS byte address lds + 16 * i (lds uniform across the wave).
+__device__ __forceinline__ void dma16(srd_t srd, uint32_t lds, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(lds), "s"(srd)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// a value the compiler must treat as produced here (orders it after preceding volatile ops)
+template <typename X>
+__device__ __forceinline__ X opaque(X x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+// wait until at most N vector-memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for LDS hand-offs: waits for this wave's LDS operations, then s_barrier.
+// Unlike __syncthreads it carries no release fence, which on this target would also wait for
+// every outstanding global load and so drain a direct-to-LDS prefetch pipeline; the waves'
+// buffer_load ... lds transfers are made complete beforehand with wait_vmcnt.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ds_read_b64_tr_b16: the 16 lanes of each quarter-wave address 16 rows R[j] of 4 16-bit
+// elements (8 bytes each); lane L of the group receives R[L/4 + 4e][L%4] for e = 0..3.
+// Addressing row j = 4 consecutive rows r0 + j/4 at columns c0 + 4*(j%4) therefore hands lane
+// L the 4 elements of column c0 + L in rows r0 .. r0+3: a transposed read of a row-major tile.
+__device__ __forceinline__ u32x2_t lds_read_tr(const void* p) {
+    const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t*)(p));
+    return __builtin_bit_cast(u32x2_t, v);
 }
 
 // bare v_exp_f32 (2^x; results below 2^-126 flush to 0, which softmax weights tolerate)

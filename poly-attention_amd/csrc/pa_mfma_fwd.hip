@@ -1,20 +1,32 @@
 // pa_mfma_fwd.hip -- MFMA forward attention pass for bf16 / f16, head dim 64 or 128 (gfx950).
 //
 // Workgroup = 4 waves = 128 query rows of one (batch, pass head); each wave owns 32 queries.
-// Per key tile (64 keys) a wave computes the transposed scores S^T = K . Q^T with
+// Per key tile (32*KB keys) a wave computes the transposed scores S^T = K . Q^T with
 // v_mfma_f32_32x32x16_{bf16,f16}: the 32x32 accumulator layout gives lane l the column
-// q = l % 32 and 16 key rows, so the online-softmax state (running max m, sum l and the
-// rescale of the output) is a per-lane scalar.  The probabilities, rounded to the input
-// type, stay in registers as the B operand of O^T += V^T . P^T (keys permuted consistently
-// between the two operands, see pa_mfma.h), V being staged transposed in LDS.  K / V tiles
-// are double buffered: the global loads of tile t+1 are in flight while tile t is computed.
-// Exponentials run in the log2 domain (bare v_exp_f32) with scale*log2(e) folded into one
-// FMA; without a key bias the running max is taken on the raw scores.  The output rescale
-// is skipped when no lane's running max moved.  Workgroups are mapped XCD-aware (pa_mfma.h)
-// and causal query blocks run heaviest first.
+// q = l % 32 and 16 key rows per block, so the online-softmax state (running max m, sum l,
+// the output rescale) is a per-lane scalar.  The probabilities, rounded to the input type,
+// stay in registers as the B operand of O^T += V^T . P^T (keys permuted consistently between
+// the two operands, see pa_mfma.h), V being staged transposed in LDS.
+//
+// Software pipeline (per wave, one barrier per tile): iteration t issues the score MFMAs of
+// tile t+1 in the same basic block as the exponentials of tile t, so the matrix cores and
+// the VALU work side by side; then O += V_t^T . P_t.  K runs one tile ahead of V in LDS: while
+// iteration t reads K_{t+1} and V_t, the global loads of K_{t+2} and V_{t+1} are in flight
+// and land in the buffers freed by the previous iteration.  The key bias travels with V.
+//
+// Softmax: log2 domain (bare v_exp_f32, scale*log2(e) folded into one FMA; without a key
+// bias the running max is taken on the raw scores).  The running max is updated lazily: it
+// moves (and the output is rescaled) only when a tile's max exceeds it by more than kFwdTau,
+// so probabilities stay <= 2^kFwdTau (exact in fp32 and within the input type's exponent
+// range); after the first tiles this almost never happens.  Row sums accumulate the rounded
+// probabilities with v_dot2 (the same values the MFMA consumes).
 //
 // Rows whose every key is masked are left with lse = NaN for k_simt_fixup, which applies the
-// reference's finite-fill semantics to them.
+// reference's finite-fill semantics to them.  Workgroups are mapped XCD-aware (pa_mfma.h) and
+// causal query blocks run heaviest first.
+#include <algorithm>
+#include <type_traits>
+
 #include "pa_common.h"
 #include "pa_launch.h"
 #include "pa_mfma.h"
@@ -27,6 +39,7 @@ namespace pa {
 
 constexpr int kFwdBM = 128;  // query rows per workgroup
 constexpr int kFwdThreads = 256;
+constexpr float kFwdTau = 8.f;  // lazy-rescale threshold (log2 units)
 
 // Key tile of BN = 32 * KB keys: KB accumulator blocks per wave and tile.
 template <int D, int KB>
@@ -71,15 +84,18 @@ __device__ __forceinline__ KeySide<T> key_side(const PassDev& P, int b, int h) {
     return s;
 }
 
-// Registers holding one tile's global loads between issue and LDS store.
+// Registers holding one K tile and one V tile (+ key bias) between global load and LDS store.
 template <int D, int KB>
 struct FwdStage {
     u32x4_t w[FwdTile<D, KB>::NB][4];
     float bias;
 };
 
+// Issue the global loads of K rows [jk, jk + BN) (when lk) and V rows / key bias [jv, jv + BN)
+// (when lv); rows past the end read as zero, their bias as -inf.
 template <typename T, int D, int KB, bool HAS_VMUL, bool HAS_BIAS>
-__device__ __forceinline__ void fwd_load_tile(const KeySide<T>& ks, int j0, FwdStage<D, KB>& st) {
+__device__ __forceinline__ void fwd_load(const KeySide<T>& ks, int jk, bool lk, int jv, bool lv,
+                                         FwdStage<D, KB>& st) {
     using TL = FwdTile<D, KB>;
     const int tid = threadIdx.x;
     const u32x4_t zero = {0u, 0u, 0u, 0u};
@@ -89,25 +105,27 @@ __device__ __forceinline__ void fwd_load_tile(const KeySide<T>& ks, int j0, FwdS
         if (task < 2 * TL::BLOCKS) {
             const int tensor = task / TL::BLOCKS, blk = task % TL::BLOCKS;
             const int rg = blk / (D / 8), cc = blk % (D / 8);
+            if (tensor == 0 ? lk : lv) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int j = j0 + rg * 4 + r;
-                u32x4_t x = zero;
-                if (j < ks.nk) {
-                    if (tensor == 0) {
-                        x = *reinterpret_cast<const u32x4_t*>(ks.k + j * ks.ksn + cc * 8);
-                    } else {
-                        x = *reinterpret_cast<const u32x4_t*>(ks.v + j * ks.vsn + cc * 8);
-                        if (HAS_VMUL)
-                            x = mul_round8<T>(x, *reinterpret_cast<const u32x4_t*>(ks.vm + j * ks.msn + cc * 8));
+                for (int r = 0; r < 4; ++r) {
+                    const int j = (tensor == 0 ? jk : jv) + rg * 4 + r;
+                    u32x4_t x = zero;
+                    if (j < ks.nk) {
+                        if (tensor == 0) {
+                            x = *reinterpret_cast<const u32x4_t*>(ks.k + j * ks.ksn + cc * 8);
+                        } else {
+                            x = *reinterpret_cast<const u32x4_t*>(ks.v + j * ks.vsn + cc * 8);
+                            if (HAS_VMUL)
+                                x = mul_round8<T>(x, *reinterpret_cast<const u32x4_t*>(ks.vm + j * ks.msn + cc * 8));
+                        }
                     }
+                    st.w[c][r] = x;
                 }
-                st.w[c][r] = x;
             }
         }
     }
-    if (HAS_BIAS && tid < TL::BN) {
-        const int j = j0 + tid;
+    if (HAS_BIAS && lv && tid < TL::BN) {
+        const int j = jv + tid;
         float bv = -INFINITY;
         if (j < ks.nk && (!ks.km || ks.km[j * ks.kmsn])) {
             bv = 0.f;
@@ -121,7 +139,8 @@ __device__ __forceinline__ void fwd_load_tile(const KeySide<T>& ks, int j0, FwdS
 }
 
 template <typename T, int D, int KB, bool HAS_BIAS>
-__device__ __forceinline__ void fwd_store_tile(const FwdStage<D, KB>& st, T* sK, T* sVt, float* sB) {
+__device__ __forceinline__ void fwd_store(const FwdStage<D, KB>& st, T* sK, bool sk, T* sVt, float* sB,
+                                          bool sv) {
     using TL = FwdTile<D, KB>;
     const int tid = threadIdx.x;
 #pragma unroll
@@ -131,158 +150,261 @@ __device__ __forceinline__ void fwd_store_tile(const FwdStage<D, KB>& st, T* sK,
             const int tensor = task / TL::BLOCKS, blk = task % TL::BLOCKS;
             const int rg = blk / (D / 8), cc = blk % (D / 8);
             if (tensor == 0) {
+                if (sk) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    *reinterpret_cast<u32x4_t*>(sK + (rg * 4 + r) * TL::KS + cc * 8) = st.w[c][r];
-            } else {
+                    for (int r = 0; r < 4; ++r)
+                        *reinterpret_cast<u32x4_t*>(sK + (rg * 4 + r) * TL::KS + cc * 8) = st.w[c][r];
+                }
+            } else if (sv) {
                 store_block_transposed(st.w[c], reinterpret_cast<uint16_t*>(sVt + (cc * 8) * TL::VS + rg * 4),
                                        TL::VS);
             }
         }
     }
-    if (HAS_BIAS && tid < TL::BN) sB[tid] = st.bias;
+    if (HAS_BIAS && sv && tid < TL::BN) sB[tid] = st.bias;
 }
+
+// Per-wave state and the pieces of one pipeline step.
+template <typename T, int D, int KB, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS>
+struct FwdWave {
+    using TL = FwdTile<D, KB>;
+    using M = Mma<T>;
+    typedef typename M::frag frag;
+    static constexpr int BN = TL::BN;
+    static constexpr bool PLAIN = !HAS_BIAS && !SOFTCLAMP;  // max taken on raw scores
+
+    frag qf[D / 16];
+    f32x16_t o[D / 32];
+    float m, l;
+    int kcol, hh, q0, qi, nk;
+    float sl2, cinv, cl2;
+
+    // S^T block kb of a key tile: s[kb] = K[kb*32 + row, :] . Q^T
+    __device__ __forceinline__ void scores(const T* K, f32x16_t (&s)[KB]) const {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            s[kb] = zero16();
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c)
+                s[kb] = M::run(ld_frag<T>(K + (kb * 32 + kcol) * TL::KS + c * 16 + 8 * hh), qf[c], s[kb]);
+        }
+    }
+
+    // causal diagonal / past-the-end keys of the tile at j0 -> -inf (raw scores).  Register i
+    // of block kb holds key j0 + kb*32 + 8*(i/4) + 4*hh + (i%4).
+    __device__ __forceinline__ void mask_edges(f32x16_t (&s)[KB], int j0) const {
+        if ((CAUSAL && j0 + BN - 1 > q0) || (!HAS_BIAS && j0 + BN > nk)) {
+            keep_branch();
+            int lim = HAS_BIAS ? (1 << 30) : nk - 1 - j0;
+            if (CAUSAL) lim = min(lim, qi - j0);
+            lim -= 4 * hh;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (kb * 32 + 8 * (i / 4) + (i % 4) > lim) s[kb][i] = -INFINITY;
+        }
+    }
+
+    // as mask_edges, but past-the-end keys are masked by position also with a key bias
+    __device__ __forceinline__ void mask_edges_nk(f32x16_t (&s)[KB], int j0) const {
+        if ((CAUSAL && j0 + BN - 1 > q0) || (j0 + BN > nk)) {
+            keep_branch();
+            int lim = nk - 1 - j0;
+            if (CAUSAL) lim = min(lim, qi - j0);
+            lim -= 4 * hh;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (kb * 32 + 8 * (i / 4) + (i % 4) > lim) s[kb][i] = -INFINITY;
+        }
+    }
+
+    // scores -> log2-domain logits in place (bias / softclamp paths); returns the max over the
+    // query's logits of this tile (PLAIN: of the raw scores, times scale*log2e)
+    __device__ __forceinline__ float logits(f32x16_t (&s)[KB], const float* sB) const {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float bv[4] = {0.f, 0.f, 0.f, 0.f};
+                if (HAS_BIAS) {
+                    const float4 bb = *reinterpret_cast<const float4*>(sB + kb * 32 + 8 * g + 4 * hh);
+                    bv[0] = bb.x;
+                    bv[1] = bb.y;
+                    bv[2] = bb.z;
+                    bv[3] = bb.w;
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = s[kb][4 * g + r];
+                    if (!PLAIN) {
+                        if (SOFTCLAMP) x = (x == -INFINITY) ? -INFINITY : cl2 * tanhf(x * cinv) + bv[r];
+                        else x = fmaf(x, sl2, bv[r]);
+                        s[kb][4 * g + r] = x;
+                    }
+                    mx = fmaxf(mx, x);
+                }
+            }
+        }
+        mx = xhalf_max(mx);
+        return PLAIN ? mx * sl2 : mx;
+    }
+
+    // probabilities against the max msub, rounded to T and packed as the PV B operands; returns
+    // the lane's sum of the rounded probabilities
+    __device__ __forceinline__ float probs(const f32x16_t (&s)[KB], float msub, u32x4_t (&pk)[KB][2]) const {
+        float lt = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float x0 = s[kb][8 * t2 + 2 * k], x1 = s[kb][8 * t2 + 2 * k + 1];
+                    const float p0 = PLAIN ? fast_exp2(fmaf(x0, sl2, -msub)) : fast_exp2(x0 - msub);
+                    const float p1 = PLAIN ? fast_exp2(fmaf(x1, sl2, -msub)) : fast_exp2(x1 - msub);
+                    const uint32_t w = pack2<T>(p0, p1);
+                    pk[kb][t2][k] = w;
+                    lt = sum_pair<T>(w, lt);
+                }
+        return lt;
+    }
+
+    // lazy rescale: only when some lane's tile max exceeds its running max by more than
+    // kFwdTau does the running max move (rescaling O and l)
+    __device__ __forceinline__ void settle(float mx) {
+        if (__any(mx > m + kFwdTau)) {
+            keep_branch();
+            const float m_new = fmaxf(m, mx);
+            const float alpha = (m_new > m) ? fast_exp2(m - m_new) : 1.f;
+            l *= alpha;
+#pragma unroll
+            for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[x][i] *= alpha;
+            m = m_new;
+        }
+    }
+
+    // V^T operand fragments of one tile (read early so the LDS latency hides behind the softmax)
+    __device__ __forceinline__ void load_v(const T* Vt, frag (&vf)[KB][2][D / 32]) const {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                for (int x = 0; x < D / 32; ++x)
+                    vf[kb][t2][x] = lds_runs<T>(Vt + (x * 32 + kcol) * TL::VS + kb * 32 + 16 * t2 + 4 * hh);
+    }
+
+    // O^T += V^T . P^T for one tile
+    __device__ __forceinline__ void pv(const frag (&vf)[KB][2][D / 32], const u32x4_t (&pk)[KB][2]) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+                const frag pb = __builtin_bit_cast(frag, pk[kb][t2]);
+#pragma unroll
+                for (int x = 0; x < D / 32; ++x) o[x] = M::run(vf[kb][t2][x], pb, o[x]);
+            }
+    }
+};
 
 template <typename T, int D, int KB, bool CAUSAL, bool SOFTCLAMP, bool HAS_VMUL, bool HAS_BIAS>
 __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassDev P) {
     using TL = FwdTile<D, KB>;
     constexpr int BN = TL::BN;
-    using M = Mma<T>;
-    typedef typename M::frag frag;
-    constexpr bool PLAIN = !HAS_BIAS && !SOFTCLAMP;  // max taken on raw scores
+    using W = FwdWave<T, D, KB, CAUSAL, SOFTCLAMP, HAS_BIAS>;
+    typedef typename W::frag frag;
     __shared__ __attribute__((aligned(16))) T sK[2][BN * TL::KS];
     __shared__ __attribute__((aligned(16))) T sVt[2][D * TL::VS];
     __shared__ __attribute__((aligned(16))) float sB[2][BN];
 
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-    const int hh = lane >> 5, kcol = lane & 31;
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
     const int qb = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;
     const int bh = lid / nqb;
     const int h = bh % P.heads, b = bh / P.heads;
-    const int q0 = qb * kFwdBM + w * 32;
-    const int qi = q0 + kcol;
 
+    W wv;
+    wv.hh = lane >> 5;
+    wv.kcol = lane & 31;
+    wv.q0 = qb * kFwdBM + w * 32;
+    wv.qi = wv.q0 + wv.kcol;
+    wv.nk = P.nk;
+    wv.sl2 = P.scale * kLog2e;
+    wv.cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
+    wv.cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
+    wv.m = -INFINITY;
+    wv.l = 0.f;
     // Q^T operand fragments: lane (q, hh) holds Q[q][c*16 + 8*hh .. +7]
-    frag qf[D / 16];
     {
+        const int qi = wv.qi;
         const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) {
             u32x4_t raw = {0u, 0u, 0u, 0u};
-            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
-            qf[c] = __builtin_bit_cast(frag, raw);
+            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * wv.hh);
+            wv.qf[c] = __builtin_bit_cast(frag, raw);
         }
     }
-    f32x16_t o[D / 32];
 #pragma unroll
-    for (int x = 0; x < D / 32; ++x) o[x] = zero16();
-    float m = -INFINITY, l = 0.f;
-    const float sl2 = P.scale * kLog2e;
-    const float cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
-    const float cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
+    for (int x = 0; x < D / 32; ++x) wv.o[x] = zero16();
 
     const KeySide<T> ks = key_side<T>(P, b, h);
     const int kend = CAUSAL ? min(P.nk, qb * kFwdBM + kFwdBM) : P.nk;
     const int ntiles = (kend + BN - 1) / BN;
+    // a wave skips the tiles that lie wholly above its causal diagonal
+    const int wave_last = CAUSAL ? (wv.q0 + 31) : (1 << 30);
 
+    // prologue: K_0, V_0 (+ bias_0), K_1 in LDS; S_0 in registers
     FwdStage<D, KB> st;
-    fwd_load_tile<T, D, KB, HAS_VMUL, HAS_BIAS>(ks, 0, st);
-    fwd_store_tile<T, D, KB, HAS_BIAS>(st, sK[0], sVt[0], sB[0]);
+    fwd_load<T, D, KB, HAS_VMUL, HAS_BIAS>(ks, 0, true, 0, true, st);
+    fwd_store<T, D, KB, HAS_BIAS>(st, sK[0], true, sVt[0], sB[0], true);
+    if (ntiles > 1) {
+        fwd_load<T, D, KB, HAS_VMUL, HAS_BIAS>(ks, BN, true, 0, false, st);
+        fwd_store<T, D, KB, HAS_BIAS>(st, sK[1], true, sVt[0], sB[0], false);
+    }
     __syncthreads();
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
+    f32x16_t sa[KB], sb[KB];
+    wv.scores(sK[0], sa);
+    wv.mask_edges(sa, 0);
+
+    // one pipeline step: softmax + PV of tile t (scores in `cur`), scores of tile t+1 into `nxt`
+    auto step = [&](f32x16_t (&cur)[KB], f32x16_t (&nxt)[KB], int t) __attribute__((always_inline)) {
         const int j0 = t * BN;
-        if (t + 1 < ntiles) fwd_load_tile<T, D, KB, HAS_VMUL, HAS_BIAS>(ks, j0 + BN, st);
-        if (!(CAUSAL && j0 > q0 + 31)) {
-            const T* K = sK[buf];
-            const T* Vt = sVt[buf];
-            f32x16_t s[KB];
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                s[kb] = zero16();
-#pragma unroll
-                for (int c = 0; c < D / 16; ++c)
-                    s[kb] = M::run(ld_frag<T>(K + (kb * 32 + kcol) * TL::KS + c * 16 + 8 * hh), qf[c], s[kb]);
-            }
-            // scores in the log2 domain (raw when PLAIN) plus the key bias
-            if (!PLAIN) {
-#pragma unroll
-                for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        float bv[4] = {0.f, 0.f, 0.f, 0.f};
-                        if (HAS_BIAS) {
-                            const float4 bb = *reinterpret_cast<const float4*>(sB[buf] + kb * 32 + 8 * g + 4 * hh);
-                            bv[0] = bb.x;
-                            bv[1] = bb.y;
-                            bv[2] = bb.z;
-                            bv[3] = bb.w;
-                        }
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float x = s[kb][4 * g + r];
-                            s[kb][4 * g + r] = (SOFTCLAMP ? cl2 * tanhf(x * cinv) : x * sl2) + bv[r];
-                        }
-                    }
-                }
-            }
-            // causal diagonal / past-the-end tiles: register i of block kb holds key
-            // j0 + kb*32 + 8*(i/4) + 4*hh + (i%4), valid while that offset stays <= lim
-            if ((CAUSAL && j0 + BN - 1 > q0) || (!HAS_BIAS && j0 + BN > P.nk)) {
-                int lim = HAS_BIAS ? (1 << 30) : P.nk - 1 - j0;
-                if (CAUSAL) lim = min(lim, qi - j0);
-                lim -= 4 * hh;
-#pragma unroll
-                for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        if (kb * 32 + 8 * (i / 4) + (i % 4) > lim) s[kb][i] = -INFINITY;
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-            mx = xhalf_max(mx);
-            if (PLAIN) mx *= sl2;
-            const float m_new = fmaxf(m, mx);
-            if (__any(m_new > m)) {
-                const float alpha = (m_new > m) ? fast_exp2(m - m_new) : 1.f;
-                l *= alpha;
-#pragma unroll
-                for (int x = 0; x < D / 32; ++x)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) o[x][i] *= alpha;
-                m = m_new;
-            }
-            const float m_sub = (m == -INFINITY) ? 0.f : m;
-            // P^T operands and O^T += V^T . P^T
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float p = PLAIN ? fast_exp2(fmaf(s[kb][i], sl2, -m_sub)) : fast_exp2(s[kb][i] - m_sub);
-                    s[kb][i] = p;
-                    l += p;
-                }
-#pragma unroll
-                for (int t2 = 0; t2 < 2; ++t2) {
-                    const frag pb = acc_to_frag<T>(s[kb], t2);
-                    const int kbase = kb * 32 + 16 * t2 + 4 * hh;
-#pragma unroll
-                    for (int x = 0; x < D / 32; ++x)
-                        o[x] = M::run(lds_runs<T>(Vt + (x * 32 + kcol) * TL::VS + kbase), pb, o[x]);
-                }
-            }
+        const bool more_k = t + 2 < ntiles, more_v = t + 1 < ntiles;
+        fwd_load<T, D, KB, HAS_VMUL, HAS_BIAS>(ks, j0 + 2 * BN, more_k, j0 + BN, more_v, st);
+        const bool act = j0 <= wave_last, act_next = more_v && j0 + BN <= wave_last;
+        const float* bt = sB[t & 1];
+        u32x4_t pk[KB][2];
+        frag vf[KB][2][D / 32];
+        if (act) {
+            wv.settle(wv.logits(cur, bt));
+            // one basic block of independent work: the score MFMAs of tile t+1 (computed even
+            // when that tile is skipped or absent; the result is then unused) beside the
+            // exponentials of tile t
+            wv.scores(sK[(t + 1) & 1], nxt);
+            wv.load_v(sVt[t & 1], vf);
+            wv.l += wv.probs(cur, wv.m == -INFINITY ? 0.f : wv.m, pk);
+            wv.pv(vf, pk);
+            if (act_next) wv.mask_edges(nxt, j0 + BN);
         }
-        if (t + 1 < ntiles) fwd_store_tile<T, D, KB, HAS_BIAS>(st, sK[buf ^ 1], sVt[buf ^ 1], sB[buf ^ 1]);
+        fwd_store<T, D, KB, HAS_BIAS>(st, sK[t & 1], more_k, sVt[(t + 1) & 1], sB[(t + 1) & 1], more_v);
         __syncthreads();
+    };
+    for (int t = 0; t < ntiles; t += 2) {
+        step(sa, sb, t);
+        if (t + 1 < ntiles) step(sb, sa, t + 1);
     }
 
-    l = xhalf_sum(l);
+    const float l = xhalf_sum(wv.l);
+    const int qi = wv.qi;
     if (qi >= P.nq) return;
     const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
     const float inv = degenerate ? 0.f : 1.f / l;
@@ -291,26 +413,260 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
     for (int x = 0; x < D / 32; ++x) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int d = x * 32 + 8 * g + 4 * hh;
+            const int d = x * 32 + 8 * g + 4 * wv.hh;
             u32x2_t pk;
-            pk[0] = pack2<T>(o[x][4 * g] * inv, o[x][4 * g + 1] * inv);
-            pk[1] = pack2<T>(o[x][4 * g + 2] * inv, o[x][4 * g + 3] * inv);
+            pk[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
+            pk[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
             *reinterpret_cast<u32x2_t*>(orow + d) = pk;
         }
     }
-    if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (m + log2f(l)) * kLn2;
+    if (wv.hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
+}
+
+// ---------------------------------------------------------------------------------------
+// Direct-to-LDS variant (no value multiplier, no key mask, unit-stride key bias): K, V and the
+// raw key bias travel HBM -> LDS with buffer_load ... lds (no registers, no VALU), three LDS
+// stages deep so that the loads of tile t+2 are in flight while tile t is computed.  K and V
+// stay row-major in LDS with the 16-byte chunks of each row XOR-swizzled, so that the K
+// fragment reads (ds_read_b128) and the transposing V^T reads (ds_read_b64_tr_b16) spread
+// over the LDS banks.  Rows past the last key lie outside the buffer range and read as zeros
+// (their scores are masked).  Every vector-memory operation inside the tile loop is one of
+// these loads, so the waits are explicit: before the barrier of step t each wave waits until
+// only tile t+1's loads are outstanding.  Each wave converts the raw bias of its tile
+// (class filter, log2 domain) into a wave-private LDS row.
+
+constexpr int kFwdStages = 3;
+
+// chunk swizzles (16-byte chunk index within a row, as a function of the row)
+template <int D>
+__device__ __forceinline__ int swz_k(int r) {
+    r &= 31;
+    return D == 64 ? ((r + (r >> 3)) & 7) : (r & 15);
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int r) {
+    return D == 64 ? 2 * (r & 3) : 4 * (r & 3);
+}
+
+template <int D, int KB>
+struct DmaTile {
+    static constexpr int BN = 32 * KB;
+    static constexpr int CPR = D / 8;                  // 16-byte chunks per row
+    static constexpr int NL = BN * CPR / kFwdThreads;  // loads per thread and tensor
+    static constexpr int ELEMS = BN * D;               // elements per tensor tile
+    static_assert(BN * CPR % kFwdThreads == 0, "tile must split evenly over the threads");
+};
+
+template <typename T, int D, int KB, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS>
+__global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(PassDev P) {
+    using TL = DmaTile<D, KB>;
+    constexpr int BN = TL::BN, NL = TL::NL;
+    // vector-memory operations per thread and tile: K and V chunks, one bias load
+    constexpr int NOPS = 2 * NL + (HAS_BIAS ? 1 : 0);
+    using W = FwdWave<T, D, KB, CAUSAL, SOFTCLAMP, HAS_BIAS>;
+    using M = Mma<T>;
+    typedef typename W::frag frag;
+    __shared__ __attribute__((aligned(16))) T sK[kFwdStages * TL::ELEMS];
+    __shared__ __attribute__((aligned(16))) T sV[kFwdStages * TL::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sBraw[kFwdStages][BN];  // raw bias bytes
+    __shared__ __attribute__((aligned(16))) float sBw[4][BN];             // per-wave converted
+
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int qb = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;
+    const int bh = lid / nqb;
+    const int h = bh % P.heads, b = bh / P.heads;
+
+    W wv;
+    wv.hh = lane >> 5;
+    wv.kcol = lane & 31;
+    wv.q0 = qb * kFwdBM + w * 32;
+    wv.qi = wv.q0 + wv.kcol;
+    wv.nk = P.nk;
+    wv.sl2 = P.scale * kLog2e;
+    wv.cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
+    wv.cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
+    wv.m = -INFINITY;
+    wv.l = 0.f;
+    {
+        const int qi = wv.qi;
+        const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+            u32x4_t raw = {0u, 0u, 0u, 0u};
+            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * wv.hh);
+            wv.qf[c] = __builtin_bit_cast(frag, raw);
+        }
+    }
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) wv.o[x] = zero16();
+    // the Q loads are the only compiler-visible vector-memory operations: retire them before
+    // the first direct load, so that no compiler-inserted wait can stall on the latter
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) wv.qf[c] = opaque(wv.qf[c]);
+
+    // buffers over this (batch, head)'s rows [0, nk) of K and V, and its key bias
+    const int ksn = (int)P.k.sn, vsn = (int)P.v.sn;
+    const srd_t rk = make_srd(P.k.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * ksn + D) * 2));
+    const srd_t rv = make_srd(P.v.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * vsn + D) * 2));
+    const int bes = P.bias.dtype == PA_F32 ? 4 : 2;  // bias element size
+    srd_t rb = {0, 0, 0, 0};
+    if (HAS_BIAS) rb = make_srd(P.bias.p + P.bias.idx(b, h, 0) * bes, (uint32_t)(P.nk * bes));
+    // per-thread byte offsets (tile-relative) of the chunks this thread loads: chunk
+    // p = n*256 + tid of the tile sits at row p / CPR, physical chunk p % CPR
+    uint32_t offk[NL], offv[NL];
+#pragma unroll
+    for (int n = 0; n < NL; ++n) {
+        const int p = n * kFwdThreads + tid, r = p / TL::CPR, ph = p % TL::CPR;
+        offk[n] = (uint32_t)((r * ksn + (ph ^ swz_k<D>(r)) * 8) * 2);
+        offv[n] = (uint32_t)((r * vsn + (ph ^ swz_v<D>(r)) * 8) * 2);
+    }
+    // bias: each wave loads a quarter of the tile's BN * bes bytes with its first lanes
+    const int bq = BN * bes / 4;  // bytes per wave
+    const uint32_t offb = (uint32_t)(w * bq + 16 * lane);
+    const uint32_t lds_k = lds_addr(sK), lds_v = lds_addr(sV), lds_b = lds_addr(&sBraw[0][0]);
+    auto issue = [&](int j0, int stage) __attribute__((always_inline)) {
+        const uint32_t tk = (uint32_t)(j0 * ksn * 2), tv = (uint32_t)(j0 * vsn * 2);
+        const uint32_t kd = lds_k + (uint32_t)(stage * TL::ELEMS * 2), vd = lds_v + (uint32_t)(stage * TL::ELEMS * 2);
+#pragma unroll
+        for (int n = 0; n < NL; ++n) {
+            dma16(rk, kd + (uint32_t)((n * kFwdThreads + w * 64) * 16), offk[n] + tk);
+            dma16(rv, vd + (uint32_t)((n * kFwdThreads + w * 64) * 16), offv[n] + tv);
+        }
+        // one (partially active) bias load per wave: lanes past the wave's quarter stay idle
+        if (HAS_BIAS && 16 * lane < bq)
+            dma16(rb, lds_b + (uint32_t)(stage * BN * 4 + w * bq), offb + (uint32_t)(j0 * bes));
+    };
+
+    // per-lane LDS element offsets of the MFMA operands (tile-relative)
+    int koff[D / 16];  // K rows kcol (+32*kb), chunk 2c + hh
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+        koff[c] = wv.kcol * D + (((2 * c + wv.hh) ^ swz_k<D>(wv.kcol)) * 8);
+    int voff[D / 32];  // V rows 4*hh + j/4 (+16*t2 + 8*u + 32*kb), columns 32x + (lane & 31)
+    {
+        const int g = lane >> 4, j = lane & 15;
+        const int r = 4 * (g >> 1) + (j >> 2);
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x) {
+            const int ch = 4 * x + 2 * (g & 1) + ((j & 3) >> 1);
+            voff[x] = r * D + ((ch ^ swz_v<D>(r)) * 8) + 4 * (j & 1);
+        }
+    }
+
+    const int kend = CAUSAL ? min(P.nk, qb * kFwdBM + kFwdBM) : P.nk;
+    const int ntiles = (kend + BN - 1) / BN;
+    const int wave_last = CAUSAL ? (wv.q0 + 31) : (1 << 30);
+
+    issue(0, 0);
+    if (ntiles > 1) issue(BN, 1);
+
+    // tiles [0, nact) hold keys at or below this wave's last query; the remaining tiles of the
+    // workgroup only pass through (loads and barriers), in a loop of their own so that the
+    // compute loop has a single path
+    const int nact = CAUSAL ? min(ntiles, wave_last / BN + 1) : ntiles;
+    int st = 0;
+    auto enter = [&](int t) __attribute__((always_inline)) {
+        if (t + 1 < ntiles) wait_vmcnt<NOPS>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        if (t + 2 < ntiles) issue((t + 2) * BN, st == 0 ? 2 : st - 1);
+    };
+    for (int t = 0; t < nact; ++t) {
+        const int j0 = t * BN;
+        enter(t);
+        {
+            const T* K = sK + st * TL::ELEMS;
+            const T* V = sV + st * TL::ELEMS;
+            if (HAS_BIAS) {
+                // this wave's converted copy of the tile's bias: class filtered, log2 domain
+                float x;
+                if (bes == 4) x = sBraw[st][lane];
+                else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
+                sBw[w][lane] = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
+            }
+            f32x16_t s[KB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                s[kb] = zero16();
+#pragma unroll
+                for (int c = 0; c < D / 16; ++c)
+                    s[kb] = M::run(ld_frag<T>(K + kb * 32 * D + koff[c]), wv.qf[c], s[kb]);
+            }
+            wv.mask_edges_nk(s, j0);
+            wv.settle(wv.logits(s, sBw[w]));
+            frag vf[KB][2][D / 32];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                    for (int x = 0; x < D / 32; ++x) {
+                        const T* base = V + (kb * 32 + 16 * t2) * D + voff[x];
+                        const u32x2_t lo = lds_read_tr(base);
+                        const u32x2_t hi = lds_read_tr(base + 8 * D);
+                        const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
+                        vf[kb][t2][x] = __builtin_bit_cast(frag, v4);
+                    }
+            u32x4_t pk[KB][2];
+            wv.l += wv.probs(s, wv.m == -INFINITY ? 0.f : wv.m, pk);
+            wv.pv(vf, pk);
+        }
+        st = st == 2 ? 0 : st + 1;
+    }
+    for (int t = nact; t < ntiles; ++t) {
+        enter(t);
+        st = st == 2 ? 0 : st + 1;
+    }
+
+    const float l = xhalf_sum(wv.l);
+    const int qi = wv.qi;
+    if (qi >= P.nq) return;
+    const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
+    const float inv = degenerate ? 0.f : 1.f / l;
+    T* orow = P.out.wrow<T>(b, h, qi);
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = x * 32 + 8 * g + 4 * wv.hh;
+            u32x2_t pk;
+            pk[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
+            pk[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
+            *reinterpret_cast<u32x2_t*>(orow + d) = pk;
+        }
+    }
+    if (wv.hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
+}
+
+// The direct-to-LDS kernel addresses K / V with 32-bit byte offsets up to the end of the last
+// tile and reads the key bias as one contiguous row; other cases take the register-staged
+// kernel.
+static bool dma_ok(const PassDev& P, int bn) {
+    const int64_t rows = (int64_t)P.nk + 2 * bn;
+    const int64_t span = std::max(P.k.sn, P.v.sn) * rows * 2;
+    if (!(span < ((int64_t)1 << 31))) return false;
+    if (P.km.p) return false;
+    if (P.bias.ok() && P.bias.sn != 1) return false;
+    if (P.bias.ok()) {
+        const int64_t es = P.bias.dtype == PA_F32 ? 4 : 2;
+        if ((uintptr_t)P.bias.p % 16 != 0 || (P.bias.sh * es) % 16 != 0 || (P.bias.sb * es) % 16 != 0) return false;
+        if ((P.nk * es) % 16 != 0) return false;  // whole 16-byte chunks in range
+    }
+    return true;
 }
 
 // ---------------------------------------------------------------------------------------
 
-// 32-key blocks per key tile: 128-key tiles at head dim 64 (without softclamp, whose tanh
-// temporaries would spill), 64-key tiles otherwise
+// 32-key blocks per key tile (64-key tiles)
 template <int D, bool SOFTCLAMP>
 constexpr int kFwdKB = (D == 64 && !SOFTCLAMP) ? PA_FWD_KB64 : 2;
 
 bool mfma_fwd_supported(const PassDev& P, int dtype) {
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
     if (P.dim != 64 && P.dim != 128) return false;
+    if (!(P.scale > 0.f)) return false;  // the raw-score running max assumes a positive scale
     if (!aligned_rows_host(P.q, 8) || !aligned_rows_host(P.k, 8) || !aligned_rows_host(P.v, 8)) return false;
     if (P.vmul.ok() && !aligned_rows_host(P.vmul, 8)) return false;
     if (!aligned_rows_host(P.out, 4)) return false;
@@ -323,7 +679,10 @@ static void launch_t(const PassDev& P, hipStream_t s) {
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     dim3 grid(nqb * P.heads * P.batch);
     ProfScope ps("mfma_fwd", s);
-    hipLaunchKernelGGL((k_mfma_fwd<T, D, KB, C, S, V, B>), grid, dim3(kFwdThreads), 0, s, P);
+    if (!V && dma_ok(P, 32 * KB))
+        hipLaunchKernelGGL((k_mfma_fwd_dma<T, D, KB, C, S, B>), grid, dim3(kFwdThreads), 0, s, P);
+    else
+        hipLaunchKernelGGL((k_mfma_fwd<T, D, KB, C, S, V, B>), grid, dim3(kFwdThreads), 0, s, P);
 }
 
 template <typename T, int D, bool C, bool S>
