@@ -1,25 +1,27 @@
 // pa_mfma_fwd.hip -- MFMA forward attention pass for bf16 / f16, head dim 64 or 128 (gfx950).
 //
-// Workgroup = 4 waves = 128 query rows of one (batch, pass head); each wave owns 32 queries.
-// Per key tile (32*KB keys) a wave computes the transposed scores S^T = K . Q^T with
-// v_mfma_f32_32x32x16_{bf16,f16}: the 32x32 accumulator layout gives lane l the column
-// q = l % 32 and 16 key rows per block, so the online-softmax state (running max m, sum l,
-// the output rescale) is a per-lane scalar.  The probabilities, rounded to the input type,
-// stay in registers as the B operand of O^T += V^T . P^T (keys permuted consistently between
-// the two operands, see pa_mfma.h), V being staged transposed in LDS.
+// Common scheme: 32 queries per wave.  Per key tile a wave computes the transposed scores
+// S^T = K . Q^T with v_mfma_f32_32x32x16_{bf16,f16}: the 32x32 accumulator layout gives lane
+// l the column q = l % 32 and 16 key rows per block, so the online-softmax state (running max
+// m, sum l, the output rescale) is a per-lane scalar.  The probabilities, rounded to the input
+// type, stay in registers as the B operand of O^T += V^T . P^T (keys permuted consistently
+// between the two operands, see pa_mfma.h).
 //
-// Software pipeline (per wave, one barrier per tile): iteration t issues the score MFMAs of
-// tile t+1 in the same basic block as the exponentials of tile t, so the matrix cores and
-// the VALU work side by side; then O += V_t^T . P_t.  K runs one tile ahead of V in LDS: while
-// iteration t reads K_{t+1} and V_t, the global loads of K_{t+2} and V_{t+1} are in flight
-// and land in the buffers freed by the previous iteration.  The key bias travels with V.
-//
-// Softmax: log2 domain (bare v_exp_f32, scale*log2(e) folded into one FMA; without a key
-// bias the running max is taken on the raw scores).  The running max is updated lazily: it
-// moves (and the output is rescaled) only when a tile's max exceeds it by more than kFwdTau,
-// so probabilities stay <= 2^kFwdTau (exact in fp32 and within the input type's exponent
-// range); after the first tiles this almost never happens.  Row sums accumulate the rounded
+// Softmax: log2 domain (bare v_exp_f32, scale*log2(e) folded into one FMA; without softclamp
+// the running max is taken on the raw scores).  The running max is updated lazily: it moves
+// (and the output is rescaled) only when a tile's max exceeds it by more than kFwdTau, so
+// probabilities stay <= 2^kFwdTau (exact in fp32 and within the input type's exponent range);
+// after the first tiles this almost never happens.  Row sums accumulate the rounded
 // probabilities with v_dot2 (the same values the MFMA consumes).
+//
+// Kernels:
+//  * k_mfma_fwd_dma (default): K, V and the key bias travel HBM -> LDS by direct loads,
+//    three stages deep; V^T operands come from transposing LDS reads; without softclamp the
+//    key bias is folded into the score accumulators.
+//  * k_mfma_fwd: register-staged loads with a transposing LDS store; the general kernel
+//    (value multiplier, key masks, strided biases, very long rows).
+//  * k_mfma_fwd_pp (PA_FWD_PINGPONG): an 8-wave ping-pong schedule, off by default (slower
+//    than k_mfma_fwd_dma on the measured workloads).
 //
 // Rows whose every key is masked are left with lse = NaN for k_simt_fixup, which applies the
 // reference's finite-fill semantics to them.  Workgroups are mapped XCD-aware (pa_mfma.h) and
@@ -35,6 +37,12 @@ namespace pa {
 
 #ifndef PA_FWD_KB64
 #define PA_FWD_KB64 2
+#endif
+#ifndef PA_FWD_PINGPONG
+#define PA_FWD_PINGPONG 0  // 1: head dim 64 without softclamp takes the 8-wave ping-pong kernel
+#endif
+#ifndef PA_FWD_QB64
+#define PA_FWD_QB64 1  // 32-query blocks per wave in the direct-to-LDS kernel at head dim 64
 #endif
 
 constexpr int kFwdBM = 128;  // query rows per workgroup
@@ -164,14 +172,16 @@ __device__ __forceinline__ void fwd_store(const FwdStage<D, KB>& st, T* sK, bool
     if (HAS_BIAS && sv && tid < TL::BN) sB[tid] = st.bias;
 }
 
-// Per-wave state and the pieces of one pipeline step.
-template <typename T, int D, int KB, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS>
+// Per-wave state and the pieces of one pipeline step.  BIAS_IN_LOGITS: the key bias is added
+// to the scores in logits() (otherwise it is absent or already inside the scores).
+template <typename T, int D, int KB, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS,
+          bool BIAS_IN_LOGITS = HAS_BIAS>
 struct FwdWave {
     using TL = FwdTile<D, KB>;
     using M = Mma<T>;
     typedef typename M::frag frag;
     static constexpr int BN = TL::BN;
-    static constexpr bool PLAIN = !HAS_BIAS && !SOFTCLAMP;  // max taken on raw scores
+    static constexpr bool PLAIN = !BIAS_IN_LOGITS && !SOFTCLAMP;  // max taken on raw scores
 
     frag qf[D / 16];
     f32x16_t o[D / 32];
@@ -224,13 +234,14 @@ struct FwdWave {
     // scores -> log2-domain logits in place (bias / softclamp paths); returns the max over the
     // query's logits of this tile (PLAIN: of the raw scores, times scale*log2e)
     __device__ __forceinline__ float logits(f32x16_t (&s)[KB], const float* sB) const {
-        float mx = -INFINITY;
+        // four independent max chains (short dependency chains), combined at the end
+        float mq[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 float bv[4] = {0.f, 0.f, 0.f, 0.f};
-                if (HAS_BIAS) {
+                if (BIAS_IN_LOGITS) {
                     const float4 bb = *reinterpret_cast<const float4*>(sB + kb * 32 + 8 * g + 4 * hh);
                     bv[0] = bb.x;
                     bv[1] = bb.y;
@@ -245,18 +256,18 @@ struct FwdWave {
                         else x = fmaf(x, sl2, bv[r]);
                         s[kb][4 * g + r] = x;
                     }
-                    mx = fmaxf(mx, x);
+                    mq[r] = fmaxf(mq[r], x);
                 }
             }
         }
-        mx = xhalf_max(mx);
+        const float mx = xhalf_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
         return PLAIN ? mx * sl2 : mx;
     }
 
     // probabilities against the max msub, rounded to T and packed as the PV B operands; returns
     // the lane's sum of the rounded probabilities
     __device__ __forceinline__ float probs(const f32x16_t (&s)[KB], float msub, u32x4_t (&pk)[KB][2]) const {
-        float lt = 0.f;
+        float lt[4] = {0.f, 0.f, 0.f, 0.f};  // independent accumulation chains
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -268,9 +279,9 @@ struct FwdWave {
                     const float p1 = PLAIN ? fast_exp2(fmaf(x1, sl2, -msub)) : fast_exp2(x1 - msub);
                     const uint32_t w = pack2<T>(p0, p1);
                     pk[kb][t2][k] = w;
-                    lt = sum_pair<T>(w, lt);
+                    lt[k] = sum_pair<T>(w, lt[k]);
                 }
-        return lt;
+        return (lt[0] + lt[1]) + (lt[2] + lt[3]);
     }
 
     // lazy rescale: only when some lane's tile max exceeds its running max by more than
@@ -457,13 +468,18 @@ struct DmaTile {
     static_assert(BN * CPR % kFwdThreads == 0, "tile must split evenly over the threads");
 };
 
-template <typename T, int D, int KB, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS>
+// QB query blocks of 32 per wave (workgroup = 128 * QB queries): with QB = 2 every K and V
+// fragment read from LDS feeds two MFMAs, and each wave carries two independent softmax chains.
+template <typename T, int D, int KB, int QB, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS>
 __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(PassDev P) {
     using TL = DmaTile<D, KB>;
-    constexpr int BN = TL::BN, NL = TL::NL;
+    constexpr int BN = TL::BN, NL = TL::NL, BM = kFwdBM * QB;
     // vector-memory operations per thread and tile: K and V chunks, one bias load
     constexpr int NOPS = 2 * NL + (HAS_BIAS ? 1 : 0);
-    using W = FwdWave<T, D, KB, CAUSAL, SOFTCLAMP, HAS_BIAS>;
+    // without softclamp the key bias enters the scores as the MFMA accumulator's initial value
+    // (bias / scale, so that scale*log2e*(s + bias/scale) is the log2-domain logit)
+    constexpr bool FOLD = HAS_BIAS && !SOFTCLAMP;
+    using W = FwdWave<T, D, KB, CAUSAL, SOFTCLAMP, HAS_BIAS, HAS_BIAS && SOFTCLAMP>;
     using M = Mma<T>;
     typedef typename W::frag frag;
     __shared__ __attribute__((aligned(16))) T sK[kFwdStages * TL::ELEMS];
@@ -472,45 +488,52 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     __shared__ __attribute__((aligned(16))) float sBw[4][BN];             // per-wave converted
 
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-    const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
+    const int nqb = (P.nq + BM - 1) / BM;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
     const int qb = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;
     const int bh = lid / nqb;
     const int h = bh % P.heads, b = bh / P.heads;
+    const int hh = lane >> 5, kcol = lane & 31;
+    const int wq0 = qb * BM + w * 32 * QB;  // this wave's first query
 
-    W wv;
-    wv.hh = lane >> 5;
-    wv.kcol = lane & 31;
-    wv.q0 = qb * kFwdBM + w * 32;
-    wv.qi = wv.q0 + wv.kcol;
-    wv.nk = P.nk;
-    wv.sl2 = P.scale * kLog2e;
-    wv.cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
-    wv.cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
-    wv.m = -INFINITY;
-    wv.l = 0.f;
-    {
-        const int qi = wv.qi;
+    W wv[QB];
+#pragma unroll
+    for (int u = 0; u < QB; ++u) {
+        W& v = wv[u];
+        v.hh = hh;
+        v.kcol = kcol;
+        v.q0 = wq0 + 32 * u;
+        v.qi = v.q0 + kcol;
+        v.nk = P.nk;
+        v.sl2 = P.scale * kLog2e;
+        v.cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
+        v.cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
+        v.m = -INFINITY;
+        v.l = 0.f;
+        const int qi = v.qi;
         const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) {
             u32x4_t raw = {0u, 0u, 0u, 0u};
-            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * wv.hh);
-            wv.qf[c] = __builtin_bit_cast(frag, raw);
+            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
+            v.qf[c] = __builtin_bit_cast(frag, raw);
         }
-    }
 #pragma unroll
-    for (int x = 0; x < D / 32; ++x) wv.o[x] = zero16();
+        for (int x = 0; x < D / 32; ++x) v.o[x] = zero16();
+    }
     // the Q loads are the only compiler-visible vector-memory operations: retire them before
     // the first direct load, so that no compiler-inserted wait can stall on the latter
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) wv.qf[c] = opaque(wv.qf[c]);
+    for (int u = 0; u < QB; ++u)
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) wv[u].qf[c] = opaque(wv[u].qf[c]);
 
     // buffers over this (batch, head)'s rows [0, nk) of K and V, and its key bias
     const int ksn = (int)P.k.sn, vsn = (int)P.v.sn;
     const srd_t rk = make_srd(P.k.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * ksn + D) * 2));
     const srd_t rv = make_srd(P.v.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * vsn + D) * 2));
     const int bes = P.bias.dtype == PA_F32 ? 4 : 2;  // bias element size
+    const float bmul = FOLD ? 1.f / P.scale : kLog2e;
     srd_t rb = {0, 0, 0, 0};
     if (HAS_BIAS) rb = make_srd(P.bias.p + P.bias.idx(b, h, 0) * bes, (uint32_t)(P.nk * bes));
     // per-thread byte offsets (tile-relative) of the chunks this thread loads: chunk
@@ -542,8 +565,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     // per-lane LDS element offsets of the MFMA operands (tile-relative)
     int koff[D / 16];  // K rows kcol (+32*kb), chunk 2c + hh
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c)
-        koff[c] = wv.kcol * D + (((2 * c + wv.hh) ^ swz_k<D>(wv.kcol)) * 8);
+    for (int c = 0; c < D / 16; ++c) koff[c] = kcol * D + (((2 * c + hh) ^ swz_k<D>(kcol)) * 8);
     int voff[D / 32];  // V rows 4*hh + j/4 (+16*t2 + 8*u + 32*kb), columns 32x + (lane & 31)
     {
         const int g = lane >> 4, j = lane & 15;
@@ -555,9 +577,9 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
         }
     }
 
-    const int kend = CAUSAL ? min(P.nk, qb * kFwdBM + kFwdBM) : P.nk;
+    const int kend = CAUSAL ? min(P.nk, qb * BM + BM) : P.nk;
     const int ntiles = (kend + BN - 1) / BN;
-    const int wave_last = CAUSAL ? (wv.q0 + 31) : (1 << 30);
+    const int wave_last = CAUSAL ? (wq0 + 32 * QB - 1) : (1 << 30);
 
     issue(0, 0);
     if (ntiles > 1) issue(BN, 1);
@@ -576,42 +598,62 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     for (int t = 0; t < nact; ++t) {
         const int j0 = t * BN;
         enter(t);
-        {
-            const T* K = sK + st * TL::ELEMS;
-            const T* V = sV + st * TL::ELEMS;
-            if (HAS_BIAS) {
-                // this wave's converted copy of the tile's bias: class filtered, log2 domain
-                float x;
-                if (bes == 4) x = sBraw[st][lane];
-                else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
-                sBw[w][lane] = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
+        const T* K = sK + st * TL::ELEMS;
+        const T* V = sV + st * TL::ELEMS;
+        if (HAS_BIAS) {
+            // this wave's converted copy of the tile's bias: class filtered; log2 domain
+            // (softclamp) or divided by the scale (folded into the scores)
+            float x;
+            if (bes == 4) x = sBraw[st][lane];
+            else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
+            sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
+        }
+        f32x16_t s[QB][KB];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            f32x16_t init = zero16();
+            if (FOLD) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 bb = *reinterpret_cast<const float4*>(&sBw[w][kb * 32 + 8 * g + 4 * hh]);
+                    init[4 * g] = bb.x;
+                    init[4 * g + 1] = bb.y;
+                    init[4 * g + 2] = bb.z;
+                    init[4 * g + 3] = bb.w;
+                }
             }
-            f32x16_t s[KB];
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                s[kb] = zero16();
+            for (int u = 0; u < QB; ++u) s[u][kb] = init;
 #pragma unroll
-                for (int c = 0; c < D / 16; ++c)
-                    s[kb] = M::run(ld_frag<T>(K + kb * 32 * D + koff[c]), wv.qf[c], s[kb]);
+            for (int c = 0; c < D / 16; ++c) {
+                const frag a = ld_frag<T>(K + kb * 32 * D + koff[c]);
+#pragma unroll
+                for (int u = 0; u < QB; ++u) s[u][kb] = M::run(a, wv[u].qf[c], s[u][kb]);
             }
-            wv.mask_edges_nk(s, j0);
-            wv.settle(wv.logits(s, sBw[w]));
-            frag vf[KB][2][D / 32];
+        }
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
+        for (int u = 0; u < QB; ++u) {
+            wv[u].mask_edges_nk(s[u], j0);
+            wv[u].settle(wv[u].logits(s[u], sBw[w]));
+        }
+        frag vf[KB][2][D / 32];
 #pragma unroll
-                for (int t2 = 0; t2 < 2; ++t2)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-                    for (int x = 0; x < D / 32; ++x) {
-                        const T* base = V + (kb * 32 + 16 * t2) * D + voff[x];
-                        const u32x2_t lo = lds_read_tr(base);
-                        const u32x2_t hi = lds_read_tr(base + 8 * D);
-                        const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
-                        vf[kb][t2][x] = __builtin_bit_cast(frag, v4);
-                    }
+            for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                for (int x = 0; x < D / 32; ++x) {
+                    const T* base = V + (kb * 32 + 16 * t2) * D + voff[x];
+                    const u32x2_t lo = lds_read_tr(base);
+                    const u32x2_t hi = lds_read_tr(base + 8 * D);
+                    const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
+                    vf[kb][t2][x] = __builtin_bit_cast(frag, v4);
+                }
+#pragma unroll
+        for (int u = 0; u < QB; ++u) {
             u32x4_t pk[KB][2];
-            wv.l += wv.probs(s, wv.m == -INFINITY ? 0.f : wv.m, pk);
-            wv.pv(vf, pk);
+            wv[u].l += wv[u].probs(s[u], wv[u].m == -INFINITY ? 0.f : wv[u].m, pk);
+            wv[u].pv(vf, pk);
         }
         st = st == 2 ? 0 : st + 1;
     }
@@ -620,24 +662,29 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
         st = st == 2 ? 0 : st + 1;
     }
 
-    const float l = xhalf_sum(wv.l);
-    const int qi = wv.qi;
-    if (qi >= P.nq) return;
-    const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
-    const float inv = degenerate ? 0.f : 1.f / l;
-    T* orow = P.out.wrow<T>(b, h, qi);
 #pragma unroll
-    for (int x = 0; x < D / 32; ++x) {
+    for (int u = 0; u < QB; ++u) {
+        const W& v = wv[u];
+        const float l = xhalf_sum(v.l);
+        const int qi = v.qi;
+        if (qi < P.nq) {
+            const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
+            const float inv = degenerate ? 0.f : 1.f / l;
+            T* orow = P.out.wrow<T>(b, h, qi);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d = x * 32 + 8 * g + 4 * wv.hh;
-            u32x2_t pk;
-            pk[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
-            pk[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
-            *reinterpret_cast<u32x2_t*>(orow + d) = pk;
+            for (int x = 0; x < D / 32; ++x) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = x * 32 + 8 * g + 4 * hh;
+                    u32x2_t pk;
+                    pk[0] = pack2<T>(v.o[x][4 * g] * inv, v.o[x][4 * g + 1] * inv);
+                    pk[1] = pack2<T>(v.o[x][4 * g + 2] * inv, v.o[x][4 * g + 3] * inv);
+                    *reinterpret_cast<u32x2_t*>(orow + d) = pk;
+                }
+            }
+            if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (v.m + log2f(l)) * kLn2;
         }
     }
-    if (wv.hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
 }
 
 // The direct-to-LDS kernel addresses K / V with 32-bit byte offsets up to the end of the last
@@ -655,6 +702,240 @@ static bool dma_ok(const PassDev& P, int bn) {
         if ((P.nk * es) % 16 != 0) return false;  // whole 16-byte chunks in range
     }
     return true;
+}
+
+// ---------------------------------------------------------------------------------------
+// Ping-pong variant (head dim 64, no softclamp, no value multiplier): 8 waves per workgroup
+// in two groups of four, one wave of each group per SIMD.  The tile loop alternates two
+// phases separated by workgroup barriers; in every phase one group issues its MFMAs (scores
+// of tile t and O += V^T P of tile t-1) while the other runs the softmax VALU work of its
+// previous tile, so that each SIMD's matrix core and VALU always have one wave to serve.
+// Group A (waves 0-3) runs MFMA(t) in phase 2t and softmax(t) in phase 2t+1; group B
+// (waves 4-7) runs softmax(t-1) in phase 2t and MFMA(t) in phase 2t+1.  Loads travel HBM ->
+// LDS directly: at phase 2t the group of K_{t+2} (+ key bias) and V_{t+1} is issued, into
+// the stages freed by tile t-1 (three K stages, three V stages).
+
+constexpr int kPpThreads = 512;
+constexpr int kPpBM = 256;  // queries per workgroup (8 waves x 32)
+
+template <typename T, bool CAUSAL, bool HAS_BIAS>
+__global__ __launch_bounds__(kPpThreads, 1) void k_mfma_fwd_pp(PassDev P) {
+    constexpr int D = 64, KB = 2, BN = 64, CPR = D / 8, ELEMS = BN * D;
+    static_assert(BN * CPR == kPpThreads, "one 16-byte chunk per thread and tensor");
+    using W = FwdWave<T, D, KB, CAUSAL, false, HAS_BIAS, false>;  // bias folded into the scores
+    using M = Mma<T>;
+    typedef typename W::frag frag;
+    __shared__ __attribute__((aligned(16))) T sK[3 * ELEMS];
+    __shared__ __attribute__((aligned(16))) T sV[3 * ELEMS];
+    __shared__ __attribute__((aligned(16))) float sBraw[3][BN];
+    __shared__ __attribute__((aligned(16))) float sBw[8][BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const bool grp_a = w < 4;
+    const int nqb = (P.nq + kPpBM - 1) / kPpBM;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int qb = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;
+    const int bh = lid / nqb;
+    const int h = bh % P.heads, b = bh / P.heads;
+    const int hh = lane >> 5, kcol = lane & 31;
+
+    W wv;
+    wv.hh = hh;
+    wv.kcol = kcol;
+    wv.q0 = qb * kPpBM + w * 32;
+    wv.qi = wv.q0 + kcol;
+    wv.nk = P.nk;
+    wv.sl2 = P.scale * kLog2e;
+    wv.cinv = 0.f;
+    wv.cl2 = 0.f;
+    wv.m = -INFINITY;
+    wv.l = 0.f;
+    {
+        const int qi = wv.qi;
+        const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+            u32x4_t raw = {0u, 0u, 0u, 0u};
+            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
+            wv.qf[c] = __builtin_bit_cast(frag, raw);
+        }
+    }
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) wv.o[x] = zero16();
+    // retire the (compiler-visible) Q loads before the first direct load
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) wv.qf[c] = opaque(wv.qf[c]);
+
+    const int ksn = (int)P.k.sn, vsn = (int)P.v.sn;
+    const srd_t rk = make_srd(P.k.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * ksn + D) * 2));
+    const srd_t rv = make_srd(P.v.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * vsn + D) * 2));
+    const int bes = P.bias.dtype == PA_F32 ? 4 : 2;
+    const float bmul = 1.f / P.scale;
+    srd_t rb = {0, 0, 0, 0};
+    if (HAS_BIAS) rb = make_srd(P.bias.p + P.bias.idx(b, h, 0) * bes, (uint32_t)(P.nk * bes));
+    // this thread's chunk of a tile: row tid / CPR, physical chunk tid % CPR
+    uint32_t offk, offv;
+    {
+        const int r = tid / CPR, ph = tid % CPR;
+        offk = (uint32_t)((r * ksn + (ph ^ swz_k<D>(r)) * 8) * 2);
+        offv = (uint32_t)((r * vsn + (ph ^ swz_v<D>(r)) * 8) * 2);
+    }
+    const int bq = BN * bes / 8;  // bias bytes per wave (every wave has lane 0 active)
+    const uint32_t offb = (uint32_t)(w * bq + 16 * lane);
+    const uint32_t lds_k = lds_addr(sK), lds_v = lds_addr(sV), lds_b = lds_addr(&sBraw[0][0]);
+    auto issue_k = [&](int j0, int stage) __attribute__((always_inline)) {
+        dma16(rk, lds_k + (uint32_t)(stage * ELEMS * 2 + w * 64 * 16), offk + (uint32_t)(j0 * ksn * 2));
+        if (HAS_BIAS && 16 * lane < bq)
+            dma16(rb, lds_b + (uint32_t)(stage * BN * 4 + w * bq), offb + (uint32_t)(j0 * bes));
+    };
+    auto issue_v = [&](int j0, int stage) __attribute__((always_inline)) {
+        dma16(rv, lds_v + (uint32_t)(stage * ELEMS * 2 + w * 64 * 16), offv + (uint32_t)(j0 * vsn * 2));
+    };
+
+    int koff[D / 16];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) koff[c] = kcol * D + (((2 * c + hh) ^ swz_k<D>(kcol)) * 8);
+    int voff[D / 32];
+    {
+        const int g = lane >> 4, j = lane & 15;
+        const int r = 4 * (g >> 1) + (j >> 2);
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x) {
+            const int ch = 4 * x + 2 * (g & 1) + ((j & 3) >> 1);
+            voff[x] = r * D + ((ch ^ swz_v<D>(r)) * 8) + 4 * (j & 1);
+        }
+    }
+
+    const int kend = CAUSAL ? min(P.nk, qb * kPpBM + kPpBM) : P.nk;
+    const int ntiles = (kend + BN - 1) / BN;
+    const int nact = CAUSAL ? min(ntiles, (wv.q0 + 31) / BN + 1) : ntiles;  // this wave's tiles
+    constexpr int KOPS = 1 + (HAS_BIAS ? 1 : 0);  // loads per thread for one K tile (+ bias)
+    // loads per thread in the group issued at even phase 2g: K_{g+2} (+ bias), V_{g+1}
+    auto group_ops = [&](int g) __attribute__((always_inline)) {
+        return (g + 2 < ntiles && g + 2 >= 0 ? KOPS : 0) + (g + 1 < ntiles && g + 1 >= 0 ? 1 : 0);
+    };
+
+    // prologue: group -2 = K_0 (+ bias_0); group -1 = K_1 (+ bias_1), V_0
+    issue_k(0, 0);
+    if (ntiles > 1) issue_k(BN, 1);
+    issue_v(0, 0);
+
+    f32x16_t s[KB];
+    u32x4_t pk[KB][2];
+    // scores S_t of tile t (accumulators seeded with the folded key bias)
+    auto scores_t = [&](int t) __attribute__((always_inline)) {
+        const int st = t % 3;
+        const T* K = sK + st * ELEMS;
+        if (HAS_BIAS) {
+            float x;
+            if (bes == 4) x = sBraw[st][lane];
+            else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
+            sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
+        }
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            f32x16_t a = zero16();
+            if (HAS_BIAS) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 bb = *reinterpret_cast<const float4*>(&sBw[w][kb * 32 + 8 * g + 4 * hh]);
+                    a[4 * g] = bb.x;
+                    a[4 * g + 1] = bb.y;
+                    a[4 * g + 2] = bb.z;
+                    a[4 * g + 3] = bb.w;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) a = M::run(ld_frag<T>(K + kb * 32 * D + koff[c]), wv.qf[c], a);
+            s[kb] = a;
+        }
+    };
+    // O += V_t^T P_t
+    auto pv_t = [&](int t) __attribute__((always_inline)) {
+        const T* V = sV + (t % 3) * ELEMS;
+        frag vf[KB][2][D / 32];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                for (int x = 0; x < D / 32; ++x) {
+                    const T* base = V + (kb * 32 + 16 * t2) * D + voff[x];
+                    const u32x2_t lo = lds_read_tr(base);
+                    const u32x2_t hi = lds_read_tr(base + 8 * D);
+                    const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
+                    vf[kb][t2][x] = __builtin_bit_cast(frag, v4);
+                }
+        wv.pv(vf, pk);
+    };
+    // softmax of tile t
+    auto softmax_t = [&](int t) __attribute__((always_inline)) {
+        wv.mask_edges_nk(s, t * BN);
+        wv.settle(wv.logits(s, nullptr));
+        wv.l += wv.probs(s, wv.m == -INFINITY ? 0.f : wv.m, pk);
+    };
+    // phase boundaries: even global phase 2e waits for load group e-2, then issues group e
+    auto sync_even = [&](int e) __attribute__((always_inline)) {
+        switch (group_ops(e - 1)) {
+            case 0: wait_vmcnt<0>(); break;
+            case 1: wait_vmcnt<1>(); break;
+            case 2: wait_vmcnt<2>(); break;
+            default: wait_vmcnt<3>(); break;
+        }
+        lds_barrier();
+        if (e + 2 < ntiles) issue_k((e + 2) * BN, (e + 2) % 3);
+        if (e + 1 < ntiles) issue_v((e + 1) * BN, (e + 1) % 3);
+    };
+    // Every wave runs the same sequence "sync, MFMA(t), sync, softmax(t)"; group B starts one
+    // phase later (its first sync is global phase 0), group A ends one phase later.
+    auto sync1 = [&](int t) __attribute__((always_inline)) {
+        if (grp_a) sync_even(t);
+        else lds_barrier();
+    };
+    auto sync2 = [&](int t) __attribute__((always_inline)) {
+        if (grp_a) lds_barrier();
+        else sync_even(t + 1);
+    };
+    if (!grp_a) sync_even(0);
+    // tile 0 (every wave has it)
+    sync1(0);
+    scores_t(0);
+    sync2(0);
+    softmax_t(0);
+    for (int t = 1; t < nact; ++t) {
+        sync1(t);
+        scores_t(t);
+        pv_t(t - 1);
+        sync2(t);
+        softmax_t(t);
+    }
+    sync1(nact);
+    pv_t(nact - 1);
+    sync2(nact);
+    for (int t = nact + 1; t <= ntiles; ++t) {
+        sync1(t);
+        sync2(t);
+    }
+    if (grp_a) sync_even(ntiles + 1);
+
+    const float l = xhalf_sum(wv.l);
+    const int qi = wv.qi;
+    if (qi >= P.nq) return;
+    const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
+    const float inv = degenerate ? 0.f : 1.f / l;
+    T* orow = P.out.wrow<T>(b, h, qi);
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = x * 32 + 8 * g + 4 * hh;
+            u32x2_t o2;
+            o2[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
+            o2[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
+            *reinterpret_cast<u32x2_t*>(orow + d) = o2;
+        }
+    }
+    if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -679,10 +960,17 @@ static void launch_t(const PassDev& P, hipStream_t s) {
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     dim3 grid(nqb * P.heads * P.batch);
     ProfScope ps("mfma_fwd", s);
-    if (!V && dma_ok(P, 32 * KB))
-        hipLaunchKernelGGL((k_mfma_fwd_dma<T, D, KB, C, S, B>), grid, dim3(kFwdThreads), 0, s, P);
-    else
+    if (D == 64 && PA_FWD_PINGPONG && !S && !V && dma_ok(P, 32 * KB)) {
+        const int nqb_pp = (P.nq + kPpBM - 1) / kPpBM;
+        hipLaunchKernelGGL((k_mfma_fwd_pp<T, C, B>), dim3(nqb_pp * P.heads * P.batch), dim3(kPpThreads), 0, s, P);
+    } else if (!V && dma_ok(P, 32 * KB)) {
+        constexpr int QB = (D == 64) ? PA_FWD_QB64 : 1;
+        const int nqb2 = (P.nq + kFwdBM * QB - 1) / (kFwdBM * QB);
+        hipLaunchKernelGGL((k_mfma_fwd_dma<T, D, KB, QB, C, S, B>), dim3(nqb2 * P.heads * P.batch),
+                           dim3(kFwdThreads), 0, s, P);
+    } else {
         hipLaunchKernelGGL((k_mfma_fwd<T, D, KB, C, S, V, B>), grid, dim3(kFwdThreads), 0, s, P);
+    }
 }
 
 template <typename T, int D, bool C, bool S>
