@@ -173,6 +173,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Each active lane loads 16 bytes at byte offset `voff` of the buffer; lane i's bytes land at
 // LDS byte address lds + 16 * i (lds uniform across the wave).
 __device__ __forceinline__ void dma16(srd_t srd, uint32_t lds, uint32_t voff) {
+    lds = __builtin_amdgcn_readfirstlane(lds);
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
                  :
                  : "v"(voff), "s"(lds), "s"(srd)

@@ -11,6 +11,8 @@
 //     sweeps the key tiles: S^T = K Q^T, dP^T = V dO^T, dS^T, then dQ^T += K^T dS^T.
 // Both recompute P from the saved lse; they do not handle fully-masked rows (the host sends
 // masked passes to the generic kernels).
+#include <algorithm>
+
 #include "pa_common.h"
 #include "pa_launch.h"
 #include "pa_mfma.h"
@@ -18,6 +20,10 @@
 namespace pa {
 
 constexpr int kBwdThreads = 256;
+
+#ifndef PA_BWD_DMA
+#define PA_BWD_DMA 1  // direct-to-LDS backward kernels where they apply
+#endif
 
 // ---------------------------------------------------------------------------------------
 // dK / dV / dbias
@@ -314,6 +320,292 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
 }
 
 // ---------------------------------------------------------------------------------------
+// Direct-to-LDS dK / dV / dbias (no value multiplier): the Q and dO tiles of every query
+// tile, with their lse and D rows, travel HBM -> LDS by buffer_load ... lds, three stages
+// deep (tile i+2 in flight while tile i is computed; the query heads of a KV group form one
+// flat tile sequence).  Q and dO stay row-major in LDS and are read both by rows (S = Q K^T,
+// dP = dO V^T) and transposed (dV^T += dO^T P, dK^T += Q^T dS, ds_read_b64_tr_b16), under a
+// chunk swizzle that serves both patterns.  Each wave converts the tile's lse and D into
+// accumulator seeds: S starts at -lse/scale (so P = exp2(scale*log2e*S + bias)) and dP at
+// -D (so dS = P dP); with softclamp the lse is kept in the log2 domain instead.
+
+// chunk swizzle for tiles read by rows (16 rows x one chunk per quarter-wave) and transposed
+// (4 rows x 4 chunks per half-wave): rows of one parity in a 16-row group get distinct
+// chunks, and rows r, r+2 of an aligned group of four differ in the chunk's bit 2 (D = 64);
+// a 4-bit reversal of the row for D = 128
+template <int D>
+__device__ __forceinline__ int swz_qt(int r) {
+    if (D == 64) {
+        const int v = (r >> 1) & 7;
+        return ((v & 1) << 2) | (v & 2) | ((v >> 2) & 1);
+    }
+    const int v = r & 15;
+    return ((v & 1) << 3) | ((v & 2) << 1) | ((v >> 1) & 2) | ((v >> 3) & 1);
+}
+
+constexpr int kKvStages = 3;
+
+template <typename T, int D, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS>
+__global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_dma(GradDev G) {
+    using M = Mma<T>;
+    typedef typename M::frag frag;
+    constexpr int BQ = kKvBQ, CPR = D / 8, ELEMS = BQ * D;
+    constexpr int NL = BQ * CPR / kBwdThreads;  // chunks per thread and tensor
+    constexpr int NOPS = 2 * NL + 2;            // + lse and D rows
+    static_assert(BQ * CPR % kBwdThreads == 0, "tile must split evenly over the threads");
+    const PassDev& P = G.f;
+    __shared__ __attribute__((aligned(16))) T sQ[kKvStages * ELEMS];
+    __shared__ __attribute__((aligned(16))) T sO[kKvStages * ELEMS];
+    __shared__ __attribute__((aligned(16))) float sLraw[kKvStages][BQ];
+    __shared__ __attribute__((aligned(16))) float sDraw[kKvStages][BQ];
+    __shared__ __attribute__((aligned(16))) float sLw[4][BQ];  // per-wave converted seeds
+    __shared__ __attribute__((aligned(16))) float sDw[4][BQ];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const int hh = lane >> 5, kcol = lane & 31;
+    const int nkb = (P.nk + kKvBK - 1) / kKvBK;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int kblk = lid % nkb;  // causal: the first key blocks carry the most work
+    const int kh = (lid / nkb) % G.hk, b = (lid / nkb) / G.hk;
+    const int rep = P.heads / G.hk;
+    const int h0 = kh * rep;
+    const int kw0 = kblk * kKvBK + w * 32;  // first key of this wave
+    const int key = kw0 + kcol;
+    const bool key_ok = key < P.nk;
+
+    frag kf[D / 16], vf[D / 16];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        u32x4_t kr = {0u, 0u, 0u, 0u}, vr = {0u, 0u, 0u, 0u};
+        if (key_ok) {
+            kr = *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h0, key) + c * 16 + 8 * hh);
+            vr = *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h0, key) + c * 16 + 8 * hh);
+        }
+        kf[c] = __builtin_bit_cast(frag, kr);
+        vf[c] = __builtin_bit_cast(frag, vr);
+    }
+    float bias_l2 = key_ok ? 0.f : -INFINITY;
+    if (HAS_BIAS && key_ok) {
+        const float x = P.bias.scalar(b, h0, key);
+        bias_l2 = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
+    }
+    // retire the compiler-visible loads before the first direct load
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        kf[c] = opaque(kf[c]);
+        vf[c] = opaque(vf[c]);
+    }
+    bias_l2 = opaque(bias_l2);
+    const float sl2 = P.scale * kLog2e;
+    const float cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
+    const float cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
+    const float lmul = SOFTCLAMP ? kLog2e : -1.f / P.scale;  // lse -> seed / log2 value
+    const bool need_dbias = G.dbias.ok();
+
+    f32x16_t dk[D / 32], dv[D / 32];
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+        dk[x] = zero16();
+        dv[x] = zero16();
+    }
+    float dbias = 0.f;
+
+    const int q_start = CAUSAL ? (kblk * kKvBK / BQ) * BQ : 0;
+    const int nt = P.nq > q_start ? (P.nq - q_start + BQ - 1) / BQ : 0;  // tiles per query head
+    const int total = nt * rep;
+
+    // direct loads: thread tid carries chunk n*256 + tid of a tile: row p / CPR, chunk p % CPR
+    const int qsn = (int)P.q.sn, osn = (int)G.dout.sn;
+    uint32_t offq[NL], offo[NL];
+#pragma unroll
+    for (int n = 0; n < NL; ++n) {
+        const int p = n * kBwdThreads + tid, r = p / CPR, ph = p % CPR;
+        offq[n] = (uint32_t)((r * qsn + (ph ^ swz_qt<D>(r)) * 8) * 2);
+        offo[n] = (uint32_t)((r * osn + (ph ^ swz_qt<D>(r)) * 8) * 2);
+    }
+    const uint32_t lds_q = lds_addr(sQ), lds_o = lds_addr(sO);
+    const uint32_t lds_l = lds_addr(&sLraw[0][0]), lds_d = lds_addr(&sDraw[0][0]);
+    const uint32_t qbytes = (uint32_t)(((int64_t)(P.nq - 1) * qsn + D) * 2);
+    const uint32_t obytes = (uint32_t)(((int64_t)(P.nq - 1) * osn + D) * 2);
+    auto issue = [&](int idx, int stage) __attribute__((always_inline)) {
+        const int h = h0 + idx / nt, q0 = q_start + (idx % nt) * BQ;
+        const srd_t rq = make_srd(P.q.row<T>(b, h, 0), qbytes);
+        const srd_t ro = make_srd(G.dout.row<T>(b, h, 0), obytes);
+        const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
+        const srd_t rl = make_srd(G.ws_lse + row0, (uint32_t)(P.nq * 4));
+        const srd_t rd = make_srd(G.ws_D + row0, (uint32_t)(P.nq * 4));
+        const uint32_t sq = lds_q + (uint32_t)(stage * ELEMS * 2), so = lds_o + (uint32_t)(stage * ELEMS * 2);
+#pragma unroll
+        for (int n = 0; n < NL; ++n) {
+            dma16(rq, sq + (uint32_t)((n * kBwdThreads + w * 64) * 16), offq[n] + (uint32_t)(q0 * qsn * 2));
+            dma16(ro, so + (uint32_t)((n * kBwdThreads + w * 64) * 16), offo[n] + (uint32_t)(q0 * osn * 2));
+        }
+        // lse and D rows: 256 bytes each, four lanes of every wave
+        if (lane < 4) {
+            const uint32_t o = (uint32_t)(w * 64 + 16 * lane);
+            dma16(rl, lds_l + (uint32_t)(stage * BQ * 4 + w * 64), o + (uint32_t)(q0 * 4));
+            dma16(rd, lds_d + (uint32_t)(stage * BQ * 4 + w * 64), o + (uint32_t)(q0 * 4));
+        }
+    };
+
+    // per-lane LDS element offsets: rows qb*32 + kcol, chunk 2c + hh (row reads) and rows
+    // 4*hh + j/4 (+16*t2 + 8*u + 32*qb), columns 32x + (lane & 31) (transposed reads)
+    int roff[D / 16];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) roff[c] = kcol * D + (((2 * c + hh) ^ swz_qt<D>(kcol)) * 8);
+    // (the swizzle depends on row bit 3, so the two 4-row runs u = 0, 1 get their own offsets)
+    int toff[2][D / 32];
+    {
+        const int g = lane >> 4, j = lane & 15;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int r = 8 * u + 4 * (g >> 1) + (j >> 2);
+#pragma unroll
+            for (int x = 0; x < D / 32; ++x) {
+                const int ch = 4 * x + 2 * (g & 1) + ((j & 3) >> 1);
+                toff[u][x] = r * D + ((ch ^ swz_qt<D>(r)) * 8) + 4 * (j & 1);
+            }
+        }
+    }
+    auto tr_frag = [&](const T* base, int row0, int x) __attribute__((always_inline)) -> frag {
+        const u32x2_t lo = lds_read_tr(base + row0 * D + toff[0][x]);
+        const u32x2_t hi = lds_read_tr(base + row0 * D + toff[1][x]);
+        const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
+        return __builtin_bit_cast(frag, v4);
+    };
+
+    if (total > 0) issue(0, 0);
+    if (total > 1) issue(1, 1);
+    int st = 0;
+    for (int idx = 0; idx < total; ++idx) {
+        if (idx + 1 < total) wait_vmcnt<NOPS>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        if (idx + 2 < total) issue(idx + 2, st == 0 ? 2 : st - 1);
+        const int q0 = q_start + (idx % nt) * BQ;
+        const T* Qt = sQ + st * ELEMS;
+        const T* Ot = sO + st * ELEMS;
+        // this wave's seeds for the tile: -lse/scale (log2-domain lse with softclamp), -D
+        sLw[w][lane] = sLraw[st][lane] * lmul;
+        sDw[w][lane] = -sDraw[st][lane];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qbase = q0 + qb * 32;
+            f32x16_t s, dp;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 lv = *reinterpret_cast<const float4*>(&sLw[w][qb * 32 + 8 * g + 4 * hh]);
+                const float4 dv4 = *reinterpret_cast<const float4*>(&sDw[w][qb * 32 + 8 * g + 4 * hh]);
+                if (SOFTCLAMP) {
+                    s[4 * g] = s[4 * g + 1] = s[4 * g + 2] = s[4 * g + 3] = 0.f;
+                } else {
+                    s[4 * g] = lv.x;
+                    s[4 * g + 1] = lv.y;
+                    s[4 * g + 2] = lv.z;
+                    s[4 * g + 3] = lv.w;
+                }
+                dp[4 * g] = dv4.x;
+                dp[4 * g + 1] = dv4.y;
+                dp[4 * g + 2] = dv4.z;
+                dp[4 * g + 3] = dv4.w;
+            }
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) {
+                const int off = qb * 32 * D + roff[c];
+                s = M::run(ld_frag<T>(Qt + off), kf[c], s);
+                dp = M::run(ld_frag<T>(Ot + off), vf[c], dp);
+            }
+            // P: register i holds query qbase + 8*(i/4) + 4*hh + (i%4) of the lane's key
+            float yv[16];
+            if (SOFTCLAMP) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 lv = *reinterpret_cast<const float4*>(&sLw[w][qb * 32 + 8 * g + 4 * hh]);
+                    const float L[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = 4 * g + r;
+                        yv[i] = tanhf(s[i] * cinv);
+                        s[i] = fast_exp2(yv[i] * cl2 + bias_l2 - L[r]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[i] = fast_exp2(fmaf(s[i], sl2, bias_l2));
+            }
+            // queries before the lane's key or past the last query: P = 0
+            if ((CAUSAL && qbase < kw0 + 32) || qbase + 32 > P.nq) {
+                keep_branch();
+                const int lo = CAUSAL ? key - qbase - 4 * hh : -(1 << 30);
+                const int hi = P.nq - qbase - 4 * hh;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int o = 8 * (i / 4) + (i % 4);
+                    if (o < lo || o >= hi) s[i] = 0.f;
+                }
+            }
+            // dS = P (dP - D); the key bias gradient is its column sum
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dp[i] *= s[i];
+            if (need_dbias) {
+                float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i += 2) {
+                    a0 += dp[i];
+                    a1 += dp[i + 1];
+                }
+                dbias += a0 + a1;
+            }
+            if (SOFTCLAMP)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) dp[i] *= (1.f - yv[i] * yv[i]);
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+                const frag pf = acc_to_frag<T>(s, t2);
+                const frag df = acc_to_frag<T>(dp, t2);
+#pragma unroll
+                for (int x = 0; x < D / 32; ++x) {
+                    dv[x] = M::run(tr_frag(Ot, qb * 32 + 16 * t2, x), pf, dv[x]);
+                    dk[x] = M::run(tr_frag(Qt, qb * 32 + 16 * t2, x), df, dk[x]);
+                }
+            }
+        }
+        st = st == 2 ? 0 : st + 1;
+    }
+
+    dbias += __shfl_xor(dbias, 32);
+    if (!key_ok) return;
+    T* dkrow = G.dk.wrow<T>(b, h0, key);
+    T* dvrow = G.dv.wrow<T>(b, h0, key);
+    const bool acc_k = (G.accumulate & PA_ACC_DK) != 0;
+    const bool acc_v = (G.accumulate & PA_ACC_DV) != 0;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = x * 32 + 8 * g + 4 * hh;
+            float kv[4], vv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                kv[r] = dk[x][4 * g + r] * P.scale + (acc_k ? to_f(dkrow[d + r]) : 0.f);
+                vv[r] = dv[x][4 * g + r] + (acc_v ? to_f(dvrow[d + r]) : 0.f);
+            }
+            u32x2_t pk;
+            pk[0] = pack2<T>(kv[0], kv[1]);
+            pk[1] = pack2<T>(kv[2], kv[3]);
+            *reinterpret_cast<u32x2_t*>(dkrow + d) = pk;
+            pk[0] = pack2<T>(vv[0], vv[1]);
+            pk[1] = pack2<T>(vv[2], vv[3]);
+            *reinterpret_cast<u32x2_t*>(dvrow + d) = pk;
+        }
+    }
+    if (hh == 0 && need_dbias) {
+        float* o = G.dbias.wrow<float>(b, h0, key);
+        *o = dbias + ((G.accumulate & PA_ACC_DBIAS) ? *o : 0.f);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // dQ
 
 constexpr int kDqBM = 128;  // queries per workgroup
@@ -570,13 +862,27 @@ bool mfma_bwd_supported(const GradDev& G, int dtype) {
     return true;
 }
 
+// the direct-to-LDS kernels address the query-side (or key-side) tensors of one head with
+// 32-bit byte offsets up to the end of the last tile
+static bool bwd_dma_ok(const GradDev& G) {
+    const PassDev& P = G.f;
+    const int64_t qspan = std::max(P.q.sn, G.dout.sn) * ((int64_t)P.nq + 2 * kKvBQ) * 2;
+    const int64_t kspan = std::max(P.k.sn, P.v.sn) * ((int64_t)P.nk + 2 * 64) * 2;
+    if (!(qspan < ((int64_t)1 << 31) && kspan < ((int64_t)1 << 31))) return false;
+    // lse / D rows travel in whole 16-byte chunks
+    return P.nq % 4 == 0;
+}
+
 template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_bwd_t(const GradDev& G, hipStream_t s) {
     const PassDev& P = G.f;
     {
         dim3 grid(((P.nk + kKvBK - 1) / kKvBK) * G.hk * P.batch);
         ProfScope ps("mfma_bwd_dkv", s);
-        hipLaunchKernelGGL((k_mfma_bwd_dkv<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
+        if (!V && PA_BWD_DMA && bwd_dma_ok(G))
+            hipLaunchKernelGGL((k_mfma_bwd_dkv_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
+        else
+            hipLaunchKernelGGL((k_mfma_bwd_dkv<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
     }
     {
         dim3 grid(((P.nq + kDqBM - 1) / kDqBM) * P.heads * P.batch);
