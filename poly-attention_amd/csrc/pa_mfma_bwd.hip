@@ -845,6 +845,235 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
 }
 
 // ---------------------------------------------------------------------------------------
+// Direct-to-LDS dQ (no value multiplier): K, V and the raw key bias of every key tile travel
+// HBM -> LDS by buffer_load ... lds, three stages deep.  K is read by rows (S^T = K Q^T) and
+// transposed (dQ^T += K^T dS^T) under the dual-pattern swizzle, V by rows only.  Each wave
+// converts the tile's key bias into accumulator seeds (bias / scale; log2 domain with
+// softclamp), so that P^T = exp2(scale*log2e*S^T - lse*log2e).
+
+template <typename T, int D, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS>
+__global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq_dma(GradDev G) {
+    using M = Mma<T>;
+    typedef typename M::frag frag;
+    constexpr int BN = kDqBN, CPR = D / 8, ELEMS = BN * D;
+    constexpr int NL = BN * CPR / kBwdThreads;
+    constexpr int NOPS = 2 * NL + (HAS_BIAS ? 1 : 0);
+    constexpr bool FOLD = HAS_BIAS && !SOFTCLAMP;
+    static_assert(BN * CPR % kBwdThreads == 0, "tile must split evenly over the threads");
+    const PassDev& P = G.f;
+    __shared__ __attribute__((aligned(16))) T sK[kKvStages * ELEMS];
+    __shared__ __attribute__((aligned(16))) T sV[kKvStages * ELEMS];
+    __shared__ __attribute__((aligned(16))) float sBraw[kKvStages][BN];
+    __shared__ __attribute__((aligned(16))) float sBw[4][BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const int hh = lane >> 5, kcol = lane & 31;
+    const int nqb = (P.nq + kDqBM - 1) / kDqBM;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int qblk = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;  // heaviest first
+    const int h = (lid / nqb) % P.heads, b = (lid / nqb) / P.heads;
+    const int qw0 = qblk * kDqBM + w * 32;
+    const int qi = qw0 + kcol;
+    const bool q_ok = qi < P.nq;
+
+    frag qf[D / 16], of[D / 16];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        u32x4_t qr = {0u, 0u, 0u, 0u}, orr = {0u, 0u, 0u, 0u};
+        if (q_ok) {
+            qr = *reinterpret_cast<const u32x4_t*>(P.q.row<T>(b, h, qi) + c * 16 + 8 * hh);
+            orr = *reinterpret_cast<const u32x4_t*>(G.dout.row<T>(b, h, qi) + c * 16 + 8 * hh);
+        }
+        qf[c] = __builtin_bit_cast(frag, qr);
+        of[c] = __builtin_bit_cast(frag, orr);
+    }
+    const int64_t row = ((int64_t)b * P.heads + h) * P.nq + (q_ok ? qi : 0);
+    float lse_l2 = q_ok ? G.ws_lse[row] * kLog2e : INFINITY;
+    float dpi = q_ok ? G.ws_D[row] : 0.f;
+    // retire the compiler-visible loads before the first direct load
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        qf[c] = opaque(qf[c]);
+        of[c] = opaque(of[c]);
+    }
+    lse_l2 = opaque(lse_l2);
+    dpi = opaque(dpi);
+    const float sl2 = P.scale * kLog2e;
+    const float cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
+    const float cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
+
+    f32x16_t dq[D / 32];
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) dq[x] = zero16();
+
+    const int ksn = (int)P.k.sn, vsn = (int)P.v.sn;
+    const srd_t rk = make_srd(P.k.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * ksn + D) * 2));
+    const srd_t rv = make_srd(P.v.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * vsn + D) * 2));
+    const int bes = P.bias.dtype == PA_F32 ? 4 : 2;
+    const float bmul = FOLD ? 1.f / P.scale : kLog2e;
+    srd_t rb = {0, 0, 0, 0};
+    if (HAS_BIAS) rb = make_srd(P.bias.p + P.bias.idx(b, h, 0) * bes, (uint32_t)(P.nk * bes));
+    uint32_t offk[NL], offv[NL];
+#pragma unroll
+    for (int n = 0; n < NL; ++n) {
+        const int p = n * kBwdThreads + tid, r = p / CPR, ph = p % CPR;
+        offk[n] = (uint32_t)((r * ksn + (ph ^ swz_qt<D>(r)) * 8) * 2);
+        offv[n] = (uint32_t)((r * vsn + (ph ^ swz_qt<D>(r)) * 8) * 2);
+    }
+    const int bq = BN * bes / 4;  // bias bytes per wave
+    const uint32_t lds_k = lds_addr(sK), lds_v = lds_addr(sV), lds_b = lds_addr(&sBraw[0][0]);
+    auto issue = [&](int j0, int stage) __attribute__((always_inline)) {
+        const uint32_t tk = (uint32_t)(j0 * ksn * 2), tv = (uint32_t)(j0 * vsn * 2);
+        const uint32_t kd = lds_k + (uint32_t)(stage * ELEMS * 2), vd = lds_v + (uint32_t)(stage * ELEMS * 2);
+#pragma unroll
+        for (int n = 0; n < NL; ++n) {
+            dma16(rk, kd + (uint32_t)((n * kBwdThreads + w * 64) * 16), offk[n] + tk);
+            dma16(rv, vd + (uint32_t)((n * kBwdThreads + w * 64) * 16), offv[n] + tv);
+        }
+        if (HAS_BIAS && 16 * lane < bq)
+            dma16(rb, lds_b + (uint32_t)(stage * BN * 4 + w * bq), (uint32_t)(w * bq + 16 * lane + j0 * bes));
+    };
+
+    int roff[D / 16];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) roff[c] = kcol * D + (((2 * c + hh) ^ swz_qt<D>(kcol)) * 8);
+    int toff[2][D / 32];
+    {
+        const int g = lane >> 4, j = lane & 15;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int r = 8 * u + 4 * (g >> 1) + (j >> 2);
+#pragma unroll
+            for (int x = 0; x < D / 32; ++x) {
+                const int ch = 4 * x + 2 * (g & 1) + ((j & 3) >> 1);
+                toff[u][x] = r * D + ((ch ^ swz_qt<D>(r)) * 8) + 4 * (j & 1);
+            }
+        }
+    }
+
+    const int kend = CAUSAL ? min(P.nk, qblk * kDqBM + kDqBM) : P.nk;
+    const int ntiles = (kend + BN - 1) / BN;
+    const int nact = CAUSAL ? min(ntiles, (qw0 + 31) / BN + 1) : ntiles;
+    if (ntiles > 0) issue(0, 0);
+    if (ntiles > 1) issue(BN, 1);
+    int st = 0;
+    auto enter = [&](int t) __attribute__((always_inline)) {
+        if (t + 1 < ntiles) wait_vmcnt<NOPS>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        if (t + 2 < ntiles) issue((t + 2) * BN, st == 0 ? 2 : st - 1);
+    };
+    for (int t = 0; t < nact; ++t) {
+        const int j0 = t * BN;
+        enter(t);
+        const T* Kt = sK + st * ELEMS;
+        const T* Vt = sV + st * ELEMS;
+        if (HAS_BIAS) {
+            float x;
+            if (bes == 4) x = sBraw[st][lane];
+            else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
+            sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x16_t s = zero16(), dp = zero16();
+            if (FOLD) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 bb = *reinterpret_cast<const float4*>(&sBw[w][kb * 32 + 8 * g + 4 * hh]);
+                    s[4 * g] = bb.x;
+                    s[4 * g + 1] = bb.y;
+                    s[4 * g + 2] = bb.z;
+                    s[4 * g + 3] = bb.w;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) {
+                const int off = kb * 32 * D + roff[c];
+                s = M::run(ld_frag<T>(Kt + off), qf[c], s);
+                dp = M::run(ld_frag<T>(Vt + off), of[c], dp);
+            }
+            // P^T: register i holds key j0 + kb*32 + 8*(i/4) + 4*hh + (i%4) of the lane's query
+            float yv[16];
+            if (SOFTCLAMP) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+                    if (HAS_BIAS) {
+                        const float4 bb = *reinterpret_cast<const float4*>(&sBw[w][kb * 32 + 8 * g + 4 * hh]);
+                        bv[0] = bb.x;
+                        bv[1] = bb.y;
+                        bv[2] = bb.z;
+                        bv[3] = bb.w;
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = 4 * g + r;
+                        yv[i] = tanhf(s[i] * cinv);
+                        s[i] = fast_exp2(yv[i] * cl2 + bv[r] - lse_l2);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[i] = fast_exp2(fmaf(s[i], sl2, -lse_l2));
+            }
+            // keys after the lane's query or past the last key: P = 0
+            const int kb0 = j0 + kb * 32;
+            if ((CAUSAL && kb0 + 31 > qw0) || kb0 + 32 > P.nk) {
+                keep_branch();
+                int lim = P.nk - 1 - kb0;
+                if (CAUSAL) lim = min(lim, qi - kb0);
+                lim -= 4 * hh;
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (8 * (i / 4) + (i % 4) > lim) s[i] = 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float dsv = s[i] * (dp[i] - dpi);
+                if (SOFTCLAMP) dsv *= (1.f - yv[i] * yv[i]);
+                s[i] = dsv;
+            }
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+                const frag df = acc_to_frag<T>(s, t2);
+#pragma unroll
+                for (int x = 0; x < D / 32; ++x) {
+                    const int row0 = kb * 32 + 16 * t2;
+                    const u32x2_t lo = lds_read_tr(Kt + row0 * D + toff[0][x]);
+                    const u32x2_t hi = lds_read_tr(Kt + row0 * D + toff[1][x]);
+                    const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
+                    dq[x] = M::run(__builtin_bit_cast(frag, v4), df, dq[x]);
+                }
+            }
+        }
+        st = st == 2 ? 0 : st + 1;
+    }
+    for (int t = nact; t < ntiles; ++t) {
+        enter(t);
+        st = st == 2 ? 0 : st + 1;
+    }
+
+    if (!q_ok) return;
+    T* dqrow = G.dq.wrow<T>(b, h, qi);
+    const bool acc = (G.accumulate & PA_ACC_DQ) != 0;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = x * 32 + 8 * g + 4 * hh;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = dq[x][4 * g + r] * P.scale + (acc ? to_f(dqrow[d + r]) : 0.f);
+            u32x2_t pk;
+            pk[0] = pack2<T>(v[0], v[1]);
+            pk[1] = pack2<T>(v[2], v[3]);
+            *reinterpret_cast<u32x2_t*>(dqrow + d) = pk;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 
 bool mfma_bwd_supported(const GradDev& G, int dtype) {
     const PassDev& P = G.f;
@@ -873,6 +1102,20 @@ static bool bwd_dma_ok(const GradDev& G) {
     return P.nq % 4 == 0;
 }
 
+// the direct-to-LDS dQ kernel also reads the key bias as one contiguous row of whole chunks
+static bool bwd_dq_dma_ok(const GradDev& G) {
+    const PassDev& P = G.f;
+    const int64_t kspan = std::max(P.k.sn, P.v.sn) * ((int64_t)P.nk + 2 * kDqBN) * 2;
+    if (!(kspan < ((int64_t)1 << 31))) return false;
+    if (P.bias.ok()) {
+        const int64_t es = P.bias.dtype == PA_F32 ? 4 : 2;
+        if (P.bias.sn != 1) return false;
+        if ((uintptr_t)P.bias.p % 16 != 0 || (P.bias.sh * es) % 16 != 0 || (P.bias.sb * es) % 16 != 0) return false;
+        if ((P.nk * es) % 16 != 0) return false;
+    }
+    return true;
+}
+
 template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_bwd_t(const GradDev& G, hipStream_t s) {
     const PassDev& P = G.f;
@@ -887,7 +1130,10 @@ static void launch_bwd_t(const GradDev& G, hipStream_t s) {
     {
         dim3 grid(((P.nq + kDqBM - 1) / kDqBM) * P.heads * P.batch);
         ProfScope ps("mfma_bwd_dq", s);
-        hipLaunchKernelGGL((k_mfma_bwd_dq<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
+        if (!V && PA_BWD_DMA && bwd_dq_dma_ok(G))
+            hipLaunchKernelGGL((k_mfma_bwd_dq_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
+        else
+            hipLaunchKernelGGL((k_mfma_bwd_dq<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
     }
 }
 
