@@ -488,10 +488,9 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
         // this wave's seeds for the tile: -lse/scale (log2-domain lse with softclamp), -D
         sLw[w][lane] = sLraw[st][lane] * lmul;
         sDw[w][lane] = -sDraw[st][lane];
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const int qbase = q0 + qb * 32;
-            f32x16_t s, dp;
+        // the two 32-query blocks in a software pipeline: the MFMAs of one block are issued in
+        // the same basic block as the VALU work of the other
+        auto scores = [&](int qb, f32x16_t& s, f32x16_t& dp) __attribute__((always_inline)) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const float4 lv = *reinterpret_cast<const float4*>(&sLw[w][qb * 32 + 8 * g + 4 * hh]);
@@ -515,7 +514,25 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
                 s = M::run(ld_frag<T>(Qt + off), kf[c], s);
                 dp = M::run(ld_frag<T>(Ot + off), vf[c], dp);
             }
-            // P: register i holds query qbase + 8*(i/4) + 4*hh + (i%4) of the lane's key
+        };
+        // queries before the lane's key or past the last query: scores -> -inf (P = 0).
+        // Register i holds query qbase + 8*(i/4) + 4*hh + (i%4) of the lane's key.
+        auto mask = [&](int qb, f32x16_t& s) __attribute__((always_inline)) {
+            const int qbase = q0 + qb * 32;
+            if ((CAUSAL && qbase < kw0 + 32) || qbase + 32 > P.nq) {
+                keep_branch();
+                const int lo = CAUSAL ? key - qbase - 4 * hh : -(1 << 30);
+                const int hi = P.nq - qbase - 4 * hh;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int o = 8 * (i / 4) + (i % 4);
+                    if (o < lo || o >= hi) s[i] = -INFINITY;
+                }
+            }
+        };
+        // P, dS = P (dP - D) (the key bias gradient is its column sum), packed as B operands
+        auto grads = [&](int qb, f32x16_t& s, f32x16_t& dp, frag (&pf)[2], frag (&df)[2])
+                         __attribute__((always_inline)) {
             float yv[16];
             if (SOFTCLAMP) {
 #pragma unroll
@@ -525,26 +542,14 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = 4 * g + r;
-                        yv[i] = tanhf(s[i] * cinv);
-                        s[i] = fast_exp2(yv[i] * cl2 + bias_l2 - L[r]);
+                        yv[i] = s[i] == -INFINITY ? 1.f : tanhf(s[i] * cinv);
+                        s[i] = s[i] == -INFINITY ? 0.f : fast_exp2(yv[i] * cl2 + bias_l2 - L[r]);
                     }
                 }
             } else {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) s[i] = fast_exp2(fmaf(s[i], sl2, bias_l2));
             }
-            // queries before the lane's key or past the last query: P = 0
-            if ((CAUSAL && qbase < kw0 + 32) || qbase + 32 > P.nq) {
-                keep_branch();
-                const int lo = CAUSAL ? key - qbase - 4 * hh : -(1 << 30);
-                const int hi = P.nq - qbase - 4 * hh;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int o = 8 * (i / 4) + (i % 4);
-                    if (o < lo || o >= hi) s[i] = 0.f;
-                }
-            }
-            // dS = P (dP - D); the key bias gradient is its column sum
 #pragma unroll
             for (int i = 0; i < 16; ++i) dp[i] *= s[i];
             if (need_dbias) {
@@ -561,15 +566,29 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
                 for (int i = 0; i < 16; ++i) dp[i] *= (1.f - yv[i] * yv[i]);
 #pragma unroll
             for (int t2 = 0; t2 < 2; ++t2) {
-                const frag pf = acc_to_frag<T>(s, t2);
-                const frag df = acc_to_frag<T>(dp, t2);
+                pf[t2] = acc_to_frag<T>(s, t2);
+                df[t2] = acc_to_frag<T>(dp, t2);
+            }
+        };
+        auto accumulate = [&](int qb, const frag (&pf)[2], const frag (&df)[2]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
                 for (int x = 0; x < D / 32; ++x) {
-                    dv[x] = M::run(tr_frag(Ot, qb * 32 + 16 * t2, x), pf, dv[x]);
-                    dk[x] = M::run(tr_frag(Qt, qb * 32 + 16 * t2, x), df, dk[x]);
+                    dv[x] = M::run(tr_frag(Ot, qb * 32 + 16 * t2, x), pf[t2], dv[x]);
+                    dk[x] = M::run(tr_frag(Qt, qb * 32 + 16 * t2, x), df[t2], dk[x]);
                 }
-            }
-        }
+        };
+        f32x16_t s0, dp0, s1, dp1;
+        frag pf0[2], df0[2], pf1[2], df1[2];
+        scores(0, s0, dp0);
+        mask(0, s0);
+        scores(1, s1, dp1);
+        grads(0, s0, dp0, pf0, df0);
+        mask(1, s1);
+        accumulate(0, pf0, df0);
+        grads(1, s1, dp1, pf1, df1);
+        accumulate(1, pf1, df1);
         st = st == 2 ? 0 : st + 1;
     }
 
