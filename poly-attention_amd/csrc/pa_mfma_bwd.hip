@@ -993,9 +993,10 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq_dm
             else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
             sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
         }
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            f32x16_t s = zero16(), dp = zero16();
+        // the two 32-key blocks in a software pipeline (MFMAs of one beside the VALU of the other)
+        auto scores = [&](int kb, f32x16_t& s, f32x16_t& dp) __attribute__((always_inline)) {
+            s = zero16();
+            dp = zero16();
             if (FOLD) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
@@ -1012,7 +1013,23 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq_dm
                 s = M::run(ld_frag<T>(Kt + off), qf[c], s);
                 dp = M::run(ld_frag<T>(Vt + off), of[c], dp);
             }
-            // P^T: register i holds key j0 + kb*32 + 8*(i/4) + 4*hh + (i%4) of the lane's query
+        };
+        // keys after the lane's query or past the last key: scores -> -inf (P = 0).  Register i
+        // holds key j0 + kb*32 + 8*(i/4) + 4*hh + (i%4) of the lane's query.
+        auto mask = [&](int kb, f32x16_t& s) __attribute__((always_inline)) {
+            const int kb0 = j0 + kb * 32;
+            if ((CAUSAL && kb0 + 31 > qw0) || kb0 + 32 > P.nk) {
+                keep_branch();
+                int lim = P.nk - 1 - kb0;
+                if (CAUSAL) lim = min(lim, qi - kb0);
+                lim -= 4 * hh;
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (8 * (i / 4) + (i % 4) > lim) s[i] = -INFINITY;
+            }
+        };
+        // dS^T = P^T (dP^T - D), packed as B operands
+        auto grads = [&](int kb, f32x16_t& s, const f32x16_t& dp, frag (&df)[2]) __attribute__((always_inline)) {
             float yv[16];
             if (SOFTCLAMP) {
 #pragma unroll
@@ -1028,24 +1045,13 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq_dm
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = 4 * g + r;
-                        yv[i] = tanhf(s[i] * cinv);
-                        s[i] = fast_exp2(yv[i] * cl2 + bv[r] - lse_l2);
+                        yv[i] = s[i] == -INFINITY ? 1.f : tanhf(s[i] * cinv);
+                        s[i] = s[i] == -INFINITY ? 0.f : fast_exp2(yv[i] * cl2 + bv[r] - lse_l2);
                     }
                 }
             } else {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) s[i] = fast_exp2(fmaf(s[i], sl2, -lse_l2));
-            }
-            // keys after the lane's query or past the last key: P = 0
-            const int kb0 = j0 + kb * 32;
-            if ((CAUSAL && kb0 + 31 > qw0) || kb0 + 32 > P.nk) {
-                keep_branch();
-                int lim = P.nk - 1 - kb0;
-                if (CAUSAL) lim = min(lim, qi - kb0);
-                lim -= 4 * hh;
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (8 * (i / 4) + (i % 4) > lim) s[i] = 0.f;
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -1054,18 +1060,30 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq_dm
                 s[i] = dsv;
             }
 #pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2) {
-                const frag df = acc_to_frag<T>(s, t2);
+            for (int t2 = 0; t2 < 2; ++t2) df[t2] = acc_to_frag<T>(s, t2);
+        };
+        auto accumulate = [&](int kb, const frag (&df)[2]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
                 for (int x = 0; x < D / 32; ++x) {
                     const int row0 = kb * 32 + 16 * t2;
                     const u32x2_t lo = lds_read_tr(Kt + row0 * D + toff[0][x]);
                     const u32x2_t hi = lds_read_tr(Kt + row0 * D + toff[1][x]);
                     const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
-                    dq[x] = M::run(__builtin_bit_cast(frag, v4), df, dq[x]);
+                    dq[x] = M::run(__builtin_bit_cast(frag, v4), df[t2], dq[x]);
                 }
-            }
-        }
+        };
+        f32x16_t s0, dp0, s1, dp1;
+        frag df0[2], df1[2];
+        scores(0, s0, dp0);
+        mask(0, s0);
+        scores(1, s1, dp1);
+        grads(0, s0, dp0, df0);
+        mask(1, s1);
+        accumulate(0, df0);
+        grads(1, s1, dp1, df1);
+        accumulate(1, df1);
         st = st == 2 ? 0 : st + 1;
     }
     for (int t = nact; t < ntiles; ++t) {
