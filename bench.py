@@ -10,10 +10,13 @@ backward (all four input gradients) for upstream grad ~ N(0,1) (seed 2).
 
 Printed: ONE JSON line with the headline metric (core TFLOP/s over the algorithmic flops of
 the step), the live per-kernel roofline of the dominant kernel (HIP events on its launch
-stream), the CPU oracle baseline timed on this host, the full module step time, and the
-config-5 GQA decode step (GB/s against 8 TB/s).
+stream), the CPU oracle baseline timed on this host, the full module step time, and, as
+extra fields, the other GPU configs of BASELINE.json: config 5 (GQA decode step, GB/s
+against 8 TB/s), config 3 (PolyViT forward, images/s and the attention core's share) and
+config 4 (order-3 causal decode loop through a PolyLM-style stack, tokens/s).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+                    [--no-module] [--no-vit] [--no-lm]
 """
 
 from __future__ import annotations
@@ -200,6 +203,235 @@ def decode_bench(dev, steps, warmup):
 
 
 # ---------------------------------------------------------------------------------------
+# config 3: PolyViT forward (poly_vit.py:56-95 with BASELINE configs[2]'s sizes)
+
+
+def _linear_flops(model, run):
+    """2 * rows * in * out summed over every nn.Linear call made by ``run()``."""
+    total = [0]
+
+    def hook(mod, inp, out):
+        total[0] += 2 * (inp[0].numel() // mod.in_features) * mod.in_features * mod.out_features
+
+    hs = [mod.register_forward_hook(hook) for mod in model.modules()
+          if isinstance(mod, torch.nn.Linear)]
+    try:
+        run()
+    finally:
+        for h in hs:
+            h.remove()
+    return total[0]
+
+
+def make_vit(dev, dtype, batch):
+    from poly_attention import PolyViT
+
+    torch.manual_seed(0)
+    m = PolyViT(image_size=256, patch_size=32, num_classes=1000, dim=1024, depth=6, heads=16,
+                mlp_dim=2048, order=2).to(dev, dtype).eval()
+    g = torch.Generator(device="cpu").manual_seed(1)
+    img = torch.randn(batch, 3, 256, 256, generator=g).to(dev, dtype)
+    return m, img
+
+
+def vit_bench(dev, steps, warmup, cpu):
+    batch = 64
+    m, img = make_vit(dev, torch.bfloat16, batch)
+    with torch.no_grad():
+        proj_flops = _linear_flops(m, lambda: m(img))
+        ms = time_steps(lambda: m(img), steps, warmup)
+        with _lib().KernelProfile() as prof:
+            for _ in range(steps):
+                m(img)
+    npatch = (256 // 32) ** 2
+    core_flops = 6 * 2 * core_flops_fwd(batch, 16, npatch, npatch, 64, False)
+    core_ms = sum(t for _, t in prof.times.values()) / steps
+    res = {
+        "workload": "PolyViT fwd (image 256, patch 32, dim 1024, depth 6, heads 16, mlp 2048, "
+                    "order 2, 1000 classes), batch 64 bf16, inference (BASELINE configs[2])",
+        "ms_per_step": round(ms, 4),
+        "images_per_s": round(batch / (ms / 1e3), 1),
+        "flops_per_step": proj_flops + core_flops,
+        "TFLOP_per_s": round((proj_flops + core_flops) / (ms / 1e3) / 1e12, 2),
+        "core_flops_per_step": core_flops,
+        "core_ms_per_step": round(core_ms, 4),
+        "core_share_of_time": round(core_ms / ms, 4),
+        "kernels": {k: {"launches": n // steps, "avg_ms": round(t / n, 4)}
+                    for k, (n, t) in prof.times.items()},
+    }
+    del m, img
+    torch.cuda.empty_cache()
+    if cpu:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        cb = 8
+        mc, imgc = make_vit(torch.device("cpu"), torch.float32, cb)
+        with torch.no_grad():
+            mc(imgc)
+            times = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                mc(imgc)
+                times.append(time.perf_counter() - t0)
+        med = sorted(times)[1]
+        res["cpu_baseline"] = {
+            "value": round(cb / med, 2), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"the same PolyViT in fp32 on this host (eager attention, the reference's "
+                      f"CPU path), batch {cb}, median of 3 after 1 warm-up, {med * 1e3:.0f} ms each"}
+    return res
+
+
+# ---------------------------------------------------------------------------------------
+# config 4: order-3 causal decode with the KV cache, through a PolyLM-style stack
+# (train_enwik8.py:112-177: token embedding, external RoPE, [RMSNorm -> NPolyAttention ->
+# residual, RMSNorm -> FeedForward -> residual] x depth, RMSNorm, logits)
+
+
+class _Block(torch.nn.Module):
+    """train_enwik8.py:112-127 with order 3 (NPolyAttention) and x-transformers' default
+    FeedForward(dim): Linear(dim, 4 dim) -> GELU -> Linear(4 dim, dim)."""
+
+    def __init__(self, dim, heads, dim_head, order):
+        super().__init__()
+        from poly_attention import NPolyAttention
+
+        self.attn = NPolyAttention(dim, order=order, heads=heads, dim_head=dim_head, causal=True)
+        self.norm1 = torch.nn.RMSNorm(dim)
+        self.norm2 = torch.nn.RMSNorm(dim)
+        self.ffn = torch.nn.Sequential(torch.nn.Linear(dim, 4 * dim), torch.nn.GELU(),
+                                       torch.nn.Linear(4 * dim, dim))
+
+    def forward(self, x, rotary_pos_emb=None, cache=None):
+        attn_out, new_cache = self.attn(self.norm1(x), rotary_pos_emb=rotary_pos_emb,
+                                        cache=cache, return_cache=True)
+        x = x + attn_out
+        x = x + self.ffn(self.norm2(x))
+        return x, new_cache
+
+
+class _PolyLM(torch.nn.Module):
+    """train_enwik8.py:129-177 (inference branch)."""
+
+    def __init__(self, num_tokens=256, dim=1024, depth=8, heads=16, dim_head=64, order=3):
+        super().__init__()
+        from poly_attention.rotary import RotaryEmbedding
+
+        self.token_emb = torch.nn.Embedding(num_tokens, dim)
+        self.rotary_emb = RotaryEmbedding(dim_head)
+        self.layers = torch.nn.ModuleList([_Block(dim, heads, dim_head, order)
+                                           for _ in range(depth)])
+        self.norm = torch.nn.RMSNorm(dim)
+        self.to_logits = torch.nn.Linear(dim, num_tokens, bias=False)
+
+    def forward(self, x, cache=None):
+        seq_len = x.shape[1]
+        past = 0 if cache is None else cache[1]
+        layer_caches = [None] * len(self.layers) if cache is None else cache[0]
+        pos = torch.arange(seq_len, device=x.device) + past
+        rot = self.rotary_emb(pos)
+        x = self.token_emb(x)
+        new = []
+        for layer, lc in zip(self.layers, layer_caches):
+            x, nc = layer(x, rotary_pos_emb=rot, cache=lc)
+            new.append(nc)
+        return self.to_logits(self.norm(x)), (new, past + seq_len)
+
+
+def _greedy(lm, prompt, steps):
+    """Prefill ``prompt`` with return_cache, then ``steps`` greedy single-token steps
+    (train_enwik8.py:85-108 with argmax in place of the gumbel top-k sample)."""
+    logits, cache = lm(prompt)
+    tok = logits[:, -1].argmax(-1, keepdim=True)
+    out = [tok]
+    for _ in range(steps - 1):
+        logits, cache = lm(tok, cache)
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        out.append(tok)
+    return torch.cat(out, dim=1)
+
+
+def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8):
+    depth, heads, dh, dim = 8, 16, 64, 1024
+    torch.manual_seed(0)
+    lm = _PolyLM(dim=dim, depth=depth, heads=heads, dim_head=dh).to(dev, torch.bfloat16).eval()
+    g = torch.Generator(device="cpu").manual_seed(1)
+    prompt = torch.randint(0, 256, (batch, prefill), generator=g).to(dev)
+    with torch.no_grad():
+        _greedy(lm, prompt[:, :256], 8)  # warm-up (allocator, kernels)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits, cache = lm(prompt)
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            logits, cache = lm(tok, cache)
+            tok = logits[:, -1].argmax(-1, keepdim=True)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        # kernel times of a few more steps (events per launch perturb the loop's own timing)
+        with _lib().KernelProfile() as prof:
+            for _ in range(16):
+                logits, cache = lm(tok, cache)
+                tok = logits[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+    decode_s = t2 - t1
+    # cache bytes per step and layer (order 3, kv heads = heads): q2, q3, v2, v3 ... every
+    # cached tensor read once: (2*order-1) kv tensors + (order-1) msg (bf16) and lse (fp32)
+    per_tok = (2 * 3 - 1) * heads * dh * 2 + (3 - 1) * heads * (dh * 2 + 4)
+    cache_bytes = sum(batch * depth * per_tok * (prefill + 1 + s) for s in range(steps))
+    weight_bytes = 2 * sum(p.numel() for n, p in lm.named_parameters()
+                           if not n.startswith("token_emb") and not n.endswith("freqs"))
+    all_bytes = cache_bytes + steps * weight_bytes
+    kern_ms = sum(t for _, t in prof.times.values()) / 16
+    res = {
+        "workload": f"order-3 causal decode, PolyLM-style stack depth {depth}, dim {dim}, heads "
+                    f"{heads}, dim_head {dh}, batch {batch}, prefill {prefill} tokens, {steps} "
+                    f"greedy steps, bf16 weights and cache, fp32 lse (BASELINE configs[3])",
+        "prefill_ms": round((t1 - t0) * 1e3, 2),
+        "ms_per_step": round(decode_s * 1e3 / steps, 4),
+        "tokens_per_s": round(batch * steps / decode_s, 1),
+        "cache_GB_per_step_mean": round(cache_bytes / steps / 1e9, 4),
+        "GB_per_s": round(all_bytes / decode_s / 1e9, 1),
+        "frac_hbm_peak": round(all_bytes / decode_s / 1e9 / PEAK_HBM_GBS, 4),
+        "attn_kernel_ms_per_step": round(kern_ms, 4),
+        "attn_kernel_GB_per_s": round(batch * depth * per_tok * (prefill + steps + 8)
+                                      / (kern_ms / 1e3) / 1e9, 1),
+        "kernels": {k: {"launches": n // 16, "avg_ms": round(t / n, 4)}
+                    for k, (n, t) in prof.times.items()},
+    }
+    del lm, cache, logits
+    torch.cuda.empty_cache()
+    if cpu:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        torch.manual_seed(0)
+        lmc = _PolyLM(dim=dim, depth=depth, heads=heads, dim_head=dh).eval()
+        cb, cprefill, csteps = 1, 512, 8
+        with torch.no_grad():
+            logits, cache = lmc(prompt[:cb, :cprefill].cpu())
+            tok = logits[:, -1].argmax(-1, keepdim=True)
+            t0 = time.perf_counter()
+            for _ in range(csteps):
+                logits, cache = lmc(tok, cache)
+                tok = logits[:, -1].argmax(-1, keepdim=True)
+            dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {
+            "value": round(cb * csteps / dt, 2), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"the same stack in fp32 on this host (eager cached steps, the reference's "
+                      f"CPU path), batch {cb}, prefill {cprefill}, {csteps} steps, "
+                      f"{dt / csteps * 1e3:.0f} ms per step"}
+    return res
+
+
+def _lib():
+    from poly_attention import _lib as lib
+
+    return lib
+
+
+# ---------------------------------------------------------------------------------------
 # CPU baseline: the oracle (the reference's eager math) on this host's cores
 
 
@@ -261,6 +493,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-module", action="store_true")
+    ap.add_argument("--no-vit", action="store_true", help="skip config 3 (PolyViT forward)")
+    ap.add_argument("--no-lm", action="store_true", help="skip config 4 (order-3 decode loop)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one plain 256 MiB device copy (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -321,6 +555,16 @@ def main():
         decode = decode_bench(dev, args.steps, args.warmup)
         log(f"[bench] decode {decode}")
 
+    vit = None
+    if not args.no_vit:
+        vit = vit_bench(dev, args.steps, args.warmup, cpu=not args.no_cpu)
+        log(f"[bench] config 3 {vit}")
+
+    lm = None
+    if not args.no_lm:
+        lm = decode_order3_bench(dev, cpu=not args.no_cpu)
+        log(f"[bench] config 4 {lm}")
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline()
@@ -353,6 +597,8 @@ def main():
         "module_ms_per_step": round(module_ms, 4) if module_ms else None,
         "cpu_baseline": cpu,
         "decode": decode,
+        "vit": vit,
+        "decode_order3": lm,
     }
     print(json.dumps(line), flush=True)
 
