@@ -323,18 +323,20 @@ class _PolyLM(torch.nn.Module):
         self.norm = torch.nn.RMSNorm(dim)
         self.to_logits = torch.nn.Linear(dim, num_tokens, bias=False)
 
-    def forward(self, x, cache=None):
+    def forward(self, x, cache=None, pos=None):
+        """``pos``: the positions as a device tensor (a captured step has no host count)."""
         seq_len = x.shape[1]
         past = 0 if cache is None else cache[1]
         layer_caches = [None] * len(self.layers) if cache is None else cache[0]
-        pos = torch.arange(seq_len, device=x.device) + past
+        if pos is None:
+            pos = torch.arange(seq_len, device=x.device) + past
         rot = self.rotary_emb(pos)
         x = self.token_emb(x)
         new = []
         for layer, lc in zip(self.layers, layer_caches):
             x, nc = layer(x, rotary_pos_emb=rot, cache=lc)
             new.append(nc)
-        return self.to_logits(self.norm(x)), (new, past + seq_len)
+        return self.to_logits(self.norm(x)), (new, None if past is None else past + seq_len)
 
 
 def _greedy(lm, prompt, steps):
@@ -350,7 +352,12 @@ def _greedy(lm, prompt, steps):
     return torch.cat(out, dim=1)
 
 
-def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8):
+def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2):
+    """Config 4 two ways: (1) the reference's calling pattern, one eager module call per
+    token with the growing cache tuples; (2) the same steps on StaticCaches, one decode step
+    (all layers, logits, argmax) captured into a HIP graph and replayed per token."""
+    from poly_attention import StaticCache
+
     depth, heads, dh, dim = 8, 16, 64, 1024
     torch.manual_seed(0)
     lm = _PolyLM(dim=dim, depth=depth, heads=heads, dim_head=dh).to(dev, torch.bfloat16).eval()
@@ -359,48 +366,108 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8):
     with torch.no_grad():
         _greedy(lm, prompt[:, :256], 8)  # warm-up (allocator, kernels)
         torch.cuda.synchronize()
+        # (1) eager steps, tuple caches
         t0 = time.perf_counter()
         logits, cache = lm(prompt)
         tok = logits[:, -1].argmax(-1, keepdim=True)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
+        toks_eager = [tok]
         for _ in range(steps):
             logits, cache = lm(tok, cache)
             tok = logits[:, -1].argmax(-1, keepdim=True)
+            toks_eager.append(tok)
         torch.cuda.synchronize()
         t2 = time.perf_counter()
-        # kernel times of a few more steps (events per launch perturb the loop's own timing)
+        toks_eager = torch.cat(toks_eager, dim=1)
+        del cache, logits
+        # (2) StaticCache + one captured step per token
+        logits, (lcs, _) = lm(prompt)
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        more = 16  # extra steps, profiled after the timed loop
+        scs = [StaticCache(c, capacity=prefill + steps + more + 1) for c in lcs]
+        del lcs, logits
+        tok_buf = tok.clone()
+        pos_buf = torch.full((1,), prefill, dtype=torch.int64, device=dev)
+        rec = torch.zeros(batch, steps + more + 1, dtype=torch.int64, device=dev)
+        rec[:, :1] = tok
+
+        def step():
+            lg, _ = lm(tok_buf, (scs, None), pos=pos_buf)
+            nxt = lg[:, -1].argmax(-1, keepdim=True)
+            tok_buf.copy_(nxt)
+            pos_buf.add_(1)
+            rec.index_copy_(1, pos_buf - prefill, nxt)
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warm):  # real decode steps, run eagerly before the capture
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        for _ in range(steps - warm):
+            graph.replay()
+        torch.cuda.synchronize()
+        t4 = time.perf_counter()
+        assert scs[0].seq_len() == prefill + steps
+        # greedy tokens of random-init weights sit on near-ties: a last-bit difference
+        # (summation order of the split-K chunks, fused vs separate roundings) can flip one
+        # argmax, after which the sequences diverge; report where the first flip happens
+        diff = (rec[:, :steps + 1] != toks_eager).any(dim=0).nonzero()
+        first_flip = int(diff[0].item()) if diff.numel() else steps + 1
+        # kernel times of a few more steps (events per launch; outside the timed loops)
         with _lib().KernelProfile() as prof:
-            for _ in range(16):
-                logits, cache = lm(tok, cache)
-                tok = logits[:, -1].argmax(-1, keepdim=True)
+            for _ in range(more):
+                step()
             torch.cuda.synchronize()
-    decode_s = t2 - t1
-    # cache bytes per step and layer (order 3, kv heads = heads): q2, q3, v2, v3 ... every
-    # cached tensor read once: (2*order-1) kv tensors + (order-1) msg (bf16) and lse (fp32)
+    eager_s, graph_s = t2 - t1, t4 - t3
+    graph_steps = steps - warm
+    # cache bytes per step and layer (order 3, kv heads = heads): every cached tensor read
+    # once -- (2*order-1) q/v tensors (bf16) + (order-1) msg (bf16) and lse (fp32)
     per_tok = (2 * 3 - 1) * heads * dh * 2 + (3 - 1) * heads * (dh * 2 + 4)
-    cache_bytes = sum(batch * depth * per_tok * (prefill + 1 + s) for s in range(steps))
     weight_bytes = 2 * sum(p.numel() for n, p in lm.named_parameters()
                            if not n.startswith("token_emb") and not n.endswith("freqs"))
-    all_bytes = cache_bytes + steps * weight_bytes
-    kern_ms = sum(t for _, t in prof.times.values()) / 16
+
+    def step_bytes(s):  # decode step s (0-based) attends over prefill + s + 1 positions
+        return batch * depth * per_tok * (prefill + s + 1) + weight_bytes
+
+    eager_bytes = sum(step_bytes(s) for s in range(steps))
+    graph_bytes = sum(step_bytes(s) for s in range(warm, steps))
+    kern = {k: {"launches": n // more, "avg_ms": round(t / n, 4)}
+            for k, (n, t) in prof.times.items()}
+    attn_ms = sum(t for _, t in prof.times.values()) / more
+    n_mid = prefill + steps + more / 2
     res = {
         "workload": f"order-3 causal decode, PolyLM-style stack depth {depth}, dim {dim}, heads "
                     f"{heads}, dim_head {dh}, batch {batch}, prefill {prefill} tokens, {steps} "
                     f"greedy steps, bf16 weights and cache, fp32 lse (BASELINE configs[3])",
         "prefill_ms": round((t1 - t0) * 1e3, 2),
-        "ms_per_step": round(decode_s * 1e3 / steps, 4),
-        "tokens_per_s": round(batch * steps / decode_s, 1),
-        "cache_GB_per_step_mean": round(cache_bytes / steps / 1e9, 4),
-        "GB_per_s": round(all_bytes / decode_s / 1e9, 1),
-        "frac_hbm_peak": round(all_bytes / decode_s / 1e9 / PEAK_HBM_GBS, 4),
-        "attn_kernel_ms_per_step": round(kern_ms, 4),
-        "attn_kernel_GB_per_s": round(batch * depth * per_tok * (prefill + steps + 8)
-                                      / (kern_ms / 1e3) / 1e9, 1),
-        "kernels": {k: {"launches": n // 16, "avg_ms": round(t / n, 4)}
-                    for k, (n, t) in prof.times.items()},
+        "ms_per_step": round(graph_s * 1e3 / graph_steps, 4),
+        "tokens_per_s": round(batch * graph_steps / graph_s, 1),
+        "GB_per_s": round(graph_bytes / graph_s / 1e9, 1),
+        "frac_hbm_peak": round(graph_bytes / graph_s / 1e9 / PEAK_HBM_GBS, 4),
+        "mode": f"StaticCache + one HIP graph per token ({warm} eager warm-up steps, "
+                f"{graph_steps} replays timed)",
+        "eager_tuple_cache": {
+            "ms_per_step": round(eager_s * 1e3 / steps, 4),
+            "tokens_per_s": round(batch * steps / eager_s, 1),
+            "GB_per_s": round(eager_bytes / eager_s / 1e9, 1)},
+        "greedy_tokens_identical_to_eager_until": first_flip,
+        "cache_GB_per_step_mean": round((eager_bytes - steps * weight_bytes) / steps / 1e9, 4),
+        "weight_GB_per_step": round(weight_bytes / 1e9, 4),
+        "poly_kernels_ms_per_step": round(attn_ms, 4),
+        "decode_kernels_GB_per_s": round(
+            batch * depth * per_tok * n_mid
+            / (sum(prof.times.get(k, (0, 0.0))[1] for k in ("dec_partial", "dec_combine"))
+               / more / 1e3) / 1e9, 1),
+        "kernels": kern,
     }
-    del lm, cache, logits
+    del lm, scs, graph
     torch.cuda.empty_cache()
     if cpu:
         threads = max(1, min(16, os.cpu_count() or 1))

@@ -16,6 +16,9 @@
  *   pa_poly_decode     the cached single-token step of Order2PolyAttention.forward
  *                      (poly_attention.py:283-287, 331-338, 360-363) and of
  *                      NPolyAttention.forward (n_poly_attention.py:196-313, 332-340).
+ *   pa_decode_prologue the q norms, rotary embedding and cache appends that precede that
+ *                      step (n_poly_attention.py:188-191, 206-207; poly_attention.py:271-276,
+ *                      282-286).
  *
  * Semantics of one pass (per batch b, pass head h, query row i, key j):
  *   s_ij  = scale * <q[b, h/rq, i], k[b, h/rk, j]>           rq = heads / q.heads, etc.
@@ -39,7 +42,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 1
+#define PA_ABI_VERSION 2
 #define PA_MAX_ORDER 8
 
 /* status codes (0 = success, negative = failure) */
@@ -133,13 +136,55 @@ typedef struct pa_decode {
     pa_decode_level levels[PA_MAX_ORDER];
     void*   workspace;
     size_t  workspace_bytes;
+    /* Optional (NULL = off): a device int32 holding the step's n, for decode loops captured
+     * into a HIP graph, where n changes between replays.  `n` above is then the capacity
+     * every view holds (n_dev[0] is clamped to 1..n; workspace and grid are sized for n),
+     * and the out / lse views of every level but the final one are the whole msg / lse
+     * caches (position 0 based): the step writes their position n_dev[0]-1. */
+    const int32_t* n_dev;
 } pa_decode;
+
+/* One tensor of the decode prologue: the new token's projection for one q / k / v of a
+ * level (pa_decode_prologue). */
+typedef struct pa_prologue_item {
+    pa_view     src;            /* [B, heads, 1, dim]: the projection (any strides, dim stride 1) */
+    const void* norm_weight;    /* [dim] RMSNorm weight, or NULL: no normalisation */
+    int32_t     weight_dtype;   /* PA_F32 / PA_F16 / PA_BF16 */
+    int32_t     rotate;         /* nonzero: rotate the leading rot_dim features after the norm */
+    pa_view     out;            /* optional [B, heads, 1, dim]: the resulting row */
+    pa_view     cache;          /* optional [B, heads, capacity, dim]: the row also goes to
+                                 * position pos of this cache buffer */
+} pa_prologue_item;
+
+/* The per-token prologue of a cached decode step: the q RMSNorms, the rotary embedding and
+ * the cache appends of one poly-attention layer in one launch.  Every item's rows are
+ *   y = round(x * rsqrt(mean(x^2) + eps) * w)                    (when norm_weight is set)
+ *   y = round(y * cos(a) + rotate_half(y) * sin(a)) on [0, rot_dim)  (when rotate is set)
+ * with rotate_half pairing features (2i, 2i+1) -> (-y[2i+1], y[2i]) and a = angles[feature],
+ * computed in fp32 from the (rounded) norm output, as torch evaluates
+ *   RMSNorm(dim_head)(q) and apply_rotary_emb(freqs, q)
+ * in n_poly_attention.py:188-191 / poly_attention.py:271-276 (the angles as built at
+ * train_enwik8.py:143,160-161).  The cache write replaces the torch.cat appends of
+ * n_poly_attention.py:206-207 and poly_attention.py:282-286 for fixed-capacity caches.
+ * The position is read from the device (pos_dev) when given, else `pos`; rows whose
+ * position falls outside [0, capacity) are not written to the cache.  All items share
+ * src's dtype. */
+typedef struct pa_prologue {
+    int32_t        batch, dim, count, capacity;
+    float          eps;         /* RMSNorm epsilon */
+    const float*   angles;      /* [rot_dim] fp32 rotary angles of the new position, or NULL */
+    int32_t        rot_dim;     /* even, <= dim */
+    int32_t        pos;         /* cache position when pos_dev is NULL */
+    const int64_t* pos_dev;     /* device: cache position (positions already held), or NULL */
+    pa_prologue_item items[2 * PA_MAX_ORDER];
+} pa_prologue;
 
 int         pa_abi_version(void);
 const char* pa_strerror(int status);
 int         pa_last_hip_error(void);   /* hipError_t of the last PA_EHIP on this thread */
 /* sizeof of the ABI structs, for binding checks: 0 pa_view, 1 pa_mask, 2 pa_pass,
- * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode; 0 for other values */
+ * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode, 6 pa_prologue_item, 7 pa_prologue;
+ * 0 for other values */
 size_t      pa_struct_size(int which);
 
 /* Kernel timing (no counterpart in the reference: a measurement facility for benchmarks).
@@ -159,6 +204,7 @@ size_t pa_attn_pass_bwd_workspace(const pa_pass_grad* g);
 int    pa_attn_pass_bwd(const pa_pass_grad* g, void* stream);
 size_t pa_poly_decode_workspace(const pa_decode* d);
 int    pa_poly_decode(const pa_decode* d, void* stream);
+int    pa_decode_prologue(const pa_prologue* p, void* stream);
 
 #ifdef __cplusplus
 }

@@ -165,6 +165,8 @@ size_t pa_struct_size(int which) {
         case 3: return sizeof(pa_pass_grad);
         case 4: return sizeof(pa_decode_level);
         case 5: return sizeof(pa_decode);
+        case 6: return sizeof(pa_prologue_item);
+        case 7: return sizeof(pa_prologue);
         default: return 0;
     }
 }
@@ -294,6 +296,13 @@ size_t pa_poly_decode_workspace(const pa_decode* d) {
 int pa_poly_decode(const pa_decode* d, void* stream) {
     if (!d) return PA_EINVAL;
     const int st = launch_decode(d, static_cast<hipStream_t>(stream));
+    if (st != PA_OK) return st;
+    return finish_launch();
+}
+
+int pa_decode_prologue(const pa_prologue* p, void* stream) {
+    if (!p) return PA_EINVAL;
+    const int st = launch_prologue(p, static_cast<hipStream_t>(stream));
     if (st != PA_OK) return st;
     return finish_launch();
 }

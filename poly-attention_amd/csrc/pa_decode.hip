@@ -24,8 +24,17 @@ struct DecLevelDev {
 struct DecodeDev {
     int32_t batch, kv_heads, n, dim, order, chunk, nchunks, rec, lpr;
     float scale, softclamp;
+    // when set, the step's position count is read here (n above is then its upper bound) and
+    // the msg / lse caches of the non-final levels are written at position n-1
+    const int32_t* n_dev;
     DecLevelDev L[PA_MAX_ORDER];
 };
+
+__device__ __forceinline__ int step_n(const DecodeDev& D) {
+    if (!D.n_dev) return D.n;
+    const int n = *D.n_dev;
+    return n < 1 ? 1 : (n > D.n ? D.n : n);  // clamped: a bad count cannot read out of bounds
+}
 
 constexpr int kDecThreads = 256;
 constexpr int kDecHB = 4;      // level heads scored per pass over a chunk's K rows
@@ -104,8 +113,17 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_partial(DecodeDev D) {
     const bool dok = d0 < D.dim;
     const int C = D.chunk;
     const int j_begin = c * C;
-    const int cnt = min(C, D.n - 1 - j_begin);
+    const int cnt = min(C, step_n(D) - 1 - j_begin);
     const int rep = L.rep, h0 = g * rep;
+    if (cnt <= 0) {
+        // a chunk past the step's positions (grid sized for the capacity): empty records
+        for (int hh = tid; hh < rep; hh += kDecThreads) {
+            float* rec = L.ws + (((int64_t)b * L.heads + h0 + hh) * D.nchunks + c) * D.rec;
+            rec[0] = -INFINITY;
+            rec[1] = 0.f;
+        }
+        return;
+    }
     const float cinv = D.softclamp > 0.f ? D.scale / D.softclamp : 0.f;
     const float cl2 = D.softclamp * kLog2e;
     const float sl2 = D.scale * kLog2e;
@@ -258,7 +276,8 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
     __shared__ float s_lse2[kDecMaxHeadsPerGroup];
     int prev_rep = 1;
     const int dim = D.dim;
-    const int nold = D.n - 1;
+    const int n = step_n(D);
+    const int nold = n - 1;
 
     for (int t = 0; t < D.order; ++t) {
         const DecLevelDev& L = D.L[t];
@@ -323,7 +342,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
                 float c1 = 0.f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[e] = 0.f;
-                for (int j = 0; j < D.n; ++j) {
+                for (int j = 0; j < n; ++j) {
                     const float bj = (j == nold) ? bnew : (L.bias.ok() ? L.bias.scalar(b, h, j) : 0.f);
                     if (bias_class(bj) != 1) continue;
                     c1 += 1.f;
@@ -344,21 +363,22 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
                 inv = c1 > 0.f ? 1.f / c1 : NAN;
             }
             // 3. write the step result (replicated over the view heads) and keep it in LDS
+            const int slot = (D.n_dev && !final_level) ? nold : 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int d = lane + 64 * e;
                 if (d >= dim) continue;
                 const float o = acc[e] * inv;
                 for (int r = 0; r < L.out_rep; ++r)
-                    L.out.wrow<T>(b, h * L.out_rep + r, 0)[d] = from_f<T>(o);
+                    L.out.wrow<T>(b, h * L.out_rep + r, slot)[d] = from_f<T>(o);
                 s_msg2[hh * dim + d] = round_to<T>(o);
             }
             if (lane == 0) {
                 float stored = lse_v;
                 if (L.lse.ok()) {
                     for (int r = 0; r < L.lse_rep; ++r)
-                        store_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep + r, 0), lse_v);
-                    stored = load_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep, 0));
+                        store_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep + r, slot), lse_v);
+                    stored = load_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep, slot));
                 }
                 s_lse2[hh] = stored;  // the value the next level's cached bias will hold
             }
@@ -370,6 +390,141 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
         __syncthreads();
         prev_rep = L.rep;
     }
+}
+
+// ---------------------------------------------------------------------------------------
+// Decode prologue: q RMSNorm + rotary + cache append for every q / k / v of one layer's
+// new token, one wave per (item, batch, head) row.
+
+struct ProItemDev {
+    DView src, out, cache;
+    const void* w;
+    int32_t wdt, rotate, heads, row0;
+};
+
+struct ProDev {
+    int32_t batch, dim, count, capacity, rot_dim, pos, rows;
+    float eps;
+    const float* angles;
+    const int64_t* pos_dev;
+    ProItemDev it[2 * PA_MAX_ORDER];
+};
+
+constexpr int kProThreads = 256;
+
+template <typename T>
+__global__ __launch_bounds__(kProThreads) void k_dec_prologue(ProDev P) {
+    // separate roundings of every product and sum, as torch's element-wise kernels do
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kProThreads / 64) + (threadIdx.x >> 6);
+    if (row >= P.rows) return;  // no barriers below: whole waves leave together
+    int k = 0;
+    while (k + 1 < P.count && row >= P.it[k + 1].row0) ++k;
+    const ProItemDev& I = P.it[k];
+    const int local = row - I.row0;
+    const int b = local / I.heads, h = local % I.heads;
+    const int dim = P.dim;
+
+    float x[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int d = lane + 64 * e;
+        x[e] = d < dim ? to_f(I.src.row<T>(b, h, 0)[d]) : 0.f;
+        ss += x[e] * x[e];
+    }
+    if (I.w) {
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        const float r = rsqrtf(ss / (float)dim + P.eps);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = lane + 64 * e;
+            const float w = d < dim ? load_any(I.w, I.wdt, d) : 0.f;
+            x[e] = round_to<T>((x[e] * r) * w);
+        }
+    }
+    if (I.rotate && P.angles) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = lane + 64 * e;
+            const float partner = __shfl_xor(x[e], 1);  // feature d ^ 1 (same 64-block)
+            if (d < P.rot_dim) {
+                const float a = P.angles[d];
+                const float rot = (d & 1) ? partner : -partner;
+                x[e] = round_to<T>(x[e] * cosf(a) + rot * sinf(a));
+            }
+        }
+    }
+    const int64_t pos = P.pos_dev ? *P.pos_dev : (int64_t)P.pos;
+    const bool to_cache = I.cache.ok() && pos >= 0 && pos < P.capacity;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int d = lane + 64 * e;
+        if (d >= dim) continue;
+        const T y = from_f<T>(x[e]);
+        if (I.out.ok()) I.out.wrow<T>(b, h, 0)[d] = y;
+        if (to_cache) I.cache.wrow<T>(b, h, pos)[d] = y;
+    }
+}
+
+int launch_prologue(const pa_prologue* p, hipStream_t s) {
+    if (p->batch < 1 || p->dim < 1 || p->count < 1 || p->count > 2 * PA_MAX_ORDER)
+        return PA_EINVAL;
+    if (p->dim > 256) return PA_EUNSUPPORTED;
+    if (p->angles && (p->rot_dim < 0 || p->rot_dim > p->dim || p->rot_dim % 2 != 0))
+        return PA_EINVAL;
+    const int T = p->items[0].src.dtype;
+    if (T != PA_F32 && T != PA_F16 && T != PA_BF16) return PA_EINVAL;
+    ProDev P;
+    P.batch = p->batch;
+    P.dim = p->dim;
+    P.count = p->count;
+    P.capacity = p->capacity;
+    P.rot_dim = p->angles ? p->rot_dim : 0;
+    P.pos = p->pos;
+    P.eps = p->eps;
+    P.angles = p->angles;
+    P.pos_dev = p->pos_dev;
+    int rows = 0;
+    for (int k = 0; k < p->count; ++k) {
+        const pa_prologue_item& it = p->items[k];
+        if (!it.src.ptr || it.src.heads < 1 || it.src.dtype != T) return PA_EINVAL;
+        if ((it.out.ptr && (it.out.dtype != T || it.out.heads != it.src.heads)) ||
+            (it.cache.ptr && (it.cache.dtype != T || it.cache.heads != it.src.heads)))
+            return PA_EINVAL;
+        if (it.cache.ptr && p->capacity < 1) return PA_EINVAL;
+        if (it.norm_weight && it.weight_dtype != PA_F32 && it.weight_dtype != PA_F16 &&
+            it.weight_dtype != PA_BF16)
+            return PA_EINVAL;
+        ProItemDev& I = P.it[k];
+        auto mk = [&](const pa_view& v) {
+            DView x;
+            x.p = static_cast<char*>(v.ptr);
+            x.sb = v.sb;
+            x.sh = v.sh;
+            x.sn = v.sn;
+            x.hdiv = 1;
+            x.dtype = v.dtype;
+            return x;
+        };
+        I.src = mk(it.src);
+        I.out = mk(it.out);
+        I.cache = mk(it.cache);
+        I.w = it.norm_weight;
+        I.wdt = it.weight_dtype;
+        I.rotate = it.rotate;
+        I.heads = it.src.heads;
+        I.row0 = rows;
+        rows += p->batch * it.src.heads;
+    }
+    P.rows = rows;
+    const dim3 grid((rows + kProThreads / 64 - 1) / (kProThreads / 64));
+    ProfScope ps("dec_prologue", s);
+    if (T == PA_F32) hipLaunchKernelGGL((k_dec_prologue<float>), grid, dim3(kProThreads), 0, s, P);
+    else if (T == PA_F16) hipLaunchKernelGGL((k_dec_prologue<f16>), grid, dim3(kProThreads), 0, s, P);
+    else hipLaunchKernelGGL((k_dec_prologue<bf16>), grid, dim3(kProThreads), 0, s, P);
+    return PA_OK;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -459,6 +614,7 @@ int launch_decode(const pa_decode* d, hipStream_t s) {
     D.batch = d->batch;
     D.kv_heads = d->kv_heads;
     D.n = d->n;
+    D.n_dev = d->n_dev;
     D.dim = d->dim;
     D.order = d->order;
     D.scale = d->scale;

@@ -30,5 +30,6 @@ void launch_mfma_bwd(const GradDev& G, int dtype, hipStream_t s);
 struct DecodeDev;
 size_t decode_workspace_bytes(const pa_decode* d, int* chunk_out, int* nchunks_out);
 int launch_decode(const pa_decode* d, hipStream_t s);
+int launch_prologue(const pa_prologue* p, hipStream_t s);
 
 }  // namespace pa

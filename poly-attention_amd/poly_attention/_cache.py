@@ -85,3 +85,65 @@ def reserve(cache: Optional[Tensor], like_step: Tensor, dim: int, dtype=None) ->
 def adopt(t: Tensor, dim: int, dtype=None) -> Tensor:
     """Copy a freshly computed full tensor into a capacity buffer (prefill -> cache)."""
     return append(None, t if dtype is None else t.to(dtype), dim)
+
+
+class StaticCache:
+    """A fixed-capacity poly KV cache whose position count lives on the device.
+
+    Holds the tensors of a module's cache tuple -- order 2: ``(q2, q3, v3, lse23, msg)``
+    (poly_attention.py:283-287, 360-363); order n: ``(qs, vs, lses, msgs)``
+    (n_poly_attention.py:206-207, 338) -- in buffers of ``capacity`` positions.  Passed as
+    ``cache=`` to PolyAttention / NPolyAttention on the fused GPU path, a single-token step
+    writes the new token in place (one prologue kernel: the q RMSNorms, the rotary embedding
+    and the appends), runs the decode kernels with the position count read on the device,
+    advances the count and returns this same object.  Every step then has the same shapes
+    and addresses, so a whole decode step can be captured once into a HIP graph
+    (``torch.cuda.CUDAGraph``) and replayed per token.
+
+    A step at full capacity writes nothing to the cache and attends over the first
+    ``capacity`` positions only (the kernels clamp the count); size it for prompt + steps.
+    """
+
+    def __init__(self, cache, capacity: int):
+        self.order2 = isinstance(cache[0], Tensor)
+        if self.order2:
+            q2, q3, v3, lse, msg = cache
+            qs, vs, lses, msgs = (q2, q3), (v3,), (lse,), (msg,)
+        else:
+            qs, vs, lses, msgs = cache
+        n = qs[0].shape[2]
+        if capacity <= n:
+            raise ValueError(f"capacity {capacity} must exceed the {n} cached positions")
+        self.capacity = int(capacity)
+
+        def grow(t: Tensor) -> Tensor:
+            shape = list(t.shape)
+            shape[2] = self.capacity
+            buf = torch.empty(shape, dtype=t.dtype, device=t.device)
+            buf.narrow(2, 0, n).copy_(t)
+            return buf
+
+        self.qs = [grow(t) for t in qs]
+        self.vs = [grow(t) for t in vs]
+        self.lses = [grow(t) for t in lses]
+        self.msgs = [grow(t) for t in msgs]
+        dev = qs[0].device
+        self.length = torch.full((1,), n, dtype=torch.int64, device=dev)  # positions held
+        self.n_step = torch.full((1,), n + 1, dtype=torch.int32, device=dev)  # n of a step
+
+    def advance(self) -> None:
+        """Count the token a step has just written (stream-ordered, capturable)."""
+        self.length.add_(1)
+        self.n_step.add_(1)
+
+    def seq_len(self) -> int:
+        """Cached positions (reads the device count: synchronises)."""
+        return min(int(self.length.item()), self.capacity)
+
+    def as_tuple(self):
+        """The cache as the module's tuple of tensors (views of the first seq_len() positions)."""
+        n = self.seq_len()
+        cut = lambda ts: tuple(t.narrow(2, 0, n) for t in ts)  # noqa: E731
+        if self.order2:
+            return (*cut(self.qs), *cut(self.vs), *cut(self.lses), *cut(self.msgs))
+        return cut(self.qs), cut(self.vs), cut(self.lses), cut(self.msgs)

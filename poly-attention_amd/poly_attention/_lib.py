@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolyattn.so"
 
-PA_ABI_VERSION = 1
+PA_ABI_VERSION = 2
 PA_MAX_ORDER = 8
 
 PA_OK = 0
@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "pa_attn_pass_bwd",
     "pa_poly_decode_workspace",
     "pa_poly_decode",
+    "pa_decode_prologue",
 )
 
 
@@ -126,6 +127,33 @@ class PaDecode(ctypes.Structure):
         ("levels", PaDecodeLevel * PA_MAX_ORDER),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("n_dev", c_void_p),
+    ]
+
+
+class PaPrologueItem(ctypes.Structure):
+    _fields_ = [
+        ("src", PaView),
+        ("norm_weight", c_void_p),
+        ("weight_dtype", c_int32),
+        ("rotate", c_int32),
+        ("out", PaView),
+        ("cache", PaView),
+    ]
+
+
+class PaPrologue(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int32),
+        ("dim", c_int32),
+        ("count", c_int32),
+        ("capacity", c_int32),
+        ("eps", c_float),
+        ("angles", c_void_p),
+        ("rot_dim", c_int32),
+        ("pos", c_int32),
+        ("pos_dev", c_void_p),
+        ("items", PaPrologueItem * (2 * PA_MAX_ORDER)),
     ]
 
 
@@ -133,7 +161,8 @@ class PaKernelTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("launches", c_int64), ("total_ms", ctypes.c_double)]
 
 
-STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode)
+STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode, PaPrologueItem,
+           PaPrologue)
 
 
 class PolyAttnError(RuntimeError):
@@ -173,6 +202,8 @@ def _configure(lib) -> None:
     lib.pa_poly_decode_workspace.argtypes = [ctypes.POINTER(PaDecode)]
     lib.pa_poly_decode.restype = c_int
     lib.pa_poly_decode.argtypes = [ctypes.POINTER(PaDecode), c_void_p]
+    lib.pa_decode_prologue.restype = c_int
+    lib.pa_decode_prologue.argtypes = [ctypes.POINTER(PaPrologue), c_void_p]
 
 
 def load(path: str | os.PathLike | None = None):

@@ -9,6 +9,8 @@
   233-313 as a right-to-left sequence of passes (each level's lse is the next level's key
   bias, each level's output its value, multiplied by that level's v in the middle levels).
 * ``poly_decode_step`` -- the cached single-token step through ``pa_poly_decode``.
+* ``decode_prologue`` -- the q norms, rotary and cache appends before a fixed-capacity
+  (StaticCache) step, through ``pa_decode_prologue``.
 """
 
 from __future__ import annotations
@@ -303,13 +305,18 @@ def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence
 def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
                      v_caches: Sequence[Tensor], msg_caches: Sequence[Tensor],
                      lse_caches: Sequence[Tensor], *, kv_heads: int, heads: int,
-                     softclamp: Optional[float], scale: float, chunk: int = 0) -> Tensor:
+                     softclamp: Optional[float], scale: float, chunk: int = 0,
+                     n_dev: Optional[Tensor] = None) -> Tensor:
     """One cached decode step through pa_poly_decode (no autograd).
 
     Level l (l = 0: q1 . q2) has query q_new[l] [B, h, 1, d] and keys k_caches[l]
     [B, kv_heads, n, d] whose position n-1 already holds the new token.  v_caches are the
     value caches v_3 .. v_{n+1}; msg_caches / lse_caches (deepest first, the reference's
     order) hold n positions whose slot n-1 this call fills.  Returns the output [B, heads, 1, d].
+
+    With ``n_dev`` (a device int32 [1]) the caches are fixed-capacity buffers (n = their
+    length is the bound) and the step's n is read on the device, so the launch is the same
+    at every position (HIP-graph capturable).
     """
     lib = _lib.load()
     order = len(q_new)
@@ -348,14 +355,57 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
             L.bias = _view(lse_caches[src])
         if lvl == 0:
             L.out = _view(out)
+        elif n_dev is not None:  # whole caches: the kernel writes position n_dev - 1
+            dst = order - 1 - lvl
+            L.out = _view(msg_caches[dst])
+            L.lse = _view(lse_caches[dst])
         else:
             dst = order - 1 - lvl
             L.out = _view(msg_caches[dst].narrow(2, n - 1, 1))
             L.lse = _view(lse_caches[dst].narrow(2, n - 1, 1))
         L.heads = heads_t
+    if n_dev is not None:
+        assert n_dev.dtype == torch.int32 and n_dev.is_cuda and n_dev.numel() == 1
+        D.n_dev = n_dev.data_ptr()
     ws_bytes = lib.pa_poly_decode_workspace(ctypes.byref(D))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=out.device)
     D.workspace, D.workspace_bytes = ws.data_ptr(), ws_bytes
     with torch.cuda.device(out.device):
         _lib.check(lib.pa_poly_decode(ctypes.byref(D), _stream(out)), "pa_poly_decode")
     return out
+
+
+def decode_prologue(items, *, eps: float, angles: Optional[Tensor], pos_dev: Tensor,
+                    capacity: int) -> None:
+    """The q norms, rotary embedding and cache appends of one decode step, one launch
+    (pa_decode_prologue).  ``items``: (src [B, h, 1, d], norm weight or None, rotate,
+    out [B, h, 1, d] or None, cache [B, h, capacity, d] or None) per tensor; ``angles`` is
+    the fp32 [rot_dim] rotary angle row of the new position; the cache position is read from
+    ``pos_dev`` (device int64 [1]) on the device."""
+    lib = _lib.load()
+    src0 = items[0][0]
+    B, _, _, d = src0.shape
+    P = _lib.PaPrologue()
+    P.batch, P.dim, P.count, P.capacity = B, d, len(items), int(capacity)
+    P.eps = float(eps)
+    keep = []
+    if angles is not None:
+        a = angles.detach().to(torch.float32).contiguous()
+        keep.append(a)
+        P.angles, P.rot_dim = a.data_ptr(), a.numel()
+    assert pos_dev.dtype == torch.int64 and pos_dev.is_cuda and pos_dev.numel() == 1
+    P.pos_dev = pos_dev.data_ptr()
+    for k, (src, w, rotate, out, cache) in enumerate(items):
+        it = P.items[k]
+        it.src = _view(src)
+        if w is not None:
+            w = w.detach().contiguous()
+            keep.append(w)
+            it.norm_weight, it.weight_dtype = w.data_ptr(), DTYPE_CODE[w.dtype]
+        it.rotate = 1 if rotate else 0
+        if out is not None:
+            it.out = _view(out)
+        if cache is not None:
+            it.cache = _view(cache)
+    with torch.cuda.device(src0.device):
+        _lib.check(lib.pa_decode_prologue(ctypes.byref(P), _stream(src0)), "pa_decode_prologue")

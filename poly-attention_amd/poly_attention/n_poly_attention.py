@@ -30,7 +30,7 @@ from ._helpers import (
     where_keys,
     where_queries,
 )
-from .poly_attention import _compute_dtype, fused_available
+from .poly_attention import _compute_dtype, _static_decode_step, fused_available
 from .rotary import RotaryEmbedding, apply_rotary_emb
 
 LinearNoBias = partial(nn.Linear, bias=False)
@@ -173,23 +173,33 @@ class NPolyAttention(Module):
             root_value = kv1[1] if self.has_root_v else None
 
         qs = (q1, *qs_rest)
-        qs = tuple(norm(q) for norm, q in zip(self.q_norms, qs))
 
-        if exists(rotary_pos_emb):
-            qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)
-
-        q1 = first(qs)
-        qs_rest = qs[1:]
-
-        if self._use_fused(q1):
-            out, new_cache = self._fused_core(q1, qs_rest, vs_for_aggregation, mask,
-                                              context_mask, rotary_pos_emb, cache, return_cache)
+        if isinstance(cache, _cache.StaticCache):
+            # fixed-capacity cache: norms, rotary and appends fused into the decode step
+            out = _static_decode_step(self, qs, vs_for_aggregation, mask, context_mask,
+                                      rotary_pos_emb, cache)
+            new_cache = cache
             if exists(root_value) and self.is_gqa:
                 root_value = repeat_kv(root_value, self.num_rep)
         else:
-            out, new_cache, root_value = self._eager_core(q1, qs_rest, vs_for_aggregation,
-                                                          root_value, mask, context_mask,
-                                                          rotary_pos_emb, cache, device)
+            qs = tuple(norm(q) for norm, q in zip(self.q_norms, qs))
+
+            if exists(rotary_pos_emb):
+                qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)
+
+            q1 = first(qs)
+            qs_rest = qs[1:]
+
+            if self._use_fused(q1):
+                out, new_cache = self._fused_core(q1, qs_rest, vs_for_aggregation, mask,
+                                                  context_mask, rotary_pos_emb, cache,
+                                                  return_cache)
+                if exists(root_value) and self.is_gqa:
+                    root_value = repeat_kv(root_value, self.num_rep)
+            else:
+                out, new_cache, root_value = self._eager_core(q1, qs_rest, vs_for_aggregation,
+                                                              root_value, mask, context_mask,
+                                                              rotary_pos_emb, cache, device)
 
         if self.multiply_root_value:
             if self.use_root_value_as_attn_gate:

@@ -43,6 +43,67 @@ def fused_available() -> bool:
     return _lib.available()
 
 
+def _static_decode_step(module, qs, vs, mask, context_mask, rotary_pos_emb,
+                        cache: _cache.StaticCache) -> Tensor:
+    """A single-token step on a StaticCache, for both module orders.
+
+    One prologue launch does the q RMSNorms (poly_attention.py:271, n_poly_attention.py:188),
+    the external rotary (:275-276, :190-191) and the cache appends (:284-286, :206-207);
+    the decode kernels then read the position count on the device, and the count advances.
+    ``qs`` = (q1, ..., q_{order+1}) are the raw projections [B, h, 1, d], ``vs`` the
+    aggregation values (v3, ...).  Returns the output [B, heads, 1, d]."""
+    from . import _ops
+
+    q1 = qs[0]
+    order = len(qs) - 1
+    if not (module.use_flash_kernel and q1.is_cuda):
+        raise RuntimeError("a StaticCache needs the fused GPU path (libpolyattn)")
+    _lib.load()
+    if q1.shape[-2] != 1:
+        raise ValueError("a StaticCache step takes exactly one new token")
+    if exists(mask) or any(exists(m) for m in context_mask):
+        raise NotImplementedError("masks are not supported with a StaticCache")
+    if not exists(rotary_pos_emb) and exists(module.rotary_emb):
+        raise NotImplementedError(
+            "the module's own rotary re-rotates the whole cache every step; pass external "
+            "rotary_pos_emb with a StaticCache")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (*qs, *vs)):
+        raise RuntimeError("StaticCache decode is inference-only: run it under torch.no_grad()")
+    if len(cache.qs) != order or len(cache.vs) != order - 1:
+        raise ValueError(f"StaticCache of order {len(cache.qs)} passed to an order-{order} module")
+    dt = cache.qs[0].dtype
+    if any(t.dtype != dt for t in (*qs, *vs)):
+        raise TypeError("StaticCache: the projections and the cache must share one dtype")
+    norms = list(module.q_norms)
+    eps = {n.eps for n in norms}
+    if len(eps) != 1:
+        raise NotImplementedError("q norms with different eps")
+    eps = eps.pop()
+    if eps is None:  # torch's rms_norm default: epsilon of the op-math type (fp32)
+        eps = torch.finfo(torch.float32).eps
+    angles = None
+    if exists(rotary_pos_emb):
+        if rotary_pos_emb.dim() not in (1, 2):
+            raise NotImplementedError("rotary_pos_emb must be [positions, dim] or [dim]")
+        angles = rotary_pos_emb if rotary_pos_emb.dim() == 1 else rotary_pos_emb[-1]
+    q_left = [torch.empty(q.shape[0], q.shape[1], 1, q.shape[3], dtype=dt, device=q.device)
+              for q in qs[:-1]]
+    items = []
+    for i, (q, norm) in enumerate(zip(qs, norms)):
+        w = norm.weight if norm.weight is not None else torch.ones(q.shape[-1], device=q.device)
+        items.append((q, w, angles is not None, q_left[i] if i < order else None,
+                      cache.qs[i - 1] if i >= 1 else None))
+    items += [(v, None, False, None, buf) for v, buf in zip(vs, cache.vs)]
+    _ops.decode_prologue(items, eps=eps, angles=angles, pos_dev=cache.length,
+                         capacity=cache.capacity)
+    out = _ops.poly_decode_step(q_left, cache.qs, cache.vs, cache.msgs, cache.lses,
+                                kv_heads=module.kv_heads, heads=module.heads,
+                                softclamp=module.softclamp_value, scale=module.scale,
+                                n_dev=cache.n_step)
+    cache.advance()
+    return out
+
+
 # attention
 
 
@@ -248,27 +309,34 @@ class Order2PolyAttention(Module):
             q3, v3 = kv2
             qs = (q1, q2, q3)
 
-        qs = tuple(norm(q) for norm, q in zip(self.q_norms, qs))
-
-        if exists(rotary_pos_emb):
-            qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)
-
-        q1, q2, q3 = qs
-
-        # dispatch: the HIP kernels take every case on the GPU (masks, contexts, GQA, caches);
-        # an explicitly requested fused kernel still refuses an explicit context_mask, as the
-        # reference does (poly_attention.py:310)
-        if self._flash_requested is True and explicit_context_mask:
-            assert not any(exists(m) for m in context_mask), \
-                "context_mask is not supported in flash poly attention"
-
-        if self._use_fused(q1):
-            out, new_cache = self._fused_core(q1, q2, q3, v3, mask, context_mask, rotary_pos_emb,
-                                              cache, return_cache)
-            v2 = repeat_kv(v2, self.num_rep) if self.is_gqa else v2
+        if isinstance(cache, _cache.StaticCache):
+            # fixed-capacity cache: norms, rotary and appends fused into the decode step
+            out = _static_decode_step(self, qs, (v3,), mask, context_mask, rotary_pos_emb,
+                                      cache)
+            new_cache = cache
+            v2 = repeat_kv(v2, self.num_rep) if self.is_gqa and exists(v2) else v2
         else:
-            out, new_cache, v2 = self._eager_core(q1, q2, q3, v2, v3, mask, context_mask,
+            qs = tuple(norm(q) for norm, q in zip(self.q_norms, qs))
+
+            if exists(rotary_pos_emb):
+                qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)
+
+            q1, q2, q3 = qs
+
+            # dispatch: the HIP kernels take every case on the GPU (masks, contexts, GQA,
+            # caches); an explicitly requested fused kernel still refuses an explicit
+            # context_mask, as the reference does (poly_attention.py:310)
+            if self._flash_requested is True and explicit_context_mask:
+                assert not any(exists(m) for m in context_mask), \
+                    "context_mask is not supported in flash poly attention"
+
+            if self._use_fused(q1):
+                out, new_cache = self._fused_core(q1, q2, q3, v3, mask, context_mask,
                                                   rotary_pos_emb, cache, return_cache)
+                v2 = repeat_kv(v2, self.num_rep) if self.is_gqa else v2
+            else:
+                out, new_cache, v2 = self._eager_core(q1, q2, q3, v2, v3, mask, context_mask,
+                                                      rotary_pos_emb, cache, return_cache)
 
         # elementwise multiply root values
 

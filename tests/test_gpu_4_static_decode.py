@@ -1,0 +1,230 @@
+"""GPU: the fixed-capacity decode path -- StaticCache, pa_decode_prologue (q RMSNorm + rotary
++ cache append in one launch) and pa_poly_decode with the position count on the device --
+against torch's own ops, the CPU oracle's parallel forward, and replays of a HIP graph.
+
+Tolerances as the other GPU suites: fp32 max-abs <= 1e-4, bf16 <= 2e-2 (relative to
+max(1, max|reference|)).
+"""
+
+import pytest
+import torch
+
+import oracle.poly_oracle as O
+
+pytestmark = pytest.mark.gpu
+param = pytest.mark.parametrize
+
+
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda")
+
+
+def assert_close(got, ref, tol, what):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    err = (got - ref).abs().max().item()
+    denom = max(1.0, ref.abs().max().item())
+    assert err / denom <= tol, f"{what}: max-abs err {err:.3e}"
+
+
+# ---------------------------------------------------------------------------------------
+# the prologue kernel against torch's RMSNorm and apply_rotary_emb
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("rotate", (False, True))
+@param("heads,dim_head", ((4, 64), (2, 128), (3, 32)))
+def test_prologue_matches_torch_ops(dtype, rotate, heads, dim_head):
+    from poly_attention import _ops
+    from poly_attention.rotary import RotaryEmbedding, apply_rotary_emb
+
+    d = dev()
+    torch.manual_seed(0)
+    B, cap, pos = 3, 16, 5
+    # a strided [B, heads, 1, dim_head] view, as the module's split of a projection gives
+    proj = torch.randn(B, 1, 2 * heads * dim_head, device=d).to(dtype)
+    src = proj.reshape(B, 1, 2, heads, dim_head).permute(2, 0, 3, 1, 4)[0]
+    norm = torch.nn.RMSNorm(dim_head).to(d, dtype)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.5 * torch.randn(dim_head, device=d))
+    freqs = RotaryEmbedding(dim_head).to(d)(torch.arange(pos + 1, device=d).float())
+    with torch.no_grad():
+        ref = norm(src)
+        if rotate:
+            ref = apply_rotary_emb(freqs, ref)
+    out = torch.empty(B, heads, 1, dim_head, device=d, dtype=dtype)
+    cache = torch.full((B, heads, cap, dim_head), 7.0, device=d, dtype=dtype)
+    vsrc = torch.randn(B, heads, 1, dim_head, device=d).to(dtype)
+    vcache = torch.full((B, heads, cap, dim_head), 7.0, device=d, dtype=dtype)
+    pos_dev = torch.full((1,), pos, dtype=torch.int64, device=d)
+    _ops.decode_prologue([(src, norm.weight, rotate, out, cache),
+                          (vsrc, None, False, None, vcache)],
+                         eps=torch.finfo(torch.float32).eps,
+                         angles=freqs[-1] if rotate else None, pos_dev=pos_dev, capacity=cap)
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert_close(out, ref, 1e-5, "prologue fp32")
+    else:
+        # one rounding apart at most: within one bf16 ulp, and nearly all bit-identical
+        diff = (out.float() - ref.float()).abs()
+        ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -7
+        assert bool((diff <= ulp).all()), f"prologue bf16: max diff {diff.max().item():.3e}"
+        assert (out == ref).float().mean().item() >= 0.97
+    assert torch.equal(cache[:, :, pos:pos + 1], out)
+    keep = torch.ones(cap, dtype=torch.bool)
+    keep[pos] = False
+    assert bool((cache[:, :, keep] == 7.0).all()), "cache positions other than pos changed"
+    assert torch.equal(vcache[:, :, pos:pos + 1], vsrc)
+    # a position outside the capacity writes nothing
+    pos_dev.fill_(cap)
+    vcache2 = torch.full_like(vcache, 7.0)
+    _ops.decode_prologue([(vsrc, None, False, None, vcache2)], eps=1e-6, angles=None,
+                         pos_dev=pos_dev, capacity=cap)
+    torch.cuda.synchronize()
+    assert bool((vcache2 == 7.0).all())
+
+
+# ---------------------------------------------------------------------------------------
+# modules: StaticCache steps equal the oracle's parallel causal forward
+
+
+def _module(order, kv_heads, d, dtype):
+    from poly_attention import NPolyAttention, Order2PolyAttention
+
+    cfg = dict(heads=4, kv_heads=kv_heads, dim_head=64, causal=True)
+    if order == 2:
+        m = Order2PolyAttention(dim=64, **cfg)
+        fwd = O.order2_forward
+    else:
+        m = NPolyAttention(dim=64, order=order, **cfg)
+        fwd = O.npoly_forward
+        cfg = dict(cfg, order=order)
+    return m.to(d, dtype).eval(), fwd, cfg
+
+
+@param("order", (2, 3))
+@param("kv_heads", (2, 4))
+@param("dtype", (torch.float32, torch.bfloat16))
+def test_static_cache_stepwise_equals_parallel(order, kv_heads, dtype):
+    """Prefill with return_cache, move the cache into a StaticCache, then single-token steps
+    with external rotary (train_enwik8.py:143,160-161): the outputs equal the oracle's
+    parallel causal forward (reference tests:103-179 pattern)."""
+    from poly_attention import StaticCache
+
+    d = dev()
+    torch.manual_seed(12)
+    m, fwd, cfg = _module(order, kv_heads, d, dtype)
+    n = 12
+    x = torch.randn(2, n, 64).to(dtype)
+    freqs = O.rotary_freqs(64, torch.arange(n))
+    params = {k: v.float().cpu() for k, v in m.state_dict().items()}
+    ref = fwd(params, cfg, x.float(), rotary_pos_emb=freqs)
+    fd = freqs.to(d)
+    with torch.no_grad():
+        out0, cache = m(x[:, :5].to(d), rotary_pos_emb=fd[:5], return_cache=True)
+        sc = StaticCache(cache, capacity=16)
+        outs = [out0]
+        for i in range(5, n):
+            o, sc2 = m(x[:, i:i + 1].to(d), rotary_pos_emb=fd[:i + 1], cache=sc,
+                       return_cache=True)
+            assert sc2 is sc
+            outs.append(o)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert_close(torch.cat(outs, dim=1), ref, tol, "static stepwise")
+    assert sc.seq_len() == n
+    tup = sc.as_tuple()
+    q_cache = tup[0] if order == 2 else tup[0][0]
+    assert q_cache.shape[2] == n
+
+
+def test_static_cache_matches_tuple_cache_steps():
+    """The fixed-capacity path and the growing-tuple path give the same step outputs and the
+    same cache contents (bf16, order 3, GQA)."""
+    from poly_attention import StaticCache
+
+    d = dev()
+    torch.manual_seed(13)
+    m, _, _ = _module(3, 2, d, torch.bfloat16)
+    x = torch.randn(2, 10, 64, device=d).to(torch.bfloat16)
+    fd = O.rotary_freqs(64, torch.arange(10)).to(d)
+    with torch.no_grad():
+        _, cache = m(x[:, :4], rotary_pos_emb=fd[:4], return_cache=True)
+        sc = StaticCache(cache, capacity=12)
+        for i in range(4, 10):
+            o_t, cache = m(x[:, i:i + 1], rotary_pos_emb=fd[:i + 1], cache=cache,
+                           return_cache=True)
+            o_s, _ = m(x[:, i:i + 1], rotary_pos_emb=fd[:i + 1], cache=sc, return_cache=True)
+            assert_close(o_s, o_t, 2e-2, f"step {i}")
+    st = sc.as_tuple()
+    for a, b in zip((*st[0], *st[1], *st[2], *st[3]), (*cache[0], *cache[1], *cache[2], *cache[3])):
+        assert a.shape == b.shape
+        assert_close(a, b, 2e-2, "cache contents")
+
+
+def test_static_cache_errors():
+    from poly_attention import StaticCache
+
+    d = dev()
+    m, _, _ = _module(2, 4, d, torch.float32)
+    x = torch.randn(1, 4, 64, device=d)
+    with torch.no_grad():
+        _, cache = m(x, return_cache=True)
+    with pytest.raises(ValueError):
+        StaticCache(cache, capacity=4)
+    sc = StaticCache(cache, capacity=8)
+    with torch.no_grad(), pytest.raises(AssertionError):
+        m(x[:, :2], cache=sc, return_cache=True)  # two tokens (the module's own assert)
+    m3, _, _ = _module(3, 4, d, torch.float32)
+    with torch.no_grad(), pytest.raises(ValueError):
+        m3(x[:, :1], cache=sc, return_cache=True)  # order-2 cache in an order-3 module
+
+
+# ---------------------------------------------------------------------------------------
+# HIP graph: one captured decode step replayed per token
+
+
+def test_static_decode_step_hip_graph_replays():
+    """Capture one StaticCache step (projections, prologue, decode kernels, output
+    projection) into a CUDAGraph and replay it per token, with the program's own eager
+    steps and synchronisations between replays; every replay equals the eager step on a
+    twin cache, and both caches end equal."""
+    from poly_attention import StaticCache
+
+    d = dev()
+    torch.manual_seed(14)
+    m, _, _ = _module(3, 2, d, torch.bfloat16)
+    n0, steps = 8, 6
+    x = torch.randn(2, n0 + steps, 64, device=d).to(torch.bfloat16)
+    fd = O.rotary_freqs(64, torch.arange(n0 + steps)).to(d)
+    with torch.no_grad():
+        _, cache = m(x[:, :n0], rotary_pos_emb=fd[:n0], return_cache=True)
+        eager_sc = StaticCache(cache, capacity=n0 + steps + 2)
+        graph_sc = StaticCache(cache, capacity=n0 + steps + 2)
+        warm_sc = StaticCache(cache, capacity=n0 + steps + 2)
+        xb = x[:, n0:n0 + 1].clone()
+        fb = fd[n0:n0 + 1].clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                m(xb, rotary_pos_emb=fb, cache=warm_sc, return_cache=True)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out_g, _ = m(xb, rotary_pos_emb=fb, cache=graph_sc, return_cache=True)
+        torch.cuda.synchronize()
+        assert graph_sc.seq_len() == n0, "capture must not execute the step"
+        for i in range(n0, n0 + steps):
+            xb.copy_(x[:, i:i + 1])
+            fb.copy_(fd[i:i + 1])
+            graph.replay()
+            torch.cuda.synchronize()
+            ref, _ = m(x[:, i:i + 1], rotary_pos_emb=fd[i:i + 1], cache=eager_sc,
+                       return_cache=True)
+            torch.cuda.synchronize()
+            assert_close(out_g, ref, 1e-2, f"replay at position {i}")
+    assert graph_sc.seq_len() == eager_sc.seq_len() == n0 + steps
+    for a, b in zip(graph_sc.qs + graph_sc.vs + graph_sc.msgs + graph_sc.lses,
+                    eager_sc.qs + eager_sc.vs + eager_sc.msgs + eager_sc.lses):
+        assert_close(a[:, :, :n0 + steps], b[:, :, :n0 + steps], 1e-2, "cache after replays")

@@ -108,3 +108,21 @@ def test_decode_rejects_invalid_order():
     d.order = 2
     d.batch = d.kv_heads = d.n = d.dim = 1
     assert lib.pa_poly_decode(ctypes.byref(d), None) == _lib.PA_EINVAL  # no level tensors
+
+
+def test_prologue_rejects_invalid():
+    lib = _lib.load()
+    p = _lib.PaPrologue()
+    assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EINVAL  # count 0
+    p.batch, p.dim, p.count = 1, 64, 1
+    assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EINVAL  # no source
+    it = p.items[0]
+    it.src.ptr, it.src.sb, it.src.sh, it.src.sn = 0x1000, 64, 64, 64
+    it.src.heads, it.src.dtype = 1, _lib.PA_BF16
+    p.angles, p.rot_dim = 0x2000, 3
+    assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EINVAL  # odd rot_dim
+    p.rot_dim, p.dim = 64, 512
+    assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EUNSUPPORTED
+    p.dim = 64
+    it.cache.ptr, it.cache.heads, it.cache.dtype = 0x3000, 1, _lib.PA_BF16
+    assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EINVAL  # capacity 0
