@@ -229,6 +229,39 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     return (x < rem) ? x * (per + 1) + slot : rem * (per + 1) + (x - rem) * per + slot;
 }
 
+// Causal grids (work per block falls with its rank): logical order in which every XCD runs
+// whole (batch, head) units and dispatches the heaviest blocks of all its units first, so the
+// light blocks fill the end of the kernel.  When the XCD ranges do not hold whole units, the
+// order is unit by unit (heaviest first inside each unit).
+__device__ __forceinline__ void heavy_first(int bid, int nblocks, int nblk, int& unit, int& rank) {
+    const int lid = xcd_remap(bid, nblocks);
+    const int per = nblocks / kNumXcd;
+    if (nblocks % kNumXcd == 0 && per % nblk == 0) {
+        const int x = lid / per, k = lid % per, nu = per / nblk;
+        unit = x * nu + k % nu;
+        rank = k / nu;
+    } else {
+        unit = lid / nblk;
+        rank = lid % nblk;
+    }
+}
+
+#ifndef PA_HEAVY_FIRST
+#define PA_HEAVY_FIRST 1
+#endif
+
+// (unit, rank) of this workgroup: causal grids in heavy_first order, others unit by unit
+template <bool CAUSAL>
+__device__ __forceinline__ void block_order(int nblk, int& unit, int& rank) {
+    if (CAUSAL && PA_HEAVY_FIRST) {
+        heavy_first(blockIdx.x, gridDim.x, nblk, unit, rank);
+    } else {
+        const int lid = xcd_remap(blockIdx.x, gridDim.x);
+        unit = lid / nblk;
+        rank = lid % nblk;
+    }
+}
+
 static inline bool aligned_rows_host(const DView& v, int elems) {
     return ((uintptr_t)v.p % 16 == 0) && v.sb % elems == 0 && v.sh % elems == 0 &&
            v.sn % elems == 0;

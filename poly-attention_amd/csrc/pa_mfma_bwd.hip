@@ -143,9 +143,9 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int hh = lane >> 5, kcol = lane & 31;
     const int nkb = (P.nk + kKvBK - 1) / kKvBK;
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int kblk = lid % nkb;  // causal: the first key blocks carry the most work
-    const int kh = (lid / nkb) % G.hk, b = (lid / nkb) / G.hk;
+    int unit, kblk;  // causal: the first key blocks carry the most work
+    block_order<CAUSAL>(nkb, unit, kblk);
+    const int kh = unit % G.hk, b = unit / G.hk;
     const int rep = P.heads / G.hk;
     const int h0 = kh * rep;
     const int kw0 = kblk * kKvBK + w * 32;  // first key of this wave
@@ -364,9 +364,9 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int hh = lane >> 5, kcol = lane & 31;
     const int nkb = (P.nk + kKvBK - 1) / kKvBK;
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int kblk = lid % nkb;  // causal: the first key blocks carry the most work
-    const int kh = (lid / nkb) % G.hk, b = (lid / nkb) / G.hk;
+    int unit, kblk;  // causal: the first key blocks carry the most work
+    block_order<CAUSAL>(nkb, unit, kblk);
+    const int kh = unit % G.hk, b = unit / G.hk;
     const int rep = P.heads / G.hk;
     const int h0 = kh * rep;
     const int kw0 = kblk * kKvBK + w * 32;  // first key of this wave
@@ -751,9 +751,10 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int hh = lane >> 5, kcol = lane & 31;
     const int nqb = (P.nq + kDqBM - 1) / kDqBM;
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int qblk = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;  // heaviest first
-    const int h = (lid / nqb) % P.heads, b = (lid / nqb) / P.heads;
+    int unit, rank;
+    block_order<CAUSAL>(nqb, unit, rank);
+    const int qblk = CAUSAL ? nqb - 1 - rank : rank;  // heaviest first
+    const int h = unit % P.heads, b = unit / P.heads;
     const int qw0 = qblk * kDqBM + w * 32;
     const int qi = qw0 + kcol;
     const bool q_ok = qi < P.nq;
@@ -888,9 +889,10 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq_dm
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int hh = lane >> 5, kcol = lane & 31;
     const int nqb = (P.nq + kDqBM - 1) / kDqBM;
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int qblk = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;  // heaviest first
-    const int h = (lid / nqb) % P.heads, b = (lid / nqb) / P.heads;
+    int unit, rank;
+    block_order<CAUSAL>(nqb, unit, rank);
+    const int qblk = CAUSAL ? nqb - 1 - rank : rank;  // heaviest first
+    const int h = unit % P.heads, b = unit / P.heads;
     const int qw0 = qblk * kDqBM + w * 32;
     const int qi = qw0 + kcol;
     const bool q_ok = qi < P.nq;

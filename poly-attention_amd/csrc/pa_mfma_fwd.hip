@@ -24,8 +24,13 @@
 //    than k_mfma_fwd_dma on the measured workloads).
 //
 // Rows whose every key is masked are left with lse = NaN for k_simt_fixup, which applies the
-// reference's finite-fill semantics to them.  Workgroups are mapped XCD-aware (pa_mfma.h) and
-// causal query blocks run heaviest first.
+// reference's finite-fill semantics to them.  Workgroups are mapped XCD-aware (pa_mfma.h); in
+// causal grids each XCD dispatches the heaviest query blocks of all its heads first.
+//
+// PA_FWD_PIPE = 1 software-pipelines the direct-to-LDS tile loop (scores of tile t+1 beside
+// the softmax of tile t, four LDS stages).  It is off: at two workgroups per CU it is 2-3%
+// faster than the plain loop at two, but the plain loop at three workgroups per CU (three
+// stages fit) is faster still.
 #include <algorithm>
 #include <type_traits>
 
@@ -43,6 +48,12 @@ namespace pa {
 #endif
 #ifndef PA_FWD_QB64
 #define PA_FWD_QB64 1  // 32-query blocks per wave in the direct-to-LDS kernel at head dim 64
+#endif
+#ifndef PA_FWD_PIPE
+#define PA_FWD_PIPE 0  // 1: software-pipelined tile loop in the direct-to-LDS kernel (QB = 1)
+#endif
+#ifndef PA_FWD_PIPE_NST
+#define PA_FWD_PIPE_NST 4  // LDS stages of the pipelined loop (tiles issued NST - 2 ahead)
 #endif
 
 constexpr int kFwdBM = 128;  // query rows per workgroup
@@ -336,9 +347,9 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
 
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int qb = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;
-    const int bh = lid / nqb;
+    int bh, rank;
+    block_order<CAUSAL>(nqb, bh, rank);
+    const int qb = CAUSAL ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
 
     W wv;
@@ -482,16 +493,19 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     using W = FwdWave<T, D, KB, CAUSAL, SOFTCLAMP, HAS_BIAS, HAS_BIAS && SOFTCLAMP>;
     using M = Mma<T>;
     typedef typename W::frag frag;
-    __shared__ __attribute__((aligned(16))) T sK[kFwdStages * TL::ELEMS];
-    __shared__ __attribute__((aligned(16))) T sV[kFwdStages * TL::ELEMS];
-    __shared__ __attribute__((aligned(16))) float sBraw[kFwdStages][BN];  // raw bias bytes
+    // pipelined loop: the scores of tile t+1 are computed beside the softmax of tile t
+    constexpr bool PIPE = PA_FWD_PIPE && QB == 1;
+    constexpr int NSTG = PIPE ? PA_FWD_PIPE_NST : kFwdStages;
+    __shared__ __attribute__((aligned(16))) T sK[NSTG * TL::ELEMS];
+    __shared__ __attribute__((aligned(16))) T sV[NSTG * TL::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sBraw[NSTG][BN];  // raw bias bytes
     __shared__ __attribute__((aligned(16))) float sBw[4][BN];             // per-wave converted
 
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int nqb = (P.nq + BM - 1) / BM;
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int qb = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;
-    const int bh = lid / nqb;
+    int bh, rank;
+    block_order<CAUSAL>(nqb, bh, rank);
+    const int qb = CAUSAL ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
     const int hh = lane >> 5, kcol = lane & 31;
     const int wq0 = qb * BM + w * 32 * QB;  // this wave's first query
@@ -581,6 +595,100 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     const int ntiles = (kend + BN - 1) / BN;
     const int wave_last = CAUSAL ? (wq0 + 32 * QB - 1) : (1 << 30);
 
+    if constexpr (PIPE) {
+        // Stage of tile t = t % NSTG.  Iteration t computes the scores of tile t+1 (K of stage
+        // t+1), the probabilities of tile t and O += V^T P^T (V of stage t).  At enter(t+1),
+        // every wave has finished iteration t-1, so tile t-1's stage is free: it receives tile
+        // t-1+NSTG = (t+1) + DIST.
+        constexpr int DIST = NSTG - 2;
+        static_assert(DIST >= 1 && DIST <= 2, "pipelined loop: 3 or 4 stages");
+        W& v = wv[0];
+        const int nact = CAUSAL ? min(ntiles, wave_last / BN + 1) : ntiles;
+        auto issue_t = [&](int t) __attribute__((always_inline)) { issue(t * BN, t % NSTG); };
+        auto enter_p = [&](int t) __attribute__((always_inline)) {
+            // tiles issued so far: 0 .. t+DIST-1; those after t may stay in flight
+            if (DIST == 2 && t + 1 < ntiles) wait_vmcnt<NOPS>();
+            else wait_vmcnt<0>();
+            lds_barrier();
+            if (t + DIST < ntiles) issue_t(t + DIST);
+        };
+        auto convert_bias = [&](int stg) __attribute__((always_inline)) {
+            if (HAS_BIAS) {
+                float x;
+                if (bes == 4) x = sBraw[stg][lane];
+                else x = (float)reinterpret_cast<const T*>(&sBraw[stg][0])[lane];
+                sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
+            }
+        };
+        auto scores_of = [&](f32x16_t (&s)[KB], int stg) __attribute__((always_inline)) {
+            const T* K = sK + stg * TL::ELEMS;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                f32x16_t init = zero16();
+                if (FOLD) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float4 bb = *reinterpret_cast<const float4*>(&sBw[w][kb * 32 + 8 * g + 4 * hh]);
+                        init[4 * g] = bb.x;
+                        init[4 * g + 1] = bb.y;
+                        init[4 * g + 2] = bb.z;
+                        init[4 * g + 3] = bb.w;
+                    }
+                }
+                s[kb] = init;
+#pragma unroll
+                for (int c = 0; c < D / 16; ++c)
+                    s[kb] = M::run(ld_frag<T>(K + kb * 32 * D + koff[c]), v.qf[c], s[kb]);
+            }
+        };
+        auto prob_pv = [&](const f32x16_t (&s)[KB], int stg) __attribute__((always_inline)) {
+            const T* V = sV + stg * TL::ELEMS;
+            u32x4_t pk[KB][2];
+            v.l += v.probs(s, v.m == -INFINITY ? 0.f : v.m, pk);
+            frag vf[KB][2][D / 32];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                    for (int x = 0; x < D / 32; ++x) {
+                        const T* base = V + (kb * 32 + 16 * t2) * D + voff[x];
+                        const u32x2_t lo = lds_read_tr(base);
+                        const u32x2_t hi = lds_read_tr(base + 8 * D);
+                        const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
+                        vf[kb][t2][x] = __builtin_bit_cast(frag, v4);
+                    }
+            v.pv(vf, pk);
+        };
+        for (int t = 0; t < DIST && t < ntiles; ++t) issue_t(t);
+        f32x16_t s[KB];
+        enter_p(0);
+        convert_bias(0);
+        scores_of(s, 0);
+        if (nact == 1) v.mask_edges_nk(s, 0);
+        v.settle(v.logits(s, sBw[w]));
+        // iteration t (tile t+1 active and not the last: no mask on its scores)
+        auto iter = [&](int t, bool mask_next) __attribute__((always_inline)) {
+            enter_p(t + 1);
+            const int stn = (t + 1) % NSTG;
+            convert_bias(stn);
+            f32x16_t sn[KB];
+            scores_of(sn, stn);
+            prob_pv(s, t % NSTG);
+            if (mask_next) v.mask_edges_nk(sn, (t + 1) * BN);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) s[kb] = sn[kb];
+            v.settle(v.logits(s, sBw[w]));
+        };
+        int t = 0;
+        for (; t + 2 < nact; ++t) iter(t, false);
+        if (t + 1 < nact) {
+            iter(t, true);
+            ++t;
+        }
+        prob_pv(s, t % NSTG);
+        for (int t2 = nact; t2 < ntiles; ++t2) enter_p(t2);
+    } else {
     issue(0, 0);
     if (ntiles > 1) issue(BN, 1);
 
@@ -661,6 +769,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
         enter(t);
         st = st == 2 ? 0 : st + 1;
     }
+    }  // !PIPE
 
 #pragma unroll
     for (int u = 0; u < QB; ++u) {
@@ -733,9 +842,9 @@ __global__ __launch_bounds__(kPpThreads, 1) void k_mfma_fwd_pp(PassDev P) {
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const bool grp_a = w < 4;
     const int nqb = (P.nq + kPpBM - 1) / kPpBM;
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int qb = CAUSAL ? nqb - 1 - lid % nqb : lid % nqb;
-    const int bh = lid / nqb;
+    int bh, rank;
+    block_order<CAUSAL>(nqb, bh, rank);
+    const int qb = CAUSAL ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
     const int hh = lane >> 5, kcol = lane & 31;
 
