@@ -869,10 +869,10 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
 // HBM -> LDS by buffer_load ... lds, three stages deep.  K is read by rows (S^T = K Q^T) and
 // transposed (dQ^T += K^T dS^T) under the dual-pattern swizzle, V by rows only.  Each wave
 // converts the tile's key bias into accumulator seeds (bias / scale; log2 domain with
-// softclamp), so that P^T = exp2(scale*log2e*S^T - lse*log2e).
-
+// softclamp), so that P^T = exp2(scale*log2e*S^T - lse*log2e).  Three workgroups per CU at
+// head dim 64 (the register budget fits without spills).
 template <typename T, int D, bool CAUSAL, bool SOFTCLAMP, bool HAS_BIAS>
-__global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq_dma(GradDev G) {
+__global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dma(GradDev G) {
     using M = Mma<T>;
     typedef typename M::frag frag;
     constexpr int BN = kDqBN, CPR = D / 8, ELEMS = BN * D;
