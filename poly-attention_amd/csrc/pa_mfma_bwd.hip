@@ -427,13 +427,21 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
     const uint32_t lds_l = lds_addr(&sLraw[0][0]), lds_d = lds_addr(&sDraw[0][0]);
     const uint32_t qbytes = (uint32_t)(((int64_t)(P.nq - 1) * qsn + D) * 2);
     const uint32_t obytes = (uint32_t)(((int64_t)(P.nq - 1) * osn + D) * 2);
-    auto issue = [&](int idx, int stage) __attribute__((always_inline)) {
-        const int h = h0 + idx / nt, q0 = q_start + (idx % nt) * BQ;
-        const srd_t rq = make_srd(P.q.row<T>(b, h, 0), qbytes);
-        const srd_t ro = make_srd(G.dout.row<T>(b, h, 0), obytes);
+    // load cursor: the tiles go head by head (the query heads of this KV group), query tiles
+    // in order; the buffer descriptors change only with the head
+    int cur_h = h0, cur_q0 = q_start;
+    const int q_end = q_start + nt * BQ;
+    srd_t rq, ro, rl, rd;
+    auto set_head = [&](int h) __attribute__((always_inline)) {
+        rq = make_srd(P.q.row<T>(b, h, 0), qbytes);
+        ro = make_srd(G.dout.row<T>(b, h, 0), obytes);
         const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
-        const srd_t rl = make_srd(G.ws_lse + row0, (uint32_t)(P.nq * 4));
-        const srd_t rd = make_srd(G.ws_D + row0, (uint32_t)(P.nq * 4));
+        rl = make_srd(G.ws_lse + row0, (uint32_t)(P.nq * 4));
+        rd = make_srd(G.ws_D + row0, (uint32_t)(P.nq * 4));
+    };
+    set_head(h0);
+    auto issue = [&](int stage) __attribute__((always_inline)) {
+        const int q0 = cur_q0;
         const uint32_t sq = lds_q + (uint32_t)(stage * ELEMS * 2), so = lds_o + (uint32_t)(stage * ELEMS * 2);
 #pragma unroll
         for (int n = 0; n < NL; ++n) {
@@ -445,6 +453,11 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
             const uint32_t o = (uint32_t)(w * 64 + 16 * lane);
             dma16(rl, lds_l + (uint32_t)(stage * BQ * 4 + w * 64), o + (uint32_t)(q0 * 4));
             dma16(rd, lds_d + (uint32_t)(stage * BQ * 4 + w * 64), o + (uint32_t)(q0 * 4));
+        }
+        cur_q0 += BQ;
+        if (cur_q0 == q_end) {
+            cur_q0 = q_start;
+            if (++cur_h < h0 + rep) set_head(cur_h);
         }
     };
 
@@ -474,15 +487,15 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
         return __builtin_bit_cast(frag, v4);
     };
 
-    if (total > 0) issue(0, 0);
-    if (total > 1) issue(1, 1);
+    if (total > 0) issue(0);
+    if (total > 1) issue(1);
     int st = 0;
-    for (int idx = 0; idx < total; ++idx) {
+    int q0 = q_start;  // first query of the tile being computed
+    for (int idx = 0; idx < total; ++idx, q0 = (q0 + BQ == q_end) ? q_start : q0 + BQ) {
         if (idx + 1 < total) wait_vmcnt<NOPS>();
         else wait_vmcnt<0>();
         lds_barrier();
-        if (idx + 2 < total) issue(idx + 2, st == 0 ? 2 : st - 1);
-        const int q0 = q_start + (idx % nt) * BQ;
+        if (idx + 2 < total) issue(st == 0 ? 2 : st - 1);
         const T* Qt = sQ + st * ELEMS;
         const T* Ot = sO + st * ELEMS;
         // this wave's seeds for the tile: -lse/scale (log2-domain lse with softclamp), -D
