@@ -47,7 +47,7 @@ namespace pa {
 #define PA_FWD_PINGPONG 0  // 1: head dim 64 without softclamp takes the 8-wave ping-pong kernel
 #endif
 #ifndef PA_FWD_QB64
-#define PA_FWD_QB64 1  // 32-query blocks per wave in the direct-to-LDS kernel at head dim 64
+#define PA_FWD_QB64 2  // 32-query blocks per wave in the direct-to-LDS kernel at head dim 64
 #endif
 #ifndef PA_FWD_PIPE
 #define PA_FWD_PIPE 0  // 1: software-pipelined tile loop in the direct-to-LDS kernel (QB = 1)
