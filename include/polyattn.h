@@ -19,6 +19,8 @@
  *   pa_decode_prologue the q norms, rotary embedding and cache appends that precede that
  *                      step (n_poly_attention.py:188-191, 206-207; poly_attention.py:271-276,
  *                      282-286).
+ *   pa_rmsnorm_fwd/bwd the per-head q/k RMSNorms of the modules in training and prefill
+ *                      (poly_attention.py:271, n_poly_attention.py:188).
  *
  * Semantics of one pass (per batch b, pass head h, query row i, key j):
  *   s_ij  = scale * <q[b, h/rq, i], k[b, h/rk, j]>           rq = heads / q.heads, etc.
@@ -179,12 +181,34 @@ typedef struct pa_prologue {
     pa_prologue_item items[2 * PA_MAX_ORDER];
 } pa_prologue;
 
+/* Row RMSNorm over the head dim of a [batch, heads, n, dim] view, forward and backward: the
+ * q/k norms of the modules, RMSNorm(dim_head) applied to the per-head projections at
+ * poly_attention.py:271 and n_poly_attention.py:188 (torch.nn.RMSNorm semantics:
+ * y = x * rsqrt(mean(x^2) + eps) * weight, computed in fp32, rounded once).
+ * Forward: x -> y, rstd.  Backward: dy, x, rstd -> dx and (when dweight is set) the weight
+ * gradient summed over all rows in fp32, deterministically (workspace:
+ * pa_rmsnorm_bwd_workspace bytes).  dim must be a multiple of 8 (4 for fp32) and <= 512;
+ * views need 16-byte aligned rows. */
+typedef struct pa_rmsnorm {
+    int32_t     batch, heads, n, dim;
+    float       eps;
+    pa_view     x;              /* input, any strides with unit feature stride */
+    const void* weight;         /* [dim] or NULL (no affine weight) */
+    int32_t     weight_dtype;   /* PA_F32 / PA_F16 / PA_BF16 */
+    pa_view     y;              /* forward output (same dtype as x) */
+    float*      rstd;           /* [batch * heads * n] fp32: written by the forward, read by the backward */
+    pa_view     dy, dx;         /* backward: upstream gradient and input gradient */
+    float*      dweight;        /* backward: [dim] fp32 weight gradient, or NULL */
+    void*       workspace;
+    size_t      workspace_bytes;
+} pa_rmsnorm;
+
 int         pa_abi_version(void);
 const char* pa_strerror(int status);
 int         pa_last_hip_error(void);   /* hipError_t of the last PA_EHIP on this thread */
 /* sizeof of the ABI structs, for binding checks: 0 pa_view, 1 pa_mask, 2 pa_pass,
- * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode, 6 pa_prologue_item, 7 pa_prologue;
- * 0 for other values */
+ * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode, 6 pa_prologue_item, 7 pa_prologue,
+ * 8 pa_rmsnorm; 0 for other values */
 size_t      pa_struct_size(int which);
 
 /* Kernel timing (no counterpart in the reference: a measurement facility for benchmarks).
@@ -205,6 +229,9 @@ int    pa_attn_pass_bwd(const pa_pass_grad* g, void* stream);
 size_t pa_poly_decode_workspace(const pa_decode* d);
 int    pa_poly_decode(const pa_decode* d, void* stream);
 int    pa_decode_prologue(const pa_prologue* p, void* stream);
+int    pa_rmsnorm_fwd(const pa_rmsnorm* r, void* stream);
+size_t pa_rmsnorm_bwd_workspace(const pa_rmsnorm* r);
+int    pa_rmsnorm_bwd(const pa_rmsnorm* r, void* stream);
 
 #ifdef __cplusplus
 }

@@ -167,6 +167,7 @@ size_t pa_struct_size(int which) {
         case 5: return sizeof(pa_decode);
         case 6: return sizeof(pa_prologue_item);
         case 7: return sizeof(pa_prologue);
+        case 8: return sizeof(pa_rmsnorm);
         default: return 0;
     }
 }
@@ -303,6 +304,25 @@ int pa_poly_decode(const pa_decode* d, void* stream) {
 int pa_decode_prologue(const pa_prologue* p, void* stream) {
     if (!p) return PA_EINVAL;
     const int st = launch_prologue(p, static_cast<hipStream_t>(stream));
+    if (st != PA_OK) return st;
+    return finish_launch();
+}
+
+int pa_rmsnorm_fwd(const pa_rmsnorm* r, void* stream) {
+    if (!r) return PA_EINVAL;
+    const int st = launch_rms_fwd(r, static_cast<hipStream_t>(stream));
+    if (st != PA_OK) return st;
+    return finish_launch();
+}
+
+size_t pa_rmsnorm_bwd_workspace(const pa_rmsnorm* r) {
+    if (!r) return 0;
+    return rms_bwd_workspace(r);
+}
+
+int pa_rmsnorm_bwd(const pa_rmsnorm* r, void* stream) {
+    if (!r) return PA_EINVAL;
+    const int st = launch_rms_bwd(r, static_cast<hipStream_t>(stream));
     if (st != PA_OK) return st;
     return finish_launch();
 }

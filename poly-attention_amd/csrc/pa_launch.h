@@ -31,5 +31,8 @@ struct DecodeDev;
 size_t decode_workspace_bytes(const pa_decode* d, int* chunk_out, int* nchunks_out);
 int launch_decode(const pa_decode* d, hipStream_t s);
 int launch_prologue(const pa_prologue* p, hipStream_t s);
+int launch_rms_fwd(const pa_rmsnorm* p, hipStream_t s);
+size_t rms_bwd_workspace(const pa_rmsnorm* p);
+int launch_rms_bwd(const pa_rmsnorm* p, hipStream_t s);
 
 }  // namespace pa

@@ -1,0 +1,283 @@
+// pa_norm.hip -- row RMSNorm over the head dim of [batch, heads, n, dim] views (the q/k norms
+// of the poly-attention modules), forward and backward.  HBM bound: a row group of LPR lanes
+// reads a whole row with 16-byte loads, reduces with DPP inside the row group, and writes the
+// row back; the backward writes dx and accumulates the weight gradient per workgroup into a
+// fixed partial row, summed afterwards in a fixed order (deterministic, no atomics).
+#include "pa_common.h"
+#include "pa_launch.h"
+
+namespace pa {
+
+struct RmsDev {
+    int32_t batch, heads, n, dim, lpr;
+    int64_t rows;
+    float eps;
+    DView x, y, dy, dx;
+    const void* w;
+    int32_t wdt;
+    float* rstd;      // [rows]
+    float* partial;   // [gridDim.x][dim] (backward)
+    float* dw;        // [dim] (backward, fp32)
+};
+
+constexpr int kRmsThreads = 256;
+constexpr int kRmsMaxBlocks = 1024;
+
+template <typename T> struct RVec;
+template <> struct RVec<bf16> { static constexpr int n = 8; };
+template <> struct RVec<f16> { static constexpr int n = 8; };
+template <> struct RVec<float> { static constexpr int n = 4; };
+
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x) {
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+template <typename T>
+__device__ __forceinline__ void load_row(const T* p, bool ok, float* out) {
+    constexpr int E = RVec<T>::n;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (ok) raw = *reinterpret_cast<const u32x4*>(p);
+    const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int i = 0; i < E; ++i) out[i] = to_f(e[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ void store_row(T* p, const float* v) {
+    constexpr int E = RVec<T>::n;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 raw;
+    T* e = reinterpret_cast<T*>(&raw);
+#pragma unroll
+    for (int i = 0; i < E; ++i) e[i] = from_f<T>(v[i]);
+    *reinterpret_cast<u32x4*>(p) = raw;
+}
+
+__device__ __forceinline__ void row_coords(const RmsDev& R, int64_t r, int& b, int& h, int& i) {
+    i = (int)(r % R.n);
+    const int64_t bh = r / R.n;
+    h = (int)(bh % R.heads);
+    b = (int)(bh / R.heads);
+}
+
+// y = round(x * rsqrt(mean(x^2) + eps) * w); rstd saved per row
+template <typename T, int LPR>
+__global__ __launch_bounds__(kRmsThreads) void k_rms_fwd(RmsDev R) {
+    constexpr int E = RVec<T>::n;
+    constexpr int RPB = kRmsThreads / LPR;  // rows per block and pass
+    const int sub = threadIdx.x % LPR, rg = threadIdx.x / LPR;
+    const int d0 = sub * E;
+    const bool dok = d0 < R.dim;
+    float w[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) w[e] = (R.w && dok) ? load_any(R.w, R.wdt, d0 + e) : 1.f;
+    for (int64_t r = (int64_t)blockIdx.x * RPB + rg; r < R.rows; r += (int64_t)gridDim.x * RPB) {
+        int b, h, i;
+        row_coords(R, r, b, h, i);
+        float x[E];
+        load_row<T>(R.x.row<T>(b, h, i) + d0, dok, x);
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss += x[e] * x[e];
+        ss = row_sum<LPR>(ss);
+        const float rs = rsqrtf(ss / (float)R.dim + R.eps);
+        if (dok) {
+            float y[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) y[e] = (x[e] * rs) * w[e];
+            store_row<T>(R.y.wrow<T>(b, h, i) + d0, y);
+        }
+        if (sub == 0) R.rstd[r] = rs;
+    }
+}
+
+// dx = rstd * (g - xhat * mean(g * xhat)), g = dy * w, xhat = x * rstd; the block's weight
+// gradient partial sum_rows dy * xhat goes to partial[blockIdx.x]
+template <typename T, int LPR>
+__global__ __launch_bounds__(kRmsThreads) void k_rms_bwd(RmsDev R) {
+    constexpr int E = RVec<T>::n;
+    constexpr int RPB = kRmsThreads / LPR;
+    __shared__ float s_dw[kRmsThreads / 64][512];
+    const int sub = threadIdx.x % LPR, rg = threadIdx.x / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d0 = sub * E;
+    const bool dok = d0 < R.dim;
+    float w[E], acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        w[e] = (R.w && dok) ? load_any(R.w, R.wdt, d0 + e) : 1.f;
+        acc[e] = 0.f;
+    }
+    for (int64_t r = (int64_t)blockIdx.x * RPB + rg; r < R.rows; r += (int64_t)gridDim.x * RPB) {
+        int b, h, i;
+        row_coords(R, r, b, h, i);
+        float x[E], dy[E];
+        load_row<T>(R.x.row<T>(b, h, i) + d0, dok, x);
+        load_row<T>(R.dy.row<T>(b, h, i) + d0, dok, dy);
+        const float rs = R.rstd[r];
+        float c = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float xh = x[e] * rs;
+            c += dy[e] * w[e] * xh;
+            acc[e] += dy[e] * xh;
+        }
+        c = row_sum<LPR>(c) / (float)R.dim;
+        if (dok) {
+            float dx[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) dx[e] = rs * (dy[e] * w[e] - x[e] * rs * c);
+            store_row<T>(R.dx.wrow<T>(b, h, i) + d0, dx);
+        }
+    }
+    if (!R.partial) return;
+    // reduce acc over the row groups of the wave (lanes sub, sub + LPR, ...), then the waves
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+        for (int off = LPR; off < 64; off <<= 1) acc[e] += __shfl_xor(acc[e], off);
+    if (lane < LPR && dok)
+#pragma unroll
+        for (int e = 0; e < E; ++e) s_dw[wave][d0 + e] = acc[e];
+    __syncthreads();
+    for (int f = threadIdx.x; f < R.dim; f += kRmsThreads) {
+        float s = 0.f;
+#pragma unroll
+        for (int v = 0; v < kRmsThreads / 64; ++v) s += s_dw[v][f];
+        R.partial[(int64_t)blockIdx.x * R.dim + f] = s;
+    }
+}
+
+// dw[f] = sum over the nparts partial rows, in a fixed order: 32 lanes stride the partials,
+// then a fixed tree; one wave per feature
+__global__ __launch_bounds__(kRmsThreads) void k_rms_dw(RmsDev R, int nparts) {
+    const int lane = threadIdx.x & 63;
+    const int f = blockIdx.x * (kRmsThreads / 64) + (threadIdx.x >> 6);
+    if (f >= R.dim) return;
+    float s = 0.f;
+    for (int p = lane; p < nparts; p += 64) s += R.partial[(int64_t)p * R.dim + f];
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0) R.dw[f] = s;
+}
+
+// ---------------------------------------------------------------------------------------
+
+static int rms_blocks(const RmsDev& R) {
+    const int64_t rpb = kRmsThreads / R.lpr;
+    const int64_t need = (R.rows + rpb - 1) / rpb;
+    return (int)(need < kRmsMaxBlocks ? need : kRmsMaxBlocks);
+}
+
+static int rms_setup(const pa_rmsnorm* p, RmsDev& R, bool bwd) {
+    if (p->batch < 1 || p->heads < 1 || p->n < 1 || p->dim < 1) return PA_EINVAL;
+    const int T = p->x.dtype;
+    if (T != PA_F32 && T != PA_F16 && T != PA_BF16) return PA_EINVAL;
+    const int es = T == PA_F32 ? 4 : 2, E = 16 / es;
+    if (p->dim % E != 0 || p->dim > 512) return PA_EUNSUPPORTED;
+    auto view_ok = [&](const pa_view& v) {
+        if (!v.ptr || v.dtype != T || v.heads != p->heads) return false;
+        return (uintptr_t)v.ptr % 16 == 0 && v.sb % E == 0 && v.sh % E == 0 && v.sn % E == 0;
+    };
+    if (!view_ok(p->x)) return PA_EINVAL;
+    if (!bwd && !view_ok(p->y)) return PA_EINVAL;
+    if (bwd && (!view_ok(p->dy) || !view_ok(p->dx))) return PA_EINVAL;
+    if (!p->rstd) return PA_EINVAL;
+    if (p->weight && p->weight_dtype != PA_F32 && p->weight_dtype != PA_F16 &&
+        p->weight_dtype != PA_BF16)
+        return PA_EINVAL;
+    int lpr = 1;
+    while (lpr * E < p->dim) lpr <<= 1;
+    auto mk = [](const pa_view& v) {
+        DView x;
+        x.p = static_cast<char*>(v.ptr);
+        x.sb = v.sb;
+        x.sh = v.sh;
+        x.sn = v.sn;
+        x.hdiv = 1;
+        x.dtype = v.dtype;
+        return x;
+    };
+    R.batch = p->batch;
+    R.heads = p->heads;
+    R.n = p->n;
+    R.dim = p->dim;
+    R.lpr = lpr;
+    R.rows = (int64_t)p->batch * p->heads * p->n;
+    R.eps = p->eps;
+    R.x = mk(p->x);
+    R.y = mk(p->y);
+    R.dy = mk(p->dy);
+    R.dx = mk(p->dx);
+    R.w = p->weight;
+    R.wdt = p->weight_dtype;
+    R.rstd = p->rstd;
+    R.partial = nullptr;
+    R.dw = p->dweight;
+    return PA_OK;
+}
+
+template <typename T>
+static void rms_launch(const RmsDev& R, bool bwd, hipStream_t s) {
+    const dim3 grid(rms_blocks(R));
+#define PA_RMS_CASE(L)                                                                       \
+    case L:                                                                                  \
+        if (bwd) hipLaunchKernelGGL((k_rms_bwd<T, L>), grid, dim3(kRmsThreads), 0, s, R);    \
+        else hipLaunchKernelGGL((k_rms_fwd<T, L>), grid, dim3(kRmsThreads), 0, s, R);        \
+        break;
+    switch (R.lpr) {
+        PA_RMS_CASE(1)
+        PA_RMS_CASE(2)
+        PA_RMS_CASE(4)
+        PA_RMS_CASE(8)
+        PA_RMS_CASE(16)
+        PA_RMS_CASE(32)
+        default: PA_RMS_CASE(64)
+    }
+#undef PA_RMS_CASE
+}
+
+int launch_rms_fwd(const pa_rmsnorm* p, hipStream_t s) {
+    RmsDev R;
+    const int st = rms_setup(p, R, false);
+    if (st != PA_OK) return st;
+    ProfScope ps("rms_fwd", s);
+    if (p->x.dtype == PA_F32) rms_launch<float>(R, false, s);
+    else if (p->x.dtype == PA_F16) rms_launch<f16>(R, false, s);
+    else rms_launch<bf16>(R, false, s);
+    return PA_OK;
+}
+
+size_t rms_bwd_workspace(const pa_rmsnorm* p) {
+    RmsDev R;
+    if (rms_setup(p, R, true) != PA_OK) return 0;
+    return (size_t)rms_blocks(R) * p->dim * sizeof(float);
+}
+
+int launch_rms_bwd(const pa_rmsnorm* p, hipStream_t s) {
+    RmsDev R;
+    const int st = rms_setup(p, R, true);
+    if (st != PA_OK) return st;
+    const int nb = rms_blocks(R);
+    if (p->dweight) {
+        const size_t need = (size_t)nb * p->dim * sizeof(float);
+        if (!p->workspace || p->workspace_bytes < need) return PA_EWORKSPACE;
+        R.partial = static_cast<float*>(p->workspace);
+    }
+    {
+        ProfScope ps("rms_bwd", s);
+        if (p->x.dtype == PA_F32) rms_launch<float>(R, true, s);
+        else if (p->x.dtype == PA_F16) rms_launch<f16>(R, true, s);
+        else rms_launch<bf16>(R, true, s);
+    }
+    if (p->dweight) {
+        ProfScope ps("rms_dw", s);
+        const dim3 grid((p->dim + kRmsThreads / 64 - 1) / (kRmsThreads / 64));
+        hipLaunchKernelGGL(k_rms_dw, grid, dim3(kRmsThreads), 0, s, R, nb);
+    }
+    return PA_OK;
+}
+
+}  // namespace pa

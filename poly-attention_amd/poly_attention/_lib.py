@@ -44,6 +44,9 @@ EXPORTED_SYMBOLS = (
     "pa_poly_decode_workspace",
     "pa_poly_decode",
     "pa_decode_prologue",
+    "pa_rmsnorm_fwd",
+    "pa_rmsnorm_bwd_workspace",
+    "pa_rmsnorm_bwd",
 )
 
 
@@ -157,12 +160,32 @@ class PaPrologue(ctypes.Structure):
     ]
 
 
+class PaRmsNorm(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int32),
+        ("heads", c_int32),
+        ("n", c_int32),
+        ("dim", c_int32),
+        ("eps", c_float),
+        ("x", PaView),
+        ("weight", c_void_p),
+        ("weight_dtype", c_int32),
+        ("y", PaView),
+        ("rstd", c_void_p),
+        ("dy", PaView),
+        ("dx", PaView),
+        ("dweight", c_void_p),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
 class PaKernelTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("launches", c_int64), ("total_ms", ctypes.c_double)]
 
 
 STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode, PaPrologueItem,
-           PaPrologue)
+           PaPrologue, PaRmsNorm)
 
 
 class PolyAttnError(RuntimeError):
@@ -204,6 +227,12 @@ def _configure(lib) -> None:
     lib.pa_poly_decode.argtypes = [ctypes.POINTER(PaDecode), c_void_p]
     lib.pa_decode_prologue.restype = c_int
     lib.pa_decode_prologue.argtypes = [ctypes.POINTER(PaPrologue), c_void_p]
+    lib.pa_rmsnorm_fwd.restype = c_int
+    lib.pa_rmsnorm_fwd.argtypes = [ctypes.POINTER(PaRmsNorm), c_void_p]
+    lib.pa_rmsnorm_bwd_workspace.restype = c_size_t
+    lib.pa_rmsnorm_bwd_workspace.argtypes = [ctypes.POINTER(PaRmsNorm)]
+    lib.pa_rmsnorm_bwd.restype = c_int
+    lib.pa_rmsnorm_bwd.argtypes = [ctypes.POINTER(PaRmsNorm), c_void_p]
 
 
 def load(path: str | os.PathLike | None = None):

@@ -11,6 +11,8 @@
 * ``poly_decode_step`` -- the cached single-token step through ``pa_poly_decode``.
 * ``decode_prologue`` -- the q norms, rotary and cache appends before a fixed-capacity
   (StaticCache) step, through ``pa_decode_prologue``.
+* ``rms_norm`` -- the per-head q/k RMSNorm (``polyattn::rms_norm`` custom op with autograd)
+  through ``pa_rmsnorm_fwd`` / ``pa_rmsnorm_bwd``.
 """
 
 from __future__ import annotations
@@ -29,6 +31,7 @@ from ._lib import (
     PaMask,
     PaPass,
     PaPassGrad,
+    PaRmsNorm,
     PaView,
 )
 
@@ -252,6 +255,109 @@ def attn_pass(q: Tensor, k: Tensor, v: Tensor, vmul: Optional[Tensor] = None,
     scale = q.shape[-1] ** -0.5 if scale is None else scale
     return pass_fwd_op(q, k, v, vmul, bias, key_mask, query_mask, bool(causal),
                        float(softclamp or 0.0), float(scale), bool(may_degenerate))
+
+
+# ---------------------------------------------------------------------------------------
+# per-head RMSNorm
+
+
+def _rms_struct(x: Tensor, weight: Optional[Tensor], eps: float) -> PaRmsNorm:
+    r = PaRmsNorm()
+    r.batch, r.heads, r.n, r.dim = x.shape
+    r.eps = float(eps)
+    r.x = _view(x)
+    if weight is not None:
+        r.weight, r.weight_dtype = weight.data_ptr(), DTYPE_CODE[weight.dtype]
+    return r
+
+
+def rms_supported(x: Tensor, weight: Optional[Tensor]) -> bool:
+    """Shapes and layouts pa_rmsnorm takes: [B, H, N, d] with 16-byte aligned rows."""
+    if x.dim() != 4 or x.dtype not in DTYPE_CODE or not x.is_cuda:
+        return False
+    e = 4 if x.dtype == torch.float32 else 8
+    d = x.shape[-1]
+    if d % e or d > 512 or x.stride(-1) != 1 or x.numel() == 0:
+        return False
+    if x.data_ptr() % 16 or any(st % e for st in x.stride()[:3]):
+        return False
+    return weight is None or (weight.dim() == 1 and weight.numel() == d
+                              and weight.dtype in DTYPE_CODE and weight.is_contiguous())
+
+
+@torch.library.custom_op("polyattn::rms_norm", mutates_args=(), device_types="cuda")
+def rms_norm_op(x: Tensor, weight: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor]:
+    lib = _lib.load()
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    rstd = torch.empty(x.shape[:3], dtype=torch.float32, device=x.device)
+    r = _rms_struct(x, weight, eps)
+    r.y, r.rstd = _view(y), rstd.data_ptr()
+    with torch.cuda.device(x.device):
+        _lib.check(lib.pa_rmsnorm_fwd(ctypes.byref(r), _stream(x)), "pa_rmsnorm_fwd")
+    return y, rstd
+
+
+@rms_norm_op.register_fake
+def _(x, weight, eps):
+    return x.new_empty(x.shape), x.new_empty(x.shape[:3], dtype=torch.float32)
+
+
+@torch.library.custom_op("polyattn::rms_norm_bwd", mutates_args=(), device_types="cuda")
+def rms_norm_bwd_op(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tensor,
+                    eps: float) -> tuple[Tensor, Tensor]:
+    lib = _lib.load()
+    dy = dy if dy.stride(-1) == 1 and dy.data_ptr() % 16 == 0 else dy.contiguous()
+    if any(st % (4 if dy.dtype == torch.float32 else 8) for st in dy.stride()[:3]):
+        dy = dy.contiguous()
+    dx = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    r = _rms_struct(x, weight, eps)
+    r.rstd = rstd.data_ptr()
+    r.dy, r.dx = _view(dy), _view(dx)
+    dw32 = None
+    if weight is not None:
+        dw32 = torch.empty(x.shape[-1], dtype=torch.float32, device=x.device)
+        r.dweight = dw32.data_ptr()
+    ws_bytes = lib.pa_rmsnorm_bwd_workspace(ctypes.byref(r))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    r.workspace, r.workspace_bytes = ws.data_ptr(), ws_bytes
+    with torch.cuda.device(x.device):
+        _lib.check(lib.pa_rmsnorm_bwd(ctypes.byref(r), _stream(x)), "pa_rmsnorm_bwd")
+    dw = dw32.to(weight.dtype) if weight is not None else x.new_empty(0)
+    return dx, dw
+
+
+@rms_norm_bwd_op.register_fake
+def _(dy, x, weight, rstd, eps):
+    return x.new_empty(x.shape), (weight.new_empty(weight.shape) if weight is not None
+                                  else x.new_empty(0))
+
+
+def _rms_setup(ctx, inputs, output):
+    x, weight, eps = inputs
+    _, rstd = output
+    ctx.save_for_backward(x, weight, rstd)
+    ctx.eps = eps
+    ctx.set_materialize_grads(False)
+
+
+def _rms_backward(ctx, dy, drstd):
+    x, weight, rstd = ctx.saved_tensors
+    if dy is None:
+        return None, None, None
+    dx, dw = rms_norm_bwd_op(dy, x, weight, rstd, ctx.eps)
+    return dx, (dw if weight is not None else None), None
+
+
+torch.library.register_autograd("polyattn::rms_norm", _rms_backward, setup_context=_rms_setup)
+
+
+def rms_norm(x: Tensor, weight: Optional[Tensor], eps: Optional[float]) -> Tensor:
+    """torch.nn.RMSNorm(d)(x) over the last dim of a [B, H, N, d] CUDA tensor on the HIP
+    kernels (the caller checks rms_supported).  eps=None is torch's default, the epsilon of
+    the fp32 op-math type."""
+    if eps is None:
+        eps = torch.finfo(torch.float32).eps
+    return rms_norm_op(x, weight, float(eps))[0]
 
 
 # ---------------------------------------------------------------------------------------

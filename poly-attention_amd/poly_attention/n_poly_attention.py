@@ -30,7 +30,7 @@ from ._helpers import (
     where_keys,
     where_queries,
 )
-from .poly_attention import _compute_dtype, _static_decode_step, fused_available
+from .poly_attention import _compute_dtype, _q_norms, _static_decode_step, fused_available
 from .rotary import RotaryEmbedding, apply_rotary_emb
 
 LinearNoBias = partial(nn.Linear, bias=False)
@@ -182,7 +182,7 @@ class NPolyAttention(Module):
             if exists(root_value) and self.is_gqa:
                 root_value = repeat_kv(root_value, self.num_rep)
         else:
-            qs = tuple(norm(q) for norm, q in zip(self.q_norms, qs))
+            qs = _q_norms(self, self.q_norms, qs)
 
             if exists(rotary_pos_emb):
                 qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)

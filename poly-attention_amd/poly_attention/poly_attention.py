@@ -43,6 +43,22 @@ def fused_available() -> bool:
     return _lib.available()
 
 
+def _q_norms(module, norms, qs):
+    """The per-head q/k RMSNorms (poly_attention.py:271, n_poly_attention.py:188): on the fused
+    GPU path through pa_rmsnorm (forward and backward), else torch.nn.RMSNorm."""
+    out = []
+    for norm, q in zip(norms, qs):
+        if (module._use_fused(q) and isinstance(norm, RMSNorm)
+                and tuple(norm.normalized_shape) == (q.shape[-1],)):
+            from . import _ops
+
+            if _ops.rms_supported(q, norm.weight):
+                out.append(_ops.rms_norm(q, norm.weight, norm.eps))
+                continue
+        out.append(norm(q))
+    return tuple(out)
+
+
 def _static_decode_step(module, qs, vs, mask, context_mask, rotary_pos_emb,
                         cache: _cache.StaticCache) -> Tensor:
     """A single-token step on a StaticCache, for both module orders.
@@ -316,7 +332,7 @@ class Order2PolyAttention(Module):
             new_cache = cache
             v2 = repeat_kv(v2, self.num_rep) if self.is_gqa and exists(v2) else v2
         else:
-            qs = tuple(norm(q) for norm, q in zip(self.q_norms, qs))
+            qs = _q_norms(self, self.q_norms, qs)
 
             if exists(rotary_pos_emb):
                 qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)

@@ -1,0 +1,130 @@
+"""GPU: the per-head q/k RMSNorm (pa_rmsnorm_fwd / pa_rmsnorm_bwd through the
+``polyattn::rms_norm`` custom op) against torch.nn.RMSNorm, and the modules' gradients with
+the fused norms against the CPU oracle.
+
+Tolerances: forward fp32 max-abs <= 1e-5, bf16 within one bf16 ulp; gradients fp32 <= 1e-4,
+bf16 <= 2e-2 (relative to max(1, max|reference|)).
+"""
+
+import pytest
+import torch
+
+import oracle.poly_oracle as O
+
+pytestmark = pytest.mark.gpu
+param = pytest.mark.parametrize
+
+
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda")
+
+
+def rel_err(got, ref):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    return (got - ref).abs().max().item() / max(1.0, ref.abs().max().item())
+
+
+def split_heads(t, heads, d):
+    """[B, N, 2*heads*d] -> the first of two [B, heads, N, d] strided views (module layout)."""
+    B, N, _ = t.shape
+    return t.reshape(B, N, 2, heads, d).permute(2, 0, 3, 1, 4)[0]
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("d", (32, 64, 128))
+@param("affine", (True, False))
+def test_rmsnorm_forward_matches_torch(dtype, d, affine):
+    from poly_attention import _ops
+
+    dv = dev()
+    torch.manual_seed(0)
+    H = 3
+    x = split_heads(torch.randn(2, 37, 2 * H * d, device=dv).to(dtype), H, d)
+    norm = torch.nn.RMSNorm(d, elementwise_affine=affine).to(dv, dtype)
+    if affine:
+        with torch.no_grad():
+            norm.weight.copy_(1 + 0.3 * torch.randn(d, device=dv))
+    assert _ops.rms_supported(x, norm.weight)
+    with torch.no_grad():
+        ref = norm(x)
+        got = _ops.rms_norm(x, norm.weight, norm.eps)
+    if dtype == torch.float32:
+        assert rel_err(got, ref) <= 1e-5
+    else:
+        diff = (got.float() - ref.float()).abs()
+        ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -7
+        assert bool((diff <= ulp).all()), diff.max().item()
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("d", (64, 128))
+def test_rmsnorm_backward_matches_fp32_reference(dtype, d):
+    from poly_attention import _ops
+
+    dv = dev()
+    torch.manual_seed(1)
+    H = 4
+    base = torch.randn(2, 50, 2 * H * d, device=dv).to(dtype)
+    w = (1 + 0.3 * torch.randn(d, device=dv)).to(dtype)
+    dy = torch.randn(2, H, 50, d, device=dv).to(dtype)
+    # fp32 reference on the same rounded inputs
+    xr = split_heads(base.float(), H, d).detach().requires_grad_()
+    wr = w.float().detach().requires_grad_()
+    torch.nn.functional.rms_norm(xr, (d,), wr, torch.finfo(torch.float32).eps).backward(dy.float())
+    x = split_heads(base, H, d).detach().requires_grad_()
+    wg = w.detach().requires_grad_()
+    _ops.rms_norm(x, wg, None).backward(dy)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert rel_err(x.grad, xr.grad) <= tol
+    assert rel_err(wg.grad, wr.grad) <= tol * 4  # a sum over 400 rows
+    assert wg.grad.dtype == dtype
+
+
+def test_rmsnorm_weight_grad_is_deterministic():
+    from poly_attention import _ops
+
+    dv = dev()
+    torch.manual_seed(2)
+    x = torch.randn(4, 16, 1000, 64, device=dv, dtype=torch.bfloat16)
+    w = torch.ones(64, device=dv, dtype=torch.bfloat16, requires_grad=True)
+    dy = torch.randn_like(x)
+    grads = []
+    for _ in range(2):
+        w.grad = None
+        _ops.rms_norm(x, w, None).backward(dy)
+        grads.append(w.grad.clone())
+    assert torch.equal(grads[0], grads[1])
+
+
+@param("order", (2, 3))
+def test_module_grads_with_fused_norms(order):
+    """Module forward + backward on the GPU (fused core and fused q/k norms) against the CPU
+    oracle's autograd: input and parameter gradients, including the q-norm weights."""
+    from poly_attention import NPolyAttention, Order2PolyAttention
+
+    dv = dev()
+    torch.manual_seed(3)
+    cfg = dict(heads=4, dim_head=64, causal=True)
+    if order == 2:
+        m = Order2PolyAttention(dim=64, **cfg)
+        fwd = O.order2_forward
+    else:
+        m = NPolyAttention(dim=64, order=3, **cfg)
+        fwd = O.npoly_forward
+        cfg = dict(cfg, order=3)
+    with torch.no_grad():
+        for n in m.q_norms:
+            n.weight.copy_(1 + 0.3 * torch.randn_like(n.weight))
+    x = torch.randn(2, 40, 64)
+    g = torch.randn(2, 40, 64)
+    params = {k: v.detach().clone().requires_grad_() for k, v in m.state_dict().items()}
+    xr = x.clone().requires_grad_()
+    fwd(params, cfg, xr).backward(g)
+    m = m.to(dv)
+    xg = x.to(dv).requires_grad_()
+    m(xg).backward(g.to(dv))
+    assert rel_err(xg.grad, xr.grad) <= 1e-4
+    for name, p in m.named_parameters():
+        assert rel_err(p.grad, params[name].grad) <= 1e-4, name

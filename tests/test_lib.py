@@ -126,3 +126,22 @@ def test_prologue_rejects_invalid():
     p.dim = 64
     it.cache.ptr, it.cache.heads, it.cache.dtype = 0x3000, 1, _lib.PA_BF16
     assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EINVAL  # capacity 0
+
+
+def test_rmsnorm_rejects_invalid():
+    lib = _lib.load()
+    r = _lib.PaRmsNorm()
+    assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL
+    r.batch = r.heads = r.n = 1
+    r.dim = 60  # not a multiple of 8 elements
+    r.x.ptr, r.x.heads, r.x.dtype = 0x1000, 1, _lib.PA_BF16
+    assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EUNSUPPORTED
+    r.dim = 64
+    r.x.sb = r.x.sh = r.x.sn = 64
+    assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # no output view
+    r.y = r.x
+    assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # no rstd
+    r.dy = r.dx = r.x
+    r.rstd, r.dweight = 0x2000, 0x3000
+    assert lib.pa_rmsnorm_bwd_workspace(ctypes.byref(r)) > 0
+    assert lib.pa_rmsnorm_bwd(ctypes.byref(r), None) == _lib.PA_EWORKSPACE
