@@ -604,9 +604,24 @@ def main():
     log(f"[bench] kernels: {kernels}")
 
     module_ms = None
+    module_kernels = None
     if not args.no_module:
         module_ms = time_steps(lambda: module_step(m, x, dx), max(3, args.steps // 2), 2)
         log(f"[bench] module fwd+bwd {module_ms:.3f} ms/step")
+        with _lib.KernelProfile() as mprof:
+            for _ in range(3):
+                module_step(m, x, dx)
+        # the per-head q/k RMSNorms: x read + y written (fwd); x, dy read + dx written (bwd)
+        norm_elems = B * H * N * DH
+        module_kernels = {}
+        for k, (n_l, t) in mprof.times.items():
+            rec = {"launches_per_step": n_l // 3, "avg_ms": round(t / n_l, 4)}
+            moved = {"rms_fwd": 2 * norm_elems * 2 + B * H * N * 4,
+                     "rms_bwd": 3 * norm_elems * 2 + B * H * N * 4}.get(k)
+            if moved:
+                rec["GB_per_s"] = round(moved / (t / n_l / 1e3) / 1e9, 1)
+            module_kernels[k] = rec
+        log(f"[bench] module kernels {module_kernels}")
     del qs, dout
     torch.cuda.empty_cache()
 
@@ -662,6 +677,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "module_ms_per_step": round(module_ms, 4) if module_ms else None,
+        "module_kernels": module_kernels,
         "cpu_baseline": cpu,
         "decode": decode,
         "vit": vit,

@@ -8,20 +8,48 @@
 
 namespace pa {
 
+// n / d for n < 2^31 by a multiply-high and a shift (d fixed per launch; l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1)
+struct FastDiv {
+    uint32_t d, m, l;
+    __device__ __forceinline__ uint32_t div(uint32_t n) const { return (__umulhi(m, n) + n) >> l; }
+};
+static FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    FastDiv f;
+    f.d = d;
+    f.l = l;
+    f.m = (uint32_t)((((1ull << 32) * ((1ull << l) - d)) / d) + 1);
+    return f;
+}
+
+// a strided [batch, heads, n, dim] tensor as the norm kernels address it (element strides)
+struct RView {
+    char* p;
+    int64_t sb, sh, sn;
+    template <typename T> __device__ __forceinline__ T* at(uint32_t b, uint32_t h, uint32_t i) const {
+        return reinterpret_cast<T*>(p) + ((int64_t)b * sb + (int64_t)h * sh + (int64_t)i * sn);
+    }
+};
+
 struct RmsDev {
     int32_t batch, heads, n, dim, lpr;
-    int64_t rows;
-    float eps;
-    DView x, y, dy, dx;
+    int32_t hfast;    // rows walk heads fastest (input laid out [B, N, H, dim])
+    uint32_t rows;    // < 2^31 (checked on the host)
+    FastDiv fd_n, fd_h;
+    float eps, inv_dim;
+    RView x, y, dy, dx;
     const void* w;
     int32_t wdt;
-    float* rstd;      // [rows]
+    float* rstd;      // [batch][heads][n]
     float* partial;   // [gridDim.x][dim] (backward)
     float* dw;        // [dim] (backward, fp32)
 };
 
 constexpr int kRmsThreads = 256;
 constexpr int kRmsMaxBlocks = 1024;
+constexpr int kRmsU = 4;  // rows per row group and pass
 
 template <typename T> struct RVec;
 template <> struct RVec<bf16> { static constexpr int n = 8; };
@@ -57,41 +85,65 @@ __device__ __forceinline__ void store_row(T* p, const float* v) {
     *reinterpret_cast<u32x4*>(p) = raw;
 }
 
-__device__ __forceinline__ void row_coords(const RmsDev& R, int64_t r, int& b, int& h, int& i) {
-    i = (int)(r % R.n);
-    const int64_t bh = r / R.n;
-    h = (int)(bh % R.heads);
-    b = (int)(bh / R.heads);
+// row r -> (batch, head, position) in the order that walks the input's memory sequentially
+__device__ __forceinline__ void row_coords(const RmsDev& R, uint32_t r, uint32_t& b, uint32_t& h,
+                                           uint32_t& i) {
+    if (R.hfast) {
+        const uint32_t q1 = R.fd_h.div(r);
+        h = r - q1 * R.fd_h.d;
+        b = R.fd_n.div(q1);
+        i = q1 - b * R.fd_n.d;
+    } else {
+        const uint32_t q1 = R.fd_n.div(r);
+        i = r - q1 * R.fd_n.d;
+        b = R.fd_h.div(q1);
+        h = q1 - b * R.fd_h.d;
+    }
 }
 
-// y = round(x * rsqrt(mean(x^2) + eps) * w); rstd saved per row
+__device__ __forceinline__ uint32_t rstd_index(const RmsDev& R, uint32_t b, uint32_t h, uint32_t i) {
+    return (b * R.fd_h.d + h) * R.fd_n.d + i;
+}
+
+// y = round(x * rsqrt(mean(x^2) + eps) * w); rstd saved per row.  Each row group handles
+// kRmsU rows per pass, their loads issued together (memory-level parallelism).
 template <typename T, int LPR>
 __global__ __launch_bounds__(kRmsThreads) void k_rms_fwd(RmsDev R) {
     constexpr int E = RVec<T>::n;
-    constexpr int RPB = kRmsThreads / LPR;  // rows per block and pass
+    constexpr int RPB = kRmsThreads / LPR;  // row groups per block
     const int sub = threadIdx.x % LPR, rg = threadIdx.x / LPR;
     const int d0 = sub * E;
     const bool dok = d0 < R.dim;
     float w[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) w[e] = (R.w && dok) ? load_any(R.w, R.wdt, d0 + e) : 1.f;
-    for (int64_t r = (int64_t)blockIdx.x * RPB + rg; r < R.rows; r += (int64_t)gridDim.x * RPB) {
-        int b, h, i;
-        row_coords(R, r, b, h, i);
-        float x[E];
-        load_row<T>(R.x.row<T>(b, h, i) + d0, dok, x);
-        float ss = 0.f;
+    const uint32_t step = gridDim.x * RPB;
+    for (uint32_t r0 = blockIdx.x * RPB + rg; r0 < R.rows; r0 += step * kRmsU) {
+        float x[kRmsU][E];
+        uint32_t b[kRmsU], h[kRmsU], i[kRmsU];
 #pragma unroll
-        for (int e = 0; e < E; ++e) ss += x[e] * x[e];
-        ss = row_sum<LPR>(ss);
-        const float rs = rsqrtf(ss / (float)R.dim + R.eps);
-        if (dok) {
-            float y[E];
-#pragma unroll
-            for (int e = 0; e < E; ++e) y[e] = (x[e] * rs) * w[e];
-            store_row<T>(R.y.wrow<T>(b, h, i) + d0, y);
+        for (int u = 0; u < kRmsU; ++u) {
+            const uint32_t r = r0 + u * step;
+            row_coords(R, r < R.rows ? r : 0u, b[u], h[u], i[u]);
+            load_row<T>(R.x.at<T>(b[u], h[u], i[u]) + d0, dok && r < R.rows, x[u]);
         }
-        if (sub == 0) R.rstd[r] = rs;
+#pragma unroll
+        for (int u = 0; u < kRmsU; ++u) {
+            const uint32_t r = r0 + u * step;
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) ss += x[u][e] * x[u][e];
+            ss = row_sum<LPR>(ss);
+            if (r >= R.rows) continue;
+            const float rs = rsqrtf(ss * R.inv_dim + R.eps);
+            if (dok) {
+                float y[E];
+#pragma unroll
+                for (int e = 0; e < E; ++e) y[e] = (x[u][e] * rs) * w[e];
+                store_row<T>(R.y.at<T>(b[u], h[u], i[u]) + d0, y);
+            }
+            if (sub == 0) R.rstd[rstd_index(R, b[u], h[u], i[u])] = rs;
+        }
     }
 }
 
@@ -112,26 +164,35 @@ __global__ __launch_bounds__(kRmsThreads) void k_rms_bwd(RmsDev R) {
         w[e] = (R.w && dok) ? load_any(R.w, R.wdt, d0 + e) : 1.f;
         acc[e] = 0.f;
     }
-    for (int64_t r = (int64_t)blockIdx.x * RPB + rg; r < R.rows; r += (int64_t)gridDim.x * RPB) {
-        int b, h, i;
-        row_coords(R, r, b, h, i);
-        float x[E], dy[E];
-        load_row<T>(R.x.row<T>(b, h, i) + d0, dok, x);
-        load_row<T>(R.dy.row<T>(b, h, i) + d0, dok, dy);
-        const float rs = R.rstd[r];
-        float c = 0.f;
+    const uint32_t step = gridDim.x * RPB;
+    for (uint32_t r0 = blockIdx.x * RPB + rg; r0 < R.rows; r0 += step * kRmsU) {
+        float x[kRmsU][E], dy[kRmsU][E], rs[kRmsU];
+        uint32_t b[kRmsU], h[kRmsU], i[kRmsU];
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const float xh = x[e] * rs;
-            c += dy[e] * w[e] * xh;
-            acc[e] += dy[e] * xh;
+        for (int u = 0; u < kRmsU; ++u) {
+            const uint32_t r = r0 + u * step;
+            const bool ok = r < R.rows;
+            row_coords(R, ok ? r : 0u, b[u], h[u], i[u]);
+            load_row<T>(R.x.at<T>(b[u], h[u], i[u]) + d0, dok && ok, x[u]);
+            load_row<T>(R.dy.at<T>(b[u], h[u], i[u]) + d0, dok && ok, dy[u]);
+            rs[u] = ok ? R.rstd[rstd_index(R, b[u], h[u], i[u])] : 0.f;
         }
-        c = row_sum<LPR>(c) / (float)R.dim;
-        if (dok) {
-            float dx[E];
 #pragma unroll
-            for (int e = 0; e < E; ++e) dx[e] = rs * (dy[e] * w[e] - x[e] * rs * c);
-            store_row<T>(R.dx.wrow<T>(b, h, i) + d0, dx);
+        for (int u = 0; u < kRmsU; ++u) {
+            float c = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float xh = x[u][e] * rs[u];
+                c += dy[u][e] * w[e] * xh;
+                acc[e] += dy[u][e] * xh;
+            }
+            c = row_sum<LPR>(c) * R.inv_dim;
+            if (r0 + u * step < R.rows && dok) {
+                float dx[E];
+#pragma unroll
+                for (int e = 0; e < E; ++e) dx[e] = rs[u] * (dy[u][e] * w[e] - x[u][e] * rs[u] * c);
+                store_row<T>(R.dx.at<T>(b[u], h[u], i[u]) + d0, dx);
+            }
         }
     }
     if (!R.partial) return;
@@ -151,23 +212,28 @@ __global__ __launch_bounds__(kRmsThreads) void k_rms_bwd(RmsDev R) {
     }
 }
 
-// dw[f] = sum over the nparts partial rows, in a fixed order: 32 lanes stride the partials,
-// then a fixed tree; one wave per feature
+// dw[f] = sum over the nparts partial rows in a fixed order: the 64 lanes of a wave stride
+// the partials, then a fixed butterfly; one wave per feature
 __global__ __launch_bounds__(kRmsThreads) void k_rms_dw(RmsDev R, int nparts) {
     const int lane = threadIdx.x & 63;
     const int f = blockIdx.x * (kRmsThreads / 64) + (threadIdx.x >> 6);
     if (f >= R.dim) return;
-    float s = 0.f;
-    for (int p = lane; p < nparts; p += 64) s += R.partial[(int64_t)p * R.dim + f];
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-    if (lane == 0) R.dw[f] = s;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};  // independent chains: the loads stay in flight
+    int p = lane;
+    for (; p + 192 < nparts; p += 256)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s[k] += R.partial[(int64_t)(p + 64 * k) * R.dim + f];
+    for (; p < nparts; p += 64) s[0] += R.partial[(int64_t)p * R.dim + f];
+    float t = (s[0] + s[1]) + (s[2] + s[3]);
+    for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+    if (lane == 0) R.dw[f] = t;
 }
 
 // ---------------------------------------------------------------------------------------
 
 static int rms_blocks(const RmsDev& R) {
-    const int64_t rpb = kRmsThreads / R.lpr;
-    const int64_t need = (R.rows + rpb - 1) / rpb;
+    const int64_t rpb = (int64_t)(kRmsThreads / R.lpr) * kRmsU;
+    const int64_t need = ((int64_t)R.rows + rpb - 1) / rpb;
     return (int)(need < kRmsMaxBlocks ? need : kRmsMaxBlocks);
 }
 
@@ -190,14 +256,14 @@ static int rms_setup(const pa_rmsnorm* p, RmsDev& R, bool bwd) {
         return PA_EINVAL;
     int lpr = 1;
     while (lpr * E < p->dim) lpr <<= 1;
+    const int64_t rows = (int64_t)p->batch * p->heads * p->n;
+    if (rows >= ((int64_t)1 << 31)) return PA_EUNSUPPORTED;
     auto mk = [](const pa_view& v) {
-        DView x;
+        RView x;
         x.p = static_cast<char*>(v.ptr);
         x.sb = v.sb;
         x.sh = v.sh;
         x.sn = v.sn;
-        x.hdiv = 1;
-        x.dtype = v.dtype;
         return x;
     };
     R.batch = p->batch;
@@ -205,8 +271,12 @@ static int rms_setup(const pa_rmsnorm* p, RmsDev& R, bool bwd) {
     R.n = p->n;
     R.dim = p->dim;
     R.lpr = lpr;
-    R.rows = (int64_t)p->batch * p->heads * p->n;
+    R.rows = (uint32_t)rows;
+    R.hfast = p->heads > 1 && p->n > 1 && p->x.sh < p->x.sn;
+    R.fd_n = make_fastdiv((uint32_t)p->n);
+    R.fd_h = make_fastdiv((uint32_t)p->heads);
     R.eps = p->eps;
+    R.inv_dim = 1.f / (float)p->dim;
     R.x = mk(p->x);
     R.y = mk(p->y);
     R.dy = mk(p->dy);

@@ -57,6 +57,22 @@ def _view(t: Optional[Tensor]) -> PaView:
     return v
 
 
+def _heads_inner(t: Tensor) -> bool:
+    """A [B, H, N, d] view whose head stride is below its position stride: the layout of the
+    modules' split projections ([B, N, H*d] seen per head)."""
+    return t.dim() == 4 and t.shape[1] > 1 and t.shape[2] > 1 and t.stride(1) < t.stride(2)
+
+
+def _empty_heads(shape, like: Tensor, dtype=None) -> Tensor:
+    """A new [B, H, N, d] tensor in the layout of ``like``: heads-inner ([B, N, H, d] storage,
+    so that merging the heads afterwards is a free view) when ``like`` is, else contiguous."""
+    dtype = like.dtype if dtype is None else dtype
+    B, H, N, d = shape
+    if _heads_inner(like):
+        return torch.empty(B, N, H, d, dtype=dtype, device=like.device).permute(0, 2, 1, 3)
+    return torch.empty(B, H, N, d, dtype=dtype, device=like.device)
+
+
 def _mask(m: Optional[Tensor]) -> PaMask:
     pm = PaMask()
     if m is None:
@@ -126,7 +142,7 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
     km, qm = _mask_u8(key_mask), _mask_u8(query_mask)
     B, _, nq, d = q.shape
     H = _pass_heads(q, k, v, vmul, bias)
-    out = torch.empty(B, H, nq, d, dtype=q.dtype, device=q.device)
+    out = _empty_heads((B, H, nq, d), q)
     lse = torch.empty(B, H, nq, dtype=torch.float32, device=q.device)
     p = _pass_struct(q, k, v, vmul, bias, km, qm, out, lse, causal, softclamp, scale,
                      may_degenerate or km is not None or qm is not None)
@@ -151,10 +167,10 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
     key_side = [t for t in (v, vmul, bias) if t is not None]
     assert all(t.shape[1] == hk for t in key_side), \
         "backward: k, v, vmul and bias must share one head count"
-    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
-    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
-    dvmul = torch.empty(vmul.shape, dtype=v.dtype, device=v.device) if vmul is not None else None
+    dq = _empty_heads(q.shape, q)
+    dk = _empty_heads(k.shape, k)
+    dv = _empty_heads(v.shape, v)
+    dvmul = _empty_heads(vmul.shape, vmul, v.dtype) if vmul is not None else None
     dbias = (torch.empty(bias.shape, dtype=torch.float32, device=q.device)
              if bias is not None else None)
     dlse32 = dlse.float() if dlse is not None else None
@@ -288,7 +304,7 @@ def rms_supported(x: Tensor, weight: Optional[Tensor]) -> bool:
 @torch.library.custom_op("polyattn::rms_norm", mutates_args=(), device_types="cuda")
 def rms_norm_op(x: Tensor, weight: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
-    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    y = _empty_heads(x.shape, x)
     rstd = torch.empty(x.shape[:3], dtype=torch.float32, device=x.device)
     r = _rms_struct(x, weight, eps)
     r.y, r.rstd = _view(y), rstd.data_ptr()
@@ -309,7 +325,7 @@ def rms_norm_bwd_op(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tenso
     dy = dy if dy.stride(-1) == 1 and dy.data_ptr() % 16 == 0 else dy.contiguous()
     if any(st % (4 if dy.dtype == torch.float32 else 8) for st in dy.stride()[:3]):
         dy = dy.contiguous()
-    dx = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    dx = _empty_heads(x.shape, x)
     r = _rms_struct(x, weight, eps)
     r.rstd = rstd.data_ptr()
     r.dy, r.dx = _view(dy), _view(dx)
