@@ -262,23 +262,161 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_partial(DecodeDev D) {
     }
 }
 
-// One workgroup per (batch, KV group): chain the levels, deepest first.
+// The new position of one (level, head) and the write of its step result: (mm, ll, acc) is
+// the merged state of the cached positions, part the raw q.k of the new position, vnew its
+// value and bnew its bias (the deeper level's step results).
+template <typename T>
+__device__ __forceinline__ void dec_finish(const DecodeDev& D, const DecLevelDev& L, int b, int h,
+                                           int hh, int lane, bool final_level, int n, float mm,
+                                           float ll, float (&acc)[4], float part,
+                                           const float (&vnew)[4], float bnew, float* s_msg2,
+                                           float* s_lse2) {
+    const int dim = D.dim, nold = n - 1;
+    const bool new_ok = bias_class(bnew) == 0;
+    if (new_ok) {
+        const float tt = (softclamp_f(part * D.scale, D.softclamp) + bnew) * kLog2e;
+        const float mn = fmaxf(mm, tt);
+        const float c1 = exp2f(mm - mn), c2 = exp2f(tt - mn);
+        ll = ll * c1 + c2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = acc[e] * c1 + vnew[e] * c2;
+        mm = mn;
+    }
+    float lse_v, inv;
+    if (ll > 0.f) {
+        lse_v = (mm + log2f(ll)) * kLn2;
+        inv = 1.f / ll;
+    } else {
+        // every position masked: uniform average over the -FLT_MAX-biased positions
+        float c1 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = 0.f;
+        for (int j = 0; j < n; ++j) {
+            const float bj = (j == nold) ? bnew : (L.bias.ok() ? L.bias.scalar(b, h, j) : 0.f);
+            if (bias_class(bj) != 1) continue;
+            c1 += 1.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = lane + 64 * e;
+                if (d >= dim) continue;
+                float v;
+                if (j == nold) v = vnew[e];
+                else {
+                    v = to_f(L.v.row<T>(b, h, j)[d]);
+                    if (L.vmul.ok()) v = round_to<T>(v * to_f(L.vmul.row<T>(b, h, j)[d]));
+                }
+                acc[e] += v;
+            }
+        }
+        lse_v = c1 > 0.f ? -FLT_MAX : -INFINITY;
+        inv = c1 > 0.f ? 1.f / c1 : NAN;
+    }
+    // write the step result (replicated over the view heads) and keep it in LDS
+    const int slot = (D.n_dev && !final_level) ? nold : 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int d = lane + 64 * e;
+        if (d >= dim) continue;
+        const float o = acc[e] * inv;
+        for (int r = 0; r < L.out_rep; ++r) L.out.wrow<T>(b, h * L.out_rep + r, slot)[d] = from_f<T>(o);
+        s_msg2[hh * dim + d] = round_to<T>(o);
+    }
+    if (lane == 0) {
+        float stored = lse_v;
+        if (L.lse.ok()) {
+            for (int r = 0; r < L.lse_rep; ++r)
+                store_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep + r, slot), lse_v);
+            stored = load_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep, slot));
+        }
+        s_lse2[hh] = stored;  // the value the next level's cached bias will hold
+    }
+}
+
+// merge the chunk partials of one (level, head): running max, sum and sum p v
+__device__ __forceinline__ void dec_merge(const DecodeDev& D, const DecLevelDev& L, int b, int h,
+                                          int lane, float& mm, float& ll, float (&acc)[4]) {
+    const int dim = D.dim;
+    mm = -INFINITY;
+    const float* recs = L.ws + ((int64_t)b * L.heads + h) * D.nchunks * D.rec;
+    for (int c = lane; c < D.nchunks; c += 64) mm = fmaxf(mm, recs[(int64_t)c * D.rec]);
+    for (int off = 32; off > 0; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
+    ll = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = 0.f;
+    if (mm == -INFINITY) return;
+    for (int c = 0; c < D.nchunks; ++c) {
+        const float* rc = recs + (int64_t)c * D.rec;
+        const float mc = rc[0];
+        if (mc == -INFINITY) continue;
+        const float w = exp2f(mc - mm);
+        ll += rc[1] * w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = lane + 64 * e;
+            if (d < dim) acc[e] += rc[2 + d] * w;
+        }
+    }
+}
+
+// One workgroup per (batch, KV group): chain the levels, deepest first.  Phase 1 merges the
+// chunk partials and reads the new position's q, k (and v) for every (level, head) of the
+// group at once, into LDS; phase 2 walks the levels, each needing only the deeper level's
+// step result.  Items beyond the kDecCombElems budget of LDS state are merged in phase 2.
+constexpr int kDecCombElems = 8192;
 template <typename T>
 __global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
     const int b = blockIdx.x / D.kv_heads, g = blockIdx.x % D.kv_heads;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int kWaves = kDecThreads / 64;
+    // per (level, head) item: [mm, ll, part, -, acc(dim), v(dim)]
+    __shared__ float s_st[kDecCombElems];
     // step results of the previous (deeper) level, per level head of this group:
     // [head][dim] flattened, heads-per-group * dim <= kDecMaxGroupElems (checked on the host)
     __shared__ float s_msg[kDecMaxGroupElems];
     __shared__ float s_lse[kDecMaxHeadsPerGroup];
     __shared__ float s_msg2[kDecMaxGroupElems];
     __shared__ float s_lse2[kDecMaxHeadsPerGroup];
-    int prev_rep = 1;
     const int dim = D.dim;
     const int n = step_n(D);
     const int nold = n - 1;
+    const int ist = 4 + 2 * dim;  // floats per item
 
+    // phase 1: all items in parallel, one wave per item
+    int nitems = 0;
+    for (int t = 0; t < D.order; ++t) nitems += D.L[t].rep;
+    const int nfit = min(nitems, kDecCombElems / ist);  // items whose state fits in LDS
+    for (int it = wave; it < nfit; it += kWaves) {
+        int t = 0, hh = it;
+        while (hh >= D.L[t].rep) hh -= D.L[t++].rep;
+        const DecLevelDev& L = D.L[t];
+        const int h = g * L.rep + hh;
+        const bool final_level = (t == D.order - 1);
+        float mm, ll, acc[4];
+        dec_merge(D, L, b, h, lane, mm, ll, acc);
+        float part = 0.f;
+        const T* qrow = L.q.row<T>(b, h, 0);
+        const T* krow = L.k.row<T>(b, h, nold);
+        float* st = s_st + it * ist;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = lane + 64 * e;
+            if (d < dim) {
+                part += to_f(qrow[d]) * to_f(krow[d]);
+                st[4 + d] = acc[e];
+                st[4 + dim + d] = final_level ? 0.f : to_f(L.v.row<T>(b, h, nold)[d]);
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+        if (lane == 0) {
+            st[0] = mm;
+            st[1] = ll;
+            st[2] = part;
+        }
+    }
+    __syncthreads();
+
+    // phase 2: the levels in order
+    int prev_rep = 1, base = 0;
     for (int t = 0; t < D.order; ++t) {
         const DecLevelDev& L = D.L[t];
         const bool deepest = (t == 0), final_level = (t == D.order - 1);
@@ -286,102 +424,48 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
             const int h = g * L.rep + hh;
             // index of this head's deeper-level result (deeper level has prev_rep heads/group)
             const int ph = (hh * prev_rep) / L.rep;
-            // 1. merge the chunk partials
-            float mm = -INFINITY;
-            const float* recs = L.ws + ((int64_t)b * L.heads + h) * D.nchunks * D.rec;
-            for (int c = lane; c < D.nchunks; c += 64) mm = fmaxf(mm, recs[(int64_t)c * D.rec]);
-            for (int off = 32; off > 0; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
-            float ll = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
-            if (mm != -INFINITY) {
-                for (int c = 0; c < D.nchunks; ++c) {
-                    const float* rc = recs + (int64_t)c * D.rec;
-                    const float mc = rc[0];
-                    if (mc == -INFINITY) continue;
-                    const float w = exp2f(mc - mm);
-                    ll += rc[1] * w;
+            float mm, ll, part, acc[4], vr[4];
+            if (base + hh < nfit) {
+                const float* st = s_st + (base + hh) * ist;
+                mm = st[0];
+                ll = st[1];
+                part = st[2];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int d = lane + 64 * e;
-                        if (d < dim) acc[e] += rc[2 + d] * w;
+                for (int e = 0; e < 4; ++e) {
+                    const int d = lane + 64 * e;
+                    acc[e] = d < dim ? st[4 + d] : 0.f;
+                    vr[e] = d < dim ? st[4 + dim + d] : 0.f;
+                }
+            } else {  // state beyond the LDS budget: merge and read here
+                dec_merge(D, L, b, h, lane, mm, ll, acc);
+                part = 0.f;
+                const T* qrow = L.q.row<T>(b, h, 0);
+                const T* krow = L.k.row<T>(b, h, nold);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int d = lane + 64 * e;
+                    vr[e] = 0.f;
+                    if (d < dim) {
+                        part += to_f(qrow[d]) * to_f(krow[d]);
+                        if (!final_level) vr[e] = to_f(L.v.row<T>(b, h, nold)[d]);
                     }
                 }
+                for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
             }
-            // 2. the new position n-1
-            float part = 0.f, vnew[4];
-            const T* qrow = L.q.row<T>(b, h, 0);
-            const T* krow = L.k.row<T>(b, h, nold);
+            float vnew[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int d = lane + 64 * e;
                 vnew[e] = 0.f;
                 if (d < dim) {
-                    part += to_f(qrow[d]) * to_f(krow[d]);
-                    if (deepest) vnew[e] = to_f(L.v.row<T>(b, h, nold)[d]);
+                    if (deepest) vnew[e] = vr[e];
                     else if (final_level) vnew[e] = s_msg[ph * dim + d];
-                    else vnew[e] = round_to<T>(to_f(L.v.row<T>(b, h, nold)[d]) * s_msg[ph * dim + d]);
+                    else vnew[e] = round_to<T>(vr[e] * s_msg[ph * dim + d]);
                 }
             }
-            for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
             const float bnew = deepest ? 0.f : s_lse[ph];
-            const bool new_ok = bias_class(bnew) == 0;
-            if (new_ok) {
-                const float tt = (softclamp_f(part * D.scale, D.softclamp) + bnew) * kLog2e;
-                const float mn = fmaxf(mm, tt);
-                const float c1 = exp2f(mm - mn), c2 = exp2f(tt - mn);
-                ll = ll * c1 + c2;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[e] = acc[e] * c1 + vnew[e] * c2;
-                mm = mn;
-            }
-            float lse_v, inv;
-            if (ll > 0.f) {
-                lse_v = (mm + log2f(ll)) * kLn2;
-                inv = 1.f / ll;
-            } else {
-                // every position masked: uniform average over the -FLT_MAX-biased positions
-                float c1 = 0.f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[e] = 0.f;
-                for (int j = 0; j < n; ++j) {
-                    const float bj = (j == nold) ? bnew : (L.bias.ok() ? L.bias.scalar(b, h, j) : 0.f);
-                    if (bias_class(bj) != 1) continue;
-                    c1 += 1.f;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int d = lane + 64 * e;
-                        if (d >= dim) continue;
-                        float v;
-                        if (j == nold) v = vnew[e];
-                        else {
-                            v = to_f(L.v.row<T>(b, h, j)[d]);
-                            if (L.vmul.ok()) v = round_to<T>(v * to_f(L.vmul.row<T>(b, h, j)[d]));
-                        }
-                        acc[e] += v;
-                    }
-                }
-                lse_v = c1 > 0.f ? -FLT_MAX : -INFINITY;
-                inv = c1 > 0.f ? 1.f / c1 : NAN;
-            }
-            // 3. write the step result (replicated over the view heads) and keep it in LDS
-            const int slot = (D.n_dev && !final_level) ? nold : 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int d = lane + 64 * e;
-                if (d >= dim) continue;
-                const float o = acc[e] * inv;
-                for (int r = 0; r < L.out_rep; ++r)
-                    L.out.wrow<T>(b, h * L.out_rep + r, slot)[d] = from_f<T>(o);
-                s_msg2[hh * dim + d] = round_to<T>(o);
-            }
-            if (lane == 0) {
-                float stored = lse_v;
-                if (L.lse.ok()) {
-                    for (int r = 0; r < L.lse_rep; ++r)
-                        store_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep + r, slot), lse_v);
-                    stored = load_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep, slot));
-                }
-                s_lse2[hh] = stored;  // the value the next level's cached bias will hold
-            }
+            dec_finish<T>(D, L, b, h, hh, lane, final_level, n, mm, ll, acc, part, vnew, bnew,
+                          s_msg2, s_lse2);
         }
         __syncthreads();
         for (int x = threadIdx.x; x < L.rep * dim; x += kDecThreads)
@@ -389,6 +473,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
         for (int x = threadIdx.x; x < L.rep; x += kDecThreads) s_lse[x] = s_lse2[x];
         __syncthreads();
         prev_rep = L.rep;
+        base += L.rep;
     }
 }
 
@@ -553,6 +638,9 @@ static int pick_chunks(const pa_decode* d, int* chunk_out) {
         if (want < 1) want = 1;
         chunk = (int)((nold + want - 1) / want);
         chunk = (chunk + 63) / 64 * 64;
+        // at least 512 positions per chunk (fewer, longer workgroups stream better)
+        const int whole = (nold + 63) / 64 * 64;
+        if (chunk < 512) chunk = whole < 512 ? whole : 512;
     }
     if (chunk > cap) chunk = cap;
     if (chunk < 64) chunk = 64;

@@ -17,6 +17,7 @@
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import Optional, Sequence
 
@@ -89,6 +90,13 @@ def _mask_u8(m: Optional[Tensor]) -> Optional[Tensor]:
     return m.to(torch.uint8)
 
 
+def _device(t: Tensor):
+    """The tensor's device as the current one (a no-op context when it already is)."""
+    if t.device.index is None or t.device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(t.device)
+
+
 def _stream(t: Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -146,7 +154,7 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
     lse = torch.empty(B, H, nq, dtype=torch.float32, device=q.device)
     p = _pass_struct(q, k, v, vmul, bias, km, qm, out, lse, causal, softclamp, scale,
                      may_degenerate or km is not None or qm is not None)
-    with torch.cuda.device(q.device):
+    with _device(q):
         _lib.check(lib.pa_attn_pass_fwd(ctypes.byref(p), _stream(q)), "pa_attn_pass_fwd")
     return out, lse
 
@@ -184,7 +192,7 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
     ws_bytes = lib.pa_attn_pass_bwd_workspace(ctypes.byref(g))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     g.workspace, g.workspace_bytes = ws.data_ptr(), ws_bytes
-    with torch.cuda.device(q.device):
+    with _device(q):
         _lib.check(lib.pa_attn_pass_bwd(ctypes.byref(g), _stream(q)), "pa_attn_pass_bwd")
     if dbias is not None and bias is not None and dbias.dtype != bias.dtype:
         dbias = dbias.to(bias.dtype)
@@ -262,6 +270,14 @@ def _pass_backward(ctx, dout, dlse):
 torch.library.register_autograd("polyattn::pass_fwd", _pass_backward, setup_context=_pass_setup)
 
 
+def _needs_op(*ts) -> bool:
+    """Whether a call must go through the registered custom op (autograd or torch.compile
+    tracing); plain inference calls the library directly (less host overhead per launch)."""
+    if torch.compiler.is_compiling():
+        return True
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
 def attn_pass(q: Tensor, k: Tensor, v: Tensor, vmul: Optional[Tensor] = None,
               bias: Optional[Tensor] = None, key_mask: Optional[Tensor] = None,
               query_mask: Optional[Tensor] = None, causal: bool = False,
@@ -269,6 +285,9 @@ def attn_pass(q: Tensor, k: Tensor, v: Tensor, vmul: Optional[Tensor] = None,
               may_degenerate: bool = False) -> tuple[Tensor, Tensor]:
     """One differentiable attention pass on the GPU: returns (out, lse[fp32])."""
     scale = q.shape[-1] ** -0.5 if scale is None else scale
+    if not _needs_op(q, k, v, vmul, bias):
+        return pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, bool(causal),
+                            float(softclamp or 0.0), float(scale), bool(may_degenerate))
     return pass_fwd_op(q, k, v, vmul, bias, key_mask, query_mask, bool(causal),
                        float(softclamp or 0.0), float(scale), bool(may_degenerate))
 
@@ -303,12 +322,16 @@ def rms_supported(x: Tensor, weight: Optional[Tensor]) -> bool:
 
 @torch.library.custom_op("polyattn::rms_norm", mutates_args=(), device_types="cuda")
 def rms_norm_op(x: Tensor, weight: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor]:
+    return _rms_fwd_raw(x, weight, eps)
+
+
+def _rms_fwd_raw(x: Tensor, weight: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
     y = _empty_heads(x.shape, x)
     rstd = torch.empty(x.shape[:3], dtype=torch.float32, device=x.device)
     r = _rms_struct(x, weight, eps)
     r.y, r.rstd = _view(y), rstd.data_ptr()
-    with torch.cuda.device(x.device):
+    with _device(x):
         _lib.check(lib.pa_rmsnorm_fwd(ctypes.byref(r), _stream(x)), "pa_rmsnorm_fwd")
     return y, rstd
 
@@ -336,7 +359,7 @@ def rms_norm_bwd_op(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tenso
     ws_bytes = lib.pa_rmsnorm_bwd_workspace(ctypes.byref(r))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
     r.workspace, r.workspace_bytes = ws.data_ptr(), ws_bytes
-    with torch.cuda.device(x.device):
+    with _device(x):
         _lib.check(lib.pa_rmsnorm_bwd(ctypes.byref(r), _stream(x)), "pa_rmsnorm_bwd")
     dw = dw32.to(weight.dtype) if weight is not None else x.new_empty(0)
     return dx, dw
@@ -373,6 +396,8 @@ def rms_norm(x: Tensor, weight: Optional[Tensor], eps: Optional[float]) -> Tenso
     the fp32 op-math type."""
     if eps is None:
         eps = torch.finfo(torch.float32).eps
+    if not _needs_op(x, weight):
+        return _rms_fwd_raw(x, weight, float(eps))[0]
     return rms_norm_op(x, weight, float(eps))[0]
 
 
@@ -492,7 +517,7 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
     ws_bytes = lib.pa_poly_decode_workspace(ctypes.byref(D))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=out.device)
     D.workspace, D.workspace_bytes = ws.data_ptr(), ws_bytes
-    with torch.cuda.device(out.device):
+    with _device(out):
         _lib.check(lib.pa_poly_decode(ctypes.byref(D), _stream(out)), "pa_poly_decode")
     return out
 
@@ -529,5 +554,5 @@ def decode_prologue(items, *, eps: float, angles: Optional[Tensor], pos_dev: Ten
             it.out = _view(out)
         if cache is not None:
             it.cache = _view(cache)
-    with torch.cuda.device(src0.device):
+    with _device(src0):
         _lib.check(lib.pa_decode_prologue(ctypes.byref(P), _stream(src0)), "pa_decode_prologue")

@@ -178,14 +178,18 @@ def test_kv_cache_stepwise_equals_parallel(order, kv_heads, use_rotary_embed):
     assert_close(torch.cat(outs, dim=1), ref, 1e-4, "stepwise")
 
 
-def test_decode_kernel_gqa_synthetic_cache():
-    """Config-5 shape class (GQA 8/2 heads, d=128) at a small cache, with a synthetic cache
-    (q/k/v/msg ~ N(0,1), lse = log(j+1) + N(0,1)) against the oracle's cached branch."""
+@param("chunk,H,G", ((0, 8, 2), (64, 8, 2), (64, 64, 2)))
+def test_decode_kernel_gqa_synthetic_cache(chunk, H, G):
+    """Config-5 shape class (GQA, d=128) at a small cache, with a synthetic cache
+    (q/k/v/msg ~ N(0,1), lse = log(j+1) + N(0,1)) against the oracle's cached branch; chunk=64
+    splits the 299 cached positions over five partial records (the merge path); 64 query heads
+    on 2 KV heads (33 level heads per group) exceed the combine kernel's LDS state budget, so
+    some heads are merged in its second phase."""
     from poly_attention import _ops
 
     d = dev()
     g = torch.Generator().manual_seed(5)
-    B, H, G, n, dh = 2, 8, 2, 300, 128
+    B, n, dh = 2, 300, 128
     r = H // G
     for dtype in (torch.float32, torch.bfloat16):
         q2c, q3c, v3c = (torch.randn(B, G, n, dh, generator=g).to(dtype) for _ in range(3))
@@ -201,7 +205,7 @@ def test_decode_kernel_gqa_synthetic_cache():
         msg_d, lse_d = msg.to(d).clone(), lse.to(d).clone()
         out = _ops.poly_decode_step([q1.to(d), q2n.to(d)], [q2c.to(d), q3c.to(d)], [v3c.to(d)],
                                     [msg_d], [lse_d], kv_heads=G, heads=H, softclamp=None,
-                                    scale=dh ** -0.5)
+                                    scale=dh ** -0.5, chunk=chunk)
         torch.cuda.synchronize()
         tol = 1e-4 if dtype == torch.float32 else 2e-2
         assert_close(out, ref, tol, f"out {dtype}")
