@@ -132,3 +132,16 @@ def test_pass_cross_lengths(dtype):
     k, v = (randn((2, 4, 33, 64), dtype, s) for s in (17, 18))
     check(run_pass(q, k, v, causal=True), dtype)
     check(run_pass(q, k, v, causal=False), dtype)
+
+
+@param("heads,n,d", ((8, 1024, 64), (3, 1000, 64), (8, 512, 128)))
+def test_pass_multi_block_causal_grids(heads, n, d):
+    """Causal passes with many query / key blocks per head: the workgroup order that runs the
+    heaviest blocks of all heads of an XCD first (8 heads: whole heads per XCD; 3 heads: the
+    unit-by-unit fallback), forward and all gradients, with a key bias as in pass 2."""
+    dtype = torch.bfloat16
+    q, k, v = (randn((1, heads, n, d), dtype, s) for s in (21, 22, 23))
+    bias = torch.log(torch.arange(1, n + 1).float())[None, None].repeat(1, heads, 1)
+    bias = bias + randn((1, heads, n), torch.float32, 24)
+    check(run_pass(q, k, v, causal=True), dtype)
+    check(run_pass(q, k, v, bias=bias, causal=True), dtype)
