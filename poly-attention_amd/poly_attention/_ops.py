@@ -160,7 +160,9 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
 
 
 def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal,
-                 softclamp, scale, may_degenerate):
+                 softclamp, scale, may_degenerate, dq_into: Optional[Tensor] = None):
+    """One pass backward.  ``dq_into``: a gradient buffer of q's shape that the query gradient
+    is added into (PA_ACC_DQ) instead of a new tensor."""
     lib = _lib.load()
     q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
     vmul = _inner_contig(vmul) if vmul is not None else None
@@ -175,7 +177,12 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
     key_side = [t for t in (v, vmul, bias) if t is not None]
     assert all(t.shape[1] == hk for t in key_side), \
         "backward: k, v, vmul and bias must share one head count"
-    dq = _empty_heads(q.shape, q)
+    accumulate = 0
+    if dq_into is not None:
+        assert dq_into.shape == q.shape and dq_into.dtype == q.dtype
+        dq, accumulate = dq_into, _lib.PA_ACC_DQ
+    else:
+        dq = _empty_heads(q.shape, q)
     dk = _empty_heads(k.shape, k)
     dv = _empty_heads(v.shape, v)
     dvmul = _empty_heads(vmul.shape, vmul, v.dtype) if vmul is not None else None
@@ -188,7 +195,7 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
     g.dout, g.dlse = _view(dout), _view(dlse32)
     g.dq, g.dk, g.dv = _view(dq), _view(dk), _view(dv)
     g.dvmul, g.dbias = _view(dvmul), _view(dbias)
-    g.accumulate = 0
+    g.accumulate = accumulate
     ws_bytes = lib.pa_attn_pass_bwd_workspace(ctypes.byref(g))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     g.workspace, g.workspace_bytes = ws.data_ptr(), ws_bytes
@@ -405,6 +412,54 @@ def rms_norm(x: Tensor, weight: Optional[Tensor], eps: Optional[float]) -> Tenso
 # the order-n chain
 
 
+class _Order2Chain(torch.autograd.Function):
+    """The order-2 chain (poly_attention.py:48-116) as one autograd node whose backward runs
+    the two pass backwards back to back: pass 2's key gradient of q2 becomes the buffer that
+    pass 1's query gradient of q2 is accumulated into (no separate add)."""
+
+    @staticmethod
+    def forward(ctx, q1, q2, q3, v3, causal, softclamp, scale):
+        msg, lse23 = pass_fwd_raw(q2, q3, v3, None, None, None, None, causal, softclamp, scale,
+                                  False)
+        out, lse = pass_fwd_raw(q1, q2, msg, None, lse23, None, None, causal, softclamp, scale,
+                                False)
+        ctx.save_for_backward(q1, q2, q3, v3, msg, lse23, out, lse)
+        ctx.cfg = (causal, softclamp, scale)
+        ctx.set_materialize_grads(False)
+        return out, lse, lse23, msg
+
+    @staticmethod
+    def backward(ctx, dout, dlse, dlse23_ext, dmsg_ext):
+        q1, q2, q3, v3, msg, lse23, out, lse = ctx.saved_tensors
+        causal, softclamp, scale = ctx.cfg
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dq1, dq2, dmsg, _, dlse23 = pass_bwd_raw(dout, dlse, q1, q2, msg, None, lse23, None,
+                                                 None, out, lse, causal, softclamp, scale,
+                                                 False)
+        if dmsg_ext is not None:
+            dmsg = dmsg + dmsg_ext
+        if dlse23_ext is not None:
+            dlse23 = dlse23 + dlse23_ext
+        _, dq3, dv3, _, _ = pass_bwd_raw(dmsg, dlse23, q2, q3, v3, None, None, None, None, msg,
+                                         lse23, causal, softclamp, scale, False, dq_into=dq2)
+        return dq1, dq2, dq3, dv3, None, None, None
+
+
+def _chain_fusable(q_left, q_right, vs, query_mask, key_masks, may_degenerate) -> bool:
+    if len(q_left) != 2 or torch.compiler.is_compiling() or may_degenerate:
+        return False
+    if query_mask is not None or any(m is not None for m in key_masks):
+        return False
+    q1, q2 = q_left
+    if q_right[0] is not q2 or q2.shape[1] != q_right[1].shape[1]:
+        return False
+    # pass 2 queries at the pass head count (no shared-query backward)
+    if q1.shape[1] != max(q1.shape[1], q2.shape[1], vs[0].shape[1]):
+        return False
+    return _needs_op(q1, q2, q_right[1], vs[0])
+
+
 def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence[Tensor], *,
                causal: bool, softclamp: Optional[float], scale: float,
                query_mask: Optional[Tensor] = None,
@@ -419,6 +474,11 @@ def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence
     n = len(q_left)
     assert len(q_right) == n and len(vs) == n - 1 and n >= 2
     key_masks = list(key_masks) if key_masks is not None else [None] * n
+    if _chain_fusable(q_left, q_right, vs, query_mask, key_masks, may_degenerate):
+        out, _, lse23, msg = _Order2Chain.apply(q_left[0], q_left[1], q_right[1], vs[0],
+                                                bool(causal), float(softclamp or 0.0),
+                                                float(scale))
+        return out, [lse23], [msg]
     may_degenerate = may_degenerate or query_mask is not None or any(
         m is not None for m in key_masks)
     lses, msgs = [], []
