@@ -279,10 +279,14 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
     G.ws_invc = reinterpret_cast<float*>(ws + 2 * align256(rows * sizeof(float)));
 
     hipStream_t s = static_cast<hipStream_t>(stream);
-    launch_simt_bwd(G, T, s, /*pre=*/true, false, false);
+    G.fused_pre = 0;
     if (mfma_bwd_supported(G, T)) {
+        // the direct-to-LDS dQ kernel computes the per-row preprocess itself when it applies
+        G.fused_pre = mfma_bwd_fuses_pre(G) ? 1 : 0;
+        if (!G.fused_pre) launch_simt_bwd(G, T, s, /*pre=*/true, false, false);
         launch_mfma_bwd(G, T, s);
     } else {
+        launch_simt_bwd(G, T, s, /*pre=*/true, false, false);
         launch_simt_bwd(G, T, s, false, /*dq=*/true, /*dkv=*/true);
     }
     return finish_launch();

@@ -24,6 +24,7 @@ void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool 
 bool mfma_fwd_supported(const PassDev& P, int dtype);
 void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s);
 bool mfma_bwd_supported(const GradDev& G, int dtype);
+bool mfma_bwd_fuses_pre(const GradDev& G);
 void launch_mfma_bwd(const GradDev& G, int dtype, hipStream_t s);
 
 // decode

@@ -922,8 +922,36 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
         of[c] = __builtin_bit_cast(frag, orr);
     }
     const int64_t row = ((int64_t)b * P.heads + h) * P.nq + (q_ok ? qi : 0);
-    float lse_l2 = q_ok ? G.ws_lse[row] * kLog2e : INFINITY;
-    float dpi = q_ok ? G.ws_D[row] : 0.f;
+    float lse_l2, dpi;
+    if (G.fused_pre) {
+        // the preprocess of this wave's rows: D = rowsum(dO * O) - dlse, lse (+inf for a
+        // fully-masked row), also written for the dK/dV kernel that runs next
+        float part = 0.f;
+        if (q_ok) {
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) {
+                const u32x4_t orow = *reinterpret_cast<const u32x4_t*>(P.out.row<T>(b, h, qi) + c * 16 + 8 * hh);
+                const T* oe = reinterpret_cast<const T*>(&orow);
+                const T* ge = reinterpret_cast<const T*>(&of[c]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) part += to_f(oe[e]) * to_f(ge[e]);
+            }
+        }
+        const float dsum = xhalf_sum(part);
+        const float l = q_ok ? *P.lse.row<float>(b, h, qi) : 0.f;
+        const float dl = (q_ok && G.dlse.ok()) ? *G.dlse.row<float>(b, h, qi) : 0.f;
+        const bool normal = l > kMaskedThreshold;
+        const float lseb = normal ? l : INFINITY;
+        dpi = normal ? dsum - dl : 0.f;
+        lse_l2 = q_ok ? lseb * kLog2e : INFINITY;
+        if (q_ok && hh == 0) {
+            G.ws_D[row] = dpi;
+            G.ws_lse[row] = lseb;
+        }
+    } else {
+        lse_l2 = q_ok ? G.ws_lse[row] * kLog2e : INFINITY;
+        dpi = q_ok ? G.ws_D[row] : 0.f;
+    }
     // retire the compiler-visible loads before the first direct load
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
@@ -1168,9 +1196,30 @@ static bool bwd_dq_dma_ok(const GradDev& G) {
     return true;
 }
 
+// The preprocess folded into the direct-to-LDS dQ kernel (which then runs first): it loads
+// the O rows of its queries beside dO with 16-byte loads.
+bool mfma_bwd_fuses_pre(const GradDev& G) {
+    const PassDev& P = G.f;
+    if (!PA_BWD_DMA || P.vmul.ok()) return false;
+    if (P.dim != 64 && P.dim != 128) return false;
+    return bwd_dq_dma_ok(G) && aligned_rows_host(P.out, 8);
+}
+
+template <typename T, int D, bool C, bool S, bool V, bool B>
+static void launch_dq(const GradDev& G, hipStream_t s) {
+    const PassDev& P = G.f;
+    dim3 grid(((P.nq + kDqBM - 1) / kDqBM) * P.heads * P.batch);
+    ProfScope ps("mfma_bwd_dq", s);
+    if (!V && PA_BWD_DMA && bwd_dq_dma_ok(G))
+        hipLaunchKernelGGL((k_mfma_bwd_dq_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
+    else
+        hipLaunchKernelGGL((k_mfma_bwd_dq<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
+}
+
 template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_bwd_t(const GradDev& G, hipStream_t s) {
     const PassDev& P = G.f;
+    if (G.fused_pre) launch_dq<T, D, C, S, V, B>(G, s);  // writes the preprocess for dK/dV
     {
         dim3 grid(((P.nk + kKvBK - 1) / kKvBK) * G.hk * P.batch);
         ProfScope ps("mfma_bwd_dkv", s);
@@ -1179,14 +1228,7 @@ static void launch_bwd_t(const GradDev& G, hipStream_t s) {
         else
             hipLaunchKernelGGL((k_mfma_bwd_dkv<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
     }
-    {
-        dim3 grid(((P.nq + kDqBM - 1) / kDqBM) * P.heads * P.batch);
-        ProfScope ps("mfma_bwd_dq", s);
-        if (!V && PA_BWD_DMA && bwd_dq_dma_ok(G))
-            hipLaunchKernelGGL((k_mfma_bwd_dq_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
-        else
-            hipLaunchKernelGGL((k_mfma_bwd_dq<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
-    }
+    if (!G.fused_pre) launch_dq<T, D, C, S, V, B>(G, s);
 }
 
 template <typename T, int D, bool C, bool S>
