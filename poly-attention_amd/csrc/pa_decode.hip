@@ -332,28 +332,61 @@ __device__ __forceinline__ void dec_finish(const DecodeDev& D, const DecLevelDev
     }
 }
 
-// merge the chunk partials of one (level, head): running max, sum and sum p v
+// merge the chunk partials of one (level, head): running max, sum and sum p v.  The chunk
+// weights come from one load per lane (lane c holds chunk c); the value rows are then summed
+// with loads that do not depend on each other (four chunks per step).
 __device__ __forceinline__ void dec_merge(const DecodeDev& D, const DecLevelDev& L, int b, int h,
                                           int lane, float& mm, float& ll, float (&acc)[4]) {
     const int dim = D.dim;
-    mm = -INFINITY;
     const float* recs = L.ws + ((int64_t)b * L.heads + h) * D.nchunks * D.rec;
-    for (int c = lane; c < D.nchunks; c += 64) mm = fmaxf(mm, recs[(int64_t)c * D.rec]);
-    for (int off = 32; off > 0; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
     ll = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] = 0.f;
+    mm = -INFINITY;
+    for (int c0 = 0; c0 < D.nchunks; c0 += 64) {
+        const int c = c0 + lane;
+        if (c < D.nchunks) mm = fmaxf(mm, recs[(int64_t)c * D.rec]);
+    }
+    for (int off = 32; off > 0; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
     if (mm == -INFINITY) return;
-    for (int c = 0; c < D.nchunks; ++c) {
-        const float* rc = recs + (int64_t)c * D.rec;
-        const float mc = rc[0];
-        if (mc == -INFINITY) continue;
-        const float w = exp2f(mc - mm);
-        ll += rc[1] * w;
+    for (int c0 = 0; c0 < D.nchunks; c0 += 64) {
+        const int c = c0 + lane;
+        float wl = 0.f, lc = 0.f;
+        if (c < D.nchunks) {
+            const float mc = recs[(int64_t)c * D.rec];
+            wl = mc == -INFINITY ? 0.f : exp2f(mc - mm);
+            lc = recs[(int64_t)c * D.rec + 1];
+        }
+        float lsum = lc * wl;
+        for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off);
+        ll += lsum;
+        const int cn = min(64, D.nchunks - c0);
+        int k = 0;
+        for (; k + 4 <= cn; k += 4) {
+            float wk[4], v[4][4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int d = lane + 64 * e;
-            if (d < dim) acc[e] += rc[2 + d] * w;
+            for (int q = 0; q < 4; ++q) {
+                wk[q] = __shfl(wl, k + q);
+                const float* rc = recs + (int64_t)(c0 + k + q) * D.rec + 2;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int d = lane + 64 * e;
+                    v[q][e] = d < dim ? rc[d] : 0.f;
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] += v[q][e] * wk[q];
+        }
+        for (; k < cn; ++k) {
+            const float wk = __shfl(wl, k);
+            const float* rc = recs + (int64_t)(c0 + k) * D.rec + 2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = lane + 64 * e;
+                if (d < dim) acc[e] += rc[d] * wk;
+            }
         }
     }
 }
