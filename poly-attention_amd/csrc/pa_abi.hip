@@ -280,6 +280,7 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     G.fused_pre = 0;
+    G.seeds = 0;
     if (mfma_bwd_supported(G, T)) {
         // the direct-to-LDS dQ kernel computes the per-row preprocess itself when it applies
         G.fused_pre = mfma_bwd_fuses_pre(G) ? 1 : 0;

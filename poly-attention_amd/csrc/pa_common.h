@@ -84,6 +84,8 @@ struct GradDev {
     float* ws_lse;         // [B, heads, nq]  lse for normal rows, +inf for degenerate rows
     float* ws_invc;        // [B, heads, nq]  1 / (#class-1 keys) for degenerate rows, else 0
     int32_t fused_pre;     // the dQ kernel computes ws_D / ws_lse for its rows (no preprocess)
+    int32_t seeds;         // with fused_pre: ws_lse / ws_D hold the dK/dV kernel's accumulator
+                           // seeds, -lse/scale (lse*log2e with softclamp) and -D
 };
 
 // class of a bias value in the finite-fill arithmetic: 0 normal, 1 = -FLT_MAX, 2 = -inf

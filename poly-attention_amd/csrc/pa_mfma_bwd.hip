@@ -325,9 +325,11 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
 // deep (tile i+2 in flight while tile i is computed; the query heads of a KV group form one
 // flat tile sequence).  Q and dO stay row-major in LDS and are read both by rows (S = Q K^T,
 // dP = dO V^T) and transposed (dV^T += dO^T P, dK^T += Q^T dS, ds_read_b64_tr_b16), under a
-// chunk swizzle that serves both patterns.  Each wave converts the tile's lse and D into
-// accumulator seeds: S starts at -lse/scale (so P = exp2(scale*log2e*S + bias)) and dP at
-// -D (so dS = P dP); with softclamp the lse is kept in the log2 domain instead.
+// chunk swizzle that serves both patterns.  The tile's lse and D rows enter as accumulator
+// seeds: S starts at -lse/scale (so P = exp2(scale*log2e*S + bias)) and dP at -D (so
+// dS = P dP); with softclamp the lse is kept in the log2 domain instead.  When the dQ kernel
+// ran first (GradDev::seeds) it wrote the rows in this form and the waves read the loaded
+// rows directly; otherwise each wave converts them into a copy of its own.
 
 // chunk swizzle for tiles read by rows (16 rows x one chunk per quarter-wave) and transposed
 // (4 rows x 4 chunks per half-wave): rows of one parity in a 16-row group get distinct
@@ -498,16 +500,24 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
         if (idx + 2 < total) issue(st == 0 ? 2 : st - 1);
         const T* Qt = sQ + st * ELEMS;
         const T* Ot = sO + st * ELEMS;
-        // this wave's seeds for the tile: -lse/scale (log2-domain lse with softclamp), -D
-        sLw[w][lane] = sLraw[st][lane] * lmul;
-        sDw[w][lane] = -sDraw[st][lane];
+        // the tile's seeds: -lse/scale (log2-domain lse with softclamp), -D; read from the
+        // loaded rows when the dQ kernel wrote them in that form, else converted into this
+        // wave's copy
+        const float* seed_l = &sLraw[st][0];
+        const float* seed_d = &sDraw[st][0];
+        if (!G.seeds) {
+            sLw[w][lane] = sLraw[st][lane] * lmul;
+            sDw[w][lane] = -sDraw[st][lane];
+            seed_l = &sLw[w][0];
+            seed_d = &sDw[w][0];
+        }
         // the two 32-query blocks in a software pipeline: the MFMAs of one block are issued in
         // the same basic block as the VALU work of the other
         auto scores = [&](int qb, f32x16_t& s, f32x16_t& dp) __attribute__((always_inline)) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const float4 lv = *reinterpret_cast<const float4*>(&sLw[w][qb * 32 + 8 * g + 4 * hh]);
-                const float4 dv4 = *reinterpret_cast<const float4*>(&sDw[w][qb * 32 + 8 * g + 4 * hh]);
+                const float4 lv = *reinterpret_cast<const float4*>(seed_l + qb * 32 + 8 * g + 4 * hh);
+                const float4 dv4 = *reinterpret_cast<const float4*>(seed_d + qb * 32 + 8 * g + 4 * hh);
                 if (SOFTCLAMP) {
                     s[4 * g] = s[4 * g + 1] = s[4 * g + 2] = s[4 * g + 3] = 0.f;
                 } else {
@@ -550,7 +560,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
             if (SOFTCLAMP) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const float4 lv = *reinterpret_cast<const float4*>(&sLw[w][qb * 32 + 8 * g + 4 * hh]);
+                    const float4 lv = *reinterpret_cast<const float4*>(seed_l + qb * 32 + 8 * g + 4 * hh);
                     const float L[4] = {lv.x, lv.y, lv.z, lv.w};
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -945,8 +955,13 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
         dpi = normal ? dsum - dl : 0.f;
         lse_l2 = q_ok ? lseb * kLog2e : INFINITY;
         if (q_ok && hh == 0) {
-            G.ws_D[row] = dpi;
-            G.ws_lse[row] = lseb;
+            if (G.seeds) {
+                G.ws_D[row] = -dpi;
+                G.ws_lse[row] = lseb * (SOFTCLAMP ? kLog2e : -1.f / P.scale);
+            } else {
+                G.ws_D[row] = dpi;
+                G.ws_lse[row] = lseb;
+            }
         }
     } else {
         lse_l2 = q_ok ? G.ws_lse[row] * kLog2e : INFINITY;
@@ -1217,13 +1232,17 @@ static void launch_dq(const GradDev& G, hipStream_t s) {
 }
 
 template <typename T, int D, bool C, bool S, bool V, bool B>
-static void launch_bwd_t(const GradDev& G, hipStream_t s) {
-    const PassDev& P = G.f;
+static void launch_bwd_t(const GradDev& G0, hipStream_t s) {
+    const PassDev& P = G0.f;
+    const bool kv_dma = !V && PA_BWD_DMA && bwd_dma_ok(G0);
+    GradDev G = G0;
+    // the dQ kernel writes the preprocess in the direct-to-LDS dK/dV kernel's seed form
+    G.seeds = (G.fused_pre && kv_dma) ? 1 : 0;
     if (G.fused_pre) launch_dq<T, D, C, S, V, B>(G, s);  // writes the preprocess for dK/dV
     {
         dim3 grid(((P.nk + kKvBK - 1) / kKvBK) * G.hk * P.batch);
         ProfScope ps("mfma_bwd_dkv", s);
-        if (!V && PA_BWD_DMA && bwd_dma_ok(G))
+        if (kv_dma)
             hipLaunchKernelGGL((k_mfma_bwd_dkv_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
         else
             hipLaunchKernelGGL((k_mfma_bwd_dkv<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
