@@ -1,13 +1,18 @@
 // pa_decode.hip -- single-token decode over the poly KV cache.
 //
 // A decode step of an order-n poly attention reads every cached tensor once; it is HBM
-// bound.  Phase 1 (k_dec_partial) splits the cached positions 0..n-2 of every level into
-// chunks and computes, per (level, batch, head, chunk), the softmax partial (m, l, sum p v)
-// with coalesced, non-temporal 16-byte loads; the K row of a position is read once and
-// shared by the query heads of its KV group.  Phase 2 (k_dec_combine) runs one workgroup
+// bound.  Phase 1 splits the cached positions 0..n-2 of every level into chunks and computes,
+// per (level, batch, head, chunk), the softmax partial (m, l, sum p v) with coalesced,
+// non-temporal 16-byte loads; the K row of a position is read once and shared by the query
+// heads of its KV group.  With one or two level heads per KV group k_dec_partial streams K,
+// values and biases in one pass with an online softmax; with more, k_dec_partial_grp scores
+// the K rows for all heads first and then streams the values head by head.  Phase 2
+// (k_dec_combine) runs one workgroup
 // per (batch, KV group): level by level (deepest first) it merges the chunk partials,
 // adds the new position n-1 -- whose value and bias are the step results of the deeper
 // level -- and writes the level's msg / lse cache slot (or the final output).
+#include <algorithm>
+
 #include "pa_common.h"
 #include "pa_launch.h"
 
@@ -37,9 +42,10 @@ __device__ __forceinline__ int step_n(const DecodeDev& D) {
 }
 
 constexpr int kDecThreads = 256;
-constexpr int kDecHB = 4;      // level heads scored per pass over a chunk's K rows
-constexpr int kDecU = 8;       // rows in flight per row group
-constexpr int kDecScoreElems = 4096;  // LDS floats for one chunk's scores (heads x positions)
+constexpr int kDecHB = 4;      // grouped kernel: level heads scored per pass over a chunk's K rows
+constexpr int kDecRows = 8;    // rows in flight per row group (streaming kernel: heads x rows)
+constexpr float kDecTau = 8.f;  // lazy-rescale headroom of the partial's running max (log2 units)
+constexpr int kDecChunkWork = 4096;  // level heads per KV group x positions of one chunk, at most
 constexpr int kDecMaxHeadsPerGroup = 64;
 constexpr int kDecMaxGroupElems = 8192;  // level heads per KV group * head dim
 
@@ -89,7 +95,189 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
-// One workgroup per (chunk of cached positions, batch, KV group, level):
+// Streaming variant (one or two level heads per KV group), one workgroup per (chunk of cached
+// positions, batch, KV group, level), one pass:
+// each row group of LPR lanes walks its positions (row groups interleaved, so a wave's loads
+// cover consecutive rows) with U = kDecRows / HB rows in flight, reads the K row once for
+// HB level heads of the group together with those heads' value rows (times vmul for middle
+// levels) and key biases, and keeps a per-head online softmax state (running max m in the
+// log2 domain, sum l, sum p v over its E elements) with a lazy rescale.  At the end the row
+// groups of a wave merge through lane exchanges, the four waves through LDS, and the chunk
+// record (m, l, sum p v) is written.  More than HB heads per group re-read the K rows per
+// batch of heads.
+template <typename T, int LPR, int HB>
+__global__ __launch_bounds__(kDecThreads) void k_dec_partial(DecodeDev D) {
+    constexpr int E = Vec16<T>::n;
+    constexpr int KG = kDecThreads / LPR;  // row groups per workgroup
+    constexpr int NW = kDecThreads / 64;
+    constexpr int U = kDecRows / HB;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    __shared__ float s_ml[NW][HB][2];
+    __shared__ float s_acc[NW][HB][256];
+
+    const int c = blockIdx.x, bg = blockIdx.y, t = blockIdx.z;
+    const int b = bg / D.kv_heads, g = bg % D.kv_heads;
+    const DecLevelDev& L = D.L[t];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = tid % LPR, kg = tid / LPR;
+    const int d0 = sub * E;
+    const bool dok = d0 < D.dim;
+    const int C = D.chunk;
+    const int j_begin = c * C;
+    const int cnt = min(C, step_n(D) - 1 - j_begin);
+    const int rep = L.rep, h0 = g * rep;
+    if (cnt <= 0) {
+        // a chunk past the step's positions (grid sized for the capacity): empty records
+        for (int hh = tid; hh < rep; hh += kDecThreads) {
+            float* rec = L.ws + (((int64_t)b * L.heads + h0 + hh) * D.nchunks + c) * D.rec;
+            rec[0] = -INFINITY;
+            rec[1] = 0.f;
+        }
+        return;
+    }
+    const float cinv = D.softclamp > 0.f ? D.scale / D.softclamp : 0.f;
+    const float cl2 = D.softclamp * kLog2e;
+    const float sl2 = D.scale * kLog2e;
+    const bool has_vmul = L.vmul.ok(), has_bias = L.bias.ok();
+    const T* kbase = L.k.row<T>(b, h0, 0) + d0;
+    const int64_t ksn = L.k.sn, vsn = L.v.sn, msn = L.vmul.sn;
+    auto raw16 = [&](const T* p) __attribute__((always_inline)) -> u32x4 {
+        return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    };
+    auto unpack = [&](const u32x4& r, float* out) __attribute__((always_inline)) {
+        const T* e = reinterpret_cast<const T*>(&r);
+#pragma unroll
+        for (int i = 0; i < E; ++i) out[i] = to_f(e[i]);
+    };
+
+    for (int hb0 = 0; hb0 < rep; hb0 += HB) {
+        const int nh = min(HB, rep - hb0);
+        float qv[HB][E], acc[HB][E], m[HB], l[HB];
+        const T* vbase[HB];
+        const T* mbase[HB];
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh) {
+            const int h = h0 + hb0 + (hh < nh ? hh : 0);
+            if (hh < nh && dok) load16<T>(L.q.row<T>(b, h, 0) + d0, qv[hh]);
+            else
+#pragma unroll
+                for (int e = 0; e < E; ++e) qv[hh][e] = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[hh][e] = 0.f;
+            m[hh] = -INFINITY;
+            l[hh] = 0.f;
+            vbase[hh] = L.v.row<T>(b, h, 0) + d0;
+            mbase[hh] = has_vmul ? L.vmul.row<T>(b, h, 0) + d0 : nullptr;
+        }
+        for (int jl0 = kg; jl0 < cnt; jl0 += KG * U) {
+            // loads of U rows: K (shared by the heads), then per head value, multiplier, bias
+            u32x4 kr[U], vr[HB][U], mr[HB][U];
+            float bz[HB][U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int jl = jl0 + u * KG;
+                const bool ok = jl < cnt && dok;
+                const int64_t j = j_begin + (jl < cnt ? jl : 0);
+                kr[u] = ok ? raw16(kbase + j * ksn) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int hh = 0; hh < HB; ++hh) {
+                    const bool hok = ok && hh < nh;
+                    vr[hh][u] = hok ? raw16(vbase[hh] + j * vsn) : u32x4{0u, 0u, 0u, 0u};
+                    mr[hh][u] = (hok && has_vmul) ? raw16(mbase[hh] + j * msn) : u32x4{0u, 0u, 0u, 0u};
+                    bz[hh][u] = (jl < cnt && hh < nh && has_bias) ? L.bias.scalar(b, h0 + hb0 + hh, (int)j) : 0.f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int jl = jl0 + u * KG;
+                float kf[E];
+                unpack(kr[u], kf);
+#pragma unroll
+                for (int hh = 0; hh < HB; ++hh) {
+                    if (hh >= nh) break;
+                    float part = 0.f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) part += qv[hh][e] * kf[e];
+                    const float dot = group_sum<LPR>(part);
+                    float x = D.softclamp > 0.f ? cl2 * tanhf(dot * cinv) : dot * sl2;
+                    const float bj = bz[hh][u];
+                    x = (jl < cnt && bias_class(bj) == 0) ? x + bj * kLog2e : -INFINITY;
+                    // lazy rescale: the running max moves only past kDecTau of headroom
+                    if (x > m[hh] + kDecTau) {
+                        const float alpha = __builtin_amdgcn_exp2f(m[hh] - x);  // 0 when m = -inf
+                        l[hh] *= alpha;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) acc[hh][e] *= alpha;
+                        m[hh] = x;
+                    }
+                    const float pj = __builtin_amdgcn_exp2f(x - (m[hh] == -INFINITY ? 0.f : m[hh]));
+                    l[hh] += pj;
+                    float vf[E];
+                    unpack(vr[hh][u], vf);
+                    if (has_vmul) {
+                        float mf[E];
+                        unpack(mr[hh][u], mf);
+#pragma unroll
+                        for (int e = 0; e < E; ++e) vf[e] = round_to<T>(vf[e] * mf[e]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < E; ++e) acc[hh][e] += pj * vf[e];
+                }
+            }
+        }
+        // merge the row groups of each wave (lanes LPR, 2 LPR, ... apart), then the waves
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh) {
+            if (hh >= nh) break;
+            float mw = m[hh];
+            for (int off = LPR; off < 64; off <<= 1) mw = fmaxf(mw, __shfl_xor(mw, off));
+            const float cs = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[hh] - mw);
+            float lw = l[hh] * cs;
+            float aw[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) aw[e] = acc[hh][e] * cs;
+            for (int off = LPR; off < 64; off <<= 1) {
+                lw += __shfl_xor(lw, off);
+#pragma unroll
+                for (int e = 0; e < E; ++e) aw[e] += __shfl_xor(aw[e], off);
+            }
+            if (lane < LPR && dok)
+#pragma unroll
+                for (int e = 0; e < E; ++e) s_acc[wave][hh][d0 + e] = aw[e];
+            if (lane == 0) {
+                s_ml[wave][hh][0] = mw;
+                s_ml[wave][hh][1] = lw;
+            }
+        }
+        __syncthreads();
+        for (int hh = 0; hh < nh; ++hh) {
+            float mt = -INFINITY;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) mt = fmaxf(mt, s_ml[w2][hh][0]);
+            float cw[NW], lt = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) {
+                cw[w2] = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_ml[w2][hh][0] - mt);
+                lt += s_ml[w2][hh][1] * cw[w2];
+            }
+            float* rec = L.ws + (((int64_t)b * L.heads + h0 + hb0 + hh) * D.nchunks + c) * D.rec;
+            for (int x = tid; x < D.dim; x += kDecThreads) {
+                float a = 0.f;
+#pragma unroll
+                for (int w2 = 0; w2 < NW; ++w2) a += s_acc[w2][hh][x] * cw[w2];
+                rec[2 + x] = a;
+            }
+            if (tid == 0) {
+                rec[0] = mt;
+                rec[1] = lt;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Grouped variant (more than two level heads per KV group), one workgroup per (chunk of
+// cached positions, batch, KV group, level), in three phases:
 //   1. the chunk's key biases (the deeper level's lse, log2 domain) are staged in LDS, then
 //      each row group of LPR lanes reads whole K rows (16 bytes per lane, kDecU rows in
 //      flight) and adds the score of every level head of the group;
@@ -97,10 +285,11 @@ __device__ __forceinline__ float group_sum(float x) {
 //   3. per head: the values (times vmul for middle levels) are streamed with one FMA per
 //      element, reduced over the row groups and written as the chunk record (m, l, sum p v).
 template <typename T, int LPR>
-__global__ __launch_bounds__(kDecThreads) void k_dec_partial(DecodeDev D) {
+__global__ __launch_bounds__(kDecThreads) void k_dec_partial_grp(DecodeDev D) {
     constexpr int E = Vec16<T>::n;
     constexpr int KG = kDecThreads / LPR;
-    __shared__ float s_sc[kDecScoreElems];
+    constexpr int kDecU = kDecRows;
+    __shared__ float s_sc[kDecChunkWork];
     __shared__ float s_ml[kDecMaxHeadsPerGroup][2];
     __shared__ float s_acc[kDecThreads / 64][256];
 
@@ -655,12 +844,12 @@ static int pick_chunks(const pa_decode* d, int* chunk_out) {
         *chunk_out = 1;
         return 0;
     }
-    // the scores of one chunk (level heads per KV group x positions) live in LDS
+    // a chunk's work (level heads per KV group x positions) stays bounded
     int max_rep = 1;
     for (int t = 0; t < d->order && t < PA_MAX_ORDER; ++t)
         if (d->kv_heads > 0 && d->levels[t].heads / d->kv_heads > max_rep)
             max_rep = d->levels[t].heads / d->kv_heads;
-    int cap = kDecScoreElems / max_rep;
+    int cap = kDecChunkWork / max_rep;
     if (cap > 1024) cap = 1024;
     cap = cap / 64 * 64;
     if (cap < 64) cap = 64;
@@ -681,17 +870,40 @@ static int pick_chunks(const pa_decode* d, int* chunk_out) {
     return (nold + chunk - 1) / chunk;
 }
 
-template <typename T>
-static void launch_partial_t(const DecodeDev& D, dim3 grid, hipStream_t s) {
+template <typename T, int HB>
+static void launch_partial_h(const DecodeDev& D, dim3 grid, hipStream_t s) {
     switch (D.lpr) {
-        case 1: hipLaunchKernelGGL((k_dec_partial<T, 1>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 2: hipLaunchKernelGGL((k_dec_partial<T, 2>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 4: hipLaunchKernelGGL((k_dec_partial<T, 4>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 8: hipLaunchKernelGGL((k_dec_partial<T, 8>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 16: hipLaunchKernelGGL((k_dec_partial<T, 16>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 32: hipLaunchKernelGGL((k_dec_partial<T, 32>), grid, dim3(kDecThreads), 0, s, D); break;
-        default: hipLaunchKernelGGL((k_dec_partial<T, 64>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 1: hipLaunchKernelGGL((k_dec_partial<T, 1, HB>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 2: hipLaunchKernelGGL((k_dec_partial<T, 2, HB>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 4: hipLaunchKernelGGL((k_dec_partial<T, 4, HB>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 8: hipLaunchKernelGGL((k_dec_partial<T, 8, HB>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 16: hipLaunchKernelGGL((k_dec_partial<T, 16, HB>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 32: hipLaunchKernelGGL((k_dec_partial<T, 32, HB>), grid, dim3(kDecThreads), 0, s, D); break;
+        default: hipLaunchKernelGGL((k_dec_partial<T, 64, HB>), grid, dim3(kDecThreads), 0, s, D); break;
     }
+}
+
+template <typename T>
+static void launch_partial_grp(const DecodeDev& D, dim3 grid, hipStream_t s) {
+    switch (D.lpr) {
+        case 1: hipLaunchKernelGGL((k_dec_partial_grp<T, 1>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 2: hipLaunchKernelGGL((k_dec_partial_grp<T, 2>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 4: hipLaunchKernelGGL((k_dec_partial_grp<T, 4>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 8: hipLaunchKernelGGL((k_dec_partial_grp<T, 8>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 16: hipLaunchKernelGGL((k_dec_partial_grp<T, 16>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 32: hipLaunchKernelGGL((k_dec_partial_grp<T, 32>), grid, dim3(kDecThreads), 0, s, D); break;
+        default: hipLaunchKernelGGL((k_dec_partial_grp<T, 64>), grid, dim3(kDecThreads), 0, s, D); break;
+    }
+}
+
+// by the largest level head count per KV group: one or two heads stream in one pass (K, values
+// and biases together); more take the grouped three-phase kernel (K rows scored for every head
+// at once, then the values of one head after another)
+template <typename T>
+static void launch_partial_t(const DecodeDev& D, int max_rep, dim3 grid, hipStream_t s) {
+    if (max_rep <= 1) launch_partial_h<T, 1>(D, grid, s);
+    else if (max_rep <= 2) launch_partial_h<T, 2>(D, grid, s);
+    else launch_partial_grp<T>(D, grid, s);
 }
 
 static int level_heads(const pa_decode_level& L) {
@@ -807,10 +1019,12 @@ int launch_decode(const pa_decode* d, hipStream_t s) {
     }
     if (D.nchunks > 0) {
         dim3 grid(D.nchunks, d->batch * d->kv_heads, d->order);
+        int max_rep = 1;
+        for (int t = 0; t < d->order; ++t) max_rep = std::max(max_rep, D.L[t].rep);
         ProfScope ps("dec_partial", s);
-        if (T == PA_F32) launch_partial_t<float>(D, grid, s);
-        else if (T == PA_F16) launch_partial_t<f16>(D, grid, s);
-        else launch_partial_t<bf16>(D, grid, s);
+        if (T == PA_F32) launch_partial_t<float>(D, max_rep, grid, s);
+        else if (T == PA_F16) launch_partial_t<f16>(D, max_rep, grid, s);
+        else launch_partial_t<bf16>(D, max_rep, grid, s);
     }
     dim3 cgrid(d->batch * d->kv_heads);
     ProfScope ps("dec_combine", s);

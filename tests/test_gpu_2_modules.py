@@ -178,20 +178,23 @@ def test_kv_cache_stepwise_equals_parallel(order, kv_heads, use_rotary_embed):
     assert_close(torch.cat(outs, dim=1), ref, 1e-4, "stepwise")
 
 
-@param("chunk,H,G", ((0, 8, 2), (64, 8, 2), (64, 64, 2)))
-def test_decode_kernel_gqa_synthetic_cache(chunk, H, G):
-    """Config-5 shape class (GQA, d=128) at a small cache, with a synthetic cache
-    (q/k/v/msg ~ N(0,1), lse = log(j+1) + N(0,1)) against the oracle's cached branch; chunk=64
-    splits the 299 cached positions over five partial records (the merge path); 64 query heads
-    on 2 KV heads (33 level heads per group) exceed the combine kernel's LDS state budget, so
-    some heads are merged in its second phase."""
+@param("chunk,H,G,dh,sc", ((0, 8, 2, 128, None), (64, 8, 2, 128, None), (64, 64, 2, 128, None),
+                           (0, 2, 2, 128, None), (64, 2, 2, 64, None), (64, 4, 2, 64, None),
+                           (0, 4, 2, 32, 5.0), (64, 3, 3, 128, 5.0)))
+def test_decode_kernel_gqa_synthetic_cache(chunk, H, G, dh, sc):
+    """Config-5 shape class (GQA) at a small cache, with a synthetic cache (q/k/v/msg ~ N(0,1),
+    lse = log(j+1) + N(0,1)) against the oracle's cached branch; chunk=64 splits the 299 cached
+    positions over five partial records (the merge path); 64 query heads on 2 KV heads (33
+    level heads per group) exceed the combine kernel's LDS state budget, so some heads are
+    merged in its second phase.  One or two heads per KV group take the streaming partial
+    kernel, more the grouped one."""
     from poly_attention import _ops
 
     d = dev()
     g = torch.Generator().manual_seed(5)
-    B, n, dh = 2, 300, 128
+    B, n = 2, 300
     r = H // G
-    for dtype in (torch.float32, torch.bfloat16):
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
         q2c, q3c, v3c = (torch.randn(B, G, n, dh, generator=g).to(dtype) for _ in range(3))
         msg = torch.randn(B, H, n, dh, generator=g).to(dtype)
         lse = (torch.log(torch.arange(1, n + 1).float()) + torch.randn(B, H, n, generator=g))
@@ -201,10 +204,10 @@ def test_decode_kernel_gqa_synthetic_cache(chunk, H, G):
         f = lambda t: O.repeat_kv(t.float(), r)  # noqa: E731
         cache = (None, None, None, lse[:, :, :-1], msg[:, :, :-1].float())
         ref, lse_step, msg_step = O.reference_poly_attention(
-            q1.float(), f(q2n), f(q2c), f(q3c), f(v3c), cache=cache)
+            q1.float(), f(q2n), f(q2c), f(q3c), f(v3c), cache=cache, softclamp_value=sc)
         msg_d, lse_d = msg.to(d).clone(), lse.to(d).clone()
         out = _ops.poly_decode_step([q1.to(d), q2n.to(d)], [q2c.to(d), q3c.to(d)], [v3c.to(d)],
-                                    [msg_d], [lse_d], kv_heads=G, heads=H, softclamp=None,
+                                    [msg_d], [lse_d], kv_heads=G, heads=H, softclamp=sc,
                                     scale=dh ** -0.5, chunk=chunk)
         torch.cuda.synchronize()
         tol = 1e-4 if dtype == torch.float32 else 2e-2
