@@ -305,8 +305,18 @@ class _Block(torch.nn.Module):
         attn_out, new_cache = self.attn(self.norm1(x), rotary_pos_emb=rotary_pos_emb,
                                         cache=cache, return_cache=True)
         x = x + attn_out
-        x = x + self.ffn(self.norm2(x))
+        h = self.ffn[1](_linear(self.ffn[0], self.norm2(x)))
+        x = x + _linear(self.ffn[2], h)
         return x, new_cache
+
+
+def _linear(layer, x):
+    """layer(x); on the GPU, decode-sized inputs stream the weight on pa_linear_small."""
+    if x.is_cuda:
+        from poly_attention import _ops
+
+        return _ops.linear(layer, x)
+    return layer(x)
 
 
 class _PolyLM(torch.nn.Module):
@@ -336,7 +346,7 @@ class _PolyLM(torch.nn.Module):
         for layer, lc in zip(self.layers, layer_caches):
             x, nc = layer(x, rotary_pos_emb=rot, cache=lc)
             new.append(nc)
-        return self.to_logits(self.norm(x)), (new, None if past is None else past + seq_len)
+        return _linear(self.to_logits, self.norm(x)), (new, None if past is None else past + seq_len)
 
 
 def _greedy(lm, prompt, steps):

@@ -21,6 +21,10 @@
  *                      282-286).
  *   pa_rmsnorm_fwd/bwd the per-head q/k RMSNorms of the modules in training and prefill
  *                      (poly_attention.py:271, n_poly_attention.py:188).
+ *   pa_linear_small    the nn.Linear projections of a single-token decode step (to_q, to_kvs,
+ *                      to_out: poly_attention.py:188-204, n_poly_attention.py:108-120; the
+ *                      decode harness's feed-forward and logits, train_enwik8.py:40,148-177)
+ *                      when the batch has at most 16 rows.
  *
  * Semantics of one pass (per batch b, pass head h, query row i, key j):
  *   s_ij  = scale * <q[b, h/rq, i], k[b, h/rk, j]>           rq = heads / q.heads, etc.
@@ -44,7 +48,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 2
+#define PA_ABI_VERSION 3
 #define PA_MAX_ORDER 8
 
 /* status codes (0 = success, negative = failure) */
@@ -203,12 +207,30 @@ typedef struct pa_rmsnorm {
     size_t      workspace_bytes;
 } pa_rmsnorm;
 
+/* Skinny linear layer for decode steps: y[m, :] = x[m, :] . w^T + bias for rows <= 16
+ * (torch.nn.functional.linear semantics, fp32 accumulation, bias added in fp32, one rounding
+ * to dtype).  w is nn.Linear's weight, [out_features, in_features] rows.  All tensors share
+ * dtype; strides are row strides in elements (unit innermost stride).  in_features must be a
+ * multiple of 8 (4 for fp32), x and w 16-byte aligned with row strides of whole 16 bytes, and
+ * rows * in_features * element size <= 64 KiB. */
+typedef struct pa_linear {
+    int32_t     rows, in_features, out_features;
+    int32_t     dtype;          /* PA_F32 / PA_F16 / PA_BF16 */
+    const void* x;              /* [rows, in_features] */
+    int64_t     x_stride;
+    const void* w;              /* [out_features, in_features] */
+    int64_t     w_stride;
+    const void* bias;           /* [out_features] or NULL */
+    void*       y;              /* [rows, out_features] */
+    int64_t     y_stride;
+} pa_linear;
+
 int         pa_abi_version(void);
 const char* pa_strerror(int status);
 int         pa_last_hip_error(void);   /* hipError_t of the last PA_EHIP on this thread */
 /* sizeof of the ABI structs, for binding checks: 0 pa_view, 1 pa_mask, 2 pa_pass,
  * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode, 6 pa_prologue_item, 7 pa_prologue,
- * 8 pa_rmsnorm; 0 for other values */
+ * 8 pa_rmsnorm, 9 pa_linear; 0 for other values */
 size_t      pa_struct_size(int which);
 
 /* Kernel timing (no counterpart in the reference: a measurement facility for benchmarks).
@@ -232,6 +254,7 @@ int    pa_decode_prologue(const pa_prologue* p, void* stream);
 int    pa_rmsnorm_fwd(const pa_rmsnorm* r, void* stream);
 size_t pa_rmsnorm_bwd_workspace(const pa_rmsnorm* r);
 int    pa_rmsnorm_bwd(const pa_rmsnorm* r, void* stream);
+int    pa_linear_small(const pa_linear* l, void* stream);
 
 #ifdef __cplusplus
 }

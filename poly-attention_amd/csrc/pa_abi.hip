@@ -168,6 +168,7 @@ size_t pa_struct_size(int which) {
         case 6: return sizeof(pa_prologue_item);
         case 7: return sizeof(pa_prologue);
         case 8: return sizeof(pa_rmsnorm);
+        case 9: return sizeof(pa_linear);
         default: return 0;
     }
 }
@@ -328,6 +329,13 @@ size_t pa_rmsnorm_bwd_workspace(const pa_rmsnorm* r) {
 int pa_rmsnorm_bwd(const pa_rmsnorm* r, void* stream) {
     if (!r) return PA_EINVAL;
     const int st = launch_rms_bwd(r, static_cast<hipStream_t>(stream));
+    if (st != PA_OK) return st;
+    return finish_launch();
+}
+
+int pa_linear_small(const pa_linear* l, void* stream) {
+    if (!l) return PA_EINVAL;
+    const int st = launch_linear_small(l, static_cast<hipStream_t>(stream));
     if (st != PA_OK) return st;
     return finish_launch();
 }

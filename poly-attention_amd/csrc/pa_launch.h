@@ -35,5 +35,6 @@ int launch_prologue(const pa_prologue* p, hipStream_t s);
 int launch_rms_fwd(const pa_rmsnorm* p, hipStream_t s);
 size_t rms_bwd_workspace(const pa_rmsnorm* p);
 int launch_rms_bwd(const pa_rmsnorm* p, hipStream_t s);
+int launch_linear_small(const pa_linear* l, hipStream_t s);
 
 }  // namespace pa

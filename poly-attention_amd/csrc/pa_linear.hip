@@ -1,0 +1,242 @@
+// pa_linear.hip -- the projections of a single-token decode step: y = x . w^T + bias for a
+// handful of rows (the batch), which is a pass over the weight matrix and nothing else.
+//
+// A library GEMM tiles such a product for large M and leaves most CUs idle at M <= 16; here
+// every wave owns R output features, streams their weight rows with 16-byte non-temporal
+// loads (the first round of chunks issued before x is staged, so both latencies overlap), and
+// takes the x rows from LDS, staged once per workgroup; 16-bit types multiply in packed dot
+// products (v_dot2_f32_{bf16,f16}, exact products, fp32 sums).  The R x MM per-lane partial sums are reduced over the wave by a
+// butterfly reduce-scatter (each exchange halves the values a lane carries), so that every
+// lane ends with one finished sum.  fp32 accumulation, bias added in fp32, one rounding.
+#include <algorithm>
+#include <type_traits>
+
+#include "pa_common.h"
+#include "pa_launch.h"
+
+namespace pa {
+
+constexpr int kLinThreads = 256;
+constexpr int kLinMaxRows = 16;
+constexpr int kLinMaxLds = 64 * 1024;  // bytes of staged x rows
+
+struct LinDev {
+    const char* x;
+    const char* w;
+    const char* bias;
+    char* y;
+    int64_t xs, ws, ys;  // row strides (elements)
+    int32_t rows, k, n;
+};
+
+template <typename T> struct LinVec { static constexpr int n = 8; };
+template <> struct LinVec<float> { static constexpr int n = 4; };
+
+// Reduce-scatter of V values over the 64 lanes: afterwards lane l holds the wave sum of value
+// index idx(l) (bits of l from bit 5 down, one per halving); lanes that differ only in the
+// bits below log2(V) + (6 - log2(V)) hold the same sum.  Returns that sum.
+template <int V>
+__device__ __forceinline__ float wave_reduce_scatter(float (&v)[V], int lane) {
+    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "power of two up to 64");
+    int cnt = V;
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        if (cnt > 1) {
+            const int h = cnt / 2;
+            const bool up = (lane & s) != 0;
+#pragma unroll
+            for (int i = 0; i < V / 2; ++i) {
+                if (i < h) {
+                    const float send = up ? v[i] : v[h + i];
+                    const float keep = up ? v[h + i] : v[i];
+                    v[i] = keep + __shfl_xor(send, s);
+                }
+            }
+            cnt = h;
+        } else {
+            v[0] += __shfl_xor(v[0], s);
+        }
+    }
+    return v[0];
+}
+
+// the value index a lane holds after wave_reduce_scatter<V>
+template <int V>
+__device__ __forceinline__ int reduce_scatter_index(int lane) {
+    int idx = 0, cnt = V;
+    for (int s = 32; s >= 1 && cnt > 1; s >>= 1) {
+        const int h = cnt / 2;
+        if (lane & s) idx += h;
+        cnt = h;
+    }
+    return idx;
+}
+
+// acc + <w, x> over one 16-byte chunk: packed dot products for 16-bit types (products exact
+// in fp32), FMAs for fp32
+template <typename T>
+__device__ __forceinline__ float chunk_dot(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                           uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, float acc) {
+    if constexpr (std::is_same<T, float>::value) {
+        acc = fmaf(__uint_as_float(w0), __uint_as_float(x0), acc);
+        acc = fmaf(__uint_as_float(w1), __uint_as_float(x1), acc);
+        acc = fmaf(__uint_as_float(w2), __uint_as_float(x2), acc);
+        return fmaf(__uint_as_float(w3), __uint_as_float(x3), acc);
+    } else if constexpr (std::is_same<T, bf16>::value) {
+        typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+        auto d = [](uint32_t a, uint32_t b, float c) {
+            return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+        };
+        return d(w3, x3, d(w2, x2, d(w1, x1, d(w0, x0, acc))));
+    } else {
+        typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+        auto d = [](uint32_t a, uint32_t b, float c) {
+            return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+        };
+        return d(w3, x3, d(w2, x2, d(w1, x1, d(w0, x0, acc))));
+    }
+}
+
+// Chunks of 16 bytes per lane and feature in flight per round: 32 registers of weights.
+template <int R>
+constexpr int kLinU = 8 / R;
+
+template <typename T, int MM, int R>
+__global__ __launch_bounds__(kLinThreads) void k_linear_small(LinDev L) {
+    constexpr int E = LinVec<T>::n;
+    constexpr int U = kLinU<R>;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    extern __shared__ u32x4 s_x[];  // rows x (k / E) chunks
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cpr = L.k / E;
+    const int rows = L.rows;
+    const int n0 = (blockIdx.x * (kLinThreads / 64) + wave) * R;
+    const T* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        wrow[r] = reinterpret_cast<const T*>(L.w) + (int64_t)min(n0 + r, L.n - 1) * L.ws;
+    const bool live = n0 < L.n;
+    u32x4 wr[U][R];
+    auto load_round = [&](int c0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + 64 * u;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                wr[u][r] = (live && c < cpr)
+                               ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + c * E))
+                               : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    // the first round of weights is in flight while x is staged (eight loads per thread in
+    // flight per round of the staging loop)
+    load_round(lane);
+    const int total = rows * cpr;
+    for (int i0 = tid; i0 < total; i0 += 8 * kLinThreads) {
+        u32x4 t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j * kLinThreads;
+            const int r = i / cpr, c = i - r * cpr;
+            if (i < total)
+                t[j] = *reinterpret_cast<const u32x4*>(L.x + ((int64_t)r * L.xs + (int64_t)c * E) * sizeof(T));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (i0 + j * kLinThreads < total) s_x[i0 + j * kLinThreads] = t[j];
+    }
+    __syncthreads();
+    if (!live) return;
+
+    float acc[R * MM];
+#pragma unroll
+    for (int i = 0; i < R * MM; ++i) acc[i] = 0.f;
+    for (int c0 = lane; c0 < cpr; c0 += 64 * U) {
+        if (c0 != lane) load_round(c0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + 64 * u;
+            if (c >= cpr) break;
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                if (m >= rows) break;
+                const u32x4 xr = s_x[m * cpr + c];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    acc[r * MM + m] = chunk_dot<T>(wr[u][r][0], wr[u][r][1], wr[u][r][2], wr[u][r][3],
+                                                   xr[0], xr[1], xr[2], xr[3], acc[r * MM + m]);
+            }
+        }
+    }
+    const float tot = wave_reduce_scatter<R * MM>(acc, lane);
+    const int idx = reduce_scatter_index<R * MM>(lane);
+    const int r = idx / MM, m = idx % MM;
+    // one writer per value: the lowest lane of those holding it
+    constexpr int V = R * MM;
+    const int dup = 64 / V;  // lanes sharing a value (adjacent in the low bits)
+    if ((lane & (dup - 1)) == 0 && m < rows && n0 + r < L.n) {
+        float out = tot;
+        if (L.bias) out += to_f(reinterpret_cast<const T*>(L.bias)[n0 + r]);
+        reinterpret_cast<T*>(L.y)[(int64_t)m * L.ys + n0 + r] = (T)out;
+    }
+}
+
+template <typename T, int MM>
+static void launch_lin_r(const LinDev& L, int R, size_t lds, hipStream_t s) {
+    const int waves_per_wg = kLinThreads / 64;
+    auto grid = [&](int r) { return dim3((L.n + waves_per_wg * r - 1) / (waves_per_wg * r)); };
+    if (R == 1) {
+        hipLaunchKernelGGL((k_linear_small<T, MM, 1>), grid(1), dim3(kLinThreads), lds, s, L);
+    } else if (R == 2 || MM > 8) {  // 16 rows: at most two features per wave (registers)
+        hipLaunchKernelGGL((k_linear_small<T, MM, 2>), grid(2), dim3(kLinThreads), lds, s, L);
+    } else if constexpr (MM <= 8) {
+        hipLaunchKernelGGL((k_linear_small<T, MM, 4>), grid(4), dim3(kLinThreads), lds, s, L);
+    }
+}
+
+template <typename T>
+static void launch_lin_t(const LinDev& L, int R, size_t lds, hipStream_t s) {
+    if (L.rows <= 1) launch_lin_r<T, 1>(L, R, lds, s);
+    else if (L.rows <= 2) launch_lin_r<T, 2>(L, R, lds, s);
+    else if (L.rows <= 4) launch_lin_r<T, 4>(L, R, lds, s);
+    else if (L.rows <= 8) launch_lin_r<T, 8>(L, R, lds, s);
+    else launch_lin_r<T, 16>(L, R, lds, s);
+}
+
+int launch_linear_small(const pa_linear* l, hipStream_t s) {
+    if (l->rows < 1 || l->in_features < 1 || l->out_features < 1) return PA_EINVAL;
+    if (!l->x || !l->w || !l->y) return PA_EINVAL;
+    const int T = l->dtype;
+    if (T != PA_F32 && T != PA_F16 && T != PA_BF16) return PA_EINVAL;
+    if (l->rows > kLinMaxRows) return PA_EUNSUPPORTED;
+    const int es = T == PA_F32 ? 4 : 2, E = 16 / es;
+    if (l->in_features % E != 0) return PA_EUNSUPPORTED;
+    if ((uintptr_t)l->x % 16 != 0 || (uintptr_t)l->w % 16 != 0) return PA_EUNSUPPORTED;
+    if (l->x_stride % E != 0 || l->w_stride % E != 0) return PA_EUNSUPPORTED;
+    if (l->w_stride < l->in_features) return PA_EINVAL;
+    if (l->rows > 1 && (l->x_stride < l->in_features || l->y_stride < l->out_features)) return PA_EINVAL;
+    if ((uintptr_t)l->y % es != 0 || (l->bias && (uintptr_t)l->bias % es != 0)) return PA_EINVAL;
+    const size_t lds = (size_t)l->rows * l->in_features * es;
+    if (lds > (size_t)kLinMaxLds) return PA_EUNSUPPORTED;
+
+    LinDev L;
+    L.x = static_cast<const char*>(l->x);
+    L.w = static_cast<const char*>(l->w);
+    L.bias = static_cast<const char*>(l->bias);
+    L.y = static_cast<char*>(l->y);
+    L.xs = l->x_stride;
+    L.ws = l->w_stride;
+    L.ys = l->y_stride;
+    L.rows = l->rows;
+    L.k = l->in_features;
+    L.n = l->out_features;
+    // features per wave (one measured fastest at decode sizes)
+    const int R = 1;
+    ProfScope ps("linear_small", s);
+    if (T == PA_F32) launch_lin_t<float>(L, R, lds, s);
+    else if (T == PA_F16) launch_lin_t<f16>(L, R, lds, s);
+    else launch_lin_t<bf16>(L, R, lds, s);
+    return PA_OK;
+}
+
+}  // namespace pa

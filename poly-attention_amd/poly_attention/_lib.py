@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolyattn.so"
 
-PA_ABI_VERSION = 2
+PA_ABI_VERSION = 3
 PA_MAX_ORDER = 8
 
 PA_OK = 0
@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "pa_rmsnorm_fwd",
     "pa_rmsnorm_bwd_workspace",
     "pa_rmsnorm_bwd",
+    "pa_linear_small",
 )
 
 
@@ -180,12 +181,28 @@ class PaRmsNorm(ctypes.Structure):
     ]
 
 
+class PaLinear(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_int32),
+        ("in_features", c_int32),
+        ("out_features", c_int32),
+        ("dtype", c_int32),
+        ("x", c_void_p),
+        ("x_stride", c_int64),
+        ("w", c_void_p),
+        ("w_stride", c_int64),
+        ("bias", c_void_p),
+        ("y", c_void_p),
+        ("y_stride", c_int64),
+    ]
+
+
 class PaKernelTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("launches", c_int64), ("total_ms", ctypes.c_double)]
 
 
 STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode, PaPrologueItem,
-           PaPrologue, PaRmsNorm)
+           PaPrologue, PaRmsNorm, PaLinear)
 
 
 class PolyAttnError(RuntimeError):
@@ -233,6 +250,8 @@ def _configure(lib) -> None:
     lib.pa_rmsnorm_bwd_workspace.argtypes = [ctypes.POINTER(PaRmsNorm)]
     lib.pa_rmsnorm_bwd.restype = c_int
     lib.pa_rmsnorm_bwd.argtypes = [ctypes.POINTER(PaRmsNorm), c_void_p]
+    lib.pa_linear_small.restype = c_int
+    lib.pa_linear_small.argtypes = [ctypes.POINTER(PaLinear), c_void_p]
 
 
 def load(path: str | os.PathLike | None = None):

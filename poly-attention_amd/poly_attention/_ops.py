@@ -409,6 +409,66 @@ def rms_norm(x: Tensor, weight: Optional[Tensor], eps: Optional[float]) -> Tenso
 
 
 # ---------------------------------------------------------------------------------------
+# projections of a single-token decode step
+
+LINEAR_MAX_ROWS = 16
+
+
+def linear_supported(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> bool:
+    """Whether pa_linear_small takes F.linear(x, weight, bias): plain inference (no autograd,
+    not under torch.compile) on CUDA tensors of one dtype, at most 16 rows of x (all leading
+    dims), in_features a multiple of 8 (4 for fp32) with x fitting the 64 KiB staging."""
+    if not (x.is_cuda and weight.is_cuda) or x.dtype not in DTYPE_CODE or weight.dtype != x.dtype:
+        return False
+    if weight.dim() != 2 or x.dim() < 1 or weight.device != x.device:
+        return False
+    if torch.compiler.is_compiling() or _needs_op(x, weight, bias):
+        return False
+    k = x.shape[-1]
+    if weight.shape[1] != k or k == 0:
+        return False
+    rows = x.numel() // k
+    e = 4 if x.dtype == torch.float32 else 8
+    if not 1 <= rows <= LINEAR_MAX_ROWS or k % e or rows * k * x.element_size() > 65536:
+        return False
+    if weight.stride(-1) != 1 or weight.stride(0) % e or weight.data_ptr() % 16:
+        return False
+    if bias is not None and (bias.dtype != x.dtype or bias.dim() != 1 or bias.stride(0) != 1
+                             or bias.shape[0] != weight.shape[0] or bias.device != x.device):
+        return False
+    return True
+
+
+def linear_small(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
+    """torch.nn.functional.linear(x, weight, bias) on pa_linear_small: the weight streamed
+    once by every CU for decode-sized x (the caller checks linear_supported)."""
+    lib = _lib.load()
+    k, n = x.shape[-1], weight.shape[0]
+    x2 = x.reshape(-1, k)
+    e = 4 if x.dtype == torch.float32 else 8
+    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % e):
+        x2 = x2.contiguous()
+    y = torch.empty(x2.shape[0], n, dtype=x.dtype, device=x.device)
+    lin = _lib.PaLinear()
+    lin.rows, lin.in_features, lin.out_features = x2.shape[0], k, n
+    lin.dtype = DTYPE_CODE[x.dtype]
+    lin.x, lin.x_stride = x2.data_ptr(), x2.stride(0)
+    lin.w, lin.w_stride = weight.data_ptr(), weight.stride(0)
+    lin.bias = bias.data_ptr() if bias is not None else None
+    lin.y, lin.y_stride = y.data_ptr(), y.stride(0)
+    with _device(x):
+        _lib.check(lib.pa_linear_small(ctypes.byref(lin), _stream(x)), "pa_linear_small")
+    return y.reshape(*x.shape[:-1], n)
+
+
+def linear(layer: torch.nn.Linear, x: Tensor) -> Tensor:
+    """layer(x), on pa_linear_small when linear_supported, else the layer itself."""
+    if x.is_cuda and linear_supported(x, layer.weight, layer.bias):
+        return linear_small(x, layer.weight, layer.bias)
+    return layer(x)
+
+
+# ---------------------------------------------------------------------------------------
 # the order-n chain
 
 

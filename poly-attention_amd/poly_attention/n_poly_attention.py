@@ -119,6 +119,15 @@ class NPolyAttention(Module):
         _lib.load()
         return True
 
+    def _proj(self, layer: nn.Linear, x: Tensor) -> Tensor:
+        """A projection; decode-sized inputs on the fused path stream the weight on
+        pa_linear_small (the reference calls the nn.Linear directly)."""
+        if self._use_fused(x):
+            from . import _ops
+
+            return _ops.linear(layer, x)
+        return layer(x)
+
     def forward(self, x, context: Tensor | tuple[Tensor, ...] | None = None, mask=None,
                 context_mask: Tensor | tuple[Tensor | None, ...] | None = None,
                 rotary_pos_emb=None, cache=None, return_cache=False):
@@ -131,7 +140,7 @@ class NPolyAttention(Module):
         orig_x = x
         x = self.norm(x)
 
-        q_and_maybe_gates = self.split_q(self.to_q(x))
+        q_and_maybe_gates = self.split_q(self._proj(self.to_q, x))
         if self.attn_gate:
             q1, gates = q_and_maybe_gates
         else:
@@ -160,8 +169,8 @@ class NPolyAttention(Module):
         else:
             context = context if has_context else ((x,) * self.order)
 
-        kv1 = self.split_kv1(first(self.to_kvs)(first(context)))
-        kvs_rest = [self.split_kv(to_kv(c)) for c, to_kv in zip(context[1:], self.to_kvs[1:])]
+        kv1 = self.split_kv1(self._proj(first(self.to_kvs), first(context)))
+        kvs_rest = [self.split_kv(self._proj(to_kv, c)) for c, to_kv in zip(context[1:], self.to_kvs[1:])]
 
         if self.shared_kv:
             qs_rest = (first(kv1), *[first(kv) for kv in kvs_rest])
@@ -209,7 +218,7 @@ class NPolyAttention(Module):
         if self.attn_gate:
             out = out * gates.sigmoid()
 
-        out = self.to_out(self.merge_heads(out))
+        out = self._proj(self.to_out, self.merge_heads(out))
 
         if not return_cache:
             return out

@@ -267,6 +267,15 @@ class Order2PolyAttention(Module):
         _lib.load()  # a GPU tensor with the fused path requested: a missing library is fatal
         return True
 
+    def _proj(self, layer: nn.Linear, x: Tensor) -> Tensor:
+        """A projection; decode-sized inputs on the fused path stream the weight on
+        pa_linear_small (the reference calls the nn.Linear directly)."""
+        if self._use_fused(x):
+            from . import _ops
+
+            return _ops.linear(layer, x)
+        return layer(x)
+
     def forward(self, x, context: Tensor | tuple[Tensor, ...] | None = None, mask=None,
                 context_mask: Tensor | tuple[Tensor | None, ...] | None = None,
                 rotary_pos_emb=None, cache=None, return_cache=False):
@@ -279,7 +288,7 @@ class Order2PolyAttention(Module):
         orig_x = x
         x = self.norm(x)
 
-        q_and_maybe_gates = self.split_q(self.to_q(x))
+        q_and_maybe_gates = self.split_q(self._proj(self.to_q, x))
         if self.attn_gate:
             q1, gates = q_and_maybe_gates
         else:
@@ -313,8 +322,8 @@ class Order2PolyAttention(Module):
 
         # kvs
 
-        kv1 = self.split_kv1(first(self.to_kvs)(ctx1))
-        kv2 = self.split_kv(self.to_kvs[1](ctx2))
+        kv1 = self.split_kv1(self._proj(first(self.to_kvs), ctx1))
+        kv2 = self.split_kv(self._proj(self.to_kvs[1], ctx2))
 
         if self.shared_kv:
             qs = (q1, first(kv1), first(kv2))
@@ -364,7 +373,7 @@ class Order2PolyAttention(Module):
         if self.attn_gate:
             out = out * gates.sigmoid()
 
-        out = self.to_out(self.merge_heads(out))
+        out = self._proj(self.to_out, self.merge_heads(out))
 
         if not return_cache:
             return out

@@ -1,0 +1,128 @@
+"""GPU: pa_linear_small (the projections of a decode step) against an fp32 restatement of
+torch.nn.functional.linear, and its use inside the modules and the decode harness.
+
+Tolerances: fp32 1e-5, f16 2e-3, bf16 2e-2, relative to max(1, max|reference|): the kernel
+accumulates in fp32 and rounds once, so it sits within one output rounding of the fp32 sum.
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+param = pytest.mark.parametrize
+
+TOL = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 2e-2}
+
+
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda")
+
+
+def assert_close(got, ref, tol, what):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    err = (got - ref).abs().max().item()
+    denom = max(1.0, ref.abs().max().item())
+    assert err / denom <= tol, f"{what}: max-abs err {err:.3e}"
+
+
+def fp32_linear(x, w, b):
+    y = x.float().cpu() @ w.float().cpu().t()
+    return y + b.float().cpu() if b is not None else y
+
+
+@param("dtype", (torch.float32, torch.bfloat16, torch.float16))
+@param("rows", (1, 3, 8, 16))
+@param("k,n", ((1024, 1024), (1024, 4096), (4096, 1024), (64, 200), (512, 257), (2048, 2048)))
+@param("with_bias", (False, True))
+def test_linear_small_matches_fp32(dtype, rows, k, n, with_bias):
+    from poly_attention import _ops
+
+    d = dev()
+    if rows * k * torch.tensor([], dtype=dtype).element_size() > 65536:
+        pytest.skip("x exceeds the staging limit (linear_supported routes it to torch)")
+    g = torch.Generator().manual_seed(rows * 7 + k + n)
+    x = torch.randn(rows, k, generator=g).to(d, dtype)
+    w = (torch.randn(n, k, generator=g) * k ** -0.5).to(d, dtype)
+    b = torch.randn(n, generator=g).to(d, dtype) if with_bias else None
+    assert _ops.linear_supported(x, w, b)
+    y = _ops.linear_small(x, w, b)
+    torch.cuda.synchronize()
+    assert y.shape == (rows, n) and y.dtype == dtype
+    assert_close(y, fp32_linear(x, w, b), TOL[dtype], f"{dtype} rows={rows} k={k} n={n}")
+
+
+def test_linear_small_strided_and_batched_inputs():
+    """x as a [B, 1, K] token batch and as a row-strided view (a column slice of a wider
+    buffer); the output keeps x's leading shape."""
+    from poly_attention import _ops
+
+    d = dev()
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(384, 512, generator=g) * 0.05).to(d, torch.bfloat16)
+    b = torch.randn(384, generator=g).to(d, torch.bfloat16)
+    x3 = torch.randn(6, 1, 512, generator=g).to(d, torch.bfloat16)
+    y3 = _ops.linear_small(x3, w, b)
+    assert y3.shape == (6, 1, 384)
+    assert_close(y3, fp32_linear(x3.reshape(6, 512), w, b).reshape(6, 1, 384), 2e-2, "batched")
+    wide = torch.randn(5, 1024, generator=g).to(d, torch.bfloat16)
+    xs = wide[:, 256:768]
+    assert xs.stride(0) == 1024
+    assert _ops.linear_supported(xs, w, b)
+    assert_close(_ops.linear_small(xs, w, b), fp32_linear(xs, w, b), 2e-2, "row-strided x")
+    torch.cuda.synchronize()
+
+
+def test_linear_small_agrees_with_torch_linear():
+    """Against torch's own GPU F.linear (hipBLASLt), the decode harness's former path: at
+    most one output rounding apart, nearly all elements identical."""
+    from poly_attention import _ops
+
+    d = dev()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(8, 1024, generator=g).to(d, torch.bfloat16)
+    w = (torch.randn(4096, 1024, generator=g) * 0.03).to(d, torch.bfloat16)
+    b = torch.randn(4096, generator=g).to(d, torch.bfloat16)
+    ours = _ops.linear_small(x, w, b).float()
+    ref = torch.nn.functional.linear(x, w, b).float()
+    ulp = ref.abs().clamp_min(1e-30) * 2.0 ** -7
+    assert bool(((ours - ref).abs() <= ulp).all())
+    assert (ours == ref).float().mean().item() >= 0.9
+
+
+def test_linear_supported_routes_other_calls_to_torch():
+    from poly_attention import _ops
+
+    d = dev()
+    w = torch.randn(64, 128, device=d)
+    lin = torch.nn.Linear(128, 64).to(d)
+    assert not _ops.linear_supported(torch.randn(17, 128, device=d), w)  # more than 16 rows
+    assert not _ops.linear_supported(torch.randn(4, 128, device=d).half(), w)  # mixed dtypes
+    xg = torch.randn(4, 128, device=d, requires_grad=True)
+    assert not _ops.linear_supported(xg, w)  # autograd keeps torch's op
+    y = _ops.linear(lin, xg)  # falls back to the layer itself
+    y.sum().backward()
+    assert xg.grad is not None
+    with torch.no_grad():
+        x = torch.randn(4, 128, device=d)
+        assert_close(_ops.linear(lin, x), fp32_linear(x, lin.weight, lin.bias), 1e-5, "layer")
+
+
+def test_decode_steps_with_streamed_projections_equal_parallel():
+    """An order-3 module's single-token steps (projections on pa_linear_small) equal its
+    parallel causal forward (projections on torch) -- the reference tests:103-179 pattern."""
+    from poly_attention import NPolyAttention
+
+    d = dev()
+    torch.manual_seed(21)
+    m = NPolyAttention(dim=256, order=3, heads=4, dim_head=64, causal=True).to(d).eval()
+    x = torch.randn(3, 10, 256, device=d)
+    with torch.no_grad():
+        ref = m(x)
+        out0, cache = m(x[:, :4], return_cache=True)
+        outs = [out0]
+        for i in range(4, 10):
+            o, cache = m(x[:, i:i + 1], cache=cache, return_cache=True)
+            outs.append(o)
+    assert_close(torch.cat(outs, dim=1), ref, 1e-4, "stepwise")
