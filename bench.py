@@ -305,9 +305,14 @@ class _Block(torch.nn.Module):
         attn_out, new_cache = self.attn(self.norm1(x), rotary_pos_emb=rotary_pos_emb,
                                         cache=cache, return_cache=True)
         x = x + attn_out
-        h = self.ffn[1](_linear(self.ffn[0], self.norm2(x)))
-        x = x + _linear(self.ffn[2], h)
-        return x, new_cache
+        if x.is_cuda:
+            # decode-sized inputs: the GELU and the residual add ride in the projections'
+            # launches (pa_linear_small), rounded as the separate ops
+            from poly_attention import _ops
+
+            h = _ops.linear(self.ffn[0], self.norm2(x), gelu=True)
+            return _ops.linear(self.ffn[2], h, residual=x), new_cache
+        return x + self.ffn(self.norm2(x)), new_cache
 
 
 def _linear(layer, x):

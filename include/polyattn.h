@@ -207,22 +207,38 @@ typedef struct pa_rmsnorm {
     size_t      workspace_bytes;
 } pa_rmsnorm;
 
-/* Skinny linear layer for decode steps: y[m, :] = x[m, :] . w^T + bias for rows <= 16
- * (torch.nn.functional.linear semantics, fp32 accumulation, bias added in fp32, one rounding
- * to dtype).  w is nn.Linear's weight, [out_features, in_features] rows.  All tensors share
- * dtype; strides are row strides in elements (unit innermost stride).  in_features must be a
- * multiple of 8 (4 for fp32), x and w 16-byte aligned with row strides of whole 16 bytes, and
- * rows * in_features * element size <= 64 KiB. */
-typedef struct pa_linear {
-    int32_t     rows, in_features, out_features;
-    int32_t     dtype;          /* PA_F32 / PA_F16 / PA_BF16 */
-    const void* x;              /* [rows, in_features] */
-    int64_t     x_stride;
+/* Skinny linear layers for decode steps: up to PA_LINEAR_MAX_OUT projections of one input x
+ * of rows <= 16 (the batch of a single-token step) in one launch.  Output o computes, with
+ * torch.nn.functional.linear semantics (fp32 accumulation, bias in fp32), rounding to dtype
+ * after every step as the separate torch ops would:
+ *   y = round(x . w^T + bias);  y = round(gelu(y)) when activation = PA_ACT_GELU (the erf
+ *   form, torch.nn.GELU());  y = round(y + residual) when residual is set.
+ * w is an nn.Linear weight, [out_features, in_features] rows.  All tensors share dtype;
+ * strides are row strides in elements (unit innermost stride).  in_features must be a
+ * multiple of 8 (4 for fp32), x and every w 16-byte aligned with row strides of whole
+ * 16 bytes, and rows * in_features * element size <= 64 KiB. */
+#define PA_LINEAR_MAX_OUT 4
+#define PA_ACT_NONE 0
+#define PA_ACT_GELU 1
+typedef struct pa_linear_out {
     const void* w;              /* [out_features, in_features] */
     int64_t     w_stride;
+    int32_t     out_features;
+    int32_t     activation;     /* PA_ACT_NONE / PA_ACT_GELU */
     const void* bias;           /* [out_features] or NULL */
+    const void* residual;       /* [rows, out_features] or NULL */
+    int64_t     residual_stride;
     void*       y;              /* [rows, out_features] */
     int64_t     y_stride;
+} pa_linear_out;
+
+typedef struct pa_linear {
+    int32_t       rows, in_features;
+    int32_t       dtype;        /* PA_F32 / PA_F16 / PA_BF16 */
+    int32_t       count;        /* outputs, 1 .. PA_LINEAR_MAX_OUT */
+    const void*   x;            /* [rows, in_features] */
+    int64_t       x_stride;
+    pa_linear_out out[PA_LINEAR_MAX_OUT];
 } pa_linear;
 
 int         pa_abi_version(void);
@@ -230,7 +246,7 @@ const char* pa_strerror(int status);
 int         pa_last_hip_error(void);   /* hipError_t of the last PA_EHIP on this thread */
 /* sizeof of the ABI structs, for binding checks: 0 pa_view, 1 pa_mask, 2 pa_pass,
  * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode, 6 pa_prologue_item, 7 pa_prologue,
- * 8 pa_rmsnorm, 9 pa_linear; 0 for other values */
+ * 8 pa_rmsnorm, 9 pa_linear, 10 pa_linear_out; 0 for other values */
 size_t      pa_struct_size(int which);
 
 /* Kernel timing (no counterpart in the reference: a measurement facility for benchmarks).

@@ -169,6 +169,7 @@ size_t pa_struct_size(int which) {
         case 7: return sizeof(pa_prologue);
         case 8: return sizeof(pa_rmsnorm);
         case 9: return sizeof(pa_linear);
+        case 10: return sizeof(pa_linear_out);
         default: return 0;
     }
 }

@@ -1,8 +1,10 @@
 // pa_linear.hip -- the projections of a single-token decode step: y = x . w^T + bias for a
 // handful of rows (the batch), which is a pass over the weight matrix and nothing else.
 //
-// A library GEMM tiles such a product for large M and leaves most CUs idle at M <= 16; here
-// every wave owns R output features, streams their weight rows with 16-byte non-temporal
+// Up to four projections of the same x (the q / k / v projections of a layer) share one
+// launch, each output optionally followed by GELU and a residual add (the feed-forward of a
+// decode harness), so that a step issues fewer kernels.  A library GEMM tiles such a product
+// for large M and leaves most CUs idle at M <= 16; here every wave owns R output features, streams their weight rows with 16-byte non-temporal
 // loads (the first round of chunks issued before x is staged, so both latencies overlap), and
 // takes the x rows from LDS, staged once per workgroup; 16-bit types multiply in packed dot
 // products (v_dot2_f32_{bf16,f16}, exact products, fp32 sums).  The R x MM per-lane partial sums are reduced over the wave by a
@@ -20,13 +22,21 @@ constexpr int kLinThreads = 256;
 constexpr int kLinMaxRows = 16;
 constexpr int kLinMaxLds = 64 * 1024;  // bytes of staged x rows
 
-struct LinDev {
-    const char* x;
+struct LinOut {
     const char* w;
     const char* bias;
+    const char* res;
     char* y;
-    int64_t xs, ws, ys;  // row strides (elements)
-    int32_t rows, k, n;
+    int64_t ws, rs, ys;  // row strides (elements)
+    int32_t n, act;
+    int32_t blk0;        // first workgroup of this output
+};
+
+struct LinDev {
+    const char* x;
+    int64_t xs;
+    int32_t rows, k, count;
+    LinOut o[PA_LINEAR_MAX_OUT];
 };
 
 template <typename T> struct LinVec { static constexpr int n = 8; };
@@ -110,12 +120,18 @@ __global__ __launch_bounds__(kLinThreads) void k_linear_small(LinDev L) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cpr = L.k / E;
     const int rows = L.rows;
-    const int n0 = (blockIdx.x * (kLinThreads / 64) + wave) * R;
+    // this workgroup's output: the last one whose first workgroup is at or before it
+    int oi = 0;
+#pragma unroll
+    for (int j = 1; j < PA_LINEAR_MAX_OUT; ++j)
+        if (j < L.count && (int)blockIdx.x >= L.o[j].blk0) oi = j;
+    const LinOut O = L.o[oi];
+    const int n0 = (((int)blockIdx.x - O.blk0) * (kLinThreads / 64) + wave) * R;
     const T* wrow[R];
 #pragma unroll
     for (int r = 0; r < R; ++r)
-        wrow[r] = reinterpret_cast<const T*>(L.w) + (int64_t)min(n0 + r, L.n - 1) * L.ws;
-    const bool live = n0 < L.n;
+        wrow[r] = reinterpret_cast<const T*>(O.w) + (int64_t)min(n0 + r, O.n - 1) * O.ws;
+    const bool live = n0 < O.n;
     u32x4 wr[U][R];
     auto load_round = [&](int c0) __attribute__((always_inline)) {
 #pragma unroll
@@ -174,68 +190,83 @@ __global__ __launch_bounds__(kLinThreads) void k_linear_small(LinDev L) {
     // one writer per value: the lowest lane of those holding it
     constexpr int V = R * MM;
     const int dup = 64 / V;  // lanes sharing a value (adjacent in the low bits)
-    if ((lane & (dup - 1)) == 0 && m < rows && n0 + r < L.n) {
+    if ((lane & (dup - 1)) == 0 && m < rows && n0 + r < O.n) {
+        const int f = n0 + r;
         float out = tot;
-        if (L.bias) out += to_f(reinterpret_cast<const T*>(L.bias)[n0 + r]);
-        reinterpret_cast<T*>(L.y)[(int64_t)m * L.ys + n0 + r] = (T)out;
+        if (O.bias) out += to_f(reinterpret_cast<const T*>(O.bias)[f]);
+        out = round_to<T>(out);
+        // torch.nn.GELU(): 0.5 y (1 + erf(y / sqrt(2))) in fp32 on the rounded product
+        if (O.act == PA_ACT_GELU) out = round_to<T>(0.5f * out * (1.f + erff(out * 0.70710678118654752f)));
+        if (O.res) out = round_to<T>(out + to_f(reinterpret_cast<const T*>(O.res)[(int64_t)m * O.rs + f]));
+        reinterpret_cast<T*>(O.y)[(int64_t)m * O.ys + f] = (T)out;
     }
 }
 
 template <typename T, int MM>
-static void launch_lin_r(const LinDev& L, int R, size_t lds, hipStream_t s) {
-    const int waves_per_wg = kLinThreads / 64;
-    auto grid = [&](int r) { return dim3((L.n + waves_per_wg * r - 1) / (waves_per_wg * r)); };
-    if (R == 1) {
-        hipLaunchKernelGGL((k_linear_small<T, MM, 1>), grid(1), dim3(kLinThreads), lds, s, L);
-    } else if (R == 2 || MM > 8) {  // 16 rows: at most two features per wave (registers)
-        hipLaunchKernelGGL((k_linear_small<T, MM, 2>), grid(2), dim3(kLinThreads), lds, s, L);
-    } else if constexpr (MM <= 8) {
-        hipLaunchKernelGGL((k_linear_small<T, MM, 4>), grid(4), dim3(kLinThreads), lds, s, L);
-    }
+static void launch_lin_r(const LinDev& L, int blocks, size_t lds, hipStream_t s) {
+    hipLaunchKernelGGL((k_linear_small<T, MM, 1>), dim3(blocks), dim3(kLinThreads), lds, s, L);
 }
 
 template <typename T>
-static void launch_lin_t(const LinDev& L, int R, size_t lds, hipStream_t s) {
-    if (L.rows <= 1) launch_lin_r<T, 1>(L, R, lds, s);
-    else if (L.rows <= 2) launch_lin_r<T, 2>(L, R, lds, s);
-    else if (L.rows <= 4) launch_lin_r<T, 4>(L, R, lds, s);
-    else if (L.rows <= 8) launch_lin_r<T, 8>(L, R, lds, s);
-    else launch_lin_r<T, 16>(L, R, lds, s);
+static void launch_lin_t(const LinDev& L, int blocks, size_t lds, hipStream_t s) {
+    if (L.rows <= 1) launch_lin_r<T, 1>(L, blocks, lds, s);
+    else if (L.rows <= 2) launch_lin_r<T, 2>(L, blocks, lds, s);
+    else if (L.rows <= 4) launch_lin_r<T, 4>(L, blocks, lds, s);
+    else if (L.rows <= 8) launch_lin_r<T, 8>(L, blocks, lds, s);
+    else launch_lin_r<T, 16>(L, blocks, lds, s);
 }
 
 int launch_linear_small(const pa_linear* l, hipStream_t s) {
-    if (l->rows < 1 || l->in_features < 1 || l->out_features < 1) return PA_EINVAL;
-    if (!l->x || !l->w || !l->y) return PA_EINVAL;
+    if (l->rows < 1 || l->in_features < 1 || l->count < 1 || l->count > PA_LINEAR_MAX_OUT) return PA_EINVAL;
+    if (!l->x) return PA_EINVAL;
     const int T = l->dtype;
     if (T != PA_F32 && T != PA_F16 && T != PA_BF16) return PA_EINVAL;
     if (l->rows > kLinMaxRows) return PA_EUNSUPPORTED;
     const int es = T == PA_F32 ? 4 : 2, E = 16 / es;
     if (l->in_features % E != 0) return PA_EUNSUPPORTED;
-    if ((uintptr_t)l->x % 16 != 0 || (uintptr_t)l->w % 16 != 0) return PA_EUNSUPPORTED;
-    if (l->x_stride % E != 0 || l->w_stride % E != 0) return PA_EUNSUPPORTED;
-    if (l->w_stride < l->in_features) return PA_EINVAL;
-    if (l->rows > 1 && (l->x_stride < l->in_features || l->y_stride < l->out_features)) return PA_EINVAL;
-    if ((uintptr_t)l->y % es != 0 || (l->bias && (uintptr_t)l->bias % es != 0)) return PA_EINVAL;
+    if ((uintptr_t)l->x % 16 != 0 || l->x_stride % E != 0) return PA_EUNSUPPORTED;
+    if (l->rows > 1 && l->x_stride < l->in_features) return PA_EINVAL;
     const size_t lds = (size_t)l->rows * l->in_features * es;
     if (lds > (size_t)kLinMaxLds) return PA_EUNSUPPORTED;
 
     LinDev L;
     L.x = static_cast<const char*>(l->x);
-    L.w = static_cast<const char*>(l->w);
-    L.bias = static_cast<const char*>(l->bias);
-    L.y = static_cast<char*>(l->y);
     L.xs = l->x_stride;
-    L.ws = l->w_stride;
-    L.ys = l->y_stride;
     L.rows = l->rows;
     L.k = l->in_features;
-    L.n = l->out_features;
-    // features per wave (one measured fastest at decode sizes)
-    const int R = 1;
+    L.count = l->count;
+    constexpr int waves = kLinThreads / 64;  // one output feature per wave
+    int blocks = 0;
+    for (int o = 0; o < PA_LINEAR_MAX_OUT; ++o) {
+        LinOut& d = L.o[o];
+        d = LinOut{};
+        if (o >= l->count) continue;
+        const pa_linear_out& u = l->out[o];
+        if (!u.w || !u.y || u.out_features < 1) return PA_EINVAL;
+        if (u.activation != PA_ACT_NONE && u.activation != PA_ACT_GELU) return PA_EINVAL;
+        if ((uintptr_t)u.w % 16 != 0 || u.w_stride % E != 0) return PA_EUNSUPPORTED;
+        if (u.w_stride < l->in_features) return PA_EINVAL;
+        if (l->rows > 1 && (u.y_stride < u.out_features || (u.residual && u.residual_stride < u.out_features)))
+            return PA_EINVAL;
+        if ((uintptr_t)u.y % es != 0 || (u.bias && (uintptr_t)u.bias % es != 0) ||
+            (u.residual && (uintptr_t)u.residual % es != 0))
+            return PA_EINVAL;
+        d.w = static_cast<const char*>(u.w);
+        d.bias = static_cast<const char*>(u.bias);
+        d.res = static_cast<const char*>(u.residual);
+        d.y = static_cast<char*>(u.y);
+        d.ws = u.w_stride;
+        d.rs = u.residual_stride;
+        d.ys = u.y_stride;
+        d.n = u.out_features;
+        d.act = u.activation;
+        d.blk0 = blocks;
+        blocks += (u.out_features + waves - 1) / waves;
+    }
     ProfScope ps("linear_small", s);
-    if (T == PA_F32) launch_lin_t<float>(L, R, lds, s);
-    else if (T == PA_F16) launch_lin_t<f16>(L, R, lds, s);
-    else launch_lin_t<bf16>(L, R, lds, s);
+    if (T == PA_F32) launch_lin_t<float>(L, blocks, lds, s);
+    else if (T == PA_F16) launch_lin_t<f16>(L, blocks, lds, s);
+    else launch_lin_t<bf16>(L, blocks, lds, s);
     return PA_OK;
 }
 

@@ -181,19 +181,33 @@ class PaRmsNorm(ctypes.Structure):
     ]
 
 
+PA_LINEAR_MAX_OUT = 4
+PA_ACT_NONE, PA_ACT_GELU = 0, 1
+
+
+class PaLinearOut(ctypes.Structure):
+    _fields_ = [
+        ("w", c_void_p),
+        ("w_stride", c_int64),
+        ("out_features", c_int32),
+        ("activation", c_int32),
+        ("bias", c_void_p),
+        ("residual", c_void_p),
+        ("residual_stride", c_int64),
+        ("y", c_void_p),
+        ("y_stride", c_int64),
+    ]
+
+
 class PaLinear(ctypes.Structure):
     _fields_ = [
         ("rows", c_int32),
         ("in_features", c_int32),
-        ("out_features", c_int32),
         ("dtype", c_int32),
+        ("count", c_int32),
         ("x", c_void_p),
         ("x_stride", c_int64),
-        ("w", c_void_p),
-        ("w_stride", c_int64),
-        ("bias", c_void_p),
-        ("y", c_void_p),
-        ("y_stride", c_int64),
+        ("out", PaLinearOut * PA_LINEAR_MAX_OUT),
     ]
 
 
@@ -202,7 +216,7 @@ class PaKernelTime(ctypes.Structure):
 
 
 STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode, PaPrologueItem,
-           PaPrologue, PaRmsNorm, PaLinear)
+           PaPrologue, PaRmsNorm, PaLinear, PaLinearOut)
 
 
 class PolyAttnError(RuntimeError):

@@ -439,33 +439,74 @@ def linear_supported(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -
     return True
 
 
-def linear_small(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
-    """torch.nn.functional.linear(x, weight, bias) on pa_linear_small: the weight streamed
-    once by every CU for decode-sized x (the caller checks linear_supported)."""
+def linear_small_group(x: Tensor, specs) -> list[Tensor]:
+    """Up to four projections of one decode-sized x in one launch of pa_linear_small.
+    ``specs``: (weight, bias, gelu, residual) per output -- F.linear(x, weight, bias), then
+    GELU (erf form) when ``gelu``, then ``+ residual`` when given, rounded after each step as
+    the separate torch ops.  The caller checks linear_supported for every (x, weight, bias)."""
     lib = _lib.load()
-    k, n = x.shape[-1], weight.shape[0]
+    assert 1 <= len(specs) <= _lib.PA_LINEAR_MAX_OUT
+    k = x.shape[-1]
     x2 = x.reshape(-1, k)
     e = 4 if x.dtype == torch.float32 else 8
     if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % e):
         x2 = x2.contiguous()
-    y = torch.empty(x2.shape[0], n, dtype=x.dtype, device=x.device)
+    rows = x2.shape[0]
     lin = _lib.PaLinear()
-    lin.rows, lin.in_features, lin.out_features = x2.shape[0], k, n
-    lin.dtype = DTYPE_CODE[x.dtype]
+    lin.rows, lin.in_features, lin.dtype, lin.count = rows, k, DTYPE_CODE[x.dtype], len(specs)
     lin.x, lin.x_stride = x2.data_ptr(), x2.stride(0)
-    lin.w, lin.w_stride = weight.data_ptr(), weight.stride(0)
-    lin.bias = bias.data_ptr() if bias is not None else None
-    lin.y, lin.y_stride = y.data_ptr(), y.stride(0)
+    outs, keep = [], []
+    for o, (w, b, gelu, res) in zip(lin.out, specs):
+        n = w.shape[0]
+        y = torch.empty(rows, n, dtype=x.dtype, device=x.device)
+        o.w, o.w_stride, o.out_features = w.data_ptr(), w.stride(0), n
+        o.activation = _lib.PA_ACT_GELU if gelu else _lib.PA_ACT_NONE
+        o.bias = b.data_ptr() if b is not None else None
+        if res is not None:
+            r2 = res.reshape(rows, n)
+            if r2.stride(-1) != 1:
+                r2 = r2.contiguous()
+            keep.append(r2)
+            o.residual, o.residual_stride = r2.data_ptr(), r2.stride(0)
+        o.y, o.y_stride = y.data_ptr(), y.stride(0)
+        outs.append(y.reshape(*x.shape[:-1], n))
     with _device(x):
         _lib.check(lib.pa_linear_small(ctypes.byref(lin), _stream(x)), "pa_linear_small")
-    return y.reshape(*x.shape[:-1], n)
+    return outs
 
 
-def linear(layer: torch.nn.Linear, x: Tensor) -> Tensor:
-    """layer(x), on pa_linear_small when linear_supported, else the layer itself."""
-    if x.is_cuda and linear_supported(x, layer.weight, layer.bias):
-        return linear_small(x, layer.weight, layer.bias)
-    return layer(x)
+def linear_small(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
+    """torch.nn.functional.linear(x, weight, bias) on pa_linear_small: the weight streamed
+    once by every CU for decode-sized x (the caller checks linear_supported)."""
+    return linear_small_group(x, [(weight, bias, False, None)])[0]
+
+
+def linear(layer: torch.nn.Linear, x: Tensor, *, gelu: bool = False,
+           residual: Optional[Tensor] = None) -> Tensor:
+    """residual + gelu?(layer(x)) (each part optional), on pa_linear_small when
+    linear_supported, else with the layer and torch ops."""
+    if x.is_cuda and linear_supported(x, layer.weight, layer.bias) and (
+            residual is None or (residual.dtype == x.dtype and residual.device == x.device
+                                 and residual.shape == (*x.shape[:-1], layer.weight.shape[0]))):
+        return linear_small_group(x, [(layer.weight, layer.bias, gelu, residual)])[0]
+    y = layer(x)
+    if gelu:
+        y = torch.nn.functional.gelu(y)
+    return y if residual is None else residual + y
+
+
+def linear_many(layers, xs) -> list[Tensor]:
+    """[layer(x) for layer, x in zip(layers, xs)], the projections of one input sharing
+    launches of pa_linear_small (up to four per launch) when every call qualifies."""
+    x = xs[0]
+    if x.is_cuda and all(xi is x for xi in xs) and all(
+            linear_supported(x, layer.weight, layer.bias) for layer in layers):
+        outs = []
+        for i in range(0, len(layers), _lib.PA_LINEAR_MAX_OUT):
+            group = layers[i:i + _lib.PA_LINEAR_MAX_OUT]
+            outs += linear_small_group(x, [(l.weight, l.bias, False, None) for l in group])
+        return outs
+    return [linear(layer, xi) for layer, xi in zip(layers, xs)]
 
 
 # ---------------------------------------------------------------------------------------

@@ -128,6 +128,15 @@ class NPolyAttention(Module):
             return _ops.linear(layer, x)
         return layer(x)
 
+    def _projs(self, layers, xs):
+        """[layer(x) for layer, x in zip(layers, xs)]; on the fused path decode-sized
+        projections of one input share pa_linear_small launches."""
+        if self._use_fused(xs[0]):
+            from . import _ops
+
+            return _ops.linear_many(list(layers), list(xs))
+        return [layer(x) for layer, x in zip(layers, xs)]
+
     def forward(self, x, context: Tensor | tuple[Tensor, ...] | None = None, mask=None,
                 context_mask: Tensor | tuple[Tensor | None, ...] | None = None,
                 rotary_pos_emb=None, cache=None, return_cache=False):
@@ -139,12 +148,6 @@ class NPolyAttention(Module):
 
         orig_x = x
         x = self.norm(x)
-
-        q_and_maybe_gates = self.split_q(self._proj(self.to_q, x))
-        if self.attn_gate:
-            q1, gates = q_and_maybe_gates
-        else:
-            q1 = first(q_and_maybe_gates)
 
         has_context = exists(context)
         context = default(context, orig_x)
@@ -169,8 +172,17 @@ class NPolyAttention(Module):
         else:
             context = context if has_context else ((x,) * self.order)
 
-        kv1 = self.split_kv1(self._proj(first(self.to_kvs), first(context)))
-        kvs_rest = [self.split_kv(self._proj(to_kv, c)) for c, to_kv in zip(context[1:], self.to_kvs[1:])]
+        # the projections (the reference computes to_q first; they are independent, and on the
+        # fused decode path the ones of a shared input go out together)
+        q_proj, kv1_proj, *rest_proj = self._projs([self.to_q, *self.to_kvs], [x, *context])
+        q_and_maybe_gates = self.split_q(q_proj)
+        if self.attn_gate:
+            q1, gates = q_and_maybe_gates
+        else:
+            q1 = first(q_and_maybe_gates)
+
+        kv1 = self.split_kv1(kv1_proj)
+        kvs_rest = [self.split_kv(p) for p in rest_proj]
 
         if self.shared_kv:
             qs_rest = (first(kv1), *[first(kv) for kv in kvs_rest])

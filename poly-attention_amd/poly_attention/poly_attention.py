@@ -276,6 +276,15 @@ class Order2PolyAttention(Module):
             return _ops.linear(layer, x)
         return layer(x)
 
+    def _projs(self, layers, xs):
+        """[layer(x) for layer, x in zip(layers, xs)]; on the fused path decode-sized
+        projections of one input share pa_linear_small launches."""
+        if self._use_fused(xs[0]):
+            from . import _ops
+
+            return _ops.linear_many(list(layers), list(xs))
+        return [layer(x) for layer, x in zip(layers, xs)]
+
     def forward(self, x, context: Tensor | tuple[Tensor, ...] | None = None, mask=None,
                 context_mask: Tensor | tuple[Tensor | None, ...] | None = None,
                 rotary_pos_emb=None, cache=None, return_cache=False):
@@ -287,12 +296,6 @@ class Order2PolyAttention(Module):
 
         orig_x = x
         x = self.norm(x)
-
-        q_and_maybe_gates = self.split_q(self._proj(self.to_q, x))
-        if self.attn_gate:
-            q1, gates = q_and_maybe_gates
-        else:
-            q1 = first(q_and_maybe_gates)
 
         # contexts
 
@@ -320,10 +323,19 @@ class Order2PolyAttention(Module):
         else:
             ctx1, ctx2 = context if has_context else (x, x)
 
+        # the projections (the reference computes to_q first; they are independent, and on the
+        # fused decode path the ones of a shared input go out together)
+        q_proj, kv1_proj, kv2_proj = self._projs([self.to_q, *self.to_kvs], [x, ctx1, ctx2])
+        q_and_maybe_gates = self.split_q(q_proj)
+        if self.attn_gate:
+            q1, gates = q_and_maybe_gates
+        else:
+            q1 = first(q_and_maybe_gates)
+
         # kvs
 
-        kv1 = self.split_kv1(self._proj(first(self.to_kvs), ctx1))
-        kv2 = self.split_kv(self._proj(self.to_kvs[1], ctx2))
+        kv1 = self.split_kv1(kv1_proj)
+        kv2 = self.split_kv(kv2_proj)
 
         if self.shared_kv:
             qs = (q1, first(kv1), first(kv2))

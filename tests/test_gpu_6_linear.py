@@ -91,6 +91,64 @@ def test_linear_small_agrees_with_torch_linear():
     assert (ours == ref).float().mean().item() >= 0.9
 
 
+def test_linear_group_with_epilogues_matches_torch_ops():
+    """Four outputs of one x in one launch -- plain, with bias, with GELU and with a residual
+    -- each equal to the separate torch ops (F.linear, nn.GELU, +), which round after every
+    step, in bf16 and fp32."""
+    from poly_attention import _ops
+
+    d = dev()
+    for dtype, tol in ((torch.bfloat16, 0.0), (torch.float32, 1e-5)):
+        g = torch.Generator().manual_seed(9)
+        x = torch.randn(8, 1024, generator=g).to(d, dtype)
+        ws = [(torch.randn(n, 1024, generator=g) * 0.03).to(d, dtype) for n in (1024, 2048, 4096, 512)]
+        b1 = torch.randn(2048, generator=g).to(d, dtype)
+        b2 = torch.randn(4096, generator=g).to(d, dtype)
+        res = torch.randn(8, 512, generator=g).to(d, dtype)
+        specs = [(ws[0], None, False, None), (ws[1], b1, False, None), (ws[2], b2, True, None),
+                 (ws[3], None, False, res)]
+        with torch.no_grad():
+            outs = _ops.linear_small_group(x, specs)
+            F = torch.nn.functional
+            lins = [F.linear(x, ws[0]), F.linear(x, ws[1], b1), F.linear(x, ws[2], b2),
+                    F.linear(x, ws[3])]
+            refs = [lins[0], lins[1], F.gelu(lins[2]), res + lins[3]]
+        torch.cuda.synchronize()
+        for i, (o, r, li) in enumerate(zip(outs, refs, lins)):
+            assert o.shape == r.shape
+            if dtype == torch.bfloat16:
+                # within one rounding of torch's bf16 chain (its GEMM sums in another order,
+                # so the product may sit one rounding away before the epilogue)
+                mag = torch.maximum(r.float().abs(), li.float().abs()).clamp_min(2.0 ** -20)
+                assert bool(((o.float() - r.float()).abs() <= 2 * mag * 2.0 ** -7).all()), f"output {i}"
+            else:
+                assert_close(o, r, 1e-5, f"output {i} fp32")
+        # against an fp32 restatement, independent of torch's GPU ops
+        ref_gelu = fp32_linear(x, ws[2], b2)
+        if dtype == torch.bfloat16:
+            ref_gelu = ref_gelu.to(dtype).float()
+        ref_gelu = torch.nn.functional.gelu(ref_gelu)
+        assert_close(outs[2], ref_gelu, max(tol, 2e-2 if dtype == torch.bfloat16 else 1e-5), "gelu")
+
+
+def test_linear_many_groups_shared_input():
+    """linear_many: projections of one input go out four per launch and equal the layers."""
+    from poly_attention import _lib, _ops
+
+    d = dev()
+    torch.manual_seed(10)
+    layers = [torch.nn.Linear(256, n, bias=(i % 2 == 0)).to(d) for i, n in enumerate((256, 512, 128, 256, 64))]
+    x = torch.randn(4, 1, 256, device=d)
+    with torch.no_grad(), _lib.KernelProfile() as prof:
+        outs = _ops.linear_many(layers, [x] * len(layers))
+        torch.cuda.synchronize()
+    assert prof.times["linear_small"][0] == 2  # 4 + 1 outputs
+    with torch.no_grad():
+        for layer, o in zip(layers, outs):
+            assert_close(o, fp32_linear(x.reshape(4, 256), layer.weight, layer.bias).reshape(4, 1, -1),
+                         1e-5, "linear_many")
+
+
 def test_linear_supported_routes_other_calls_to_torch():
     from poly_attention import _ops
 

@@ -151,19 +151,25 @@ def test_linear_small_rejects_invalid():
     lib = _lib.load()
     lin = _lib.PaLinear()
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # no rows
-    lin.rows, lin.in_features, lin.out_features, lin.dtype = 8, 1024, 1024, _lib.PA_BF16
-    assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # no pointers
-    lin.x, lin.w, lin.y = 0x1000, 0x2000, 0x3000
-    lin.x_stride, lin.w_stride, lin.y_stride = 1024, 1024, 1024
-    lin.rows = 17  # more rows than a decode batch
+    lin.rows, lin.in_features, lin.dtype, lin.count = 8, 1024, _lib.PA_BF16, 1
+    assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # no x
+    lin.x, lin.x_stride = 0x1000, 1024
+    o = lin.out[0]
+    assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # no w / y
+    o.w, o.w_stride, o.out_features, o.y, o.y_stride = 0x2000, 1024, 1024, 0x3000, 1024
+    lin.count = 5  # more outputs than PA_LINEAR_MAX_OUT
+    assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL
+    lin.count, lin.rows = 1, 17  # more rows than a decode batch
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EUNSUPPORTED
     lin.rows, lin.in_features = 8, 1020  # not whole 16-byte chunks
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EUNSUPPORTED
     lin.in_features, lin.x = 1024, 0x1008  # misaligned x
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EUNSUPPORTED
-    lin.x, lin.in_features, lin.x_stride, lin.w_stride = 0x1000, 8192, 8192, 8192
+    lin.x, lin.in_features, lin.x_stride, o.w_stride = 0x1000, 8192, 8192, 8192
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EUNSUPPORTED  # 128 KiB of x
-    lin.in_features, lin.x_stride, lin.w_stride, lin.y_stride = 1024, 1024, 512, 1024
+    lin.in_features, lin.x_stride, o.w_stride = 1024, 1024, 512
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # w rows overlap
-    lin.dtype = 7
+    o.w_stride, o.activation = 1024, 7
+    assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # unknown activation
+    o.activation, lin.dtype = _lib.PA_ACT_GELU, 7
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL
