@@ -172,16 +172,17 @@ typedef struct pa_prologue_item {
  * in n_poly_attention.py:188-191 / poly_attention.py:271-276 (the angles as built at
  * train_enwik8.py:143,160-161).  The cache write replaces the torch.cat appends of
  * n_poly_attention.py:206-207 and poly_attention.py:282-286 for fixed-capacity caches.
- * The position is read from the device (pos_dev) when given, else `pos`; rows whose
- * position falls outside [0, capacity) are not written to the cache.  All items share
- * src's dtype. */
+ * The position is n_dev[0] - 1 when n_dev is given (the step's position count, the same
+ * device counter pa_decode.n_dev reads), else `pos`; rows whose position falls outside
+ * [0, capacity) are not written to the cache.  All items share src's dtype. */
 typedef struct pa_prologue {
     int32_t        batch, dim, count, capacity;
     float          eps;         /* RMSNorm epsilon */
-    const float*   angles;      /* [rot_dim] fp32 rotary angles of the new position, or NULL */
+    const void*    angles;      /* [rot_dim] rotary angles of the new position, or NULL */
+    int32_t        angles_dtype;/* PA_F32 / PA_F16 / PA_BF16 */
     int32_t        rot_dim;     /* even, <= dim */
-    int32_t        pos;         /* cache position when pos_dev is NULL */
-    const int64_t* pos_dev;     /* device: cache position (positions already held), or NULL */
+    int32_t        pos;         /* cache position when n_dev is NULL */
+    const int32_t* n_dev;       /* device: the step's n (positions after the append), or NULL */
     pa_prologue_item items[2 * PA_MAX_ORDER];
 } pa_prologue;
 

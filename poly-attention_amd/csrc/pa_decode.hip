@@ -712,8 +712,9 @@ struct ProItemDev {
 struct ProDev {
     int32_t batch, dim, count, capacity, rot_dim, pos, rows;
     float eps;
-    const float* angles;
-    const int64_t* pos_dev;
+    const void* angles;
+    int32_t adt;
+    const int32_t* n_dev;
     ProItemDev it[2 * PA_MAX_ORDER];
 };
 
@@ -757,13 +758,13 @@ __global__ __launch_bounds__(kProThreads) void k_dec_prologue(ProDev P) {
             const int d = lane + 64 * e;
             const float partner = __shfl_xor(x[e], 1);  // feature d ^ 1 (same 64-block)
             if (d < P.rot_dim) {
-                const float a = P.angles[d];
+                const float a = load_any(P.angles, P.adt, d);
                 const float rot = (d & 1) ? partner : -partner;
                 x[e] = round_to<T>(x[e] * cosf(a) + rot * sinf(a));
             }
         }
     }
-    const int64_t pos = P.pos_dev ? *P.pos_dev : (int64_t)P.pos;
+    const int64_t pos = P.n_dev ? (int64_t)*P.n_dev - 1 : (int64_t)P.pos;
     const bool to_cache = I.cache.ok() && pos >= 0 && pos < P.capacity;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -781,6 +782,8 @@ int launch_prologue(const pa_prologue* p, hipStream_t s) {
     if (p->dim > 256) return PA_EUNSUPPORTED;
     if (p->angles && (p->rot_dim < 0 || p->rot_dim > p->dim || p->rot_dim % 2 != 0))
         return PA_EINVAL;
+    if (p->angles && p->angles_dtype != PA_F32 && p->angles_dtype != PA_F16 && p->angles_dtype != PA_BF16)
+        return PA_EINVAL;
     const int T = p->items[0].src.dtype;
     if (T != PA_F32 && T != PA_F16 && T != PA_BF16) return PA_EINVAL;
     ProDev P;
@@ -792,7 +795,8 @@ int launch_prologue(const pa_prologue* p, hipStream_t s) {
     P.pos = p->pos;
     P.eps = p->eps;
     P.angles = p->angles;
-    P.pos_dev = p->pos_dev;
+    P.adt = p->angles_dtype;
+    P.n_dev = p->n_dev;
     int rows = 0;
     for (int k = 0; k < p->count; ++k) {
         const pa_prologue_item& it = p->items[k];

@@ -128,17 +128,16 @@ class StaticCache:
         self.lses = [grow(t) for t in lses]
         self.msgs = [grow(t) for t in msgs]
         dev = qs[0].device
-        self.length = torch.full((1,), n, dtype=torch.int64, device=dev)  # positions held
-        self.n_step = torch.full((1,), n + 1, dtype=torch.int32, device=dev)  # n of a step
+        # the next step's n (positions held + 1): its new token goes to position n - 1
+        self.n_step = torch.full((1,), n + 1, dtype=torch.int32, device=dev)
 
     def advance(self) -> None:
         """Count the token a step has just written (stream-ordered, capturable)."""
-        self.length.add_(1)
         self.n_step.add_(1)
 
     def seq_len(self) -> int:
         """Cached positions (reads the device count: synchronises)."""
-        return min(int(self.length.item()), self.capacity)
+        return min(int(self.n_step.item()) - 1, self.capacity)
 
     def as_tuple(self):
         """The cache as the module's tuple of tensors (views of the first seq_len() positions)."""

@@ -154,9 +154,10 @@ class PaPrologue(ctypes.Structure):
         ("capacity", c_int32),
         ("eps", c_float),
         ("angles", c_void_p),
+        ("angles_dtype", c_int32),
         ("rot_dim", c_int32),
         ("pos", c_int32),
-        ("pos_dev", c_void_p),
+        ("n_dev", c_void_p),
         ("items", PaPrologueItem * (2 * PA_MAX_ORDER)),
     ]
 

@@ -683,13 +683,13 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
     return out
 
 
-def decode_prologue(items, *, eps: float, angles: Optional[Tensor], pos_dev: Tensor,
+def decode_prologue(items, *, eps: float, angles: Optional[Tensor], n_dev: Tensor,
                     capacity: int) -> None:
     """The q norms, rotary embedding and cache appends of one decode step, one launch
     (pa_decode_prologue).  ``items``: (src [B, h, 1, d], norm weight or None, rotate,
     out [B, h, 1, d] or None, cache [B, h, capacity, d] or None) per tensor; ``angles`` is
-    the fp32 [rot_dim] rotary angle row of the new position; the cache position is read from
-    ``pos_dev`` (device int64 [1]) on the device."""
+    the [rot_dim] rotary angle row of the new position (fp32, f16 or bf16); the cache
+    position, n - 1, is read from ``n_dev`` (device int32 [1], the step's n) on the device."""
     lib = _lib.load()
     src0 = items[0][0]
     B, _, _, d = src0.shape
@@ -698,11 +698,14 @@ def decode_prologue(items, *, eps: float, angles: Optional[Tensor], pos_dev: Ten
     P.eps = float(eps)
     keep = []
     if angles is not None:
-        a = angles.detach().to(torch.float32).contiguous()
+        a = angles.detach()
+        if a.dtype not in DTYPE_CODE:
+            a = a.to(torch.float32)
+        a = a.contiguous()
         keep.append(a)
-        P.angles, P.rot_dim = a.data_ptr(), a.numel()
-    assert pos_dev.dtype == torch.int64 and pos_dev.is_cuda and pos_dev.numel() == 1
-    P.pos_dev = pos_dev.data_ptr()
+        P.angles, P.angles_dtype, P.rot_dim = a.data_ptr(), DTYPE_CODE[a.dtype], a.numel()
+    assert n_dev.dtype == torch.int32 and n_dev.is_cuda and n_dev.numel() == 1
+    P.n_dev = n_dev.data_ptr()
     for k, (src, w, rotate, out, cache) in enumerate(items):
         it = P.items[k]
         it.src = _view(src)

@@ -110,7 +110,7 @@ def _static_decode_step(module, qs, vs, mask, context_mask, rotary_pos_emb,
         items.append((q, w, angles is not None, q_left[i] if i < order else None,
                       cache.qs[i - 1] if i >= 1 else None))
     items += [(v, None, False, None, buf) for v, buf in zip(vs, cache.vs)]
-    _ops.decode_prologue(items, eps=eps, angles=angles, pos_dev=cache.length,
+    _ops.decode_prologue(items, eps=eps, angles=angles, n_dev=cache.n_step,
                          capacity=cache.capacity)
     out = _ops.poly_decode_step(q_left, cache.qs, cache.vs, cache.msgs, cache.lses,
                                 kv_heads=module.kv_heads, heads=module.heads,

@@ -35,7 +35,8 @@ def assert_close(got, ref, tol, what):
 @param("dtype", (torch.float32, torch.bfloat16))
 @param("rotate", (False, True))
 @param("heads,dim_head", ((4, 64), (2, 128), (3, 32)))
-def test_prologue_matches_torch_ops(dtype, rotate, heads, dim_head):
+@param("adt", (torch.float32, torch.bfloat16))
+def test_prologue_matches_torch_ops(dtype, rotate, heads, dim_head, adt):
     from poly_attention import _ops
     from poly_attention.rotary import RotaryEmbedding, apply_rotary_emb
 
@@ -48,7 +49,9 @@ def test_prologue_matches_torch_ops(dtype, rotate, heads, dim_head):
     norm = torch.nn.RMSNorm(dim_head).to(d, dtype)
     with torch.no_grad():
         norm.weight.copy_(1 + 0.5 * torch.randn(dim_head, device=d))
+    # angles as the kernel receives them (bf16 angle rows are read as given, in fp32 math)
     freqs = RotaryEmbedding(dim_head).to(d)(torch.arange(pos + 1, device=d).float())
+    freqs = freqs.to(adt).float()
     with torch.no_grad():
         ref = norm(src)
         if rotate:
@@ -57,11 +60,11 @@ def test_prologue_matches_torch_ops(dtype, rotate, heads, dim_head):
     cache = torch.full((B, heads, cap, dim_head), 7.0, device=d, dtype=dtype)
     vsrc = torch.randn(B, heads, 1, dim_head, device=d).to(dtype)
     vcache = torch.full((B, heads, cap, dim_head), 7.0, device=d, dtype=dtype)
-    pos_dev = torch.full((1,), pos, dtype=torch.int64, device=d)
+    n_dev = torch.full((1,), pos + 1, dtype=torch.int32, device=d)  # the step's n
     _ops.decode_prologue([(src, norm.weight, rotate, out, cache),
                           (vsrc, None, False, None, vcache)],
                          eps=torch.finfo(torch.float32).eps,
-                         angles=freqs[-1] if rotate else None, pos_dev=pos_dev, capacity=cap)
+                         angles=freqs[-1].to(adt) if rotate else None, n_dev=n_dev, capacity=cap)
     torch.cuda.synchronize()
     if dtype == torch.float32:
         assert_close(out, ref, 1e-5, "prologue fp32")
@@ -77,10 +80,10 @@ def test_prologue_matches_torch_ops(dtype, rotate, heads, dim_head):
     assert bool((cache[:, :, keep] == 7.0).all()), "cache positions other than pos changed"
     assert torch.equal(vcache[:, :, pos:pos + 1], vsrc)
     # a position outside the capacity writes nothing
-    pos_dev.fill_(cap)
+    n_dev.fill_(cap + 1)
     vcache2 = torch.full_like(vcache, 7.0)
     _ops.decode_prologue([(vsrc, None, False, None, vcache2)], eps=1e-6, angles=None,
-                         pos_dev=pos_dev, capacity=cap)
+                         n_dev=n_dev, capacity=cap)
     torch.cuda.synchronize()
     assert bool((vcache2 == 7.0).all())
 

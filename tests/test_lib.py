@@ -124,6 +124,9 @@ def test_prologue_rejects_invalid():
     p.rot_dim, p.dim = 64, 512
     assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EUNSUPPORTED
     p.dim = 64
+    p.angles_dtype = 9
+    assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EINVAL  # angle dtype
+    p.angles_dtype = _lib.PA_BF16
     it.cache.ptr, it.cache.heads, it.cache.dtype = 0x3000, 1, _lib.PA_BF16
     assert lib.pa_decode_prologue(ctypes.byref(p), None) == _lib.PA_EINVAL  # capacity 0
 
