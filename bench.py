@@ -304,24 +304,17 @@ class _Block(torch.nn.Module):
     def forward(self, x, rotary_pos_emb=None, cache=None):
         attn_out, new_cache = self.attn(self.norm1(x), rotary_pos_emb=rotary_pos_emb,
                                         cache=cache, return_cache=True)
-        x = x + attn_out
         if x.is_cuda:
-            # decode-sized inputs: the GELU and the residual add ride in the projections'
-            # launches (pa_linear_small), rounded as the separate ops
+            # decode-sized inputs: the residual add, the norm, the GELU and the second residual
+            # add ride in the projections' launches (pa_linear_small), rounded as the separate
+            # ops; larger ones take the same torch ops
             from poly_attention import _ops
 
-            h = _ops.linear(self.ffn[0], self.norm2(x), gelu=True)
+            h, x = _ops.linear(self.ffn[0], x, x_add=attn_out, norm=self.norm2, gelu=True,
+                               return_sum=True)
             return _ops.linear(self.ffn[2], h, residual=x), new_cache
+        x = x + attn_out
         return x + self.ffn(self.norm2(x)), new_cache
-
-
-def _linear(layer, x):
-    """layer(x); on the GPU, decode-sized inputs stream the weight on pa_linear_small."""
-    if x.is_cuda:
-        from poly_attention import _ops
-
-        return _ops.linear(layer, x)
-    return layer(x)
 
 
 class _PolyLM(torch.nn.Module):
@@ -351,7 +344,13 @@ class _PolyLM(torch.nn.Module):
         for layer, lc in zip(self.layers, layer_caches):
             x, nc = layer(x, rotary_pos_emb=rot, cache=lc)
             new.append(nc)
-        return _linear(self.to_logits, self.norm(x)), (new, None if past is None else past + seq_len)
+        if x.is_cuda:
+            from poly_attention import _ops
+
+            logits = _ops.linear(self.to_logits, x, norm=self.norm)
+        else:
+            logits = self.to_logits(self.norm(x))
+        return logits, (new, None if past is None else past + seq_len)
 
 
 def _greedy(lm, prompt, steps):
@@ -400,7 +399,9 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2):
         logits, (lcs, _) = lm(prompt)
         tok = logits[:, -1].argmax(-1, keepdim=True)
         more = 16  # extra steps, profiled after the timed loop
-        scs = [StaticCache(c, capacity=prefill + steps + more + 1) for c in lcs]
+        # one step counter shared by the layers' caches, advanced once per token
+        counter = StaticCache.make_counter(lcs[0])
+        scs = [StaticCache(c, capacity=prefill + steps + more + 1, counter=counter) for c in lcs]
         del lcs, logits
         tok_buf = tok.clone()
         pos_buf = torch.full((1,), prefill, dtype=torch.int64, device=dev)
@@ -411,6 +412,7 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2):
             lg, _ = lm(tok_buf, (scs, None), pos=pos_buf)
             nxt = lg[:, -1].argmax(-1, keepdim=True)
             tok_buf.copy_(nxt)
+            StaticCache.advance_counter(counter)
             pos_buf.add_(1)
             rec.index_copy_(1, pos_buf - prefill, nxt)
 

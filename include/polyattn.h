@@ -239,6 +239,18 @@ typedef struct pa_linear {
     int32_t       count;        /* outputs, 1 .. PA_LINEAR_MAX_OUT */
     const void*   x;            /* [rows, in_features] */
     int64_t       x_stride;
+    /* optional input steps, applied to x before the products (the residual add and pre-norm
+     * of a transformer block):  x := round(x + x_add);  x_sum receives that x;
+     * x := round(x * rsqrt(mean(x^2) + norm_eps) * norm_weight) when norm is nonzero
+     * (torch.nn.RMSNorm(in_features); norm_weight NULL: no affine weight) */
+    const void*   x_add;        /* [rows, in_features] or NULL */
+    int64_t       x_add_stride;
+    void*         x_sum;        /* [rows, in_features] or NULL */
+    int64_t       x_sum_stride;
+    int32_t       norm;
+    int32_t       norm_dtype;   /* dtype of norm_weight */
+    const void*   norm_weight;  /* [in_features] or NULL */
+    float         norm_eps;
     pa_linear_out out[PA_LINEAR_MAX_OUT];
 } pa_linear;
 

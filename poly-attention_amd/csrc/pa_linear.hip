@@ -2,8 +2,9 @@
 // handful of rows (the batch), which is a pass over the weight matrix and nothing else.
 //
 // Up to four projections of the same x (the q / k / v projections of a layer) share one
-// launch, each output optionally followed by GELU and a residual add (the feed-forward of a
-// decode harness), so that a step issues fewer kernels.  A library GEMM tiles such a product
+// launch, each output optionally followed by GELU and a residual add, and x itself optionally
+// preceded by a residual add and an RMSNorm (the feed-forward of a decode harness), so that a
+// step issues fewer kernels.  A library GEMM tiles such a product
 // for large M and leaves most CUs idle at M <= 16; here every wave owns R output features, streams their weight rows with 16-byte non-temporal
 // loads (the first round of chunks issued before x is staged, so both latencies overlap), and
 // takes the x rows from LDS, staged once per workgroup; 16-bit types multiply in packed dot
@@ -34,8 +35,12 @@ struct LinOut {
 
 struct LinDev {
     const char* x;
-    int64_t xs;
-    int32_t rows, k, count;
+    const char* xadd;
+    char* xsum;
+    const void* nw;
+    int64_t xs, xas, xss;
+    int32_t rows, k, count, norm, nwdt;
+    float eps;
     LinOut o[PA_LINEAR_MAX_OUT];
 };
 
@@ -107,14 +112,12 @@ __device__ __forceinline__ float chunk_dot(uint32_t w0, uint32_t w1, uint32_t w2
     }
 }
 
-// Chunks of 16 bytes per lane and feature in flight per round: 32 registers of weights.
-template <int R>
-constexpr int kLinU = 8 / R;
-
-template <typename T, int MM, int R>
+// U: chunks of 16 bytes per lane and feature in flight per round (the weight row of a
+// feature is in flight whole up to 64 * U chunks), chosen per launch from in_features so that
+// short rows do not hold registers that lower the occupancy.
+template <typename T, int MM, int R, int U>
 __global__ __launch_bounds__(kLinThreads) void k_linear_small(LinDev L) {
     constexpr int E = LinVec<T>::n;
-    constexpr int U = kLinU<R>;
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     extern __shared__ u32x4 s_x[];  // rows x (k / E) chunks
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -144,24 +147,90 @@ __global__ __launch_bounds__(kLinThreads) void k_linear_small(LinDev L) {
                                : u32x4{0u, 0u, 0u, 0u};
         }
     };
-    // the first round of weights is in flight while x is staged (eight loads per thread in
-    // flight per round of the staging loop)
+    // the first round of weights is in flight while x is staged (SU loads per thread in
+    // flight per round of the staging loop); the RMSNorm weights, when they share x's dtype,
+    // are staged behind x as one more row of chunks
+    constexpr int SU = U >= 8 ? 8 : 4;
     load_round(lane);
     const int total = rows * cpr;
-    for (int i0 = tid; i0 < total; i0 += 8 * kLinThreads) {
-        u32x4 t[8];
+    u32x4* s_w = s_x + total;
+    const bool wvec = L.norm && L.nw && L.nwdt == (std::is_same<T, float>::value ? PA_F32
+                                                  : std::is_same<T, bf16>::value ? PA_BF16 : PA_F16);
+    const int staged = total + (wvec ? cpr : 0);
+    for (int i0 = tid; i0 < staged; i0 += SU * kLinThreads) {
+        u32x4 t[SU], ta[SU];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < SU; ++j) {
             const int i = i0 + j * kLinThreads;
             const int r = i / cpr, c = i - r * cpr;
-            if (i < total)
+            if (i < total) {
                 t[j] = *reinterpret_cast<const u32x4*>(L.x + ((int64_t)r * L.xs + (int64_t)c * E) * sizeof(T));
+                if (L.xadd)
+                    ta[j] = *reinterpret_cast<const u32x4*>(L.xadd + ((int64_t)r * L.xas + (int64_t)c * E) * sizeof(T));
+            } else if (i < staged) {
+                t[j] = *reinterpret_cast<const u32x4*>(static_cast<const char*>(L.nw) + (int64_t)(i - total) * 16);
+            }
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (i0 + j * kLinThreads < total) s_x[i0 + j * kLinThreads] = t[j];
+        for (int j = 0; j < SU; ++j) {
+            const int i = i0 + j * kLinThreads;
+            if (i >= staged) continue;
+            if (i >= total) {
+                s_x[i] = t[j];  // a norm weight chunk
+                continue;
+            }
+            if (L.xadd) {
+                // the residual add, rounded as torch's element-wise add
+                T* a = reinterpret_cast<T*>(&t[j]);
+                const T* bb = reinterpret_cast<const T*>(&ta[j]);
+#pragma unroll
+                for (int e = 0; e < E; ++e) a[e] = (T)(to_f(a[e]) + to_f(bb[e]));
+                if (L.xsum && blockIdx.x == 0) {
+                    const int r = i / cpr, c = i - r * cpr;
+                    *reinterpret_cast<u32x4*>(L.xsum + ((int64_t)r * L.xss + (int64_t)c * E) * sizeof(T)) = t[j];
+                }
+            }
+            s_x[i] = t[j];
+        }
     }
     __syncthreads();
+    if (L.norm) {
+        // torch.nn.RMSNorm over each staged row: rstd in fp32, y = round((x * rstd) * w)
+        __shared__ float s_rstd[kLinMaxRows];
+        for (int r = wave; r < rows; r += kLinThreads / 64) {
+            float ss = 0.f;
+            for (int c = lane; c < cpr; c += 64) {
+                const u32x4 v = s_x[r * cpr + c];
+                const T* e = reinterpret_cast<const T*>(&v);
+#pragma unroll
+                for (int j = 0; j < E; ++j) ss += to_f(e[j]) * to_f(e[j]);
+            }
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+            if (lane == 0) s_rstd[r] = rsqrtf(ss / (float)L.k + L.eps);
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int i = tid; i < total; i += kLinThreads) {
+            const int r = i / cpr, c = i - r * cpr;
+            u32x4 v = s_x[i];
+            T* e = reinterpret_cast<T*>(&v);
+            const float rs = s_rstd[r];
+            if (wvec) {
+                const u32x4 wr = s_w[c];
+                const T* we = reinterpret_cast<const T*>(&wr);
+#pragma unroll
+                for (int j = 0; j < E; ++j) e[j] = (T)((to_f(e[j]) * rs) * to_f(we[j]));
+            } else {
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const float w = L.nw ? load_any(L.nw, L.nwdt, c * E + j) : 1.f;
+                    e[j] = (T)((to_f(e[j]) * rs) * w);
+                }
+            }
+            s_x[i] = v;
+        }
+        __syncthreads();
+    }
     if (!live) return;
 
     float acc[R * MM];
@@ -204,7 +273,12 @@ __global__ __launch_bounds__(kLinThreads) void k_linear_small(LinDev L) {
 
 template <typename T, int MM>
 static void launch_lin_r(const LinDev& L, int blocks, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((k_linear_small<T, MM, 1>), dim3(blocks), dim3(kLinThreads), lds, s, L);
+    constexpr int E = LinVec<T>::n;
+    const int rounds = (L.k / E + 63) / 64;  // chunks per lane of one weight row
+    if (rounds <= 1) hipLaunchKernelGGL((k_linear_small<T, MM, 1, 1>), dim3(blocks), dim3(kLinThreads), lds, s, L);
+    else if (rounds <= 2) hipLaunchKernelGGL((k_linear_small<T, MM, 1, 2>), dim3(blocks), dim3(kLinThreads), lds, s, L);
+    else if (rounds <= 4) hipLaunchKernelGGL((k_linear_small<T, MM, 1, 4>), dim3(blocks), dim3(kLinThreads), lds, s, L);
+    else hipLaunchKernelGGL((k_linear_small<T, MM, 1, 8>), dim3(blocks), dim3(kLinThreads), lds, s, L);
 }
 
 template <typename T>
@@ -226,12 +300,31 @@ int launch_linear_small(const pa_linear* l, hipStream_t s) {
     if (l->in_features % E != 0) return PA_EUNSUPPORTED;
     if ((uintptr_t)l->x % 16 != 0 || l->x_stride % E != 0) return PA_EUNSUPPORTED;
     if (l->rows > 1 && l->x_stride < l->in_features) return PA_EINVAL;
-    const size_t lds = (size_t)l->rows * l->in_features * es;
+    size_t lds = (size_t)l->rows * l->in_features * es;
     if (lds > (size_t)kLinMaxLds) return PA_EUNSUPPORTED;
+    if (l->norm && l->norm_weight && l->norm_dtype == T) lds += (size_t)l->in_features * es;  // staged weight
+
+    if ((l->x_add && ((uintptr_t)l->x_add % 16 != 0 || l->x_add_stride % E != 0)) ||
+        (l->x_sum && ((uintptr_t)l->x_sum % 16 != 0 || l->x_sum_stride % E != 0)))
+        return PA_EUNSUPPORTED;
+    if (l->x_sum && !l->x_add) return PA_EINVAL;
+    if (l->norm && l->norm_weight && l->norm_dtype != PA_F32 && l->norm_dtype != PA_F16 &&
+        l->norm_dtype != PA_BF16)
+        return PA_EINVAL;
+    if (l->norm && l->norm_weight && l->norm_dtype == T && (uintptr_t)l->norm_weight % 16 != 0)
+        return PA_EUNSUPPORTED;
 
     LinDev L;
     L.x = static_cast<const char*>(l->x);
     L.xs = l->x_stride;
+    L.xadd = static_cast<const char*>(l->x_add);
+    L.xas = l->x_add_stride;
+    L.xsum = static_cast<char*>(l->x_sum);
+    L.xss = l->x_sum_stride;
+    L.norm = l->norm ? 1 : 0;
+    L.nw = l->norm ? l->norm_weight : nullptr;
+    L.nwdt = l->norm_dtype;
+    L.eps = l->norm_eps;
     L.rows = l->rows;
     L.k = l->in_features;
     L.count = l->count;

@@ -102,9 +102,14 @@ class StaticCache:
 
     A step at full capacity writes nothing to the cache and attends over the first
     ``capacity`` positions only (the kernels clamp the count); size it for prompt + steps.
+
+    ``counter``: an int32 device tensor [1] shared by the caches of one model's layers (all
+    holding the same positions), which the caller advances once per decode step, after
+    every layer ran (``StaticCache.advance_counter``): one device add per token instead of
+    one per layer.  Without it each cache owns its count and advances it itself.
     """
 
-    def __init__(self, cache, capacity: int):
+    def __init__(self, cache, capacity: int, counter: Tensor | None = None):
         self.order2 = isinstance(cache[0], Tensor)
         if self.order2:
             q2, q3, v3, lse, msg = cache
@@ -129,11 +134,31 @@ class StaticCache:
         self.msgs = [grow(t) for t in msgs]
         dev = qs[0].device
         # the next step's n (positions held + 1): its new token goes to position n - 1
-        self.n_step = torch.full((1,), n + 1, dtype=torch.int32, device=dev)
+        self.shared = counter is not None
+        if self.shared:
+            if counter.dtype != torch.int32 or counter.numel() != 1 or counter.device != dev:
+                raise ValueError("counter: an int32 tensor of one element on the cache's device")
+            self.n_step = counter
+        else:
+            self.n_step = torch.full((1,), n + 1, dtype=torch.int32, device=dev)
+
+    @staticmethod
+    def make_counter(cache, device=None) -> Tensor:
+        """A shared step counter for caches holding the positions of ``cache`` (a module's
+        cache tuple): the next step's n."""
+        q = cache[0] if isinstance(cache[0], Tensor) else cache[0][0]
+        return torch.full((1,), q.shape[2] + 1, dtype=torch.int32, device=device or q.device)
+
+    @staticmethod
+    def advance_counter(counter: Tensor) -> None:
+        """Count the token every layer of a step has just written (shared counter)."""
+        counter.add_(1)
 
     def advance(self) -> None:
-        """Count the token a step has just written (stream-ordered, capturable)."""
-        self.n_step.add_(1)
+        """Count the token a step has just written (stream-ordered, capturable); with a
+        shared counter the caller advances it once per step instead."""
+        if not self.shared:
+            self.n_step.add_(1)
 
     def seq_len(self) -> int:
         """Cached positions (reads the device count: synchronises)."""

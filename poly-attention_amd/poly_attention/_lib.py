@@ -208,6 +208,14 @@ class PaLinear(ctypes.Structure):
         ("count", c_int32),
         ("x", c_void_p),
         ("x_stride", c_int64),
+        ("x_add", c_void_p),
+        ("x_add_stride", c_int64),
+        ("x_sum", c_void_p),
+        ("x_sum_stride", c_int64),
+        ("norm", c_int32),
+        ("norm_dtype", c_int32),
+        ("norm_weight", c_void_p),
+        ("norm_eps", c_float),
         ("out", PaLinearOut * PA_LINEAR_MAX_OUT),
     ]
 

@@ -439,23 +439,47 @@ def linear_supported(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -
     return True
 
 
-def linear_small_group(x: Tensor, specs) -> list[Tensor]:
+def _rows2d(t: Tensor, k: int, e: int) -> Tensor:
+    t2 = t.reshape(-1, k)
+    if t2.stride(-1) != 1 or t2.data_ptr() % 16 or (t2.shape[0] > 1 and t2.stride(0) % e):
+        t2 = t2.contiguous()
+    return t2
+
+
+def linear_small_group(x: Tensor, specs, *, x_add: Optional[Tensor] = None,
+                       norm: Optional[torch.nn.Module] = None, return_sum: bool = False):
     """Up to four projections of one decode-sized x in one launch of pa_linear_small.
     ``specs``: (weight, bias, gelu, residual) per output -- F.linear(x, weight, bias), then
     GELU (erf form) when ``gelu``, then ``+ residual`` when given, rounded after each step as
-    the separate torch ops.  The caller checks linear_supported for every (x, weight, bias)."""
+    the separate torch ops.  Before the products x may take ``+ x_add`` and an RMSNorm
+    (``norm``: a torch.nn.RMSNorm over the features); ``return_sum`` also returns x + x_add.
+    The caller checks linear_supported for every (x, weight, bias)."""
     lib = _lib.load()
     assert 1 <= len(specs) <= _lib.PA_LINEAR_MAX_OUT
     k = x.shape[-1]
-    x2 = x.reshape(-1, k)
     e = 4 if x.dtype == torch.float32 else 8
-    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % e):
-        x2 = x2.contiguous()
+    x2 = _rows2d(x, k, e)
     rows = x2.shape[0]
     lin = _lib.PaLinear()
     lin.rows, lin.in_features, lin.dtype, lin.count = rows, k, DTYPE_CODE[x.dtype], len(specs)
     lin.x, lin.x_stride = x2.data_ptr(), x2.stride(0)
-    outs, keep = [], []
+    keep, xs = [x2], None
+    if x_add is not None:
+        a2 = _rows2d(x_add.to(x.dtype), k, e)
+        keep.append(a2)
+        lin.x_add, lin.x_add_stride = a2.data_ptr(), a2.stride(0)
+        if return_sum:
+            xs = torch.empty(rows, k, dtype=x.dtype, device=x.device)
+            lin.x_sum, lin.x_sum_stride = xs.data_ptr(), xs.stride(0)
+    if norm is not None:
+        lin.norm = 1
+        eps = norm.eps if norm.eps is not None else torch.finfo(torch.float32).eps
+        lin.norm_eps = float(eps)
+        if norm.weight is not None:
+            w = norm.weight.detach().contiguous()
+            keep.append(w)
+            lin.norm_weight, lin.norm_dtype = w.data_ptr(), DTYPE_CODE[w.dtype]
+    outs = []
     for o, (w, b, gelu, res) in zip(lin.out, specs):
         n = w.shape[0]
         y = torch.empty(rows, n, dtype=x.dtype, device=x.device)
@@ -472,6 +496,8 @@ def linear_small_group(x: Tensor, specs) -> list[Tensor]:
         outs.append(y.reshape(*x.shape[:-1], n))
     with _device(x):
         _lib.check(lib.pa_linear_small(ctypes.byref(lin), _stream(x)), "pa_linear_small")
+    if return_sum:
+        return outs, xs.reshape(x.shape)
     return outs
 
 
@@ -481,18 +507,37 @@ def linear_small(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Te
     return linear_small_group(x, [(weight, bias, False, None)])[0]
 
 
+def _norm_fusable(norm: Optional[torch.nn.Module], x: Tensor) -> bool:
+    if norm is None:
+        return True
+    return (isinstance(norm, torch.nn.RMSNorm) and tuple(norm.normalized_shape) == (x.shape[-1],)
+            and (norm.weight is None or (norm.weight.dtype in DTYPE_CODE and norm.weight.is_cuda)))
+
+
 def linear(layer: torch.nn.Linear, x: Tensor, *, gelu: bool = False,
-           residual: Optional[Tensor] = None) -> Tensor:
-    """residual + gelu?(layer(x)) (each part optional), on pa_linear_small when
-    linear_supported, else with the layer and torch ops."""
-    if x.is_cuda and linear_supported(x, layer.weight, layer.bias) and (
+           residual: Optional[Tensor] = None, x_add: Optional[Tensor] = None,
+           norm: Optional[torch.nn.Module] = None, return_sum: bool = False):
+    """residual + gelu?(layer(norm?(x + x_add?))) with each part optional -- on one launch of
+    pa_linear_small when linear_supported, else with the layer and torch ops.  With
+    ``return_sum`` returns (y, x + x_add)."""
+    n = layer.weight.shape[0]
+    if x.is_cuda and linear_supported(x, layer.weight, layer.bias) and _norm_fusable(norm, x) and (
             residual is None or (residual.dtype == x.dtype and residual.device == x.device
-                                 and residual.shape == (*x.shape[:-1], layer.weight.shape[0]))):
-        return linear_small_group(x, [(layer.weight, layer.bias, gelu, residual)])[0]
-    y = layer(x)
+                                 and residual.shape == (*x.shape[:-1], n))) and (
+            x_add is None or (x_add.shape == x.shape and x_add.dtype == x.dtype
+                              and x_add.device == x.device)):
+        r = linear_small_group(x, [(layer.weight, layer.bias, gelu, residual)], x_add=x_add,
+                               norm=norm, return_sum=return_sum and x_add is not None)
+        if return_sum:
+            return (r[0][0], r[1]) if x_add is not None else (r[0], x)
+        return r[0]
+    xs = x if x_add is None else x + x_add
+    y = layer(norm(xs) if norm is not None else xs)
     if gelu:
         y = torch.nn.functional.gelu(y)
-    return y if residual is None else residual + y
+    if residual is not None:
+        y = residual + y
+    return (y, xs) if return_sum else y
 
 
 def linear_many(layers, xs) -> list[Tensor]:

@@ -165,6 +165,36 @@ def test_static_cache_matches_tuple_cache_steps():
         assert_close(a, b, 2e-2, "cache contents")
 
 
+def test_static_caches_with_shared_counter_two_layers():
+    """Two stacked order-3 layers whose StaticCaches share one step counter, advanced once
+    per token after both layers: the steps equal the stack's parallel causal forward."""
+    from poly_attention import StaticCache
+
+    d = dev()
+    torch.manual_seed(15)
+    m1, _, _ = _module(3, 2, d, torch.float32)
+    m2, _, _ = _module(3, 2, d, torch.float32)
+    x = torch.randn(2, 9, 64, device=d)
+    fd = O.rotary_freqs(64, torch.arange(9)).to(d)
+    with torch.no_grad():
+        ref = m2(m1(x, rotary_pos_emb=fd), rotary_pos_emb=fd)
+        h, c1 = m1(x[:, :4], rotary_pos_emb=fd[:4], return_cache=True)
+        out0, c2 = m2(h, rotary_pos_emb=fd[:4], return_cache=True)
+        counter = StaticCache.make_counter(c1)
+        s1 = StaticCache(c1, capacity=12, counter=counter)
+        s2 = StaticCache(c2, capacity=12, counter=counter)
+        outs = [out0]
+        for i in range(4, 9):
+            h, _ = m1(x[:, i:i + 1], rotary_pos_emb=fd[:i + 1], cache=s1, return_cache=True)
+            o, _ = m2(h, rotary_pos_emb=fd[:i + 1], cache=s2, return_cache=True)
+            StaticCache.advance_counter(counter)
+            outs.append(o)
+    assert_close(torch.cat(outs, dim=1), ref, 1e-4, "two layers, shared counter")
+    assert s1.seq_len() == s2.seq_len() == 9
+    with pytest.raises(ValueError):
+        StaticCache(c1, capacity=12, counter=torch.zeros(1, dtype=torch.int64, device=d))
+
+
 def test_static_cache_errors():
     from poly_attention import StaticCache
 

@@ -131,6 +131,45 @@ def test_linear_group_with_epilogues_matches_torch_ops():
         assert_close(outs[2], ref_gelu, max(tol, 2e-2 if dtype == torch.bfloat16 else 1e-5), "gelu")
 
 
+@param("dtype", (torch.bfloat16, torch.float32))
+def test_linear_pre_add_and_norm_match_torch_ops(dtype):
+    """x + x_add (also returned), RMSNorm, the product, GELU -- one launch -- against the
+    separate torch ops of a pre-norm feed-forward block; the returned sum is bit-identical."""
+    from poly_attention import _ops
+
+    d = dev()
+    torch.manual_seed(11)
+    layer = torch.nn.Linear(1024, 2048).to(d, dtype)
+    norm = torch.nn.RMSNorm(1024).to(d, dtype)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.3 * torch.randn(1024, device=d))
+        x = torch.randn(8, 1, 1024, device=d).to(dtype)
+        a = torch.randn(8, 1, 1024, device=d).to(dtype)
+        y, xs = _ops.linear(layer, x, x_add=a, norm=norm, gelu=True, return_sum=True)
+        ref_xs = x + a
+        lin = layer(norm(ref_xs))
+        ref = torch.nn.functional.gelu(lin)
+        torch.cuda.synchronize()
+    assert torch.equal(xs, ref_xs)
+    assert y.shape == ref.shape
+    if dtype == torch.bfloat16:
+        # the norm output and the product may each sit one rounding from torch's
+        mag = torch.maximum(ref.float().abs(), lin.float().abs()).clamp_min(2.0 ** -20)
+        assert bool(((y.float() - ref.float()).abs() <= 4 * mag * 2.0 ** -7).all())
+    else:
+        assert_close(y, ref, 1e-5, "fp32")
+    # the norm alone, without weight and without the add (the logits projection)
+    plain = torch.nn.RMSNorm(1024, elementwise_affine=False).to(d)
+    with torch.no_grad():
+        y2 = _ops.linear(layer, x, norm=plain)
+        ref2 = layer(plain(x))
+    if dtype == torch.bfloat16:
+        mag = ref2.float().abs().clamp_min(2.0 ** -20)
+        assert bool(((y2.float() - ref2.float()).abs() <= 4 * mag * 2.0 ** -7 + 1e-3).all())
+    else:
+        assert_close(y2, ref2, 1e-5, "fp32 plain norm")
+
+
 def test_linear_many_groups_shared_input():
     """linear_many: projections of one input go out four per launch and equal the layers."""
     from poly_attention import _lib, _ops

@@ -174,5 +174,9 @@ def test_linear_small_rejects_invalid():
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # w rows overlap
     o.w_stride, o.activation = 1024, 7
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # unknown activation
-    o.activation, lin.dtype = _lib.PA_ACT_GELU, 7
+    o.activation, lin.x_sum, lin.x_sum_stride = _lib.PA_ACT_GELU, 0x5000, 1024
+    assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # x_sum without x_add
+    lin.x_sum, lin.norm, lin.norm_weight, lin.norm_dtype = None, 1, 0x6000, 5
+    assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL  # norm weight dtype
+    lin.norm, lin.dtype = 0, 7
     assert lib.pa_linear_small(ctypes.byref(lin), None) == _lib.PA_EINVAL
