@@ -235,11 +235,30 @@ def make_vit(dev, dtype, batch):
 
 
 def vit_bench(dev, steps, warmup, cpu):
+    """Config 3 forward, eagerly (one Python call per step; at batch 64 the host issues the
+    launches no faster than the GPU runs them) and replayed from a HIP graph captured once
+    (fixed shapes: the inference deployment), checked equal to the eager output."""
     batch = 64
     m, img = make_vit(dev, torch.bfloat16, batch)
     with torch.no_grad():
         proj_flops = _linear_flops(m, lambda: m(img))
-        ms = time_steps(lambda: m(img), steps, warmup)
+        eager_ms = time_steps(lambda: m(img), steps, warmup)
+        ref = m(img)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                m(img)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = m(img)
+        graph.replay()
+        torch.cuda.synchronize()
+        graph_diff = (out.float() - ref.float()).abs().max().item()
+        assert graph_diff <= 2e-2 * max(1.0, ref.float().abs().max().item()), \
+            f"graph replay differs from the eager forward by {graph_diff}"
+        ms = time_steps(graph.replay, steps, warmup)
         with _lib().KernelProfile() as prof:
             for _ in range(steps):
                 m(img)
@@ -251,6 +270,10 @@ def vit_bench(dev, steps, warmup, cpu):
                     "order 2, 1000 classes), batch 64 bf16, inference (BASELINE configs[2])",
         "ms_per_step": round(ms, 4),
         "images_per_s": round(batch / (ms / 1e3), 1),
+        "mode": "forward captured once into a HIP graph, replayed per step",
+        "eager_ms_per_step": round(eager_ms, 4),
+        "eager_images_per_s": round(batch / (eager_ms / 1e3), 1),
+        "graph_vs_eager_max_abs_diff": graph_diff,
         "flops_per_step": proj_flops + core_flops,
         "TFLOP_per_s": round((proj_flops + core_flops) / (ms / 1e3) / 1e12, 2),
         "core_flops_per_step": core_flops,
@@ -259,7 +282,7 @@ def vit_bench(dev, steps, warmup, cpu):
         "kernels": {k: {"launches": n // steps, "avg_ms": round(t / n, 4)}
                     for k, (n, t) in prof.times.items()},
     }
-    del m, img
+    del m, img, graph, out, ref
     torch.cuda.empty_cache()
     if cpu:
         threads = max(1, min(16, os.cpu_count() or 1))
@@ -366,10 +389,11 @@ def _greedy(lm, prompt, steps):
     return torch.cat(out, dim=1)
 
 
-def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2):
+def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2, eager=True):
     """Config 4 two ways: (1) the reference's calling pattern, one eager module call per
-    token with the growing cache tuples; (2) the same steps on StaticCaches, one decode step
-    (all layers, logits, argmax) captured into a HIP graph and replayed per token."""
+    token with the growing cache tuples (skipped with ``eager=False``, for profiling runs);
+    (2) the same steps on StaticCaches, one decode step (all layers, logits, argmax)
+    captured into a HIP graph and replayed per token."""
     from poly_attention import StaticCache
 
     depth, heads, dh, dim = 8, 16, 64, 1024
@@ -387,7 +411,7 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2):
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         toks_eager = [tok]
-        for _ in range(steps):
+        for _ in range(steps if eager else 0):
             logits, cache = lm(tok, cache)
             tok = logits[:, -1].argmax(-1, keepdim=True)
             toks_eager.append(tok)
@@ -435,8 +459,10 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2):
         # greedy tokens of random-init weights sit on near-ties: a last-bit difference
         # (summation order of the split-K chunks, fused vs separate roundings) can flip one
         # argmax, after which the sequences diverge; report where the first flip happens
-        diff = (rec[:, :steps + 1] != toks_eager).any(dim=0).nonzero()
-        first_flip = int(diff[0].item()) if diff.numel() else steps + 1
+        first_flip = None
+        if eager:
+            diff = (rec[:, :steps + 1] != toks_eager).any(dim=0).nonzero()
+            first_flip = int(diff[0].item()) if diff.numel() else steps + 1
         # kernel times of a few more steps (events per launch; outside the timed loops)
         with _lib().KernelProfile() as prof:
             for _ in range(more):
@@ -457,7 +483,8 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2):
     graph_bytes = sum(step_bytes(s) for s in range(warm, steps))
     kern = {k: {"launches": n // more, "avg_ms": round(t / n, 4)}
             for k, (n, t) in prof.times.items()}
-    attn_ms = sum(t for _, t in prof.times.values()) / more
+    lib_ms = sum(t for _, t in prof.times.values()) / more
+    attn_ms = sum(t for k, (_, t) in prof.times.items() if k.startswith("dec_")) / more
     n_mid = prefill + steps + more / 2
     res = {
         "workload": f"order-3 causal decode, PolyLM-style stack depth {depth}, dim {dim}, heads "
@@ -470,14 +497,15 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2):
         "frac_hbm_peak": round(graph_bytes / graph_s / 1e9 / PEAK_HBM_GBS, 4),
         "mode": f"StaticCache + one HIP graph per token ({warm} eager warm-up steps, "
                 f"{graph_steps} replays timed)",
-        "eager_tuple_cache": {
+        "eager_tuple_cache": None if not eager else {
             "ms_per_step": round(eager_s * 1e3 / steps, 4),
             "tokens_per_s": round(batch * steps / eager_s, 1),
             "GB_per_s": round(eager_bytes / eager_s / 1e9, 1)},
         "greedy_tokens_identical_to_eager_until": first_flip,
         "cache_GB_per_step_mean": round((eager_bytes - steps * weight_bytes) / steps / 1e9, 4),
         "weight_GB_per_step": round(weight_bytes / 1e9, 4),
-        "poly_kernels_ms_per_step": round(attn_ms, 4),
+        "library_kernels_ms_per_step": round(lib_ms, 4),
+        "decode_attention_ms_per_step": round(attn_ms, 4),
         "decode_kernels_GB_per_s": round(
             batch * depth * per_tok * n_mid
             / (sum(prof.times.get(k, (0, 0.0))[1] for k in ("dec_partial", "dec_combine"))
@@ -579,6 +607,9 @@ def main():
     ap.add_argument("--no-module", action="store_true")
     ap.add_argument("--no-vit", action="store_true", help="skip config 3 (PolyViT forward)")
     ap.add_argument("--no-lm", action="store_true", help="skip config 4 (order-3 decode loop)")
+    ap.add_argument("--lm-steps", type=int, default=512, help="config 4: greedy decode steps")
+    ap.add_argument("--lm-no-eager", action="store_true",
+                    help="config 4: skip the eager tuple-cache loop (profiling runs)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one plain 256 MiB device copy (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -661,7 +692,8 @@ def main():
 
     lm = None
     if not args.no_lm:
-        lm = decode_order3_bench(dev, cpu=not args.no_cpu)
+        lm = decode_order3_bench(dev, cpu=not args.no_cpu, steps=args.lm_steps,
+                                 eager=not args.lm_no_eager)
         log(f"[bench] config 4 {lm}")
 
     cpu = None

@@ -418,14 +418,14 @@ def linear_supported(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -
     """Whether pa_linear_small takes F.linear(x, weight, bias): plain inference (no autograd,
     not under torch.compile) on CUDA tensors of one dtype, at most 16 rows of x (all leading
     dims), in_features a multiple of 8 (4 for fp32) with x fitting the 64 KiB staging."""
+    k = x.shape[-1] if x.dim() >= 1 else 0
+    if k == 0 or x.numel() > LINEAR_MAX_ROWS * k:  # the common, large case first
+        return False
     if not (x.is_cuda and weight.is_cuda) or x.dtype not in DTYPE_CODE or weight.dtype != x.dtype:
         return False
-    if weight.dim() != 2 or x.dim() < 1 or weight.device != x.device:
+    if weight.dim() != 2 or weight.device != x.device or weight.shape[1] != k:
         return False
     if torch.compiler.is_compiling() or _needs_op(x, weight, bias):
-        return False
-    k = x.shape[-1]
-    if weight.shape[1] != k or k == 0:
         return False
     rows = x.numel() // k
     e = 4 if x.dtype == torch.float32 else 8

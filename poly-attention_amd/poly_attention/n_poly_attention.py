@@ -30,7 +30,8 @@ from ._helpers import (
     where_keys,
     where_queries,
 )
-from .poly_attention import _compute_dtype, _q_norms, _static_decode_step, fused_available
+from .poly_attention import (_DECODE_ROWS, _compute_dtype, _q_norms, _static_decode_step,
+                             fused_available)
 from .rotary import RotaryEmbedding, apply_rotary_emb
 
 LinearNoBias = partial(nn.Linear, bias=False)
@@ -122,7 +123,7 @@ class NPolyAttention(Module):
     def _proj(self, layer: nn.Linear, x: Tensor) -> Tensor:
         """A projection; decode-sized inputs on the fused path stream the weight on
         pa_linear_small (the reference calls the nn.Linear directly)."""
-        if self._use_fused(x):
+        if x.numel() <= _DECODE_ROWS * x.shape[-1] and self._use_fused(x):
             from . import _ops
 
             return _ops.linear(layer, x)
@@ -131,7 +132,8 @@ class NPolyAttention(Module):
     def _projs(self, layers, xs):
         """[layer(x) for layer, x in zip(layers, xs)]; on the fused path decode-sized
         projections of one input share pa_linear_small launches."""
-        if self._use_fused(xs[0]):
+        x0 = xs[0]
+        if x0.numel() <= _DECODE_ROWS * x0.shape[-1] and self._use_fused(x0):
             from . import _ops
 
             return _ops.linear_many(list(layers), list(xs))

@@ -37,6 +37,9 @@ from .rotary import RotaryEmbedding, apply_rotary_emb
 
 LinearNoBias = partial(nn.Linear, bias=False)
 
+# inputs of at most this many rows (a decode step's batch) take pa_linear_small projections
+_DECODE_ROWS = 16
+
 
 def fused_available() -> bool:
     """The HIP path's plugin switch: libpolyattn.so loads (poly_attention.py:17-20)."""
@@ -270,7 +273,7 @@ class Order2PolyAttention(Module):
     def _proj(self, layer: nn.Linear, x: Tensor) -> Tensor:
         """A projection; decode-sized inputs on the fused path stream the weight on
         pa_linear_small (the reference calls the nn.Linear directly)."""
-        if self._use_fused(x):
+        if x.numel() <= _DECODE_ROWS * x.shape[-1] and self._use_fused(x):
             from . import _ops
 
             return _ops.linear(layer, x)
@@ -279,7 +282,8 @@ class Order2PolyAttention(Module):
     def _projs(self, layers, xs):
         """[layer(x) for layer, x in zip(layers, xs)]; on the fused path decode-sized
         projections of one input share pa_linear_small launches."""
-        if self._use_fused(xs[0]):
+        x0 = xs[0]
+        if x0.numel() <= _DECODE_ROWS * x0.shape[-1] and self._use_fused(x0):
             from . import _ops
 
             return _ops.linear_many(list(layers), list(xs))

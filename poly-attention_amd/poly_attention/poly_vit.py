@@ -86,10 +86,22 @@ class PolyViT(Module):
                                        use_flash_kernel=use_flash_kernel)
         self.linear_head = nn.Linear(dim, num_classes, bias=False)
 
+    def _pos(self, device, dtype):
+        """The sincos position table on the input's device and dtype (the reference moves it
+        every call, poly_vit.py:96); the moved copy is kept while the table is unchanged, so
+        that a forward issues no host-to-device copy (and can be captured into a HIP graph)."""
+        pe = self.pos_embedding
+        key = (device, dtype, id(pe), pe._version)
+        cached = getattr(self, "_pos_cached", None)
+        if cached is None or cached[0] != key:
+            cached = (key, pe.to(device, dtype=dtype))
+            self._pos_cached = cached
+        return cached[1]
+
     def forward(self, img):
         device, dtype = img.device, img.dtype
         x = self.to_patch_embedding(img)
-        x = x + self.pos_embedding.to(device, dtype=dtype)
+        x = x + self._pos(device, dtype)
         x = self.transformer(x)
         x = reduce(x, "b n d -> b d", "mean")
         return self.linear_head(x)
