@@ -223,3 +223,40 @@ def test_decode_steps_with_streamed_projections_equal_parallel():
             o, cache = m(x[:, i:i + 1], cache=cache, return_cache=True)
             outs.append(o)
     assert_close(torch.cat(outs, dim=1), ref, 1e-4, "stepwise")
+
+
+@param("dtype", (torch.float32, torch.bfloat16, torch.float16))
+@param("rows", (1, 5, 16))
+@param("k", (64, 512, 2048))
+def test_linear_fused_options_sweep(dtype, rows, k):
+    """Every input/output option together (x_add + sum, RMSNorm with weight, two outputs: GELU
+    with bias, residual) across dtypes, row counts and widths, against an fp32 restatement
+    that rounds at the same steps."""
+    from poly_attention import _ops
+
+    d = dev()
+    es = torch.tensor([], dtype=dtype).element_size()
+    if rows * k * es > 65536:
+        pytest.skip("x exceeds the staging limit")
+    g = torch.Generator().manual_seed(rows * 31 + k)
+    rnd = lambda *s: torch.randn(*s, generator=g).to(d, dtype)  # noqa: E731
+    x, xa = rnd(rows, k), rnd(rows, k)
+    norm = torch.nn.RMSNorm(k).to(d, dtype)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.25 * torch.randn(k, generator=g).to(d))
+    w1, b1 = (rnd(96, k) * k ** -0.5), rnd(96)
+    w2, res = (rnd(40, k) * k ** -0.5), rnd(rows, 40)
+    with torch.no_grad():
+        (y1, y2), xs = _ops.linear_small_group(x, [(w1, b1, True, None), (w2, None, False, res)],
+                                               x_add=xa, norm=norm, return_sum=True)
+    torch.cuda.synchronize()
+    r = lambda t: t.to(dtype).float()  # noqa: E731  (one rounding to the dtype)
+    xs_ref = r(x.float().cpu() + xa.float().cpu())
+    assert torch.equal(xs.float().cpu(), xs_ref)
+    rstd = torch.rsqrt(xs_ref.pow(2).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps)
+    xn = r(xs_ref * rstd * norm.weight.float().cpu())
+    y1_ref = r(torch.nn.functional.gelu(r(xn @ w1.float().cpu().t() + b1.float().cpu())))
+    y2_ref = r(res.float().cpu() + r(xn @ w2.float().cpu().t()))
+    tol = {torch.float32: 1e-5, torch.float16: 4e-3, torch.bfloat16: 3e-2}[dtype]
+    assert_close(y1, y1_ref, tol, f"gelu output {dtype} rows={rows} k={k}")
+    assert_close(y2, y2_ref, tol, f"residual output {dtype} rows={rows} k={k}")
