@@ -189,11 +189,16 @@ typedef struct pa_prologue {
 /* Row RMSNorm over the head dim of a [batch, heads, n, dim] view, forward and backward: the
  * q/k norms of the modules, RMSNorm(dim_head) applied to the per-head projections at
  * poly_attention.py:271 and n_poly_attention.py:188 (torch.nn.RMSNorm semantics:
- * y = x * rsqrt(mean(x^2) + eps) * weight, computed in fp32, rounded once).
+ * y = x * rsqrt(mean(x^2) + eps) * weight, computed in fp32, rounded once), optionally followed
+ * by the rotary embedding those lines apply next (poly_attention.py:275-276,
+ * n_poly_attention.py:190-191: y = round(t * cos(a) + rotate_half(t) * sin(a)) on the leading
+ * rot_dim features, t the rounded norm output, rotate_half pairing (2i, 2i+1) ->
+ * (-t[2i+1], t[2i]), a = angles[position * angles_stride + feature]).
  * Forward: x -> y, rstd.  Backward: dy, x, rstd -> dx and (when dweight is set) the weight
  * gradient summed over all rows in fp32, deterministically (workspace:
- * pa_rmsnorm_bwd_workspace bytes).  dim must be a multiple of 8 (4 for fp32) and <= 512;
- * views need 16-byte aligned rows. */
+ * pa_rmsnorm_bwd_workspace bytes); with angles, dy is the gradient of the rotated output and
+ * is first rotated back (rounded to the dtype, as the gradient of t).  dim must be a multiple
+ * of 8 (4 for fp32) and <= 512; views need 16-byte aligned rows. */
 typedef struct pa_rmsnorm {
     int32_t     batch, heads, n, dim;
     float       eps;
@@ -206,6 +211,10 @@ typedef struct pa_rmsnorm {
     float*      dweight;        /* backward: [dim] fp32 weight gradient, or NULL */
     void*       workspace;
     size_t      workspace_bytes;
+    const void* angles;         /* rotary angles [n positions][angles_stride], or NULL */
+    int32_t     angles_dtype;   /* PA_F32 / PA_F16 / PA_BF16 */
+    int32_t     rot_dim;        /* even, <= dim */
+    int64_t     angles_stride;  /* elements between positions (0: one row for all) */
 } pa_rmsnorm;
 
 /* Skinny linear layers for decode steps: up to PA_LINEAR_MAX_OUT projections of one input x

@@ -1,5 +1,6 @@
 // pa_norm.hip -- row RMSNorm over the head dim of [batch, heads, n, dim] views (the q/k norms
-// of the poly-attention modules), forward and backward.  HBM bound: a row group of LPR lanes
+// of the poly-attention modules), optionally followed by the rotary embedding, forward and
+// backward.  HBM bound: a row group of LPR lanes
 // reads a whole row with 16-byte loads, reduces with DPP inside the row group, and writes the
 // row back; the backward writes dx and accumulates the weight gradient per workgroup into a
 // fixed partial row, summed afterwards in a fixed order (deterministic, no atomics).
@@ -45,7 +46,42 @@ struct RmsDev {
     float* rstd;      // [batch][heads][n]
     float* partial;   // [gridDim.x][dim] (backward)
     float* dw;        // [dim] (backward, fp32)
+    const void* ang;  // rotary angles [n][astride] or null
+    int32_t adt, rot_dim;
+    int64_t astride;
 };
+
+// rotary embedding of the E features d0.. of one row in place (fp32 math on the rounded
+// norm output t, one rounding when stored): y[2i] = t[2i] cos a[2i] - t[2i+1] sin a[2i],
+// y[2i+1] = t[2i+1] cos a[2i+1] + t[2i] sin a[2i+1]
+template <int E>
+__device__ __forceinline__ void rope_fwd(const RmsDev& R, uint32_t pos, int d0, float (&t)[E]) {
+#pragma unroll
+    for (int e = 0; e < E; e += 2) {
+        const int d = d0 + e;
+        if (d >= R.rot_dim) break;
+        const int64_t o = (int64_t)pos * R.astride + d;
+        const float a0 = load_any(R.ang, R.adt, o), a1 = load_any(R.ang, R.adt, o + 1);
+        const float t0 = t[e], t1 = t[e + 1];
+        t[e] = t0 * cosf(a0) - t1 * sinf(a0);
+        t[e + 1] = t1 * cosf(a1) + t0 * sinf(a1);
+    }
+}
+
+// the gradient of t from the gradient g of the rotated row (the transposed rotation)
+template <int E>
+__device__ __forceinline__ void rope_bwd(const RmsDev& R, uint32_t pos, int d0, float (&g)[E]) {
+#pragma unroll
+    for (int e = 0; e < E; e += 2) {
+        const int d = d0 + e;
+        if (d >= R.rot_dim) break;
+        const int64_t o = (int64_t)pos * R.astride + d;
+        const float a0 = load_any(R.ang, R.adt, o), a1 = load_any(R.ang, R.adt, o + 1);
+        const float g0 = g[e], g1 = g[e + 1];
+        g[e] = g0 * cosf(a0) + g1 * sinf(a1);
+        g[e + 1] = g1 * cosf(a1) - g0 * sinf(a0);
+    }
+}
 
 constexpr int kRmsThreads = 256;
 constexpr int kRmsMaxBlocks = 1024;
@@ -107,7 +143,7 @@ __device__ __forceinline__ uint32_t rstd_index(const RmsDev& R, uint32_t b, uint
 
 // y = round(x * rsqrt(mean(x^2) + eps) * w); rstd saved per row.  Each row group handles
 // kRmsU rows per pass, their loads issued together (memory-level parallelism).
-template <typename T, int LPR>
+template <typename T, int LPR, bool ROPE>
 __global__ __launch_bounds__(kRmsThreads) void k_rms_fwd(RmsDev R) {
     constexpr int E = RVec<T>::n;
     constexpr int RPB = kRmsThreads / LPR;  // row groups per block
@@ -140,6 +176,12 @@ __global__ __launch_bounds__(kRmsThreads) void k_rms_fwd(RmsDev R) {
                 float y[E];
 #pragma unroll
                 for (int e = 0; e < E; ++e) y[e] = (x[u][e] * rs) * w[e];
+                if (ROPE && d0 < R.rot_dim) {
+                    // the norm output is a tensor of T before the rotation
+#pragma unroll
+                    for (int e = 0; e < E; ++e) y[e] = round_to<T>(y[e]);
+                    rope_fwd<E>(R, i[u], d0, y);
+                }
                 store_row<T>(R.y.at<T>(b[u], h[u], i[u]) + d0, y);
             }
             if (sub == 0) R.rstd[rstd_index(R, b[u], h[u], i[u])] = rs;
@@ -149,7 +191,7 @@ __global__ __launch_bounds__(kRmsThreads) void k_rms_fwd(RmsDev R) {
 
 // dx = rstd * (g - xhat * mean(g * xhat)), g = dy * w, xhat = x * rstd; the block's weight
 // gradient partial sum_rows dy * xhat goes to partial[blockIdx.x]
-template <typename T, int LPR>
+template <typename T, int LPR, bool ROPE>
 __global__ __launch_bounds__(kRmsThreads) void k_rms_bwd(RmsDev R) {
     constexpr int E = RVec<T>::n;
     constexpr int RPB = kRmsThreads / LPR;
@@ -176,6 +218,15 @@ __global__ __launch_bounds__(kRmsThreads) void k_rms_bwd(RmsDev R) {
             load_row<T>(R.x.at<T>(b[u], h[u], i[u]) + d0, dok && ok, x[u]);
             load_row<T>(R.dy.at<T>(b[u], h[u], i[u]) + d0, dok && ok, dy[u]);
             rs[u] = ok ? R.rstd[rstd_index(R, b[u], h[u], i[u])] : 0.f;
+        }
+        if (ROPE && d0 < R.rot_dim) {
+            // back through the rotation: the gradient of the norm output, a tensor of T
+#pragma unroll
+            for (int u = 0; u < kRmsU; ++u) {
+                rope_bwd<E>(R, i[u], d0, dy[u]);
+#pragma unroll
+                for (int e = 0; e < E; ++e) dy[u][e] = round_to<T>(dy[u][e]);
+            }
         }
 #pragma unroll
         for (int u = 0; u < kRmsU; ++u) {
@@ -254,6 +305,10 @@ static int rms_setup(const pa_rmsnorm* p, RmsDev& R, bool bwd) {
     if (p->weight && p->weight_dtype != PA_F32 && p->weight_dtype != PA_F16 &&
         p->weight_dtype != PA_BF16)
         return PA_EINVAL;
+    if (p->angles && (p->rot_dim < 0 || p->rot_dim > p->dim || p->rot_dim % 2 != 0 ||
+                      p->angles_stride < 0 ||
+                      (p->angles_dtype != PA_F32 && p->angles_dtype != PA_F16 && p->angles_dtype != PA_BF16)))
+        return PA_EINVAL;
     int lpr = 1;
     while (lpr * E < p->dim) lpr <<= 1;
     const int64_t rows = (int64_t)p->batch * p->heads * p->n;
@@ -286,16 +341,20 @@ static int rms_setup(const pa_rmsnorm* p, RmsDev& R, bool bwd) {
     R.rstd = p->rstd;
     R.partial = nullptr;
     R.dw = p->dweight;
+    R.ang = (p->angles && p->rot_dim > 0) ? p->angles : nullptr;
+    R.adt = p->angles_dtype;
+    R.rot_dim = R.ang ? p->rot_dim : 0;
+    R.astride = p->angles_stride;
     return PA_OK;
 }
 
-template <typename T>
-static void rms_launch(const RmsDev& R, bool bwd, hipStream_t s) {
+template <typename T, bool ROPE>
+static void rms_launch_r(const RmsDev& R, bool bwd, hipStream_t s) {
     const dim3 grid(rms_blocks(R));
-#define PA_RMS_CASE(L)                                                                       \
-    case L:                                                                                  \
-        if (bwd) hipLaunchKernelGGL((k_rms_bwd<T, L>), grid, dim3(kRmsThreads), 0, s, R);    \
-        else hipLaunchKernelGGL((k_rms_fwd<T, L>), grid, dim3(kRmsThreads), 0, s, R);        \
+#define PA_RMS_CASE(L)                                                                          \
+    case L:                                                                                     \
+        if (bwd) hipLaunchKernelGGL((k_rms_bwd<T, L, ROPE>), grid, dim3(kRmsThreads), 0, s, R); \
+        else hipLaunchKernelGGL((k_rms_fwd<T, L, ROPE>), grid, dim3(kRmsThreads), 0, s, R);     \
         break;
     switch (R.lpr) {
         PA_RMS_CASE(1)
@@ -307,6 +366,12 @@ static void rms_launch(const RmsDev& R, bool bwd, hipStream_t s) {
         default: PA_RMS_CASE(64)
     }
 #undef PA_RMS_CASE
+}
+
+template <typename T>
+static void rms_launch(const RmsDev& R, bool bwd, hipStream_t s) {
+    if (R.ang) rms_launch_r<T, true>(R, bwd, s);
+    else rms_launch_r<T, false>(R, bwd, s);
 }
 
 int launch_rms_fwd(const pa_rmsnorm* p, hipStream_t s) {

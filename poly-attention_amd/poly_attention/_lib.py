@@ -179,6 +179,10 @@ class PaRmsNorm(ctypes.Structure):
         ("dweight", c_void_p),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("angles", c_void_p),
+        ("angles_dtype", c_int32),
+        ("rot_dim", c_int32),
+        ("angles_stride", c_int64),
     ]
 
 

@@ -303,18 +303,36 @@ def attn_pass(q: Tensor, k: Tensor, v: Tensor, vmul: Optional[Tensor] = None,
 # per-head RMSNorm
 
 
-def _rms_struct(x: Tensor, weight: Optional[Tensor], eps: float) -> PaRmsNorm:
+def _rms_angles(x: Tensor, angles: Optional[Tensor]) -> Optional[Tensor]:
+    """The rotary angle rows of x's positions as pa_rmsnorm reads them: a [rot_dim] row for
+    every position, or the last N rows of [positions, rot_dim] (apply_rotary_emb's slicing)."""
+    if angles is None:
+        return None
+    if angles.dim() == 2:
+        angles = angles.narrow(0, angles.shape[0] - x.shape[2], x.shape[2])
+    return angles
+
+
+def _rms_struct(x: Tensor, weight: Optional[Tensor], eps: float,
+                angles: Optional[Tensor] = None) -> PaRmsNorm:
     r = PaRmsNorm()
     r.batch, r.heads, r.n, r.dim = x.shape
     r.eps = float(eps)
     r.x = _view(x)
     if weight is not None:
         r.weight, r.weight_dtype = weight.data_ptr(), DTYPE_CODE[weight.dtype]
+    a = _rms_angles(x, angles)
+    if a is not None:
+        r.angles, r.angles_dtype = a.data_ptr(), DTYPE_CODE[a.dtype]
+        r.rot_dim = a.shape[-1]
+        r.angles_stride = a.stride(0) if a.dim() == 2 else 0
     return r
 
 
-def rms_supported(x: Tensor, weight: Optional[Tensor]) -> bool:
-    """Shapes and layouts pa_rmsnorm takes: [B, H, N, d] with 16-byte aligned rows."""
+def rms_supported(x: Tensor, weight: Optional[Tensor], angles: Optional[Tensor] = None) -> bool:
+    """Shapes and layouts pa_rmsnorm takes: [B, H, N, d] with 16-byte aligned rows; rotary
+    angles (optional) as apply_rotary_emb takes them for such an x: [rot_dim] or
+    [positions >= N, rot_dim], rot_dim even and <= d, no gradient."""
     if x.dim() != 4 or x.dtype not in DTYPE_CODE or not x.is_cuda:
         return False
     e = 4 if x.dtype == torch.float32 else 8
@@ -323,20 +341,30 @@ def rms_supported(x: Tensor, weight: Optional[Tensor]) -> bool:
         return False
     if x.data_ptr() % 16 or any(st % e for st in x.stride()[:3]):
         return False
+    if angles is not None:
+        if angles.dim() not in (1, 2) or angles.dtype not in DTYPE_CODE or angles.requires_grad:
+            return False
+        if angles.device != x.device or angles.stride(-1) != 1:
+            return False
+        rot = angles.shape[-1]
+        if rot % 2 or rot > d or (angles.dim() == 2 and angles.shape[0] < x.shape[2]):
+            return False
     return weight is None or (weight.dim() == 1 and weight.numel() == d
                               and weight.dtype in DTYPE_CODE and weight.is_contiguous())
 
 
 @torch.library.custom_op("polyattn::rms_norm", mutates_args=(), device_types="cuda")
-def rms_norm_op(x: Tensor, weight: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor]:
-    return _rms_fwd_raw(x, weight, eps)
+def rms_norm_op(x: Tensor, weight: Optional[Tensor], eps: float,
+                angles: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
+    return _rms_fwd_raw(x, weight, eps, angles)
 
 
-def _rms_fwd_raw(x: Tensor, weight: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor]:
+def _rms_fwd_raw(x: Tensor, weight: Optional[Tensor], eps: float,
+                 angles: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
     y = _empty_heads(x.shape, x)
     rstd = torch.empty(x.shape[:3], dtype=torch.float32, device=x.device)
-    r = _rms_struct(x, weight, eps)
+    r = _rms_struct(x, weight, eps, angles)
     r.y, r.rstd = _view(y), rstd.data_ptr()
     with _device(x):
         _lib.check(lib.pa_rmsnorm_fwd(ctypes.byref(r), _stream(x)), "pa_rmsnorm_fwd")
@@ -344,19 +372,19 @@ def _rms_fwd_raw(x: Tensor, weight: Optional[Tensor], eps: float) -> tuple[Tenso
 
 
 @rms_norm_op.register_fake
-def _(x, weight, eps):
+def _(x, weight, eps, angles=None):
     return x.new_empty(x.shape), x.new_empty(x.shape[:3], dtype=torch.float32)
 
 
 @torch.library.custom_op("polyattn::rms_norm_bwd", mutates_args=(), device_types="cuda")
 def rms_norm_bwd_op(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tensor,
-                    eps: float) -> tuple[Tensor, Tensor]:
+                    eps: float, angles: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
     dy = dy if dy.stride(-1) == 1 and dy.data_ptr() % 16 == 0 else dy.contiguous()
     if any(st % (4 if dy.dtype == torch.float32 else 8) for st in dy.stride()[:3]):
         dy = dy.contiguous()
     dx = _empty_heads(x.shape, x)
-    r = _rms_struct(x, weight, eps)
+    r = _rms_struct(x, weight, eps, angles)
     r.rstd = rstd.data_ptr()
     r.dy, r.dx = _view(dy), _view(dx)
     dw32 = None
@@ -373,39 +401,40 @@ def rms_norm_bwd_op(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tenso
 
 
 @rms_norm_bwd_op.register_fake
-def _(dy, x, weight, rstd, eps):
+def _(dy, x, weight, rstd, eps, angles=None):
     return x.new_empty(x.shape), (weight.new_empty(weight.shape) if weight is not None
                                   else x.new_empty(0))
 
 
 def _rms_setup(ctx, inputs, output):
-    x, weight, eps = inputs
+    x, weight, eps, angles = inputs
     _, rstd = output
-    ctx.save_for_backward(x, weight, rstd)
+    ctx.save_for_backward(x, weight, rstd, angles)
     ctx.eps = eps
     ctx.set_materialize_grads(False)
 
 
 def _rms_backward(ctx, dy, drstd):
-    x, weight, rstd = ctx.saved_tensors
+    x, weight, rstd, angles = ctx.saved_tensors
     if dy is None:
-        return None, None, None
-    dx, dw = rms_norm_bwd_op(dy, x, weight, rstd, ctx.eps)
-    return dx, (dw if weight is not None else None), None
+        return None, None, None, None
+    dx, dw = rms_norm_bwd_op(dy, x, weight, rstd, ctx.eps, angles)
+    return dx, (dw if weight is not None else None), None, None
 
 
 torch.library.register_autograd("polyattn::rms_norm", _rms_backward, setup_context=_rms_setup)
 
 
-def rms_norm(x: Tensor, weight: Optional[Tensor], eps: Optional[float]) -> Tensor:
+def rms_norm(x: Tensor, weight: Optional[Tensor], eps: Optional[float],
+             angles: Optional[Tensor] = None) -> Tensor:
     """torch.nn.RMSNorm(d)(x) over the last dim of a [B, H, N, d] CUDA tensor on the HIP
-    kernels (the caller checks rms_supported).  eps=None is torch's default, the epsilon of
-    the fp32 op-math type."""
+    kernels, followed by apply_rotary_emb(angles, .) when angles are given (the caller checks
+    rms_supported).  eps=None is torch's default, the epsilon of the fp32 op-math type."""
     if eps is None:
         eps = torch.finfo(torch.float32).eps
     if not _needs_op(x, weight):
-        return _rms_fwd_raw(x, weight, float(eps))[0]
-    return rms_norm_op(x, weight, float(eps))[0]
+        return _rms_fwd_raw(x, weight, float(eps), angles)[0]
+    return rms_norm_op(x, weight, float(eps), angles)[0]
 
 
 # ---------------------------------------------------------------------------------------

@@ -205,10 +205,8 @@ class NPolyAttention(Module):
             if exists(root_value) and self.is_gqa:
                 root_value = repeat_kv(root_value, self.num_rep)
         else:
-            qs = _q_norms(self, self.q_norms, qs)
-
-            if exists(rotary_pos_emb):
-                qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)
+            # the q norms and the external rotary (fused into one kernel on the GPU path)
+            qs = _q_norms(self, self.q_norms, qs, rotary_pos_emb)
 
             q1 = first(qs)
             qs_rest = qs[1:]

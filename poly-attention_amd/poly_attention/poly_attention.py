@@ -46,19 +46,26 @@ def fused_available() -> bool:
     return _lib.available()
 
 
-def _q_norms(module, norms, qs):
-    """The per-head q/k RMSNorms (poly_attention.py:271, n_poly_attention.py:188): on the fused
-    GPU path through pa_rmsnorm (forward and backward), else torch.nn.RMSNorm."""
+def _q_norms(module, norms, qs, rotary_pos_emb=None):
+    """The per-head q/k RMSNorms (poly_attention.py:271, n_poly_attention.py:188), then the
+    external rotary when given (:275-276, :190-191): on the fused GPU path through pa_rmsnorm
+    (forward and backward, the rotation inside the same kernel), else torch.nn.RMSNorm and
+    apply_rotary_emb."""
     out = []
     for norm, q in zip(norms, qs):
         if (module._use_fused(q) and isinstance(norm, RMSNorm)
                 and tuple(norm.normalized_shape) == (q.shape[-1],)):
             from . import _ops
 
-            if _ops.rms_supported(q, norm.weight):
-                out.append(_ops.rms_norm(q, norm.weight, norm.eps))
+            if _ops.rms_supported(q, norm.weight, rotary_pos_emb):
+                out.append(_ops.rms_norm(q, norm.weight, norm.eps, rotary_pos_emb))
                 continue
-        out.append(norm(q))
+            if _ops.rms_supported(q, norm.weight):
+                q = _ops.rms_norm(q, norm.weight, norm.eps)
+                out.append(apply_rotary_emb(rotary_pos_emb, q) if exists(rotary_pos_emb) else q)
+                continue
+        q = norm(q)
+        out.append(apply_rotary_emb(rotary_pos_emb, q) if exists(rotary_pos_emb) else q)
     return tuple(out)
 
 
@@ -357,10 +364,8 @@ class Order2PolyAttention(Module):
             new_cache = cache
             v2 = repeat_kv(v2, self.num_rep) if self.is_gqa and exists(v2) else v2
         else:
-            qs = _q_norms(self, self.q_norms, qs)
-
-            if exists(rotary_pos_emb):
-                qs = tuple(apply_rotary_emb(rotary_pos_emb, q) for q in qs)
+            # the q norms and the external rotary (fused into one kernel on the GPU path)
+            qs = _q_norms(self, self.q_norms, qs, rotary_pos_emb)
 
             q1, q2, q3 = qs
 

@@ -1,6 +1,7 @@
-"""GPU: the per-head q/k RMSNorm (pa_rmsnorm_fwd / pa_rmsnorm_bwd through the
-``polyattn::rms_norm`` custom op) against torch.nn.RMSNorm, and the modules' gradients with
-the fused norms against the CPU oracle.
+"""GPU: the per-head q/k RMSNorm, alone and with the rotary embedding in the same kernel
+(pa_rmsnorm_fwd / pa_rmsnorm_bwd through the ``polyattn::rms_norm`` custom op) against
+torch.nn.RMSNorm and apply_rotary_emb, and the modules' gradients with the fused norms against
+the CPU oracle.
 
 Tolerances: forward fp32 max-abs <= 1e-5, bf16 within one bf16 ulp; gradients fp32 <= 1e-4,
 bf16 <= 2e-2 (relative to max(1, max|reference|)).
@@ -82,6 +83,68 @@ def test_rmsnorm_backward_matches_fp32_reference(dtype, d):
     assert wg.grad.dtype == dtype
 
 
+def _angles(rot, positions, two_d, device):
+    from poly_attention.rotary import RotaryEmbedding
+
+    freqs = RotaryEmbedding(rot)(torch.arange(positions).float()).to(device)
+    return freqs if two_d else freqs[-1]
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("d,rot", ((64, 64), (64, 32), (128, 64)))
+@param("two_d", (True, False))
+def test_rmsnorm_rope_forward_matches_torch_ops(dtype, d, rot, two_d):
+    """norm -> apply_rotary_emb in one kernel equals the two torch ops (rotation in fp32 on the
+    rounded norm output, one rounding), angles as [positions >= N, rot] (the last N rows) or
+    one [rot] row for every position."""
+    from poly_attention import _ops
+    from poly_attention.rotary import apply_rotary_emb
+
+    dv = dev()
+    torch.manual_seed(4)
+    H = 3
+    x = split_heads(torch.randn(2, 37, 2 * H * d, device=dv).to(dtype), H, d)
+    norm = torch.nn.RMSNorm(d).to(dv, dtype)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.3 * torch.randn(d, device=dv))
+    ang = _angles(rot, 45, two_d, dv)
+    assert _ops.rms_supported(x, norm.weight, ang)
+    with torch.no_grad():
+        ref = apply_rotary_emb(ang, norm(x))
+        got = _ops.rms_norm(x, norm.weight, norm.eps, ang)
+    if dtype == torch.float32:
+        assert rel_err(got, ref) <= 1e-5
+    else:
+        diff = (got.float() - ref.float()).abs()
+        ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -7
+        assert bool((diff <= ulp).all()), diff.max().item()
+
+
+@param("dtype", (torch.float32, torch.bfloat16))
+@param("rot", (64, 32))
+def test_rmsnorm_rope_backward_matches_fp32_reference(dtype, rot):
+    from poly_attention import _ops
+    from poly_attention.rotary import apply_rotary_emb
+
+    dv = dev()
+    torch.manual_seed(5)
+    H, d = 4, 64
+    base = torch.randn(2, 50, 2 * H * d, device=dv).to(dtype)
+    w = (1 + 0.3 * torch.randn(d, device=dv)).to(dtype)
+    dy = torch.randn(2, H, 50, d, device=dv).to(dtype)
+    ang = _angles(rot, 60, True, dv)
+    xr = split_heads(base.float(), H, d).detach().requires_grad_()
+    wr = w.float().detach().requires_grad_()
+    yr = apply_rotary_emb(ang, torch.nn.functional.rms_norm(xr, (d,), wr, torch.finfo(torch.float32).eps))
+    yr.backward(dy.float())
+    x = split_heads(base, H, d).detach().requires_grad_()
+    wg = w.detach().requires_grad_()
+    _ops.rms_norm(x, wg, None, ang).backward(dy)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert rel_err(x.grad, xr.grad) <= tol
+    assert rel_err(wg.grad, wr.grad) <= tol * 4
+
+
 def test_rmsnorm_weight_grad_is_deterministic():
     from poly_attention import _ops
 
@@ -99,9 +162,11 @@ def test_rmsnorm_weight_grad_is_deterministic():
 
 
 @param("order", (2, 3))
-def test_module_grads_with_fused_norms(order):
-    """Module forward + backward on the GPU (fused core and fused q/k norms) against the CPU
-    oracle's autograd: input and parameter gradients, including the q-norm weights."""
+@param("rotary", (False, True))
+def test_module_grads_with_fused_norms(order, rotary):
+    """Module forward + backward on the GPU (fused core and fused q/k norms, with the external
+    rotary inside the norm kernel) against the CPU oracle's autograd: input and parameter
+    gradients, including the q-norm weights."""
     from poly_attention import NPolyAttention, Order2PolyAttention
 
     dv = dev()
@@ -119,12 +184,13 @@ def test_module_grads_with_fused_norms(order):
             n.weight.copy_(1 + 0.3 * torch.randn_like(n.weight))
     x = torch.randn(2, 40, 64)
     g = torch.randn(2, 40, 64)
+    freqs = O.rotary_freqs(64, torch.arange(40)) if rotary else None
     params = {k: v.detach().clone().requires_grad_() for k, v in m.state_dict().items()}
     xr = x.clone().requires_grad_()
-    fwd(params, cfg, xr).backward(g)
+    fwd(params, cfg, xr, rotary_pos_emb=freqs).backward(g)
     m = m.to(dv)
     xg = x.to(dv).requires_grad_()
-    m(xg).backward(g.to(dv))
+    m(xg, rotary_pos_emb=freqs.to(dv) if rotary else None).backward(g.to(dv))
     assert rel_err(xg.grad, xr.grad) <= 1e-4
     for name, p in m.named_parameters():
         assert rel_err(p.grad, params[name].grad) <= 1e-4, name

@@ -144,6 +144,12 @@ def test_rmsnorm_rejects_invalid():
     assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # no output view
     r.y = r.x
     assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # no rstd
+    r.y, r.rstd = r.x, 0x2000
+    r.angles, r.rot_dim, r.angles_dtype = 0x4000, 63, _lib.PA_F32
+    assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # odd rot_dim
+    r.rot_dim, r.angles_dtype = 64, 9
+    assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # angle dtype
+    r.angles, r.rot_dim = None, 0
     r.dy = r.dx = r.x
     r.rstd, r.dweight = 0x2000, 0x3000
     assert lib.pa_rmsnorm_bwd_workspace(ctypes.byref(r)) > 0
