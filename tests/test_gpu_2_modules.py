@@ -180,7 +180,8 @@ def test_kv_cache_stepwise_equals_parallel(order, kv_heads, use_rotary_embed):
 
 @param("chunk,H,G,dh,sc", ((0, 8, 2, 128, None), (64, 8, 2, 128, None), (64, 64, 2, 128, None),
                            (0, 2, 2, 128, None), (64, 2, 2, 64, None), (64, 4, 2, 64, None),
-                           (0, 4, 2, 32, 5.0), (64, 3, 3, 128, 5.0)))
+                           (0, 4, 2, 32, 5.0), (64, 3, 3, 128, 5.0), (0, 2, 2, 256, None),
+                           (64, 8, 4, 256, None)))
 def test_decode_kernel_gqa_synthetic_cache(chunk, H, G, dh, sc):
     """Config-5 shape class (GQA) at a small cache, with a synthetic cache (q/k/v/msg ~ N(0,1),
     lse = log(j+1) + N(0,1)) against the oracle's cached branch; chunk=64 splits the 299 cached
