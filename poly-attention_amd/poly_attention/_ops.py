@@ -584,6 +584,78 @@ def linear_many(layers, xs) -> list[Tensor]:
 
 
 # ---------------------------------------------------------------------------------------
+# head split of the training / prefill projections
+
+
+class _SplitHeads(torch.autograd.Function):
+    """``rearrange(t, 'b n (p h d) -> p b h n d')`` of a [B, N, F] projection as one [B, h, N, d]
+    view per piece (pieces may differ in head count).  The backward concatenates the pieces'
+    gradients into the projection's gradient in one copy; the kernels produce those gradients
+    heads-inner, so each is already a [B, N, h*d] view, and a single piece costs nothing.
+    (Through einops, autograd would zero-fill the selected slots, stack the pieces and copy
+    the permuted stack back: three to five copies of the projection per step.)"""
+
+    @staticmethod
+    def forward(ctx, t, heads, d):
+        ctx.meta = (t.shape, t.dtype, t.device, heads, d)
+        ctx.set_materialize_grads(False)
+        outs, off = [], 0
+        for h in heads:
+            outs.append(t[..., off:off + h * d].unflatten(-1, (h, d)).transpose(1, 2))
+            off += h * d
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        (B, N, _), dtype, device, heads, d = ctx.meta
+        parts = [torch.zeros(B, N, h * d, dtype=dtype, device=device) if g is None
+                 else g.transpose(1, 2).reshape(B, N, h * d) for g, h in zip(grads, heads)]
+        return (parts[0] if len(parts) == 1 else torch.cat(parts, dim=-1)), None, None
+
+
+def _plain_linear(layer) -> bool:
+    # exactly nn.Linear with no hooks: bypassing layer(x) must not skip anything a caller added
+    return (type(layer) is torch.nn.Linear and not layer._forward_hooks
+            and not layer._forward_pre_hooks)
+
+
+def project_heads(layers, xs, splits):
+    """The modules' projections followed by their head splits
+    (poly_attention.py:258-266, 322-340; n_poly_attention.py:103-110, 177-196):
+    ``[rearrange(layer(x), 'b n (p h d) -> p b h n d') for ...]`` with ``splits[i] = (p, h)``,
+    each result a list of p views [B, h, N, d].  When every layer reads the same input and is
+    a plain bias-free nn.Linear, the projections run as one GEMM over the concatenated
+    weights (one dx GEMM and one weight-gradient GEMM in the backward instead of one per layer
+    plus the adds of dx); the head splits are views with a one-copy backward."""
+    x = xs[0]
+    d = []
+    for layer, (p, h) in zip(layers, splits):
+        assert layer.weight.shape[0] % (p * h) == 0
+        d.append(layer.weight.shape[0] // (p * h))
+    fuse = (len(layers) > 1 and all(xi is x for xi in xs) and x.dim() == 3
+            and len(set(d)) == 1 and not torch.compiler.is_compiling()
+            and not torch.nn.modules.module._global_forward_hooks
+            and not torch.nn.modules.module._global_forward_pre_hooks
+            and all(_plain_linear(l) and l.bias is None for l in layers)
+            and len({l.weight.dtype for l in layers}) == 1)
+    if fuse:
+        w = torch.cat([l.weight for l in layers])
+        heads = tuple(h for p, h in splits for _ in range(p))
+        pieces = _SplitHeads.apply(torch.nn.functional.linear(x, w), heads, d[0])
+        out, i = [], 0
+        for p, _ in splits:
+            out.append(list(pieces[i:i + p]))
+            i += p
+        return out
+    out = []
+    for layer, xi, (p, h), di in zip(layers, xs, splits, d):
+        y = layer(xi)
+        assert y.dim() == 3, "expected a [batch, n, features] projection"
+        out.append(list(_SplitHeads.apply(y, (h,) * p, di)))
+    return out
+
+
+# ---------------------------------------------------------------------------------------
 # the order-n chain
 
 

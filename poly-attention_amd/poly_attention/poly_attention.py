@@ -336,17 +336,25 @@ class Order2PolyAttention(Module):
 
         # the projections (the reference computes to_q first; they are independent, and on the
         # fused decode path the ones of a shared input go out together)
-        q_proj, kv1_proj, kv2_proj = self._projs([self.to_q, *self.to_kvs], [x, ctx1, ctx2])
-        q_and_maybe_gates = self.split_q(q_proj)
+        if x.dim() == 3 and x.numel() > _DECODE_ROWS * x.shape[-1] and self._use_fused(x):
+            # fused path: one GEMM for the projections of a shared input, views for the heads
+            from . import _ops
+
+            q_and_maybe_gates, kv1, kv2 = _ops.project_heads(
+                [self.to_q, *self.to_kvs], [x, ctx1, ctx2],
+                [(2 if self.attn_gate else 1, self.heads),
+                 (2 if self.has_root_v else 1, self.kv_heads),
+                 (1 if self.shared_kv else 2, self.kv_heads)])
+        else:
+            q_proj, kv1_proj, kv2_proj = self._projs([self.to_q, *self.to_kvs], [x, ctx1, ctx2])
+            q_and_maybe_gates = self.split_q(q_proj)
+            kv1 = self.split_kv1(kv1_proj)
+            kv2 = self.split_kv(kv2_proj)
+
         if self.attn_gate:
             q1, gates = q_and_maybe_gates
         else:
             q1 = first(q_and_maybe_gates)
-
-        # kvs
-
-        kv1 = self.split_kv1(kv1_proj)
-        kv2 = self.split_kv(kv2_proj)
 
         if self.shared_kv:
             qs = (q1, first(kv1), first(kv2))

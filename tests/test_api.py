@@ -283,3 +283,56 @@ def test_reference_poly_attention_matches_oracle():
                                        causal=causal, softclamp_value=4.0)
         for x, y in zip(a, b):
             torch.testing.assert_close(x, y, rtol=0, atol=0)
+
+
+@param("shared", (True, False))
+@param("splits", (((1, 4), (1, 4), (2, 4)), ((2, 4), (2, 2), (1, 2), (2, 2))))
+def test_project_heads_matches_rearrange_split(shared, splits):
+    """The fused path's projections + head splits (one GEMM over concatenated weights when the
+    input is shared; views with a one-copy backward) against layer(x) + einops Rearrange, in
+    values and in every gradient; one piece of a two-piece layer is left unused (its gradient
+    is None)."""
+    from einops.layers.torch import Rearrange
+
+    from poly_attention import _ops
+
+    d = 8
+    layers = [torch.nn.Linear(32, p * h * d, bias=False).double() for p, h in splits]
+    x = torch.randn(2, 5, 32, dtype=torch.float64, requires_grad=True)
+    xs = [x] * len(layers) if shared else [
+        torch.randn(2, 5, 32, dtype=torch.float64, requires_grad=True) for _ in layers]
+
+    def run(fused):
+        for t in (*xs, *(l.weight for l in layers)):
+            t.grad = None
+        if fused:
+            groups = _ops.project_heads(layers, xs, list(splits))
+        else:
+            groups = [list(Rearrange("b n (s h d) -> s b h n d", s=p, h=h)(l(xi)))
+                      for l, xi, (p, h) in zip(layers, xs, splits)]
+        pieces = [t for g in groups for t in g]
+        assert all(t.shape[1] == h for g, (_, h) in zip(groups, splits) for t in g)
+        g = torch.Generator().manual_seed(3)
+        loss = sum((t * torch.randn(t.shape, generator=g, dtype=t.dtype)).sum()
+                   for t in pieces[:-1])  # the last piece unused
+        loss.backward()
+        return ([t.detach().clone() for t in pieces],
+                [t.grad.clone() for t in (*dict.fromkeys(xs), *(l.weight for l in layers))])
+
+    vals, grads = run(True)
+    vals_ref, grads_ref = run(False)
+    for a, b in zip(vals + grads, vals_ref + grads_ref):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_project_heads_keeps_hooked_layers():
+    """A layer with a forward hook is called as a module (the hook fires), not folded into
+    the concatenated GEMM."""
+    from poly_attention import _ops
+
+    layers = [torch.nn.Linear(16, 8, bias=False) for _ in range(2)]
+    seen = []
+    layers[1].register_forward_hook(lambda m, i, o: seen.append(o.shape))
+    x = torch.randn(1, 3, 16)
+    _ops.project_heads(layers, [x, x], [(1, 2), (1, 2)])
+    assert seen == [torch.Size([1, 3, 8])]
