@@ -159,10 +159,21 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
     return out, lse
 
 
+def _out_buffer(buf: Optional[Tensor], like: Tensor) -> Tensor:
+    if buf is None:
+        return _empty_heads(like.shape, like)
+    assert buf.shape == like.shape and buf.dtype == like.dtype and buf.stride(-1) == 1
+    return buf
+
+
 def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal,
-                 softclamp, scale, may_degenerate, dq_into: Optional[Tensor] = None):
+                 softclamp, scale, may_degenerate, dq_into: Optional[Tensor] = None,
+                 dq_out: Optional[Tensor] = None, dk_out: Optional[Tensor] = None,
+                 dv_out: Optional[Tensor] = None):
     """One pass backward.  ``dq_into``: a gradient buffer of q's shape that the query gradient
-    is added into (PA_ACC_DQ) instead of a new tensor."""
+    is added into (PA_ACC_DQ) instead of a new tensor.  ``dq_out`` / ``dk_out`` / ``dv_out``:
+    buffers (any strided view of the right shape) that the gradients are written to instead
+    of new tensors."""
     lib = _lib.load()
     q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
     vmul = _inner_contig(vmul) if vmul is not None else None
@@ -173,6 +184,7 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
         # queries shared by several pass heads: the backward wants them per pass head (the
         # caller sums the per-head dq back)
         q = q.repeat_interleave(H // q.shape[1], dim=1)
+        dq_out = None
     hk = k.shape[1]
     key_side = [t for t in (v, vmul, bias) if t is not None]
     assert all(t.shape[1] == hk for t in key_side), \
@@ -182,9 +194,9 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
         assert dq_into.shape == q.shape and dq_into.dtype == q.dtype
         dq, accumulate = dq_into, _lib.PA_ACC_DQ
     else:
-        dq = _empty_heads(q.shape, q)
-    dk = _empty_heads(k.shape, k)
-    dv = _empty_heads(v.shape, v)
+        dq = _out_buffer(dq_out, q)
+    dk = _out_buffer(dk_out, k)
+    dv = _out_buffer(dv_out, v)
     dvmul = _empty_heads(vmul.shape, vmul, v.dtype) if vmul is not None else None
     dbias = (torch.empty(bias.shape, dtype=torch.float32, device=q.device)
              if bias is not None else None)
@@ -258,6 +270,7 @@ def _pass_setup(ctx, inputs, output):
     ctx.causal, ctx.softclamp, ctx.scale = causal, softclamp, scale
     ctx.may_degenerate = may_degenerate
     ctx.has_vmul, ctx.has_bias = vmul is not None, bias is not None
+    ctx.slots = [slot_ref(t) for t in (q, k, v)]
     ctx.set_materialize_grads(False)
 
 
@@ -265,9 +278,24 @@ def _pass_backward(ctx, dout, dlse):
     q, k, v, vmul, bias, key_mask, query_mask, out, lse = ctx.saved_tensors
     if dout is None:
         dout = torch.zeros_like(out)
-    dq, dk, dv, dvmul, dbias = pass_bwd_op(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask,
-                                           out, lse, ctx.causal, ctx.softclamp, ctx.scale,
-                                           ctx.may_degenerate)
+    # a q / k / v that is a piece of a head-split projection: its gradient goes straight into
+    # the projection's gradient buffer (eager only; the op is opaque to tracing)
+    outs = [claim_slot(r, t) for r, t in zip(ctx.slots, (q, k, v))]
+    if q.shape[1] != out.shape[1]:
+        outs[0] = None
+    if any(o is not None for o in outs):
+        dq, dk, dv, dvmul, dbias = pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask,
+                                                query_mask, out, lse, ctx.causal, ctx.softclamp,
+                                                ctx.scale, ctx.may_degenerate, dq_out=outs[0],
+                                                dk_out=outs[1], dv_out=outs[2])
+        if dvmul is None:
+            dvmul = q.new_empty(0)
+        if dbias is None:
+            dbias = q.new_empty(0)
+    else:
+        dq, dk, dv, dvmul, dbias = pass_bwd_op(dout, dlse, q, k, v, vmul, bias, key_mask,
+                                               query_mask, out, lse, ctx.causal, ctx.softclamp,
+                                               ctx.scale, ctx.may_degenerate)
     if dq.shape[1] != q.shape[1]:  # queries were shared across pass heads: sum their grads
         dq = dq.unflatten(1, (q.shape[1], -1)).sum(2)
     return (dq, dk, dv, dvmul if ctx.has_vmul else None, dbias if ctx.has_bias else None,
@@ -379,11 +407,19 @@ def _(x, weight, eps, angles=None):
 @torch.library.custom_op("polyattn::rms_norm_bwd", mutates_args=(), device_types="cuda")
 def rms_norm_bwd_op(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tensor,
                     eps: float, angles: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
+    return _rms_bwd_raw(dy, x, weight, rstd, eps, angles)
+
+
+def _rms_bwd_raw(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tensor, eps: float,
+                 angles: Optional[Tensor] = None,
+                 dx_out: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
     dy = dy if dy.stride(-1) == 1 and dy.data_ptr() % 16 == 0 else dy.contiguous()
     if any(st % (4 if dy.dtype == torch.float32 else 8) for st in dy.stride()[:3]):
         dy = dy.contiguous()
-    dx = _empty_heads(x.shape, x)
+    dx = _empty_heads(x.shape, x) if dx_out is None else dx_out
+    if dx_out is not None and not rms_supported(dx_out, weight, angles):
+        dx = _empty_heads(x.shape, x)
     r = _rms_struct(x, weight, eps, angles)
     r.rstd = rstd.data_ptr()
     r.dy, r.dx = _view(dy), _view(dx)
@@ -411,6 +447,7 @@ def _rms_setup(ctx, inputs, output):
     _, rstd = output
     ctx.save_for_backward(x, weight, rstd, angles)
     ctx.eps = eps
+    ctx.slot = slot_ref(x)
     ctx.set_materialize_grads(False)
 
 
@@ -418,7 +455,11 @@ def _rms_backward(ctx, dy, drstd):
     x, weight, rstd, angles = ctx.saved_tensors
     if dy is None:
         return None, None, None, None
-    dx, dw = rms_norm_bwd_op(dy, x, weight, rstd, ctx.eps, angles)
+    dx_out = claim_slot(ctx.slot, x)
+    if dx_out is not None:  # eager: write dx into the split projection's gradient
+        dx, dw = _rms_bwd_raw(dy, x, weight, rstd, ctx.eps, angles, dx_out)
+    else:
+        dx, dw = rms_norm_bwd_op(dy, x, weight, rstd, ctx.eps, angles)
     return dx, (dw if weight is not None else None), None, None
 
 
@@ -587,17 +628,70 @@ def linear_many(layers, xs) -> list[Tensor]:
 # head split of the training / prefill projections
 
 
+class _GradSlots:
+    """The gradient buffer of a head-split projection ([B, N, F]), allocated on first use in the
+    backward.  A backward that produces the gradient of a piece (the pass and RMSNorm
+    backwards) may claim the piece's slot -- a [B, h, N, d] view of the buffer -- and write its
+    result there, so that the split's backward finds the pieces already in place.  Each slot
+    is handed out once per backward; a second consumer of the same piece allocates its own
+    gradient (autograd sums the two, and the split copies the sum into the slot)."""
+
+    def __init__(self, shape, dtype, device, heads, d):
+        self.shape, self.dtype, self.device, self.heads, self.d = shape, dtype, device, heads, d
+        self.offsets = [0]
+        for h in heads:
+            self.offsets.append(self.offsets[-1] + h * d)
+        self.buf = None
+        self.claimed = set()
+
+    def view(self, i: int) -> Tensor:
+        if self.buf is None:
+            self.buf = torch.empty(self.shape, dtype=self.dtype, device=self.device)
+        o, h = self.offsets[i], self.heads[i]
+        return self.buf[..., o:o + h * self.d].unflatten(-1, (h, self.d)).transpose(1, 2)
+
+    def claim(self, i: int) -> Optional[Tensor]:
+        if i in self.claimed:
+            return None
+        self.claimed.add(i)
+        return self.view(i)
+
+    def take(self) -> Tensor:
+        # the finished buffer leaves with the split's gradient: a later backward over the same
+        # graph (retain_graph) starts over with a new buffer
+        buf, self.buf, self.claimed = self.buf, None, set()
+        return buf
+
+
+def slot_ref(t: Optional[Tensor]):
+    """At a consumer's forward: the gradient-slot reference of ``t`` when it is a piece of a
+    head-split projection (``project_heads``), else None."""
+    return getattr(t, "_pa_grad_slot", None) if t is not None else None
+
+
+def claim_slot(ref, like: Tensor) -> Optional[Tensor]:
+    """At the consumer's backward: the piece's gradient slot, claimed for writing, when it
+    matches ``like`` (the gradient the consumer would allocate) in shape and dtype."""
+    if ref is None:
+        return None
+    slots, i = ref
+    if (tuple(like.shape) != (slots.shape[0], slots.heads[i], slots.shape[1], slots.d)
+            or like.dtype != slots.dtype or like.device != slots.device):
+        return None
+    return slots.claim(i)
+
+
 class _SplitHeads(torch.autograd.Function):
     """``rearrange(t, 'b n (p h d) -> p b h n d')`` of a [B, N, F] projection as one [B, h, N, d]
-    view per piece (pieces may differ in head count).  The backward concatenates the pieces'
-    gradients into the projection's gradient in one copy; the kernels produce those gradients
-    heads-inner, so each is already a [B, N, h*d] view, and a single piece costs nothing.
-    (Through einops, autograd would zero-fill the selected slots, stack the pieces and copy
-    the permuted stack back: three to five copies of the projection per step.)"""
+    view per piece (pieces may differ in head count).  The backward assembles the projection's
+    gradient in a ``_GradSlots`` buffer: pieces whose consumers wrote their gradient into its
+    slot cost nothing, the others are copied in (or zero-filled when unused).  (Through einops,
+    autograd would zero-fill the selected slots, stack the pieces and copy the permuted stack
+    back: three to five copies of the projection per step.)"""
 
     @staticmethod
-    def forward(ctx, t, heads, d):
-        ctx.meta = (t.shape, t.dtype, t.device, heads, d)
+    def forward(ctx, t, heads, d, slots):
+        ctx.slots = slots
         ctx.set_materialize_grads(False)
         outs, off = [], 0
         for h in heads:
@@ -607,10 +701,23 @@ class _SplitHeads(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        (B, N, _), dtype, device, heads, d = ctx.meta
-        parts = [torch.zeros(B, N, h * d, dtype=dtype, device=device) if g is None
-                 else g.transpose(1, 2).reshape(B, N, h * d) for g, h in zip(grads, heads)]
-        return (parts[0] if len(parts) == 1 else torch.cat(parts, dim=-1)), None, None
+        slots = ctx.slots
+        B, N, _ = slots.shape
+        if slots.buf is None:
+            # no consumer wrote in place: one concatenation (a single piece is a free view,
+            # the kernels' gradients being heads-inner)
+            parts = [torch.zeros(B, N, h * slots.d, dtype=slots.dtype, device=slots.device)
+                     if g is None else g.transpose(1, 2).reshape(B, N, h * slots.d)
+                     for g, h in zip(grads, slots.heads)]
+            slots.claimed = set()
+            return (parts[0] if len(parts) == 1 else torch.cat(parts, dim=-1)), None, None, None
+        for i, g in enumerate(grads):
+            v = slots.view(i)
+            if g is None:
+                v.zero_()
+            elif not (g.data_ptr() == v.data_ptr() and g.stride() == v.stride()):
+                v.copy_(g)
+        return slots.take(), None, None, None
 
 
 def _plain_linear(layer) -> bool:
@@ -626,7 +733,8 @@ def project_heads(layers, xs, splits):
     each result a list of p views [B, h, N, d].  When every layer reads the same input and is
     a plain bias-free nn.Linear, the projections run as one GEMM over the concatenated
     weights (one dx GEMM and one weight-gradient GEMM in the backward instead of one per layer
-    plus the adds of dx); the head splits are views with a one-copy backward."""
+    plus the adds of dx).  The head splits are views; the pass and RMSNorm backwards write
+    their pieces' gradients straight into the projection's gradient buffer."""
     x = xs[0]
     d = []
     for layer, (p, h) in zip(layers, splits):
@@ -641,7 +749,7 @@ def project_heads(layers, xs, splits):
     if fuse:
         w = torch.cat([l.weight for l in layers])
         heads = tuple(h for p, h in splits for _ in range(p))
-        pieces = _SplitHeads.apply(torch.nn.functional.linear(x, w), heads, d[0])
+        pieces = _split_heads(torch.nn.functional.linear(x, w), heads, d[0])
         out, i = [], 0
         for p, _ in splits:
             out.append(list(pieces[i:i + p]))
@@ -651,8 +759,17 @@ def project_heads(layers, xs, splits):
     for layer, xi, (p, h), di in zip(layers, xs, splits, d):
         y = layer(xi)
         assert y.dim() == 3, "expected a [batch, n, features] projection"
-        out.append(list(_SplitHeads.apply(y, (h,) * p, di)))
+        out.append(list(_split_heads(y, (h,) * p, di)))
     return out
+
+
+def _split_heads(t: Tensor, heads, d: int):
+    slots = _GradSlots(t.shape, t.dtype, t.device, tuple(heads), d)
+    pieces = _SplitHeads.apply(t, tuple(heads), d, slots)
+    if t.requires_grad and not torch.compiler.is_compiling():
+        for i, piece in enumerate(pieces):
+            piece._pa_grad_slot = (slots, i)
+    return pieces
 
 
 # ---------------------------------------------------------------------------------------
@@ -672,6 +789,7 @@ class _Order2Chain(torch.autograd.Function):
                                 False)
         ctx.save_for_backward(q1, q2, q3, v3, msg, lse23, out, lse)
         ctx.cfg = (causal, softclamp, scale)
+        ctx.slots = [slot_ref(t) for t in (q1, q2, q3, v3)]
         ctx.set_materialize_grads(False)
         return out, lse, lse23, msg
 
@@ -681,15 +799,20 @@ class _Order2Chain(torch.autograd.Function):
         causal, softclamp, scale = ctx.cfg
         if dout is None:
             dout = torch.zeros_like(out)
+        # inputs that are pieces of a head-split projection get their gradients written into
+        # its gradient buffer
+        dq1_out, dq2_out, dq3_out, dv3_out = (claim_slot(r, t) for r, t in
+                                              zip(ctx.slots, (q1, q2, q3, v3)))
         dq1, dq2, dmsg, _, dlse23 = pass_bwd_raw(dout, dlse, q1, q2, msg, None, lse23, None,
                                                  None, out, lse, causal, softclamp, scale,
-                                                 False)
+                                                 False, dq_out=dq1_out, dk_out=dq2_out)
         if dmsg_ext is not None:
             dmsg = dmsg + dmsg_ext
         if dlse23_ext is not None:
             dlse23 = dlse23 + dlse23_ext
         _, dq3, dv3, _, _ = pass_bwd_raw(dmsg, dlse23, q2, q3, v3, None, None, None, None, msg,
-                                         lse23, causal, softclamp, scale, False, dq_into=dq2)
+                                         lse23, causal, softclamp, scale, False, dq_into=dq2,
+                                         dk_out=dq3_out, dv_out=dv3_out)
         return dq1, dq2, dq3, dv3, None, None, None
 
 

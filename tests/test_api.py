@@ -336,3 +336,69 @@ def test_project_heads_keeps_hooked_layers():
     x = torch.randn(1, 3, 16)
     _ops.project_heads(layers, [x, x], [(1, 2), (1, 2)])
     assert seen == [torch.Size([1, 3, 8])]
+
+
+class _Twice(torch.autograd.Function):
+    """A consumer that, like the pass and RMSNorm backwards, writes its input gradient into
+    the head-split projection's gradient buffer when its input is a piece of one."""
+
+    @staticmethod
+    def forward(ctx, x):
+        from poly_attention import _ops
+
+        ctx.slot = _ops.slot_ref(x)
+        ctx.like = (x.shape, x.dtype)
+        return 2 * x
+
+    @staticmethod
+    def backward(ctx, dy):
+        from poly_attention import _ops
+
+        out = _ops.claim_slot(ctx.slot, torch.empty(ctx.like[0], dtype=ctx.like[1]))
+        if out is None:
+            return 2 * dy
+        torch.mul(dy, 2, out=out)
+        return out
+
+
+@param("retain", (False, True))
+def test_project_heads_gradient_slots(retain):
+    """Consumers that write their gradients into the projection's gradient buffer: a piece
+    used once (written in place), a piece used by two such consumers (the second one's claim
+    is refused; autograd's sum is copied in), a piece used by a plain op and an unused piece.
+    A second backward over the retained graph gives the same gradients."""
+    from poly_attention import _ops
+
+    splits = [(2, 3), (2, 3)]
+    layers = [torch.nn.Linear(24, p * h * 4, bias=False).double() for p, h in splits]
+    x = torch.randn(2, 5, 24, dtype=torch.float64, requires_grad=True)
+    g = [torch.randn(2, 3, 5, 4, dtype=torch.float64) for _ in range(4)]
+
+    def loss_of(pieces, twice):
+        a, b, c, _ = pieces
+        return ((twice(a) * g[0]).sum() + (twice(b) * g[1]).sum() + (twice(b) * g[2]).sum()
+                + (c.sin() * g[3]).sum())
+
+    def grads(fused):
+        for t in (x, *(l.weight for l in layers)):
+            t.grad = None
+        if fused:
+            pieces = [t for grp in _ops.project_heads(layers, [x, x], splits) for t in grp]
+            loss = loss_of(pieces, _Twice.apply)
+        else:
+            pieces = [t for l, (p, h) in zip(layers, splits)
+                      for t in l(x).unflatten(-1, (p, h, 4)).permute(2, 0, 3, 1, 4).unbind(0)]
+            loss = loss_of(pieces, lambda t: 2 * t)
+        loss.backward(retain_graph=retain)
+        first = [t.grad.clone() for t in (x, *(l.weight for l in layers))]
+        if retain:
+            for t in (x, *(l.weight for l in layers)):
+                t.grad = None
+            loss.backward()
+            again = [t.grad for t in (x, *(l.weight for l in layers))]
+            for a, b in zip(first, again):
+                torch.testing.assert_close(a, b, rtol=0, atol=0)
+        return first
+
+    for a, b in zip(grads(True), grads(False)):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
