@@ -121,12 +121,15 @@ class NPolyAttention(Module):
         return True
 
     def _proj(self, layer: nn.Linear, x: Tensor) -> Tensor:
-        """A projection; decode-sized inputs on the fused path stream the weight on
-        pa_linear_small (the reference calls the nn.Linear directly)."""
-        if x.numel() <= _DECODE_ROWS * x.shape[-1] and self._use_fused(x):
+        """A projection (the reference calls the nn.Linear directly); on the fused path
+        decode-sized inputs stream the weight on pa_linear_small, larger ones take the split-K
+        weight gradient in training."""
+        if self._use_fused(x):
             from . import _ops
 
-            return _ops.linear(layer, x)
+            if x.numel() <= _DECODE_ROWS * x.shape[-1]:
+                return _ops.linear(layer, x)
+            return _ops.layer_train(layer, x)
         return layer(x)
 
     def _projs(self, layers, xs):

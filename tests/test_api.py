@@ -402,3 +402,19 @@ def test_project_heads_gradient_slots(retain):
 
     for a, b in zip(grads(True), grads(False)):
         torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_weight_grad_split_choice():
+    """The split-K weight gradient's batch count: 8 for outputs up to 2^20 elements, 4 up to
+    2^22, else none; halved until every batch holds >= 2048 rows and divides the rows."""
+    from poly_attention import _ops
+
+    assert _ops._dw_splits(16384, 1024, 1024) == 8
+    assert _ops._dw_splits(16384, 4096, 1024) == 4
+    assert _ops._dw_splits(16384, 4096, 4096) == 1
+    assert _ops._dw_splits(6144, 256, 512) == 2
+    assert _ops._dw_splits(2048, 1024, 1024) == 1
+    assert _ops._dw_splits(16383, 1024, 1024) == 1
+    x = torch.randn(4, 8, 16, requires_grad=True)
+    lin = torch.nn.Linear(16, 8)
+    torch.testing.assert_close(_ops.layer_train(lin, x), lin(x))  # CPU: plain F.linear

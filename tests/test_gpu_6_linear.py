@@ -188,6 +188,30 @@ def test_linear_many_groups_shared_input():
                          1e-5, "linear_many")
 
 
+@param("rows,n,k", ((16384, 1024, 1024), (8192, 4096, 1024), (6144, 256, 512)))
+def test_linear_train_split_k_weight_grad(rows, n, k):
+    """The training projections' split-K weight gradient (bf16 batches with fp32 partial
+    sums) and the rest of its backward against fp32 references, bf16 tolerance."""
+    from poly_attention import _ops
+
+    d = dev()
+    torch.manual_seed(5)
+    assert _ops._dw_splits(rows, n, k) > 1
+    lin = torch.nn.Linear(k, n).to(d, torch.bfloat16)
+    x = torch.randn(2, rows // 2, k, device=d, dtype=torch.bfloat16, requires_grad=True)
+    y = _ops.layer_train(lin, x)
+    assert y.grad_fn is not None and "LinearTrain" in type(y.grad_fn).__name__
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    x32 = x.detach().float().reshape(rows, k)
+    w32, dy32 = lin.weight.detach().float(), dy.float().reshape(rows, n)
+    tol = TOL[torch.bfloat16]
+    assert_close(y.reshape(rows, n), x32 @ w32.t() + lin.bias.detach().float(), tol, "y")
+    assert_close(x.grad.reshape(rows, k), dy32 @ w32, tol, "dx")
+    assert_close(lin.weight.grad, dy32.t() @ x32, tol, "dw")
+    assert_close(lin.bias.grad, dy32.sum(0), tol, "db")
+
+
 def test_linear_supported_routes_other_calls_to_torch():
     from poly_attention import _ops
 
