@@ -75,6 +75,22 @@ ORDER2_CFGS = [
 ]
 
 
+def _grad_params(m):
+    # the module's weights as CPU leaves for the oracle, so that it returns their gradients
+    return {k: v.detach().cpu().clone().requires_grad_(v.is_floating_point())
+            for k, v in m.state_dict().items()}
+
+
+def _check_param_grads(m, params):
+    """Every parameter gradient (projections through the fused head split and concatenated
+    GEMM, q/k norm weights, output projection) against the oracle's."""
+    for k, p in m.named_parameters():
+        ref = params[k].grad
+        assert (p.grad is None) == (ref is None), k
+        if ref is not None:
+            assert_close(p.grad, ref, 1e-4, f"d{k}", grad=True)
+
+
 @param("cfg", ORDER2_CFGS)
 @param("masked", (False, True))
 @param("seq_len", (31, 64))
@@ -92,7 +108,7 @@ def test_order2_module_e2e(cfg, masked, seq_len):
         mask[:, seq_len // 2:] = False
     xg = x.to(d).requires_grad_()
     out = m(xg, mask=mask.to(d) if masked else None)
-    params = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    params = _grad_params(m)
     xo = x.clone().requires_grad_()
     ref = O.order2_forward(params, cfg, xo, mask=mask)
     dout = torch.randn_like(ref)
@@ -100,6 +116,7 @@ def test_order2_module_e2e(cfg, masked, seq_len):
     ref.backward(dout)
     assert_close(out, ref, 1e-4, "out")
     assert_close(xg.grad, xo.grad, 1e-4, "dx", grad=True)
+    _check_param_grads(m, params)
 
 
 @param("order", (2, 3, 4))
@@ -115,7 +132,7 @@ def test_npoly_module_e2e(order, kv_heads, causal):
     x = torch.randn(2, 40, 64)
     xg = x.to(d).requires_grad_()
     out = m(xg)
-    params = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    params = _grad_params(m)
     xo = x.clone().requires_grad_()
     ref = O.npoly_forward(params, cfg, xo)
     dout = torch.randn_like(ref)
@@ -123,6 +140,7 @@ def test_npoly_module_e2e(order, kv_heads, causal):
     ref.backward(dout)
     assert_close(out, ref, 1e-4, "out")
     assert_close(xg.grad, xo.grad, 1e-4, "dx", grad=True)
+    _check_param_grads(m, params)
 
 
 def test_contexts_and_context_masks_e2e():
