@@ -798,6 +798,25 @@ def layer_train(layer, x: Tensor) -> Tensor:
     return layer(x)
 
 
+def _concat_weights(layers) -> Tensor:
+    """torch.cat of the layers' weights.  Without autograd (inference, a captured decode or
+    ViT forward) the concatenation is cached on the first layer and rebuilt only when a
+    weight changes (storage, dtype or in-place version)."""
+    ws = [l.weight for l in layers]
+    if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
+        return torch.cat(ws)
+    if any(w.is_inference() for w in ws):
+        return torch.cat(ws)  # no version counter to key a cache on
+    key = tuple((w.data_ptr(), w._version, w.dtype, w.device, tuple(w.shape)) for w in ws)
+    cached = layers[0].__dict__.get("_pa_weight_cat")
+    if cached is not None and cached[0] == key and cached[2] == len(ws):
+        return cached[1]
+    with torch.no_grad():
+        w = torch.cat(ws)
+    layers[0].__dict__["_pa_weight_cat"] = (key, w, len(ws))
+    return w
+
+
 def project_heads(layers, xs, splits):
     """The modules' projections followed by their head splits
     (poly_attention.py:258-266, 322-340; n_poly_attention.py:103-110, 177-196):
@@ -819,7 +838,7 @@ def project_heads(layers, xs, splits):
             and all(_plain_linear(l) and l.bias is None for l in layers)
             and len({l.weight.dtype for l in layers}) == 1)
     if fuse:
-        w = torch.cat([l.weight for l in layers])
+        w = _concat_weights(layers)
         heads = tuple(h for p, h in splits for _ in range(p))
         pieces = _split_heads(linear_train(x, w), heads, d[0])
         out, i = [], 0

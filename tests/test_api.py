@@ -418,3 +418,35 @@ def test_weight_grad_split_choice():
     x = torch.randn(4, 8, 16, requires_grad=True)
     lin = torch.nn.Linear(16, 8)
     torch.testing.assert_close(_ops.layer_train(lin, x), lin(x))  # CPU: plain F.linear
+
+
+def test_project_heads_weight_cache_follows_weight_updates():
+    """Without autograd the concatenated projection weight is cached; an in-place update of a
+    weight (an optimizer step) or a new weight tensor invalidates it."""
+    from poly_attention import _ops
+
+    layers = [torch.nn.Linear(16, n, bias=False) for n in (8, 16)]
+    x = torch.randn(2, 3, 16)
+    splits = [(1, 2), (2, 2)]
+
+    def run():
+        with torch.no_grad():
+            return [t.clone() for g in _ops.project_heads(layers, [x, x], splits) for t in g]
+
+    def ref():
+        with torch.no_grad():
+            return [t for l, (p, h) in zip(layers, splits)
+                    for t in l(x).unflatten(-1, (p, h, 4)).permute(2, 0, 3, 1, 4).unbind(0)]
+
+    for a, b in zip(run(), ref()):
+        torch.testing.assert_close(a, b)
+    first = layers[0].__dict__["_pa_weight_cat"][1]
+    run()
+    assert layers[0].__dict__["_pa_weight_cat"][1] is first  # reused
+    with torch.no_grad():
+        layers[1].weight.mul_(2.0)  # in place: new version
+    for a, b in zip(run(), ref()):
+        torch.testing.assert_close(a, b)
+    layers[0].weight = torch.nn.Parameter(torch.randn(8, 16))  # new tensor
+    for a, b in zip(run(), ref()):
+        torch.testing.assert_close(a, b)
