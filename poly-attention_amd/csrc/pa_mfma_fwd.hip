@@ -460,10 +460,17 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
 constexpr int kFwdStages = 3;
 
 // chunk swizzles (16-byte chunk index within a row, as a function of the row)
+// K (read as 16-byte fragments, 32 rows per block): for d = 64 the chunk is XORed with a
+// permutation of row bits 1-3, which the counters measure as free of LDS bank conflicts (a
+// row + row/8 rotation cost about one conflict cycle per LDS read)
 template <int D>
 __device__ __forceinline__ int swz_k(int r) {
     r &= 31;
-    return D == 64 ? ((r + (r >> 3)) & 7) : (r & 15);
+    if (D == 64) {
+        const int v = (r >> 1) & 7;
+        return ((v & 1) << 2) | (v & 2) | ((v >> 2) & 1);
+    }
+    return r & 15;
 }
 template <int D>
 __device__ __forceinline__ int swz_v(int r) {
