@@ -285,7 +285,7 @@ def vit_bench(dev, steps, warmup, cpu):
     del m, img, graph, out, ref
     torch.cuda.empty_cache()
     if cpu:
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = cpu_threads()[0]
         torch.set_num_threads(threads)
         cb = 8
         mc, imgc = make_vit(torch.device("cpu"), torch.float32, cb)
@@ -515,7 +515,7 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2, eage
     del lm, scs, graph
     torch.cuda.empty_cache()
     if cpu:
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = cpu_threads()[0]
         torch.set_num_threads(threads)
         torch.manual_seed(0)
         lmc = _PolyLM(dim=dim, depth=depth, heads=heads, dim_head=dh).eval()
@@ -547,10 +547,45 @@ def _lib():
 # CPU baseline: the oracle (the reference's eager math) on this host's cores
 
 
+def cpu_threads():
+    """Threads for the CPU baseline: the CPUs this process may run on, capped by
+    OMP_NUM_THREADS when set.  A GPU box of this pool gives each GPU a share of the host (16
+    CPUs, with OMP_NUM_THREADS=16 exported) while os.cpu_count() reports the whole host; more
+    threads than the share only oversubscribe it.  Returns (threads, os.cpu_count(), usable)."""
+    total = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = total
+    threads = usable
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    return max(1, threads), total, usable
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    names = []
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        names += [ln.split(":", 1)[1].strip() for ln in out.splitlines()
+                  if ln.startswith("Model name")]
+    except Exception:  # noqa: BLE001
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            names += [ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")][:1]
+    except OSError:
+        pass
+    names = [n for n in names if n]
+    return max(names, key=len) if names else (platform.processor() or "unknown")
+
+
 def cpu_baseline(max_seconds=20.0):
     import oracle.poly_oracle as O
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads, total, usable = cpu_threads()
     torch.set_num_threads(threads)
     hs = 2
     g = torch.Generator().manual_seed(4)
@@ -574,18 +609,16 @@ def cpu_baseline(max_seconds=20.0):
     med = times[len(times) // 2]
     fwd, bwd = step_flops()
     flops_sample = (fwd + bwd) / (B * H) * hs
-    cpu_name = platform.processor() or ""
-    try:
-        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        for line in out.splitlines():
-            if line.startswith("Model name"):
-                cpu_name = line.split(":", 1)[1].strip()
-    except Exception:  # noqa: BLE001
-        pass
+    cpu_name = cpu_model()
     return {
         "value": round(flops_sample / med / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": threads,
+        "host_cpus": total,
+        "usable_cpus": usable,
+        "cpu_model": cpu_name,
+        "threads_reason": "torch threads = CPUs this process may use, capped by OMP_NUM_THREADS "
+                          "(the box's per-GPU CPU share)",
         "kind": "port",
         "sample": f"oracle reference_poly_attention fp32 causal fwd+bwd, B=1 heads={hs} N={N} d={DH} "
                   f"(1/{B * H // hs} of the step), median of {len(times)} after 1 warm-up, "

@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 3
+#define PA_ABI_VERSION 4
 #define PA_MAX_ORDER 8
 
 /* status codes (0 = success, negative = failure) */
@@ -174,7 +174,9 @@ typedef struct pa_prologue_item {
  * n_poly_attention.py:206-207 and poly_attention.py:282-286 for fixed-capacity caches.
  * The position is n_dev[0] - 1 when n_dev is given (the step's position count, the same
  * device counter pa_decode.n_dev reads), else `pos`; rows whose position falls outside
- * [0, capacity) are not written to the cache.  All items share src's dtype. */
+ * [0, capacity) are not written to the cache, and then, when `overflow` is given, the kernel
+ * sets overflow[0] = 1 (a full fixed-capacity cache; the caller reads the flag after its
+ * loop).  All items share src's dtype. */
 typedef struct pa_prologue {
     int32_t        batch, dim, count, capacity;
     float          eps;         /* RMSNorm epsilon */
@@ -183,6 +185,8 @@ typedef struct pa_prologue {
     int32_t        rot_dim;     /* even, <= dim */
     int32_t        pos;         /* cache position when n_dev is NULL */
     const int32_t* n_dev;       /* device: the step's n (positions after the append), or NULL */
+    int32_t*       overflow;    /* device int32 [1] set to 1 when the position is outside
+                                 * [0, capacity), or NULL */
     pa_prologue_item items[2 * PA_MAX_ORDER];
 } pa_prologue;
 

@@ -715,6 +715,7 @@ struct ProDev {
     const void* angles;
     int32_t adt;
     const int32_t* n_dev;
+    int32_t* overflow;
     ProItemDev it[2 * PA_MAX_ORDER];
 };
 
@@ -765,7 +766,9 @@ __global__ __launch_bounds__(kProThreads) void k_dec_prologue(ProDev P) {
         }
     }
     const int64_t pos = P.n_dev ? (int64_t)*P.n_dev - 1 : (int64_t)P.pos;
-    const bool to_cache = I.cache.ok() && pos >= 0 && pos < P.capacity;
+    const bool in_range = pos >= 0 && pos < P.capacity;
+    const bool to_cache = I.cache.ok() && in_range;
+    if (!in_range && P.overflow && row == 0 && lane == 0) *P.overflow = 1;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int d = lane + 64 * e;
@@ -797,6 +800,7 @@ int launch_prologue(const pa_prologue* p, hipStream_t s) {
     P.angles = p->angles;
     P.adt = p->angles_dtype;
     P.n_dev = p->n_dev;
+    P.overflow = p->overflow;
     int rows = 0;
     for (int k = 0; k < p->count; ++k) {
         const pa_prologue_item& it = p->items[k];

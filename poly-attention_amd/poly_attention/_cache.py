@@ -87,6 +87,20 @@ def adopt(t: Tensor, dim: int, dtype=None) -> Tensor:
     return append(None, t if dtype is None else t.to(dtype), dim)
 
 
+def _set_host_count(counter: Tensor, n: int) -> None:
+    counter._pa_host_n = int(n)
+
+
+def _advance_host_count(counter: Tensor) -> None:
+    """Mirror a device count's advance on the host; a captured advance runs again at every
+    replay without the host seeing it, so capture ends the mirror."""
+    n = getattr(counter, "_pa_host_n", None)
+    if n is None:
+        return
+    capturing = counter.is_cuda and torch.cuda.is_current_stream_capturing()
+    counter._pa_host_n = None if capturing else n + 1
+
+
 class StaticCache:
     """A fixed-capacity poly KV cache whose position count lives on the device.
 
@@ -100,8 +114,12 @@ class StaticCache:
     and addresses, so a whole decode step can be captured once into a HIP graph
     (``torch.cuda.CUDAGraph``) and replayed per token.
 
-    A step at full capacity writes nothing to the cache and attends over the first
-    ``capacity`` positions only (the kernels clamp the count); size it for prompt + steps.
+    A step past the capacity is refused with an error when the position count is known on
+    the host (eager steps).  Inside captured graphs the count lives only on the device: such a
+    step stays inside the buffers (the kernels clamp the count to the capacity, so its token
+    is not appended and the last position's msg / lse are rewritten) and sets a device flag,
+    which ``check_overflow()`` reads after the loop; the cache is not valid after it.  Size
+    the cache for prompt + steps.
 
     ``counter``: an int32 device tensor [1] shared by the caches of one model's layers (all
     holding the same positions), which the caller advances once per decode step, after
@@ -141,24 +159,42 @@ class StaticCache:
             self.n_step = counter
         else:
             self.n_step = torch.full((1,), n + 1, dtype=torch.int32, device=dev)
+            _set_host_count(self.n_step, n + 1)
+        # set to 1 by the prologue kernel when a step's position is past the capacity
+        self.overflow = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def host_step(self):
+        """The next step's n as the host knows it, or None once graph replays (or a counter
+        not made by ``make_counter``) advance it on the device only."""
+        return getattr(self.n_step, "_pa_host_n", None)
+
+    def check_overflow(self) -> None:
+        """Raise if a step ran past the capacity (reads the device flag: synchronises)."""
+        if int(self.overflow.item()):
+            raise RuntimeError(f"StaticCache overflow: a step ran past the capacity "
+                               f"{self.capacity}; its token was not cached")
 
     @staticmethod
     def make_counter(cache, device=None) -> Tensor:
         """A shared step counter for caches holding the positions of ``cache`` (a module's
         cache tuple): the next step's n."""
         q = cache[0] if isinstance(cache[0], Tensor) else cache[0][0]
-        return torch.full((1,), q.shape[2] + 1, dtype=torch.int32, device=device or q.device)
+        c = torch.full((1,), q.shape[2] + 1, dtype=torch.int32, device=device or q.device)
+        _set_host_count(c, q.shape[2] + 1)
+        return c
 
     @staticmethod
     def advance_counter(counter: Tensor) -> None:
         """Count the token every layer of a step has just written (shared counter)."""
         counter.add_(1)
+        _advance_host_count(counter)
 
     def advance(self) -> None:
         """Count the token a step has just written (stream-ordered, capturable); with a
         shared counter the caller advances it once per step instead."""
         if not self.shared:
             self.n_step.add_(1)
+            _advance_host_count(self.n_step)
 
     def seq_len(self) -> int:
         """Cached positions (reads the device count: synchronises)."""

@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolyattn.so"
 
-PA_ABI_VERSION = 3
+PA_ABI_VERSION = 4
 PA_MAX_ORDER = 8
 
 PA_OK = 0
@@ -158,6 +158,7 @@ class PaPrologue(ctypes.Structure):
         ("rot_dim", c_int32),
         ("pos", c_int32),
         ("n_dev", c_void_p),
+        ("overflow", c_void_p),
         ("items", PaPrologueItem * (2 * PA_MAX_ORDER)),
     ]
 

@@ -232,9 +232,11 @@ def pass_fwd_op(q: Tensor, k: Tensor, v: Tensor, vmul: Optional[Tensor], bias: O
 
 @pass_fwd_op.register_fake
 def _(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale, may_degenerate):
+    # the layouts pass_fwd_raw allocates (heads-inner output for heads-inner queries)
+    q = _inner_contig(q)
     B, _, nq, d = q.shape
     H = _pass_heads(q, k, v, vmul, bias)
-    return (q.new_empty(B, H, nq, d), q.new_empty(B, H, nq, dtype=torch.float32))
+    return (_empty_heads((B, H, nq, d), q), q.new_empty(B, H, nq, dtype=torch.float32))
 
 
 @torch.library.custom_op("polyattn::pass_bwd", mutates_args=(), device_types="cuda")
@@ -256,11 +258,16 @@ def pass_bwd_op(dout: Tensor, dlse: Optional[Tensor], q: Tensor, k: Tensor, v: T
 @pass_bwd_op.register_fake
 def _(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal, softclamp, scale,
       may_degenerate):
+    # the layouts pass_bwd_raw allocates
+    q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
     H = out.shape[1]
-    dq = q.new_empty(q.shape[0], H, *q.shape[2:]) if q.shape[1] != H else q.new_empty(q.shape)
-    dvmul = vmul.new_empty(vmul.shape) if vmul is not None else q.new_empty(0)
+    if q.shape[1] != H:
+        dq = q.new_empty(q.shape[0], H, *q.shape[2:])
+    else:
+        dq = _empty_heads(q.shape, q)
+    dvmul = _empty_heads(vmul.shape, vmul, v.dtype) if vmul is not None else q.new_empty(0)
     dbias = bias.new_empty(bias.shape) if bias is not None else q.new_empty(0)
-    return dq, k.new_empty(k.shape), v.new_empty(v.shape), dvmul, dbias
+    return dq, _empty_heads(k.shape, k), _empty_heads(v.shape, v), dvmul, dbias
 
 
 def _pass_setup(ctx, inputs, output):
@@ -401,7 +408,7 @@ def _rms_fwd_raw(x: Tensor, weight: Optional[Tensor], eps: float,
 
 @rms_norm_op.register_fake
 def _(x, weight, eps, angles=None):
-    return x.new_empty(x.shape), x.new_empty(x.shape[:3], dtype=torch.float32)
+    return _empty_heads(x.shape, x), x.new_empty(x.shape[:3], dtype=torch.float32)
 
 
 @torch.library.custom_op("polyattn::rms_norm_bwd", mutates_args=(), device_types="cuda")
@@ -438,8 +445,8 @@ def _rms_bwd_raw(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tensor, 
 
 @rms_norm_bwd_op.register_fake
 def _(dy, x, weight, rstd, eps, angles=None):
-    return x.new_empty(x.shape), (weight.new_empty(weight.shape) if weight is not None
-                                  else x.new_empty(0))
+    return _empty_heads(x.shape, x), (weight.new_empty(weight.shape) if weight is not None
+                                      else x.new_empty(0))
 
 
 def _rms_setup(ctx, inputs, output):
@@ -799,22 +806,12 @@ def layer_train(layer, x: Tensor) -> Tensor:
 
 
 def _concat_weights(layers) -> Tensor:
-    """torch.cat of the layers' weights.  Without autograd (inference, a captured decode or
-    ViT forward) the concatenation is cached on the first layer and rebuilt only when a
-    weight changes (storage, dtype or in-place version)."""
-    ws = [l.weight for l in layers]
-    if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
-        return torch.cat(ws)
-    if any(w.is_inference() for w in ws):
-        return torch.cat(ws)  # no version counter to key a cache on
-    key = tuple((w.data_ptr(), w._version, w.dtype, w.device, tuple(w.shape)) for w in ws)
-    cached = layers[0].__dict__.get("_pa_weight_cat")
-    if cached is not None and cached[0] == key and cached[2] == len(ws):
-        return cached[1]
-    with torch.no_grad():
-        w = torch.cat(ws)
-    layers[0].__dict__["_pa_weight_cat"] = (key, w, len(ws))
-    return w
+    """torch.cat of the layers' weights, built on every call: a cached copy would miss
+    in-place updates that bypass the version counter (``weight.data.copy_``), and a copy
+    made under inference mode cannot be saved for a later backward.  Inside a captured HIP
+    graph the concatenation is one of the captured kernels, so replays see the current
+    weights."""
+    return torch.cat([l.weight for l in layers])
 
 
 def project_heads(layers, xs, splits):
@@ -855,8 +852,8 @@ def project_heads(layers, xs, splits):
 
 
 def _split_heads(t: Tensor, heads, d: int):
-    if not (torch.is_grad_enabled() and t.requires_grad):
-        # no gradient: plain views, without the autograd node (less host time per call)
+    if not (torch.is_grad_enabled() and t.requires_grad) or torch.compiler.is_compiling():
+        # no gradient (or traced): plain views, without the gradient-slot autograd node
         outs, off = [], 0
         for h in heads:
             outs.append(t[..., off:off + h * d].unflatten(-1, (h, d)).transpose(1, 2))
@@ -874,17 +871,53 @@ def _split_heads(t: Tensor, heads, d: int):
 # the order-n chain
 
 
+def order2_forward(q1, q2, q3, v3, key_mask, causal, softclamp, scale):
+    """The two forward passes of the order-2 chain (poly_attention.py:48-116 with q2 as both
+    the pass-1 queries and the pass-2 keys); ``key_mask`` masks the keys of both passes.
+    Returns (out, lse, lse23, msg)."""
+    degenerate = key_mask is not None
+    msg, lse23 = pass_fwd_raw(q2, q3, v3, None, None, key_mask, None, causal, softclamp, scale,
+                              degenerate)
+    out, lse = pass_fwd_raw(q1, q2, msg, None, lse23, key_mask, None, causal, softclamp, scale,
+                            degenerate)
+    return out, lse, lse23, msg
+
+
+def order2_backward(saved, key_mask, cfg, slots, dout, dlse=None, dlse23_ext=None,
+                    dmsg_ext=None):
+    """The two pass backwards of ``order2_forward``, back to back: pass 2's key gradient of
+    q2 is the buffer that pass 1's query gradient of q2 is accumulated into (no separate
+    add).  ``saved`` = (q1, q2, q3, v3, msg, lse23, out, lse); ``slots`` the head-split
+    gradient slots of q1..v3 (or Nones).  Returns (dq1, dq2, dq3, dv3)."""
+    q1, q2, q3, v3, msg, lse23, out, lse = saved
+    causal, softclamp, scale = cfg
+    degenerate = key_mask is not None
+    if dout is None:
+        dout = torch.zeros_like(out)
+    # inputs that are pieces of a head-split projection get their gradients written into
+    # its gradient buffer
+    dq1_out, dq2_out, dq3_out, dv3_out = (claim_slot(r, t) for r, t in
+                                          zip(slots, (q1, q2, q3, v3)))
+    dq1, dq2, dmsg, _, dlse23 = pass_bwd_raw(dout, dlse, q1, q2, msg, None, lse23, key_mask,
+                                             None, out, lse, causal, softclamp, scale,
+                                             degenerate, dq_out=dq1_out, dk_out=dq2_out)
+    if dmsg_ext is not None:
+        dmsg = dmsg + dmsg_ext
+    if dlse23_ext is not None:
+        dlse23 = dlse23 + dlse23_ext
+    _, dq3, dv3, _, _ = pass_bwd_raw(dmsg, dlse23, q2, q3, v3, None, None, key_mask, None, msg,
+                                     lse23, causal, softclamp, scale, degenerate, dq_into=dq2,
+                                     dk_out=dq3_out, dv_out=dv3_out)
+    return dq1, dq2, dq3, dv3
+
+
 class _Order2Chain(torch.autograd.Function):
-    """The order-2 chain (poly_attention.py:48-116) as one autograd node whose backward runs
-    the two pass backwards back to back: pass 2's key gradient of q2 becomes the buffer that
-    pass 1's query gradient of q2 is accumulated into (no separate add)."""
+    """The order-2 chain (poly_attention.py:48-116) as one autograd node
+    (``order2_forward`` / ``order2_backward``)."""
 
     @staticmethod
     def forward(ctx, q1, q2, q3, v3, causal, softclamp, scale):
-        msg, lse23 = pass_fwd_raw(q2, q3, v3, None, None, None, None, causal, softclamp, scale,
-                                  False)
-        out, lse = pass_fwd_raw(q1, q2, msg, None, lse23, None, None, causal, softclamp, scale,
-                                False)
+        out, lse, lse23, msg = order2_forward(q1, q2, q3, v3, None, causal, softclamp, scale)
         ctx.save_for_backward(q1, q2, q3, v3, msg, lse23, out, lse)
         ctx.cfg = (causal, softclamp, scale)
         ctx.slots = [slot_ref(t) for t in (q1, q2, q3, v3)]
@@ -893,25 +926,9 @@ class _Order2Chain(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, dlse, dlse23_ext, dmsg_ext):
-        q1, q2, q3, v3, msg, lse23, out, lse = ctx.saved_tensors
-        causal, softclamp, scale = ctx.cfg
-        if dout is None:
-            dout = torch.zeros_like(out)
-        # inputs that are pieces of a head-split projection get their gradients written into
-        # its gradient buffer
-        dq1_out, dq2_out, dq3_out, dv3_out = (claim_slot(r, t) for r, t in
-                                              zip(ctx.slots, (q1, q2, q3, v3)))
-        dq1, dq2, dmsg, _, dlse23 = pass_bwd_raw(dout, dlse, q1, q2, msg, None, lse23, None,
-                                                 None, out, lse, causal, softclamp, scale,
-                                                 False, dq_out=dq1_out, dk_out=dq2_out)
-        if dmsg_ext is not None:
-            dmsg = dmsg + dmsg_ext
-        if dlse23_ext is not None:
-            dlse23 = dlse23 + dlse23_ext
-        _, dq3, dv3, _, _ = pass_bwd_raw(dmsg, dlse23, q2, q3, v3, None, None, None, None, msg,
-                                         lse23, causal, softclamp, scale, False, dq_into=dq2,
-                                         dk_out=dq3_out, dv_out=dv3_out)
-        return dq1, dq2, dq3, dv3, None, None, None
+        grads = order2_backward(ctx.saved_tensors, None, ctx.cfg, ctx.slots, dout, dlse,
+                                dlse23_ext, dmsg_ext)
+        return (*grads, None, None, None)
 
 
 def _chain_fusable(q_left, q_right, vs, query_mask, key_masks, may_degenerate) -> bool:
@@ -1051,7 +1068,7 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
 
 
 def decode_prologue(items, *, eps: float, angles: Optional[Tensor], n_dev: Tensor,
-                    capacity: int) -> None:
+                    capacity: int, overflow: Optional[Tensor] = None) -> None:
     """The q norms, rotary embedding and cache appends of one decode step, one launch
     (pa_decode_prologue).  ``items``: (src [B, h, 1, d], norm weight or None, rotate,
     out [B, h, 1, d] or None, cache [B, h, capacity, d] or None) per tensor; ``angles`` is
@@ -1073,6 +1090,9 @@ def decode_prologue(items, *, eps: float, angles: Optional[Tensor], n_dev: Tenso
         P.angles, P.angles_dtype, P.rot_dim = a.data_ptr(), DTYPE_CODE[a.dtype], a.numel()
     assert n_dev.dtype == torch.int32 and n_dev.is_cuda and n_dev.numel() == 1
     P.n_dev = n_dev.data_ptr()
+    if overflow is not None:
+        assert overflow.dtype == torch.int32 and overflow.is_cuda and overflow.numel() >= 1
+        P.overflow = overflow.data_ptr()
     for k, (src, w, rotate, out, cache) in enumerate(items):
         it = P.items[k]
         it.src = _view(src)

@@ -379,9 +379,10 @@ class NPolyAttention(Module):
 
         needs_grad = torch.is_grad_enabled() and any(
             t.requires_grad for t in (q1, *qs_rest, *vs, *c_qs, *c_vs, *c_lses, *c_msgs))
-        if needs_grad:
+        masked = exists(mask) or any(exists(m) for m in context_mask)
+        if needs_grad or masked:
             return self._fused_step_autograd(q_left, q_right, vs_cache, c_lses, c_msgs, rep,
-                                             qs_cache)
+                                             qs_cache, mask, context_mask)
 
         lses_full = [_cache.reserve(l, l[:, :, :1], -1) for l in c_lses]
         msgs_full = [_cache.reserve(m, m[:, :, :1], -2) for m in c_msgs]
@@ -390,8 +391,12 @@ class NPolyAttention(Module):
                                     softclamp=self.softclamp_value, scale=self.scale)
         return out, (tuple(qs_cache), tuple(vs_cache), tuple(lses_full), tuple(msgs_full))
 
-    def _fused_step_autograd(self, q_left, q_right, vs_cache, c_lses, c_msgs, rep, qs_cache):
-        """A differentiable cached step: the reference's level loop with HIP passes."""
+    def _fused_step_autograd(self, q_left, q_right, vs_cache, c_lses, c_msgs, rep, qs_cache,
+                             mask=None, context_mask=None):
+        """A differentiable (or masked) cached step: the reference's level loop with HIP
+        passes.  Level l's context mask masks the keys of its whole cache, ``mask`` the new
+        query of the final level (n_poly_attention.py:253-259)."""
+        context_mask = list(context_mask) if context_mask is not None else [None] * self.order
         from . import _ops
 
         order = self.order
@@ -413,8 +418,10 @@ class NPolyAttention(Module):
                 k = repeat_kv(k, rep)
                 if q.shape[1] != H:
                     q = repeat_kv(q, rep)
-            o, lse = _ops.attn_pass(q, k, v, vmul, bias, softclamp=self.softclamp_value,
-                                    scale=self.scale, may_degenerate=True)
+            o, lse = _ops.attn_pass(q, k, v, vmul, bias, key_mask=context_mask[lvl],
+                                    query_mask=mask if lvl == 0 else None,
+                                    softclamp=self.softclamp_value, scale=self.scale,
+                                    may_degenerate=True)
             if lvl > 0:
                 o_h = repeat_kv(o, H // o.shape[1])
                 l_h = repeat_kv(lse[:, :, :, None], H // lse.shape[1])[..., 0]

@@ -97,6 +97,10 @@ def _static_decode_step(module, qs, vs, mask, context_mask, rotary_pos_emb,
         raise RuntimeError("StaticCache decode is inference-only: run it under torch.no_grad()")
     if len(cache.qs) != order or len(cache.vs) != order - 1:
         raise ValueError(f"StaticCache of order {len(cache.qs)} passed to an order-{order} module")
+    n_host = cache.host_step()
+    if n_host is not None and n_host > cache.capacity:
+        raise RuntimeError(f"StaticCache is full: a step needs position {n_host - 1}, the "
+                           f"capacity is {cache.capacity}")
     dt = cache.qs[0].dtype
     if any(t.dtype != dt for t in (*qs, *vs)):
         raise TypeError("StaticCache: the projections and the cache must share one dtype")
@@ -121,7 +125,7 @@ def _static_decode_step(module, qs, vs, mask, context_mask, rotary_pos_emb,
                       cache.qs[i - 1] if i >= 1 else None))
     items += [(v, None, False, None, buf) for v, buf in zip(vs, cache.vs)]
     _ops.decode_prologue(items, eps=eps, angles=angles, n_dev=cache.n_step,
-                         capacity=cache.capacity)
+                         capacity=cache.capacity, overflow=cache.overflow)
     out = _ops.poly_decode_step(q_left, cache.qs, cache.vs, cache.msgs, cache.lses,
                                 kv_heads=module.kv_heads, heads=module.heads,
                                 softclamp=module.softclamp_value, scale=module.scale,
@@ -487,15 +491,20 @@ class Order2PolyAttention(Module):
 
         needs_grad = torch.is_grad_enabled() and any(
             t.requires_grad for t in (q1, q2, q3, v3, cq2, cq3, cv3, clse23, cmsg))
-        if needs_grad:
-            # differentiable step: the two passes as autograd ops (the reference's math)
-            msg_step, lse_step = _ops.attn_pass(q2_left, q3_full, v3_cache,
+        key_mask1, key_mask2 = context_mask
+        masked = exists(mask) or exists(key_mask1) or exists(key_mask2)
+        if needs_grad or masked:
+            # differentiable or masked step: the two passes as pass ops (the reference's math:
+            # the context masks mask the keys of the whole cache, `mask` the new query of
+            # pass 2; poly_attention.py:75-76,101-105)
+            msg_step, lse_step = _ops.attn_pass(q2_left, q3_full, v3_cache, key_mask=key_mask2,
                                                 softclamp=self.softclamp_value,
-                                                scale=self.scale)
+                                                scale=self.scale, may_degenerate=masked)
             lse_step_h = repeat_kv(lse_step[:, :, :, None], rep)[..., 0]
             lse23_full = torch.cat((clse23, lse_step_h.to(clse23.dtype)), dim=-1)
             msg_full = torch.cat((cmsg, repeat_kv(msg_step, rep).to(cmsg.dtype)), dim=-2)
             out, _ = _ops.attn_pass(q1r, repeat_kv(q2_right, rep), msg_full, bias=lse23_full,
+                                    key_mask=key_mask1, query_mask=mask,
                                     softclamp=self.softclamp_value, scale=self.scale,
                                     may_degenerate=True)
             return out, (q2_cache, q3_cache, v3_cache, lse23_full, msg_full)

@@ -420,33 +420,71 @@ def test_weight_grad_split_choice():
     torch.testing.assert_close(_ops.layer_train(lin, x), lin(x))  # CPU: plain F.linear
 
 
-def test_project_heads_weight_cache_follows_weight_updates():
-    """Without autograd the concatenated projection weight is cached; an in-place update of a
-    weight (an optimizer step) or a new weight tensor invalidates it."""
+def test_project_heads_follows_weight_updates():
+    """The fused projection concatenates the current weights on every call: updates through
+    ``.data`` (which do not bump the version counter), in-place optimizer steps, new weight
+    tensors and an inference-mode warm-up followed by a forward with gradients all see the
+    weights as they are."""
     from poly_attention import _ops
 
     layers = [torch.nn.Linear(16, n, bias=False) for n in (8, 16)]
     x = torch.randn(2, 3, 16)
     splits = [(1, 2), (2, 2)]
 
-    def run():
-        with torch.no_grad():
-            return [t.clone() for g in _ops.project_heads(layers, [x, x], splits) for t in g]
+    def run(grad=False):
+        with torch.set_grad_enabled(grad):
+            return [t for g in _ops.project_heads(layers, [x, x], splits) for t in g]
 
     def ref():
         with torch.no_grad():
             return [t for l, (p, h) in zip(layers, splits)
                     for t in l(x).unflatten(-1, (p, h, 4)).permute(2, 0, 3, 1, 4).unbind(0)]
 
-    for a, b in zip(run(), ref()):
-        torch.testing.assert_close(a, b)
-    first = layers[0].__dict__["_pa_weight_cat"][1]
-    run()
-    assert layers[0].__dict__["_pa_weight_cat"][1] is first  # reused
+    def check(grad=False):
+        for a, b in zip(run(grad), ref()):
+            torch.testing.assert_close(a.detach(), b)
+
+    check()
+    layers[1].weight.data.copy_(torch.randn(16, 16))  # no version bump
+    check()
     with torch.no_grad():
-        layers[1].weight.mul_(2.0)  # in place: new version
-    for a, b in zip(run(), ref()):
-        torch.testing.assert_close(a, b)
-    layers[0].weight = torch.nn.Parameter(torch.randn(8, 16))  # new tensor
-    for a, b in zip(run(), ref()):
-        torch.testing.assert_close(a, b)
+        layers[1].weight.mul_(2.0)
+    check()
+    layers[0].weight = torch.nn.Parameter(torch.randn(8, 16))
+    check()
+    with torch.inference_mode():
+        run()
+    outs = run(grad=True)
+    sum(o.sum() for o in outs).backward()
+    assert all(l.weight.grad is not None for l in layers)
+    check()
+
+
+def test_poly_flash_attention_is_an_autograd_function():
+    """PolyFlashAttention subclasses torch.autograd.Function, as the reference's does
+    (flash_poly_attention.py:319), with apply(q1, q2, q3, v3, mask, softclamp_value,
+    is_causal)."""
+    import inspect
+
+    from poly_attention.flash_poly_attention import PolyFlashAttention
+
+    assert issubclass(PolyFlashAttention, torch.autograd.Function)
+    params = list(inspect.signature(PolyFlashAttention.forward).parameters)
+    assert params == ["ctx", "q1", "q2", "q3", "v3", "mask", "softclamp_value", "is_causal"]
+
+
+def test_static_cache_host_count_mirror():
+    """The StaticCache's host mirror of the device count: set by construction and
+    make_counter, advanced with the count outside capture."""
+    from poly_attention import StaticCache
+    from poly_attention._cache import _advance_host_count, _set_host_count
+
+    c = torch.zeros(1, dtype=torch.int32)
+    _set_host_count(c, 5)
+    _advance_host_count(c)
+    assert c._pa_host_n == 6
+    cache = (torch.zeros(1, 2, 3, 4),) * 3 + (torch.zeros(1, 2, 3), torch.zeros(1, 2, 3, 4))
+    counter = StaticCache.make_counter(cache)
+    assert counter._pa_host_n == 4 and int(counter) == 4
+    StaticCache.advance_counter(counter)
+    assert counter._pa_host_n == 5 and int(counter) == 5

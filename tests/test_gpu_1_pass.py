@@ -1,21 +1,18 @@
 """GPU parity of single attention passes (libpolyattn through its C ABI) vs the CPU oracle.
 
-Tolerances (the north star's): fp32 -- max-abs error <= 1e-4; bf16 / f16 -- max-abs error
-<= 2e-2 against the fp32 oracle evaluated on the same low-precision-rounded inputs.  Both are
-applied as max-abs error / max(1, max|reference|): outputs and gradients of order 1 are held
-to the absolute bound, larger ones (gradients grow with the sequence length, products of two
-N(0,1) values feed the middle levels) to the same bound relative to their magnitude.
+Bound (tests/parity.py): fp32 results max-abs <= 1e-4; bf16 / f16 results max-abs <= 2e-2
+against the fp32 oracle on the same low-precision-rounded inputs, plus one rounding of the
+result's storage type per element; the raw max-abs error of every check is printed.
 """
 
 import pytest
 import torch
 
 import oracle.poly_oracle as O
+from parity import TOL, assert_parity
 
 pytestmark = pytest.mark.gpu
 param = pytest.mark.parametrize
-
-TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
 
 
 def dev():
@@ -27,17 +24,6 @@ def dev():
 def randn(shape, dtype, seed, scale=1.0):
     g = torch.Generator().manual_seed(seed)
     return (torch.randn(shape, generator=g) * scale).to(dtype)
-
-
-def max_err(a, b):
-    return (a.float().cpu() - b.float().cpu()).abs().max().item()
-
-
-def assert_close(got, ref, tol, what):
-    ref = ref.float().cpu()
-    err = max_err(got, ref)
-    denom = max(1.0, ref.abs().max().item())
-    assert err / denom <= tol, f"{what}: max-abs err {err:.3e} (ref max {ref.abs().max():.3e})"
 
 
 def run_pass(q, k, v, vmul=None, bias=None, key_mask=None, query_mask=None, causal=False,
@@ -69,16 +55,17 @@ def run_pass(q, k, v, vmul=None, bias=None, key_mask=None, query_mask=None, caus
     return res
 
 
-def check(res, dtype):
-    tol = TOL[dtype]
+def check(res, dtype, what=""):
     for name, (got, ref) in res.items():
-        if name == "lse":
+        if name == "lse":  # fp32 in both, from inputs rounded to dtype
             got = got.float().cpu()
-            ok = ref > -1e30
-            assert_close(got[ok], ref[ok], max(tol, 1e-4), name)
+            ok = ref.detach() > -1e30
+            assert_parity(got[ok], ref.detach()[ok], torch.float32, f"{what} lse", tol=TOL[dtype])
             assert bool((got[~ok] <= -1e30).all()), "fully-masked rows must keep lse = -finfo.max"
             continue
-        assert_close(got, ref, tol, name)
+        # dbias is fp32 (the deeper level's lse gradient); everything else is in dtype
+        rdt = torch.float32 if name == "dbias" else dtype
+        assert_parity(got, ref, rdt, f"{what} {name}", tol=TOL[dtype])
 
 
 @param("dtype", (torch.float32, torch.bfloat16, torch.float16))
@@ -89,14 +76,15 @@ def test_pass_basic(dtype, n, causal, softclamp):
     """The reference's fused-op test grid (tests:213-240): N in {31,32,127,128}, d = 64."""
     shape = (2, 4, n, 64)
     q, k, v = (randn(shape, dtype, s) for s in (1, 2, 3))
-    check(run_pass(q, k, v, causal=causal, softclamp=softclamp), dtype)
+    check(run_pass(q, k, v, causal=causal, softclamp=softclamp), dtype,
+          f"basic {dtype} n={n} causal={causal} sc={softclamp}")
 
 
 @param("dtype", (torch.float32, torch.bfloat16))
 @param("d", (16, 32, 128))
 def test_pass_head_dims(dtype, d):
     q, k, v = (randn((1, 2, 40, d), dtype, s) for s in (4, 5, 6))
-    check(run_pass(q, k, v, causal=True), dtype)
+    check(run_pass(q, k, v, causal=True), dtype, f"head dim {d} {dtype}")
 
 
 @param("dtype", (torch.float32, torch.bfloat16))
@@ -107,7 +95,8 @@ def test_pass_gqa_bias_vmul(dtype, causal):
     q = randn((2, 8, 50, 64), dtype, 7)
     k, v, vmul = (randn((2, 2, 50, 64), dtype, s) for s in (8, 9, 10))
     bias = randn((2, 2, 50), torch.float32, 11, scale=2.0)
-    check(run_pass(q, k, v, vmul=vmul, bias=bias, causal=causal), dtype)
+    check(run_pass(q, k, v, vmul=vmul, bias=bias, causal=causal), dtype,
+          f"gqa+bias+vmul {dtype} causal={causal}")
 
 
 @param("dtype", (torch.float32, torch.bfloat16))
@@ -122,7 +111,8 @@ def test_pass_masks_and_degenerate_rows(dtype, causal):
     qm[0, 20:] = False
     bias = randn((2, 2, 24), torch.float32, 15)
     bias[1, 1, 5] = -torch.finfo(torch.float32).max
-    check(run_pass(q, k, v, bias=bias, key_mask=km, query_mask=qm, causal=causal), dtype)
+    check(run_pass(q, k, v, bias=bias, key_mask=km, query_mask=qm, causal=causal), dtype,
+          f"masks {dtype} causal={causal}")
 
 
 @param("dtype", (torch.float32, torch.bfloat16))
@@ -130,8 +120,8 @@ def test_pass_cross_lengths(dtype):
     """Different query and key lengths (contexts), causal with a top-left aligned mask."""
     q = randn((2, 4, 20, 64), dtype, 16)
     k, v = (randn((2, 4, 33, 64), dtype, s) for s in (17, 18))
-    check(run_pass(q, k, v, causal=True), dtype)
-    check(run_pass(q, k, v, causal=False), dtype)
+    check(run_pass(q, k, v, causal=True), dtype, f"cross lengths {dtype} causal")
+    check(run_pass(q, k, v, causal=False), dtype, f"cross lengths {dtype}")
 
 
 @param("heads,n,d", ((8, 1024, 64), (3, 1000, 64), (8, 512, 128)))
@@ -143,5 +133,5 @@ def test_pass_multi_block_causal_grids(heads, n, d):
     q, k, v = (randn((1, heads, n, d), dtype, s) for s in (21, 22, 23))
     bias = torch.log(torch.arange(1, n + 1).float())[None, None].repeat(1, heads, 1)
     bias = bias + randn((1, heads, n), torch.float32, 24)
-    check(run_pass(q, k, v, causal=True), dtype)
-    check(run_pass(q, k, v, bias=bias, causal=True), dtype)
+    check(run_pass(q, k, v, causal=True), dtype, f"grid h={heads} n={n} d={d}")
+    check(run_pass(q, k, v, bias=bias, causal=True), dtype, f"grid h={heads} n={n} d={d} bias")

@@ -1,12 +1,15 @@
 """GPU: pa_linear_small (the projections of a decode step) against an fp32 restatement of
 torch.nn.functional.linear, and its use inside the modules and the decode harness.
 
-Tolerances: fp32 1e-5, f16 2e-3, bf16 2e-2, relative to max(1, max|reference|): the kernel
-accumulates in fp32 and rounds once, so it sits within one output rounding of the fp32 sum.
+Tolerances: max-abs fp32 1e-5, f16 2e-3, bf16 2e-2, each plus one rounding of the result's
+dtype per element (tests/parity.py): the kernel accumulates in fp32 and rounds once, so it
+sits within one output rounding of the fp32 sum.
 """
 
 import pytest
 import torch
+
+from parity import assert_parity
 
 pytestmark = pytest.mark.gpu
 param = pytest.mark.parametrize
@@ -21,10 +24,9 @@ def dev():
 
 
 def assert_close(got, ref, tol, what):
-    got, ref = got.float().cpu(), ref.float().cpu()
-    err = (got - ref).abs().max().item()
-    denom = max(1.0, ref.abs().max().item())
-    assert err / denom <= tol, f"{what}: max-abs err {err:.3e}"
+    """Max-abs error of the result (in its own dtype) within ``tol`` plus one rounding of that
+    dtype per element (tests/parity.py)."""
+    assert_parity(got, ref, got.dtype, what, tol=tol)
 
 
 def fp32_linear(x, w, b):
