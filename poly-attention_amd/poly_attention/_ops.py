@@ -364,17 +364,30 @@ def _rms_struct(x: Tensor, weight: Optional[Tensor], eps: float,
     return r
 
 
+def _aligned16(t: Tensor) -> Tensor:
+    """t itself when its data starts on a 16-byte boundary, else a copy in the same layout
+    (fresh storage is aligned)."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def rms_supported(x: Tensor, weight: Optional[Tensor], angles: Optional[Tensor] = None) -> bool:
-    """Shapes and layouts pa_rmsnorm takes: [B, H, N, d] with 16-byte aligned rows; rotary
-    angles (optional) as apply_rotary_emb takes them for such an x: [rot_dim] or
+    """Shapes and layouts pa_rmsnorm takes (on a CUDA tensor): ``rms_layout_supported``."""
+    return x.is_cuda and rms_layout_supported(x, weight, angles)
+
+
+def rms_layout_supported(x: Tensor, weight: Optional[Tensor],
+                         angles: Optional[Tensor] = None) -> bool:
+    """[B, H, N, d] with strides that keep rows 16-byte aligned (a misaligned base pointer is
+    copied by the call itself, so that traced code never reads a pointer); rotary angles
+    (optional) as apply_rotary_emb takes them for such an x: [rot_dim] or
     [positions >= N, rot_dim], rot_dim even and <= d, no gradient."""
-    if x.dim() != 4 or x.dtype not in DTYPE_CODE or not x.is_cuda:
+    if x.dim() != 4 or x.dtype not in DTYPE_CODE:
         return False
     e = 4 if x.dtype == torch.float32 else 8
     d = x.shape[-1]
     if d % e or d > 512 or x.stride(-1) != 1 or x.numel() == 0:
         return False
-    if x.data_ptr() % 16 or any(st % e for st in x.stride()[:3]):
+    if any(st % e for st in x.stride()[:3]):
         return False
     if angles is not None:
         if angles.dim() not in (1, 2) or angles.dtype not in DTYPE_CODE or angles.requires_grad:
@@ -399,7 +412,7 @@ def _rms_fwd_raw(x: Tensor, weight: Optional[Tensor], eps: float,
     lib = _lib.load()
     y = _empty_heads(x.shape, x)
     rstd = torch.empty(x.shape[:3], dtype=torch.float32, device=x.device)
-    r = _rms_struct(x, weight, eps, angles)
+    r = _rms_struct(_aligned16(x), weight, eps, angles)
     r.y, r.rstd = _view(y), rstd.data_ptr()
     with _device(x):
         _lib.check(lib.pa_rmsnorm_fwd(ctypes.byref(r), _stream(x)), "pa_rmsnorm_fwd")
@@ -421,13 +434,14 @@ def _rms_bwd_raw(dy: Tensor, x: Tensor, weight: Optional[Tensor], rstd: Tensor, 
                  angles: Optional[Tensor] = None,
                  dx_out: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
-    dy = dy if dy.stride(-1) == 1 and dy.data_ptr() % 16 == 0 else dy.contiguous()
-    if any(st % (4 if dy.dtype == torch.float32 else 8) for st in dy.stride()[:3]):
+    if dy.stride(-1) != 1 or any(st % (4 if dy.dtype == torch.float32 else 8)
+                                 for st in dy.stride()[:3]):
         dy = dy.contiguous()
+    dy = _aligned16(dy)
     dx = _empty_heads(x.shape, x) if dx_out is None else dx_out
-    if dx_out is not None and not rms_supported(dx_out, weight, angles):
+    if dx_out is not None and (not rms_supported(dx_out, weight, angles) or dx_out.data_ptr() % 16):
         dx = _empty_heads(x.shape, x)
-    r = _rms_struct(x, weight, eps, angles)
+    r = _rms_struct(_aligned16(x), weight, eps, angles)
     r.rstd = rstd.data_ptr()
     r.dy, r.dx = _view(dy), _view(dx)
     dw32 = None
@@ -518,9 +532,9 @@ def linear_supported(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -
 
 def _rows2d(t: Tensor, k: int, e: int) -> Tensor:
     t2 = t.reshape(-1, k)
-    if t2.stride(-1) != 1 or t2.data_ptr() % 16 or (t2.shape[0] > 1 and t2.stride(0) % e):
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) % e):
         t2 = t2.contiguous()
-    return t2
+    return _aligned16(t2)
 
 
 def linear_small_group(x: Tensor, specs, *, x_add: Optional[Tensor] = None,

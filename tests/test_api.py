@@ -488,3 +488,26 @@ def test_static_cache_host_count_mirror():
     assert counter._pa_host_n == 4 and int(counter) == 4
     StaticCache.advance_counter(counter)
     assert counter._pa_host_n == 5 and int(counter) == 5
+
+
+def test_norm_layout_check_traces_without_graph_breaks():
+    """The q/k-norm dispatch check reads no data pointer, so torch.compile traces through it
+    in one graph (a pointer read splits the module's graph, and the split graphs' aliased
+    outputs were what torch's compiled-autograd cache failed to serialise)."""
+    from poly_attention import _ops
+
+    torch._dynamo.reset()
+    w = torch.ones(64)
+
+    def f(x):
+        return x * 2 if _ops.rms_layout_supported(x, w) else x - 1
+
+    x = torch.randn(2, 3, 5, 64)
+    ex = torch._dynamo.explain(f)(x)
+    assert ex.graph_break_count == 0 and ex.graph_count == 1
+    # a misaligned base pointer is copied by the call itself, keeping the layout
+    base = torch.randn(2 * 3 * 5 * 64 + 1)
+    xm = base[1:].view(2, 3, 5, 64)
+    assert xm.data_ptr() % 16 != 0
+    xa = _ops._aligned16(xm)
+    assert xa.data_ptr() % 16 == 0 and torch.equal(xa, xm) and xa.stride() == xm.stride()

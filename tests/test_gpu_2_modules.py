@@ -46,7 +46,7 @@ def test_flash_poly_attention(dtype, causal, softclamp_value, seq_len):
     what = f"flash op {dtype} n={seq_len} causal={causal} sc={softclamp_value}"
     assert_parity(out, out_ref, dtype, f"{what} out")
     for i, (a, b) in enumerate(zip(g_t, o_t)):
-        assert_parity(a.grad, b.grad, dtype, f"{what} grad {i}")
+        assert_parity(a.grad, b.grad, dtype, f"{what} grad {i}", grad=True)
 
 
 def test_flash_poly_attention_context_mask_disallowed():  # reference tests:541-558

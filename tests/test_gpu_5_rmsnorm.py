@@ -73,8 +73,8 @@ def test_rmsnorm_backward_matches_fp32_reference(dtype, d):
     x = split_heads(base, H, d).detach().requires_grad_()
     wg = w.detach().requires_grad_()
     _ops.rms_norm(x, wg, None).backward(dy)
-    assert_parity(x.grad, xr.grad, dtype, f"rmsnorm dx d={d} {dtype}")
-    assert_parity(wg.grad, wr.grad, dtype, f"rmsnorm dw d={d} {dtype}")
+    assert_parity(x.grad, xr.grad, dtype, f"rmsnorm dx d={d} {dtype}", grad=True)
+    assert_parity(wg.grad, wr.grad, dtype, f"rmsnorm dw d={d} {dtype}", grad=True)
     assert wg.grad.dtype == dtype
 
 
@@ -135,8 +135,8 @@ def test_rmsnorm_rope_backward_matches_fp32_reference(dtype, rot):
     x = split_heads(base, H, d).detach().requires_grad_()
     wg = w.detach().requires_grad_()
     _ops.rms_norm(x, wg, None, ang).backward(dy)
-    assert_parity(x.grad, xr.grad, dtype, f"rmsnorm+rope dx rot={rot} {dtype}")
-    assert_parity(wg.grad, wr.grad, dtype, f"rmsnorm+rope dw rot={rot} {dtype}")
+    assert_parity(x.grad, xr.grad, dtype, f"rmsnorm+rope dx rot={rot} {dtype}", grad=True)
+    assert_parity(wg.grad, wr.grad, dtype, f"rmsnorm+rope dw rot={rot} {dtype}", grad=True)
 
 
 def test_rmsnorm_weight_grad_is_deterministic():

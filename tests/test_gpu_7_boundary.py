@@ -106,7 +106,7 @@ def test_flash_op_mask_masks_keys_of_both_passes(dtype, causal):
     what = f"flash op key mask {dtype} causal={causal}"
     assert_parity(out, ref, dtype, f"{what} out")
     for i, (a, b) in enumerate(zip(g, o)):
-        assert_parity(a.grad, b.grad, dtype, f"{what} grad {i}")
+        assert_parity(a.grad, b.grad, dtype, f"{what} grad {i}", grad=True)
 
 
 # ---------------------------------------------------------------------------------------
@@ -185,4 +185,4 @@ def test_compile_autocast_module_matches_oracle():
     ref = O.order2_forward(params, cfg, xo)
     ref.sum().backward()
     assert_parity(out, ref, torch.float16, "compile+autocast out")
-    assert_parity(xg.grad, xo.grad, torch.float16, "compile+autocast dx")
+    assert_parity(xg.grad, xo.grad, torch.float16, "compile+autocast dx", grad=True)
