@@ -14,6 +14,9 @@ Contents and what pins each function (see tests/test_oracle.py):
                              (path-sum closed forms), order-2 == reference_poly_attention
   order2_forward             poly_attention.py:206-365 (module forward, functional)
   npoly_forward              n_poly_attention.py:122-340 (module forward, functional)
+  polyvit_forward            poly_vit.py:19-101 (PolyViT forward, functional) -- the position
+                             table and the patch order pinned by closed forms / direct pixel
+                             indexing, the composition by the drop-in module on the CPU
   rotary_*                   rotary-embedding-torch's RoPE (absent here; parity unpinned for
                              the pair layout, pinned by rotation properties)
   brute_* / masked_pass_classes   independent float64 closed forms used as pins
@@ -375,6 +378,59 @@ def npoly_forward(p: dict, cfg: dict, x, context=None, mask=None, context_mask=N
     if not return_cache:
         return out
     return out, (qs_rest_cache, vs_cache, tuple(lses), tuple(msgs))
+
+
+# ---------------------------------------------------------------------------------------
+# PolyViT (poly_vit.py:13-101), functional
+
+
+def posemb_sincos_2d(h: int, w: int, dim: int, temperature: int = 10000) -> Tensor:
+    """poly_vit.py:19-30: frequencies 1 / T^(k / (dim/4 - 1)); per patch of a row-major h x w
+    grid the features [sin(col f), cos(col f), sin(row f), cos(row f)] in fp32."""
+    omega = torch.arange(dim // 4) / (dim // 4 - 1)
+    omega = 1.0 / (temperature ** omega)
+    y, x = torch.meshgrid(torch.arange(h), torch.arange(w), indexing="ij")
+    y = y.reshape(-1, 1) * omega
+    x = x.reshape(-1, 1) * omega
+    return torch.cat((x.sin(), x.cos(), y.sin(), y.cos()), dim=-1)
+
+
+def patchify(img: Tensor, ph: int, pw: int) -> Tensor:
+    """'b c (h p1) (w p2) -> b (h w) (p1 p2 c)' (poly_vit.py:76)."""
+    b, c, H, W = img.shape
+    t = img.reshape(b, c, H // ph, ph, W // pw, pw)
+    return t.permute(0, 2, 4, 3, 5, 1).reshape(b, (H // ph) * (W // pw), ph * pw * c)
+
+
+def _sub(p: dict, prefix: str) -> dict:
+    return {k[len(prefix):]: v for k, v in p.items() if k.startswith(prefix)}
+
+
+def polyvit_forward(p: dict, cfg: dict, img: Tensor) -> Tensor:
+    """PolyViT.forward (poly_vit.py:92-101) with the Transformer of :42-63; ``p`` the
+    module's state_dict, ``cfg`` its constructor arguments."""
+    ph, pw = (cfg["patch_size"],) * 2 if not isinstance(cfg["patch_size"], tuple) else cfg["patch_size"]
+    ih, iw = (cfg["image_size"],) * 2 if not isinstance(cfg["image_size"], tuple) else cfg["image_size"]
+    dim, order = cfg["dim"], cfg.get("order", 2)
+    x = patchify(img, ph, pw)
+    x = F.layer_norm(x, (x.shape[-1],), p["to_patch_embedding.1.weight"], p["to_patch_embedding.1.bias"])
+    x = F.linear(x, p["to_patch_embedding.2.weight"], p["to_patch_embedding.2.bias"])
+    x = F.layer_norm(x, (dim,), p["to_patch_embedding.3.weight"], p["to_patch_embedding.3.bias"])
+    x = x + posemb_sincos_2d(ih // ph, iw // pw, dim).to(x.device, dtype=x.dtype)
+    acfg = dict(heads=cfg["heads"], dim_head=cfg.get("dim_head", 64), causal=False, prenorm=True)
+    for i in range(cfg["depth"]):
+        pa = _sub(p, f"transformer.layers.{i}.0.")
+        if order == 2:
+            a = order2_forward(pa, acfg, x)
+        else:
+            a = npoly_forward(pa, dict(acfg, order=order), x)
+        x = a + x
+        pf = _sub(p, f"transformer.layers.{i}.1.")
+        h = F.layer_norm(x, (dim,), pf["0.weight"], pf["0.bias"])
+        h = F.gelu(F.linear(h, pf["1.weight"], pf["1.bias"]))
+        x = F.linear(h, pf["3.weight"], pf["3.bias"]) + x
+    x = F.layer_norm(x, (dim,), p["transformer.norm.weight"], p["transformer.norm.bias"])
+    return F.linear(x.mean(dim=1), p["linear_head.weight"])
 
 
 # ---------------------------------------------------------------------------------------

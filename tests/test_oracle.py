@@ -161,3 +161,57 @@ def test_rotary_properties():
     x[..., 1, 0] = 1.0
     y = O.apply_rotary(O.rotary_freqs(d, torch.arange(2)), x)
     torch.testing.assert_close(y[0, 0, 1, :2], torch.tensor([math.cos(1.0), math.sin(1.0)]))
+
+
+def test_polyvit_position_table_closed_form():
+    """The oracle's sincos table against its closed form evaluated in float64: patch
+    p = r*w + c of an h x w grid has [sin(c f_k), cos(c f_k), sin(r f_k), cos(r f_k)] with
+    f_k = 10000^(-k / (q - 1)), q = dim / 4 (so f_0 = 1, f_{q-1} = 1e-4); a swapped row / column
+    or sin / cos quarter fails."""
+    h, w, dim = 3, 5, 16
+    q = dim // 4
+    pe = O.posemb_sincos_2d(h, w, dim)
+    assert pe.shape == (h * w, dim) and pe.dtype == torch.float32
+    for r in range(h):
+        for c in range(w):
+            p = r * w + c
+            for k in range(q):
+                f = 10000.0 ** (-k / (q - 1))
+                want = (math.sin(c * f), math.cos(c * f), math.sin(r * f), math.cos(r * f))
+                got = [pe[p, j * q + k].item() for j in range(4)]
+                assert max(abs(a - b) for a, b in zip(got, want)) < 1e-6, (r, c, k)
+
+
+def test_polyvit_patch_order_by_pixel_indexing():
+    """The oracle's patch cut ('b c (h p1) (w p2) -> b (h w) (p1 p2 c)') checked pixel by
+    pixel: token r*gw + c, feature (i*pw + j)*C + ch holds img[b, ch, r*ph + i, c*pw + j]."""
+    g = torch.Generator().manual_seed(7)
+    b, C, ph, pw, gh, gw = 2, 3, 2, 4, 3, 2
+    img = torch.randn(b, C, gh * ph, gw * pw, generator=g)
+    tok = O.patchify(img, ph, pw)
+    assert tok.shape == (b, gh * gw, ph * pw * C)
+    for bi in range(b):
+        for r in range(gh):
+            for c in range(gw):
+                for i in range(ph):
+                    for j in range(pw):
+                        for ch in range(C):
+                            assert tok[bi, r * gw + c, (i * pw + j) * C + ch] == \
+                                img[bi, ch, r * ph + i, c * pw + j]
+
+
+@pytest.mark.parametrize("order", (2, 3))
+def test_polyvit_oracle_matches_module_on_cpu(order):
+    """The oracle's PolyViT forward against the drop-in module's CPU (eager) path in float64
+    on the same state dict."""
+    from poly_attention import PolyViT
+
+    cfg = dict(image_size=32, patch_size=8, num_classes=7, dim=64, depth=2, heads=4,
+               mlp_dim=96, dim_head=16, order=order)
+    torch.manual_seed(3)
+    m = PolyViT(use_flash_kernel=False, **cfg).double().eval()
+    img = torch.randn(2, 3, 32, 32, dtype=torch.float64)
+    with torch.no_grad():
+        want = m(img)
+        got = O.polyvit_forward(m.state_dict(), cfg, img)
+    torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10)
