@@ -557,10 +557,12 @@ __device__ __forceinline__ void dec_merge(const DecodeDev& D, const DecLevelDev&
             for (int q = 0; q < 4; ++q) {
                 wk[q] = __shfl(wl, k + q);
                 const float* rc = recs + (int64_t)(c0 + k + q) * D.rec + 2;
+                // a zero weight (an empty record: its vector part is never written) adds
+                // nothing and is not read, so stale contents cannot turn into 0 * NaN
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int d = lane + 64 * e;
-                    v[q][e] = d < dim ? rc[d] : 0.f;
+                    v[q][e] = (d < dim && wk[q] != 0.f) ? rc[d] : 0.f;
                 }
             }
 #pragma unroll
@@ -570,6 +572,7 @@ __device__ __forceinline__ void dec_merge(const DecodeDev& D, const DecLevelDev&
         }
         for (; k < cn; ++k) {
             const float wk = __shfl(wl, k);
+            if (wk == 0.f) continue;  // uniform across the wave
             const float* rc = recs + (int64_t)(c0 + k) * D.rec + 2;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
