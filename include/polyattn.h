@@ -57,6 +57,7 @@ extern "C" {
 #define PA_EUNSUPPORTED -2   /* valid request this build does not implement */
 #define PA_EHIP         -3   /* a HIP runtime call failed (pa_last_hip_error) */
 #define PA_EWORKSPACE   -4   /* workspace missing or too small */
+#define PA_ESCRATCH     -5   /* needs more than the library's static scratch (no-alloc calls) */
 
 /* element types */
 #define PA_F32  0
@@ -292,6 +293,20 @@ size_t pa_attn_pass_bwd_workspace(const pa_pass_grad* g);
 int    pa_attn_pass_bwd(const pa_pass_grad* g, void* stream);
 size_t pa_poly_decode_workspace(const pa_decode* d);
 int    pa_poly_decode(const pa_decode* d, void* stream);
+
+/* pa_poly_decode without a caller workspace.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  The split-K partial records go to a device array
+ * of the library instead of d->workspace (ignored, as workspace_bytes): PA_DECODE_SCRATCH_BYTES
+ * per GPU, each GPU holding its own copy until the process ends.  A request whose
+ * pa_poly_decode_workspace exceeds it returns PA_ESCRATCH without launching.  The call makes
+ * no hipMalloc / hipFree or other allocating call; its first call on a device looks the
+ * array's device address up once (hipGetSymbolAddress, with that device current).  Every
+ * call on one GPU shares that GPU's array and it keeps the last call's contents: each call
+ * writes every record it reads before reading it, so nothing has to start at zero, and calls
+ * that overlap on one GPU (other streams, other threads) race. */
+#define PA_DECODE_SCRATCH_BYTES (16u << 20)
+int    pa_poly_decode_noalloc(const pa_decode* d, void* stream);
 int    pa_decode_prologue(const pa_prologue* p, void* stream);
 int    pa_rmsnorm_fwd(const pa_rmsnorm* r, void* stream);
 size_t pa_rmsnorm_bwd_workspace(const pa_rmsnorm* r);

@@ -151,6 +151,9 @@ const char* pa_strerror(int status) {
         case PA_EUNSUPPORTED: return "unsupported by this build of libpolyattn";
         case PA_EHIP: return "HIP runtime error";
         case PA_EWORKSPACE: return "workspace missing or too small";
+        case PA_ESCRATCH:
+            return "the request needs more split-K scratch than the library's static "
+                   "PA_DECODE_SCRATCH_BYTES per device (use pa_poly_decode with a workspace)";
         default: return "unknown libpolyattn status";
     }
 }
@@ -304,6 +307,15 @@ size_t pa_poly_decode_workspace(const pa_decode* d) {
 int pa_poly_decode(const pa_decode* d, void* stream) {
     if (!d) return PA_EINVAL;
     const int st = launch_decode(d, static_cast<hipStream_t>(stream));
+    if (st != PA_OK) return st;
+    return finish_launch();
+}
+
+int pa_poly_decode_noalloc(const pa_decode* d, void* stream) {
+    if (!d) return PA_EINVAL;
+    int hip_err = 0;
+    const int st = launch_decode_noalloc(d, static_cast<hipStream_t>(stream), &hip_err);
+    if (st == PA_EHIP) g_last_hip_error = hip_err;
     if (st != PA_OK) return st;
     return finish_launch();
 }

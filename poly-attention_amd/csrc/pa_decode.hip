@@ -12,6 +12,7 @@
 // adds the new position n-1 -- whose value and bias are the step results of the deeper
 // level -- and writes the level's msg / lse cache slot (or the final output).
 #include <algorithm>
+#include <mutex>
 
 #include "pa_common.h"
 #include "pa_launch.h"
@@ -1043,6 +1044,57 @@ int launch_decode(const pa_decode* d, hipStream_t s) {
     else if (T == PA_F16) hipLaunchKernelGGL((k_dec_combine<f16>), cgrid, dim3(kDecThreads), 0, s, D);
     else hipLaunchKernelGGL((k_dec_combine<bf16>), cgrid, dim3(kDecThreads), 0, s, D);
     return PA_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// Static scratch of pa_poly_decode_noalloc: the split-K partial records live in a device
+// array of the library instead of a caller workspace.  Each GPU the library runs on holds its
+// own copy at its own address; host code takes that address from hipGetSymbolAddress, looked
+// up once per device, and never uses the array's name (a host-side stand-in) as a pointer.
+
+static __device__ __align__(256) unsigned char scratch[PA_DECODE_SCRATCH_BYTES];
+
+constexpr int kScratchMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchMaxDevices];
+
+// the current device's copy of `scratch`
+static int scratch_address(void** out, int* hip_err) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        *hip_err = static_cast<int>(e);
+        return PA_EHIP;
+    }
+    if (dev < 0 || dev >= kScratchMaxDevices) return PA_EUNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            *hip_err = static_cast<int>(e);
+            return PA_EHIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return PA_OK;
+}
+
+int launch_decode_noalloc(const pa_decode* d, hipStream_t s, int* hip_err) {
+    if (d->order < 2 || d->order > PA_MAX_ORDER) return PA_EINVAL;
+    if (d->batch < 1 || d->kv_heads < 1 || d->n < 1 || d->dim < 1) return PA_EINVAL;
+    for (int t = 0; t < d->order; ++t)
+        if (d->levels[t].heads < 1) return PA_EINVAL;
+    int chunk = 0, nchunks = 0;
+    if (decode_workspace_bytes(d, &chunk, &nchunks) > PA_DECODE_SCRATCH_BYTES) return PA_ESCRATCH;
+    void* ptr = nullptr;
+    const int st = scratch_address(&ptr, hip_err);
+    if (st != PA_OK) return st;
+    pa_decode local = *d;
+    local.workspace = ptr;
+    local.workspace_bytes = PA_DECODE_SCRATCH_BYTES;
+    return launch_decode(&local, s);
 }
 
 }  // namespace pa

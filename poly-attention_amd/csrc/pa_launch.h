@@ -31,6 +31,9 @@ void launch_mfma_bwd(const GradDev& G, int dtype, hipStream_t s);
 struct DecodeDev;
 size_t decode_workspace_bytes(const pa_decode* d, int* chunk_out, int* nchunks_out);
 int launch_decode(const pa_decode* d, hipStream_t s);
+// launch_decode on the library's static per-device scratch; *hip_err receives the HIP error
+// behind a PA_EHIP
+int launch_decode_noalloc(const pa_decode* d, hipStream_t s, int* hip_err);
 int launch_prologue(const pa_prologue* p, hipStream_t s);
 int launch_rms_fwd(const pa_rmsnorm* p, hipStream_t s);
 size_t rms_bwd_workspace(const pa_rmsnorm* p);

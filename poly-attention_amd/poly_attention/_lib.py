@@ -23,6 +23,10 @@ PA_EINVAL = -1
 PA_EUNSUPPORTED = -2
 PA_EHIP = -3
 PA_EWORKSPACE = -4
+PA_ESCRATCH = -5
+
+# the static split-K scratch of pa_poly_decode_noalloc, bytes per device
+PA_DECODE_SCRATCH_BYTES = 16 << 20
 
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 PA_FLAG_MAY_DEGENERATE = 1
@@ -43,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "pa_attn_pass_bwd",
     "pa_poly_decode_workspace",
     "pa_poly_decode",
+    "pa_poly_decode_noalloc",
     "pa_decode_prologue",
     "pa_rmsnorm_fwd",
     "pa_rmsnorm_bwd_workspace",
@@ -270,6 +275,8 @@ def _configure(lib) -> None:
     lib.pa_poly_decode_workspace.argtypes = [ctypes.POINTER(PaDecode)]
     lib.pa_poly_decode.restype = c_int
     lib.pa_poly_decode.argtypes = [ctypes.POINTER(PaDecode), c_void_p]
+    lib.pa_poly_decode_noalloc.restype = c_int
+    lib.pa_poly_decode_noalloc.argtypes = [ctypes.POINTER(PaDecode), c_void_p]
     lib.pa_decode_prologue.restype = c_int
     lib.pa_decode_prologue.argtypes = [ctypes.POINTER(PaPrologue), c_void_p]
     lib.pa_rmsnorm_fwd.restype = c_int

@@ -1012,7 +1012,8 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
                      v_caches: Sequence[Tensor], msg_caches: Sequence[Tensor],
                      lse_caches: Sequence[Tensor], *, kv_heads: int, heads: int,
                      softclamp: Optional[float], scale: float, chunk: int = 0,
-                     n_dev: Optional[Tensor] = None) -> Tensor:
+                     n_dev: Optional[Tensor] = None, noalloc: bool = False,
+                     out: Optional[Tensor] = None) -> Tensor:
     """One cached decode step through pa_poly_decode (no autograd).
 
     Level l (l = 0: q1 . q2) has query q_new[l] [B, h, 1, d] and keys k_caches[l]
@@ -1023,6 +1024,10 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
     With ``n_dev`` (a device int32 [1]) the caches are fixed-capacity buffers (n = their
     length is the bound) and the step's n is read on the device, so the launch is the same
     at every position (HIP-graph capturable).
+
+    ``noalloc``: through pa_poly_decode_noalloc, whose split-K records use the library's static
+    per-device scratch (no workspace tensor); with ``out`` given as well, the call allocates
+    nothing on the device.
     """
     lib = _lib.load()
     order = len(q_new)
@@ -1030,7 +1035,9 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
     assert len(msg_caches) == order - 1 and len(lse_caches) == order - 1
     B, _, n, d = k_caches[0].shape
     dt = q_new[0].dtype
-    out = torch.empty(B, heads, 1, d, dtype=dt, device=q_new[0].device)
+    if out is None:
+        out = torch.empty(B, heads, 1, d, dtype=dt, device=q_new[0].device)
+    assert out.shape == (B, heads, 1, d) and out.dtype == dt and out.stride(-1) == 1
     D = PaDecode()
     D.batch, D.kv_heads, D.n, D.dim, D.order = B, kv_heads, n, d, order
     D.scale = float(scale)
@@ -1073,6 +1080,11 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
     if n_dev is not None:
         assert n_dev.dtype == torch.int32 and n_dev.is_cuda and n_dev.numel() == 1
         D.n_dev = n_dev.data_ptr()
+    if noalloc:
+        with _device(out):
+            _lib.check(lib.pa_poly_decode_noalloc(ctypes.byref(D), _stream(out)),
+                       "pa_poly_decode_noalloc")
+        return out
     ws_bytes = lib.pa_poly_decode_workspace(ctypes.byref(D))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=out.device)
     D.workspace, D.workspace_bytes = ws.data_ptr(), ws_bytes
