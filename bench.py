@@ -389,18 +389,45 @@ def _greedy(lm, prompt, steps):
     return torch.cat(out, dim=1)
 
 
-def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2, eager=True):
-    """Config 4 two ways: (1) the reference's calling pattern, one eager module call per
-    token with the growing cache tuples (skipped with ``eager=False``, for profiling runs);
-    (2) the same steps on StaticCaches, one decode step (all layers, logits, argmax)
-    captured into a HIP graph and replayed per token."""
-    from poly_attention import StaticCache
+def _flip_margins(logits, tok_eager, tok_graph):
+    """At the first step where the eager and the graph paths pick different greedy tokens: per
+    differing batch row, the eager logits' top-2 margin, their gap between the two picked
+    tokens, and that gap in units of one bf16 rounding of the logit (2^-8 |logit|)."""
+    rows = (tok_eager != tok_graph).nonzero().flatten().tolist()
+    out = []
+    for r in rows:
+        lg = logits[r].float()
+        top = lg.topk(2).values
+        te, tg = int(tok_eager[r]), int(tok_graph[r])
+        gap = float(lg[te] - lg[tg])
+        out.append({"row": r, "eager_token": te, "graph_token": tg,
+                    "eager_top2_margin": round(float(top[0] - top[1]), 6),
+                    "eager_gap_between_picks": round(gap, 6),
+                    "gap_in_bf16_roundings": round(gap / (2.0 ** -8 * float(lg[te].abs())), 3)})
+    return out
 
-    depth, heads, dh, dim = 8, 16, 64, 1024
+
+def make_lm(dev, depth=8, heads=16, dh=64, dim=1024, batch=8, prefill=2048):
+    """Config 4's stack (random-init bf16 weights, seed 0) and its uniform random prompt."""
     torch.manual_seed(0)
     lm = _PolyLM(dim=dim, depth=depth, heads=heads, dim_head=dh).to(dev, torch.bfloat16).eval()
     g = torch.Generator(device="cpu").manual_seed(1)
     prompt = torch.randint(0, 256, (batch, prefill), generator=g).to(dev)
+    return lm, prompt
+
+
+def decode_two_ways(lm, prompt, steps, warm=2, eager=True, more=16, profile=True):
+    """The config-4 decode two ways: (1) the reference's calling pattern, one eager module call
+    per token with the growing cache tuples (skipped with ``eager=False``); (2) the same steps
+    on StaticCaches, one decode step (all layers, logits, argmax) captured into a HIP graph and
+    replayed per token.  Returns the tokens of both (the prefill's pick first), the eager
+    logits behind each token, the wall times and (``profile``) the per-launch kernel times of
+    ``more`` further eager StaticCache steps."""
+    from poly_attention import StaticCache
+
+    dev = prompt.device
+    batch, prefill = prompt.shape
+    out = {}
     with torch.no_grad():
         _greedy(lm, prompt[:, :256], 8)  # warm-up (allocator, kernels)
         torch.cuda.synchronize()
@@ -411,18 +438,20 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2, eage
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         toks_eager = [tok]
+        logits_eager = [logits[:, -1]]  # the logits behind each greedy token (device)
         for _ in range(steps if eager else 0):
             logits, cache = lm(tok, cache)
             tok = logits[:, -1].argmax(-1, keepdim=True)
             toks_eager.append(tok)
+            logits_eager.append(logits[:, -1])
         torch.cuda.synchronize()
         t2 = time.perf_counter()
-        toks_eager = torch.cat(toks_eager, dim=1)
+        out["toks_eager"] = torch.cat(toks_eager, dim=1)
+        out["logits_eager"] = logits_eager
         del cache, logits
         # (2) StaticCache + one captured step per token
         logits, (lcs, _) = lm(prompt)
         tok = logits[:, -1].argmax(-1, keepdim=True)
-        more = 16  # extra steps, profiled after the timed loop
         # one step counter shared by the layers' caches, advanced once per token
         counter = StaticCache.make_counter(lcs[0])
         scs = [StaticCache(c, capacity=prefill + steps + more + 1, counter=counter) for c in lcs]
@@ -456,18 +485,41 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2, eage
         torch.cuda.synchronize()
         t4 = time.perf_counter()
         assert scs[0].seq_len() == prefill + steps
-        # greedy tokens of random-init weights sit on near-ties: a last-bit difference
-        # (summation order of the split-K chunks, fused vs separate roundings) can flip one
-        # argmax, after which the sequences diverge; report where the first flip happens
-        first_flip = None
-        if eager:
-            diff = (rec[:, :steps + 1] != toks_eager).any(dim=0).nonzero()
-            first_flip = int(diff[0].item()) if diff.numel() else steps + 1
-        # kernel times of a few more steps (events per launch; outside the timed loops)
-        with _lib().KernelProfile() as prof:
-            for _ in range(more):
-                step()
-            torch.cuda.synchronize()
+        scs[0].check_overflow()
+        out["toks_graph"] = rec[:, :steps + 1].clone()
+        out["times"] = (t0, t1, t2, t3, t4)
+        if profile:
+            # kernel times of a few more steps (events per launch, eager steps: host gaps count)
+            with _lib().KernelProfile() as prof:
+                for _ in range(more):
+                    step()
+                torch.cuda.synchronize()
+            out["prof"] = prof
+        del scs, graph
+    return out
+
+
+def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2, eager=True):
+    """Config 4 timed two ways (``decode_two_ways``); the graph replays are the figure."""
+    depth, heads, dh, dim = 8, 16, 64, 1024
+    more = 16
+    lm, prompt = make_lm(dev, depth, heads, dh, dim, batch, prefill)
+    runs = decode_two_ways(lm, prompt, steps, warm, eager, more)
+    t0, t1, t2, t3, t4 = runs["times"]
+    prof = runs["prof"]
+    # greedy tokens of random-init weights sit on near-ties: a last-bit difference
+    # (summation order of the split-K chunks, fused vs separate roundings) can flip one
+    # argmax, after which the sequences diverge; report where the first flip happens and the
+    # eager logits' margins there
+    first_flip = None
+    flip = None
+    if eager:
+        toks_eager, rec = runs["toks_eager"], runs["toks_graph"]
+        diff = (rec != toks_eager).any(dim=0).nonzero()
+        first_flip = int(diff[0].item()) if diff.numel() else steps + 1
+        if first_flip <= steps:
+            flip = _flip_margins(runs["logits_eager"][first_flip], toks_eager[:, first_flip],
+                                 rec[:, first_flip])
     eager_s, graph_s = t2 - t1, t4 - t3
     graph_steps = steps - warm
     # cache bytes per step and layer (order 3, kv heads = heads): every cached tensor read
@@ -483,9 +535,6 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2, eage
     graph_bytes = sum(step_bytes(s) for s in range(warm, steps))
     kern = {k: {"launches": n // more, "avg_ms": round(t / n, 4)}
             for k, (n, t) in prof.times.items()}
-    lib_ms = sum(t for _, t in prof.times.values()) / more
-    attn_ms = sum(t for k, (_, t) in prof.times.items() if k.startswith("dec_")) / more
-    n_mid = prefill + steps + more / 2
     res = {
         "workload": f"order-3 causal decode, PolyLM-style stack depth {depth}, dim {dim}, heads "
                     f"{heads}, dim_head {dh}, batch {batch}, prefill {prefill} tokens, {steps} "
@@ -502,17 +551,15 @@ def decode_order3_bench(dev, cpu, steps=512, prefill=2048, batch=8, warm=2, eage
             "tokens_per_s": round(batch * steps / eager_s, 1),
             "GB_per_s": round(eager_bytes / eager_s / 1e9, 1)},
         "greedy_tokens_identical_to_eager_until": first_flip,
+        "first_flip": flip,
         "cache_GB_per_step_mean": round((eager_bytes - steps * weight_bytes) / steps / 1e9, 4),
         "weight_GB_per_step": round(weight_bytes / 1e9, 4),
-        "library_kernels_ms_per_step": round(lib_ms, 4),
-        "decode_attention_ms_per_step": round(attn_ms, 4),
-        "decode_kernels_GB_per_s": round(
-            batch * depth * per_tok * n_mid
-            / (sum(prof.times.get(k, (0, 0.0))[1] for k in ("dec_partial", "dec_combine"))
-               / more / 1e3) / 1e9, 1),
+        "kernels_timer": "HIP events around each launch over 16 eager StaticCache steps "
+                         "(host gaps between launches count; rocprofv3 kernel traces in "
+                         "profiles/ give the kernels' own durations)",
         "kernels": kern,
     }
-    del lm, scs, graph
+    del lm, runs
     torch.cuda.empty_cache()
     if cpu:
         threads = cpu_threads()[0]
