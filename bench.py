@@ -139,6 +139,41 @@ def module_step(m, x, dx):
     out.backward(dx)
 
 
+def masked_core_bench(qs, dout, steps, warmup):
+    """Config 2's core step with the op's mask (a key mask of both passes,
+    flash_poly_attention.py:109-112 of the reference) as padding: batch rows keep N, 7N/8, 3N/4
+    and N/2 keys.  right_pad masks the trailing keys; left_pad the leading ones, so the first
+    causal rows of the padded batch rows are fully masked in both passes (the backward's
+    fix-up path).  Same nominal work as the unmasked step."""
+    from poly_attention import _lib
+    from poly_attention.flash_poly_attention import flash_poly_attention
+
+    lengths = (N, N - N // 8, N - N // 4, N // 2)
+    masks = {"right_pad": torch.ones(B, N, dtype=torch.bool),
+             "left_pad": torch.ones(B, N, dtype=torch.bool)}
+    for b, keep in enumerate(lengths):
+        masks["right_pad"][b, keep:] = False
+        masks["left_pad"][b, :N - keep] = False
+    res = {"kept_keys_per_batch_row": list(lengths)}
+    for name, mask in masks.items():
+        mk = mask.to(dout.device)
+
+        def step():
+            for t in qs:
+                t.grad = None
+            out = flash_poly_attention(*qs, mask=mk, is_causal=True)
+            out.backward(dout)
+
+        ms = time_steps(step, steps, warmup)
+        with _lib.KernelProfile() as prof:
+            for _ in range(3):
+                step()
+        res[name] = {"ms_per_step": round(ms, 4),
+                     "kernels": {k: {"launches_per_step": n // 3, "avg_ms": round(t / n, 4)}
+                                 for k, (n, t) in prof.times.items()}}
+    return res
+
+
 def time_steps(fn, steps, warmup):
     for _ in range(warmup):
         fn()
@@ -685,6 +720,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-module", action="store_true")
+    ap.add_argument("--no-masked", action="store_true", help="skip the masked config-2 steps")
     ap.add_argument("--no-vit", action="store_true", help="skip config 3 (PolyViT forward)")
     ap.add_argument("--no-lm", action="store_true", help="skip config 4 (order-3 decode loop)")
     ap.add_argument("--lm-steps", type=int, default=512, help="config 4: greedy decode steps")
@@ -750,6 +786,10 @@ def main():
                 rec["GB_per_s"] = round(moved / (t / n_l / 1e3) / 1e9, 1)
             module_kernels[k] = rec
         log(f"[bench] module kernels {module_kernels}")
+    masked = None
+    if not args.no_masked:
+        masked = masked_core_bench(qs, dout, max(3, args.steps // 2), 2)
+        log(f"[bench] masked core steps {masked}")
     del qs, dout
     torch.cuda.empty_cache()
 
@@ -805,6 +845,7 @@ def main():
         "flops_per_step": fwd_f + bwd_f,
         "roofline": roofline,
         "kernels": kernels,
+        "masked_core": masked,
         "module_ms_per_step": round(module_ms, 4) if module_ms else None,
         "module_kernels": module_kernels,
         "cpu_baseline": cpu,

@@ -133,9 +133,25 @@ int finish_launch() {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+bool pass_masked(const pa_pass& f) {
+    return f.key_mask.ptr || f.query_mask.ptr || (f.flags & PA_FLAG_MAY_DEGENERATE);
+}
+
+// key-term row stride: whole 16-byte chunks
+int key_term_stride(const pa_pass& f) { return (f.nk + 3) & ~3; }
+
+// [D | lse | 1/c1] per query row; masked passes add the key term (with a key mask), the
+// per-head fully-masked-row sums and the per-key-head bias-class counts
 size_t bwd_ws_bytes(const pa_pass& f) {
     const size_t rows = (size_t)f.batch * f.heads * f.nq;
-    return 3 * align256(rows * sizeof(float));
+    size_t n = 3 * align256(rows * sizeof(float));
+    if (pass_masked(f)) {
+        const size_t kheads = (size_t)f.batch * f.k.heads;
+        if (f.key_mask.ptr) n += align256(kheads * key_term_stride(f) * sizeof(float));
+        n += align256((size_t)f.batch * f.heads * (f.dim + 2) * sizeof(float));
+        n += align256(kheads * 2 * sizeof(int32_t));
+    }
+    return n;
 }
 
 }  // namespace
@@ -227,7 +243,7 @@ int pa_attn_pass_fwd(const pa_pass* p, void* stream) {
         launch_mfma_fwd(P, T, s);
         const bool may_degenerate = (p->flags & PA_FLAG_MAY_DEGENERATE) || p->key_mask.ptr ||
                                     p->query_mask.ptr;
-        if (may_degenerate) launch_simt_fixup(P, T, s);
+        if (may_degenerate) launch_fwd_fixup(P, T, s);
     } else {
         launch_simt_fwd(P, T, s);
     }
@@ -286,7 +302,39 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     G.fused_pre = 0;
     G.seeds = 0;
-    if (mfma_bwd_supported(G, T)) {
+    G.ws_kcnt = nullptr;
+    G.ws_part = nullptr;
+    if (mfma_bwd_supported(G, T) && pass_masked(*p)) {
+        // normal rows on the MFMA kernels with the key mask folded into the key bias; the
+        // preprocess marks fully-masked rows (lse = +inf), whose part the fix-ups add
+        char* w = ws + 3 * align256(rows * sizeof(float));
+        float* kterm = nullptr;
+        const int nkp = key_term_stride(*p);
+        if (p->key_mask.ptr) {
+            kterm = reinterpret_cast<float*>(w);
+            w += align256((size_t)p->batch * hk * nkp * sizeof(float));
+        }
+        G.ws_part = reinterpret_cast<float*>(w);
+        w += align256((size_t)p->batch * H * (p->dim + 2) * sizeof(float));
+        int32_t* kcnt = reinterpret_cast<int32_t*>(w);
+        G.ws_kcnt = kcnt;
+        launch_key_terms(G, kterm, nkp, kcnt, s);
+        launch_simt_bwd(G, T, s, /*pre=*/true, false, false);
+        GradDev Gm = G;
+        if (kterm) {
+            DView& kb = Gm.f.bias;
+            kb.p = reinterpret_cast<char*>(kterm);
+            kb.sb = (int64_t)hk * nkp;
+            kb.sh = nkp;
+            kb.sn = 1;
+            kb.hdiv = H / hk;
+            kb.dtype = PA_F32;
+        }
+        Gm.f.km.p = nullptr;
+        Gm.f.qm.p = nullptr;
+        launch_mfma_bwd(Gm, T, s);
+        launch_mask_fixups(G, T, s);
+    } else if (mfma_bwd_supported(G, T)) {
         // the direct-to-LDS dQ kernel computes the per-row preprocess itself when it applies
         G.fused_pre = mfma_bwd_fuses_pre(G) ? 1 : 0;
         if (!G.fused_pre) launch_simt_bwd(G, T, s, /*pre=*/true, false, false);

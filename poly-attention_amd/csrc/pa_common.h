@@ -86,6 +86,10 @@ struct GradDev {
     int32_t fused_pre;     // the dQ kernel computes ws_D / ws_lse for its rows (no preprocess)
     int32_t seeds;         // with fused_pre: ws_lse / ws_D hold the dK/dV kernel's accumulator
                            // seeds, -lse/scale (lse*log2e with softclamp) and -D
+    // masked passes on the MFMA kernels (null otherwise)
+    const int32_t* ws_kcnt;  // [B, hk, 2]: keys of bias class 0 and of bias class 1
+    float* ws_part;          // [B, heads, dim + 2]: over the fully-masked rows of a head,
+                             // sum dO / c1, sum D / c1 and their number
 };
 
 // class of a bias value in the finite-fill arithmetic: 0 normal, 1 = -FLT_MAX, 2 = -inf

@@ -17,8 +17,13 @@ struct ProfScope {
 
 // generic (one lane per row) kernels: every dtype, head dim <= 256, every mask feature
 void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s);
-void launch_simt_fixup(const PassDev& P, int dtype, hipStream_t s);
+// finish the fully-masked rows of an MFMA forward (head dim 64 or 128)
+void launch_fwd_fixup(const PassDev& P, int dtype, hipStream_t s);
 void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool dq, bool dkv);
+// masked passes on the MFMA backward: per-key-head bias-class counts (and, with kterm, the
+// key mask folded into a per-key term of row stride nkp), then the fully-masked rows' part
+void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, hipStream_t s);
+void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s);
 
 // MFMA kernels (bf16 / f16, head dim 64 or 128); return false when they do not cover P
 bool mfma_fwd_supported(const PassDev& P, int dtype);

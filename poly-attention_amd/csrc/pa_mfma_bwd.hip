@@ -9,8 +9,9 @@
 //     Q and dO, and the key bias gradient is the column sum of dS.
 //   k_mfma_bwd_dq (query-major, no atomics): a workgroup owns 128 queries (4 waves x 32) and
 //     sweeps the key tiles: S^T = K Q^T, dP^T = V dO^T, dS^T, then dQ^T += K^T dS^T.
-// Both recompute P from the saved lse; they do not handle fully-masked rows (the host sends
-// masked passes to the generic kernels).
+// Both recompute P from the saved lse.  They read no masks: for a masked pass the host folds
+// the key mask into the key bias and gives fully-masked rows lse = +inf (probability 0 here),
+// and the generic kernels add those rows' part afterwards.
 #include <algorithm>
 
 #include "pa_common.h"
@@ -1174,7 +1175,6 @@ bool mfma_bwd_supported(const GradDev& G, int dtype) {
     const PassDev& P = G.f;
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
     if (P.dim != 64 && P.dim != 128) return false;
-    if (P.km.p || P.qm.p || (P.flags & PA_FLAG_MAY_DEGENERATE)) return false;
     const DView* loads[] = {&P.q, &P.k, &P.v, &G.dout};
     for (const DView* v : loads)
         if (!aligned_rows_host(*v, 8)) return false;

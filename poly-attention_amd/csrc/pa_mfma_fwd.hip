@@ -23,7 +23,7 @@
 //  * k_mfma_fwd_pp (PA_FWD_PINGPONG): an 8-wave ping-pong schedule, off by default (slower
 //    than k_mfma_fwd_dma on the measured workloads).
 //
-// Rows whose every key is masked are left with lse = NaN for k_simt_fixup, which applies the
+// Rows whose every key is masked are left with lse = NaN for k_fwd_fixup, which applies the
 // reference's finite-fill semantics to them.  Workgroups are mapped XCD-aware (pa_mfma.h); in
 // causal grids each XCD dispatches the heaviest query blocks of all its heads first.
 //

@@ -3,8 +3,8 @@
 // These kernels implement every feature of a pass (any head dim up to 256, masks with the
 // reference's finite-fill semantics, bias classes, value multiplier, GQA head mapping) in
 // fp32 arithmetic.  They run whenever the MFMA kernels do not cover a request (fp32 data,
-// head dims other than 64/128, masked rows) and they finish the rare fully-masked rows of
-// an MFMA forward (k_simt_fixup).
+// head dims other than 64/128).  The same file holds the kernels that finish the fully-masked
+// rows of the MFMA forward and backward kernels (k_fwd_fixup, the k_fix_* kernels).
 #include "pa_common.h"
 #include "pa_launch.h"
 
@@ -134,29 +134,135 @@ __global__ __launch_bounds__(kSimtRows) void k_simt_fwd(PassDev P) {
     if (row && !degen) simt_write_row<T, D>(P, b, h, i, acc, 1.f / l, (m + log2f(l)) * kLn2);
 }
 
-// Finish the rows an MFMA forward left fully masked (their lse holds NaN).
+constexpr int kFixThreads = 1024;  // per-head reductions: many rows in flight on one CU
+
+// Finish the rows an MFMA forward left fully masked (their lse holds NaN), one workgroup per
+// (b, query head).  Every key of bias class 0 is masked for such a row (else the row would
+// hold a normal entry), so its class-1 entries are all bias-class-0 keys plus its own
+// unmasked bias-class-1 keys, and its output is (S0 + the latter's values) / c1, with S0 the
+// sum of the bias-class-0 keys' effective values -- one sum for every such row of the head.
 template <typename T, int D>
-__global__ __launch_bounds__(kSimtRows) void k_simt_fixup(PassDev P) {
-    __shared__ float sK[kSimtKT][D];
-    __shared__ float sV[kSimtKT][D];
-    __shared__ float sB[kSimtKT];
-    __shared__ uint8_t sKM[kSimtKT];
-    const int b = blockIdx.z, h = blockIdx.y;
-    const int i = blockIdx.x * kSimtRows + threadIdx.x;
-    const bool row = i < P.nq;
-    const bool degen = row && isnan(*P.lse.row<float>(b, h, i));
-    if (!__syncthreads_or(degen)) return;
-    const bool qok = row && P.qm.keep(b, i);
-    float acc[D], c1;
-    simt_degenerate_rows<T, D>(P, b, h, i, degen, qok, sK, sV, sB, sKM, acc, c1);
-    if (degen) {
-        if (c1 > 0.f) simt_write_row<T, D>(P, b, h, i, acc, 1.f / c1, -FLT_MAX);
-        else simt_write_row<T, D>(P, b, h, i, acc, NAN, -INFINITY);
+__global__ __launch_bounds__(kFixThreads) void k_fwd_fixup(PassDev P) {
+    constexpr int LPR = D / 8, R = kFixThreads / LPR;  // lanes per key row, key slots
+    constexpr int E = D / 64;  // columns per lane when finishing a row
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x;
+    bool any = false;
+    for (int i = tid; i < P.nq; i += blockDim.x) any |= isnan(*P.lse.row<float>(b, h, i));
+    if (!__syncthreads_or(any)) return;
+
+    // S0 and the counts of bias-class-0 and unmasked bias-class-1 keys
+    const int slot = tid / LPR, c0 = (tid % LPR) * 8;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    int n0 = 0, n1 = 0;
+#pragma unroll 4
+    for (int j = slot; j < P.nk; j += R) {
+        const int cls = P.bias.ok() ? bias_class(P.bias.scalar(b, h, j)) : 0;
+        if (cls == 1 && P.km.keep(b, j)) ++n1;
+        if (cls != 0) continue;
+        ++n0;
+        const uint4 raw = *reinterpret_cast<const uint4*>(P.v.row<T>(b, h, j) + c0);
+        const T* v8 = reinterpret_cast<const T*>(&raw);
+        if (P.vmul.ok()) {
+            const uint4 mraw = *reinterpret_cast<const uint4*>(P.vmul.row<T>(b, h, j) + c0);
+            const T* m8 = reinterpret_cast<const T*>(&mraw);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] += round_to<T>(to_f(v8[e]) * to_f(m8[e]));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] += to_f(v8[e]);
+        }
+    }
+    __shared__ float sS[R][D];
+    __shared__ int sN[R][2];
+    __shared__ float sT[D];
+    __shared__ int sCnt[2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sS[slot][c0 + e] = acc[e];
+    if (c0 == 0) {
+        sN[slot][0] = n0;
+        sN[slot][1] = n1;
+    }
+    __syncthreads();
+    if (tid < D) {
+        float a = 0.f;
+        for (int r = 0; r < R; ++r) a += sS[r][tid];
+        sT[tid] = a;
+    } else if (tid < D + 2) {
+        int a = 0;
+        for (int r = 0; r < R; ++r) a += sN[r][tid - D];
+        sCnt[tid - D] = a;
+    }
+    __syncthreads();
+    const int N0 = sCnt[0], N1 = sCnt[1];
+
+    // each wave finds its fully-masked rows 64 at a time and writes them, lanes as columns
+    const int w = tid / 64, lane = tid % 64;
+    for (int i0 = w * 64; i0 < P.nq; i0 += blockDim.x) {
+        const int i = i0 + lane;
+        uint64_t m = __ballot(i < P.nq && isnan(*P.lse.row<float>(b, h, i)));
+        while (m) {
+            const int r = i0 + __ffsll((unsigned long long)m) - 1;
+            m &= m - 1;
+            float sum[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) sum[e] = sT[lane + 64 * e];
+            int c1 = N0;
+            if (N1 > 0 && P.qm.keep(b, r)) {  // the row's unmasked bias-class-1 keys
+                const int jend = P.causal ? min(P.nk, r + 1) : P.nk;
+                for (int j0 = 0; j0 < jend; j0 += 64) {
+                    const int j = j0 + lane;
+                    const bool f = j < jend && P.km.keep(b, j) &&
+                                   bias_class(P.bias.scalar(b, h, j)) == 1;
+                    uint64_t fm = __ballot(f);
+                    c1 += __popcll(fm);
+                    while (fm) {
+                        const int jk = j0 + __ffsll((unsigned long long)fm) - 1;
+                        fm &= fm - 1;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) {
+                            const int d = lane + 64 * e;
+                            float vv = to_f(P.v.row<T>(b, h, jk)[d]);
+                            if (P.vmul.ok()) vv = round_to<T>(vv * to_f(P.vmul.row<T>(b, h, jk)[d]));
+                            sum[e] += vv;
+                        }
+                    }
+                }
+            }
+            const float inv = c1 > 0 ? 1.f / (float)c1 : NAN;
+            T* o = P.out.wrow<T>(b, h, r);
+#pragma unroll
+            for (int e = 0; e < E; ++e) o[lane + 64 * e] = from_f<T>(sum[e] * inv);
+            if (lane == 0) *P.lse.wrow<float>(b, h, r) = c1 > 0 ? -FLT_MAX : -INFINITY;
+        }
     }
 }
 
 // ---------------------------------------------------------------------------------------
 // backward
+
+// Number of class-1 entries (score -finfo.max) of the fully-masked row i.  Every key of bias
+// class 0 is masked for such a row (else the row would hold a normal entry), so the count is
+// the (b, key head)'s bias-class-0 keys plus the row's unmasked bias-class-1 keys; the latter
+// exist only where the bias holds -finfo.max on kept keys and the row's query is kept.  With
+// the per-key-head counts of a masked MFMA backward (G.ws_kcnt) the row loop runs only then.
+__device__ __forceinline__ float degenerate_count(const GradDev& G, int b, int h, int i) {
+    const PassDev& P = G.f;
+    const bool qok = P.qm.keep(b, i);
+    if (G.ws_kcnt) {
+        const int32_t* kc = G.ws_kcnt + 2 * ((int64_t)b * G.hk + h / (P.heads / G.hk));
+        if (!qok || kc[1] == 0) return (float)kc[0];
+    }
+    float c1 = 0.f;
+    for (int j = 0; j < P.nk; ++j) {
+        const bool own_masked = !qok || (P.causal && j > i) || !P.km.keep(b, j);
+        const float bj = P.bias.ok() ? P.bias.scalar(b, h, j) : 0.f;
+        if ((own_masked ? 1 : 0) + bias_class(bj) == 1) c1 += 1.f;
+    }
+    return c1;
+}
 
 // Per row: D = rowsum(dO * O) - dlse, so that dS = P (dP - D) carries the softmax and the
 // logsumexp gradients.  A fully-masked row has P = 1/c1 on its c1 class-1 entries, and its
@@ -178,13 +284,7 @@ __global__ __launch_bounds__(kSimtRows) void k_bwd_pre(GradDev G) {
     if (l > kMaskedThreshold) {
         dsum -= dl;
     } else {
-        const bool qok = P.qm.keep(b, i);
-        float c1 = 0.f;
-        for (int j = 0; j < P.nk; ++j) {
-            const bool own_masked = !qok || (P.causal && j > i) || !P.km.keep(b, j);
-            const float bj = P.bias.ok() ? P.bias.scalar(b, h, j) : 0.f;
-            if ((own_masked ? 1 : 0) + bias_class(bj) == 1) c1 += 1.f;
-        }
+        const float c1 = degenerate_count(G, b, h, i);
         lseb = INFINITY;
         invc = c1 > 0.f ? 1.f / c1 : 0.f;
         // an all -inf row (c1 == 0): its NaN output has no gradient here
@@ -227,13 +327,7 @@ __global__ __launch_bounds__(256) void k_bwd_pre_vec(GradDev G) {
     if (l > kMaskedThreshold) {
         dsum -= dl;
     } else {  // fully-masked row (rare): count its class-1 entries
-        const bool qok = P.qm.keep(b, i);
-        float c1 = 0.f;
-        for (int j = 0; j < P.nk; ++j) {
-            const bool own_masked = !qok || (P.causal && j > i) || !P.km.keep(b, j);
-            const float bj = P.bias.ok() ? P.bias.scalar(b, h, j) : 0.f;
-            if ((own_masked ? 1 : 0) + bias_class(bj) == 1) c1 += 1.f;
-        }
+        const float c1 = degenerate_count(G, b, h, i);
         lseb = INFINITY;
         invc = c1 > 0.f ? 1.f / c1 : 0.f;
         dsum = c1 > 0.f ? dsum - c1 * dl : 0.f;
@@ -426,6 +520,350 @@ __global__ __launch_bounds__(kSimtRows) void k_simt_bwd_dkv(GradDev G) {
 }
 
 // ---------------------------------------------------------------------------------------
+// masked passes on the MFMA backward kernels
+//
+// The MFMA kernels compute the normal rows of a masked pass exactly once the key mask is
+// folded into a per-key additive term (the raw bias on kept keys, -inf on masked ones: the
+// kernels turn any non-class-0 term into probability 0), and the preprocess gives every
+// fully-masked row lse = +inf, which makes its probabilities 0 there.  The kernels below add
+// the fully-masked rows' part.  Such a row i has probability 1/c1_i on its class-1 entries:
+//   (A) every key of bias class 0 (all masked for the row, so no score gradient), and
+//   (B) its unmasked keys of bias class 1 (only where the bias holds -finfo.max).
+// Part A is the same key set for every fully-masked row of a head, so over those rows it is a
+// rank-one update: dV[j] += u = sum_i dO_i / c1_i and dbias[j] += u . V[j] - sum_i D_i / c1_i
+// on each bias-class-0 key j.  Part B is a plain loop over the rare (row, key) pairs.
+
+// Per (b, key head): the count of bias-class-0 keys and of unmasked bias-class-1 keys (part
+// B exists only where the latter is nonzero), and (with kterm) the per-key term the MFMA
+// kernels read as their bias, rows of stride nkp.
+__global__ __launch_bounds__(256) void k_key_terms(GradDev G, float* kterm, int nkp,
+                                                   int32_t* kcnt) {
+    const PassDev& P = G.f;
+    const int kh = blockIdx.x, b = blockIdx.y;
+    const int h0 = kh * (P.heads / G.hk);
+    int c0 = 0, c1 = 0;
+    for (int j = threadIdx.x; j < P.nk; j += blockDim.x) {
+        const float x = P.bias.ok() ? P.bias.scalar(b, h0, j) : 0.f;
+        const int cls = bias_class(x);
+        const bool kept = P.km.keep(b, j);
+        c0 += cls == 0;
+        c1 += cls == 1 && kept;
+        if (kterm) kterm[((int64_t)b * G.hk + kh) * nkp + j] = kept ? x : -INFINITY;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        c0 += __shfl_xor(c0, off);
+        c1 += __shfl_xor(c1, off);
+    }
+    __shared__ int s0[4], s1[4];
+    const int w = threadIdx.x / 64;
+    if (threadIdx.x % 64 == 0) {
+        s0[w] = c0;
+        s1[w] = c1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int t0 = 0, t1 = 0;
+        for (int k = 0; k < (int)blockDim.x / 64; ++k) {
+            t0 += s0[k];
+            t1 += s1[k];
+        }
+        kcnt[2 * ((int64_t)b * G.hk + kh)] = t0;
+        kcnt[2 * ((int64_t)b * G.hk + kh) + 1] = t1;
+    }
+}
+
+__device__ __forceinline__ bool degenerate_row(const GradDev& G, int64_t r) {
+    return G.ws_lse[r] == INFINITY && G.ws_invc[r] > 0.f;
+}
+
+// Part A sums, one workgroup per (b, query head): D/8 lanes per row, 16 bytes of dO each, all
+// rows in flight at once; the row slots are then summed through LDS.
+template <typename T, int D>
+__global__ __launch_bounds__(kFixThreads) void k_fix_rows(GradDev G) {
+    const PassDev& P = G.f;
+    constexpr int LPR = D / 8, R = kFixThreads / LPR;  // lanes per row, row slots
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int slot = threadIdx.x / LPR, c0 = (threadIdx.x % LPR) * 8;
+    const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
+    float u[8], wsum = 0.f, cnt = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) u[e] = 0.f;
+#pragma unroll 4
+    for (int i = slot; i < P.nq; i += R) {
+        if (!degenerate_row(G, row0 + i)) continue;
+        const float ic = G.ws_invc[row0 + i];
+        const uint4 raw = *reinterpret_cast<const uint4*>(G.dout.row<T>(b, h, i) + c0);
+        const T* e8 = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) u[e] += ic * to_f(e8[e]);
+        wsum += ic * G.ws_D[row0 + i];
+        cnt += 1.f;
+    }
+    __shared__ float sU[R][D];
+    __shared__ float sW[R], sC[R];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sU[slot][c0 + e] = u[e];
+    if (c0 == 0) {
+        sW[slot] = wsum;
+        sC[slot] = cnt;
+    }
+    __syncthreads();
+    float* part = G.ws_part + ((int64_t)b * P.heads + h) * (D + 2);
+    if (threadIdx.x < D) {
+        float a = 0.f;
+        for (int r = 0; r < R; ++r) a += sU[r][threadIdx.x];
+        part[threadIdx.x] = a;
+    } else if (threadIdx.x < D + 2) {
+        const float* src = threadIdx.x == D ? sW : sC;
+        float a = 0.f;
+        for (int r = 0; r < R; ++r) a += src[r];
+        part[threadIdx.x] = a;
+    }
+}
+
+// 8 consecutive elements to / from fp32: 16-byte aligned rows (the MFMA kernels' loads), and
+// 8-byte aligned rows (their stores) as two 8-byte accesses
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* f) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[k] = to_f(e[k]);
+}
+template <typename T>
+__device__ __forceinline__ void load8_a8(const T* p, float* f) {
+    const uint2 a = reinterpret_cast<const uint2*>(p)[0], c = reinterpret_cast<const uint2*>(p)[1];
+    const T* ea = reinterpret_cast<const T*>(&a);
+    const T* ec = reinterpret_cast<const T*>(&c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        f[k] = to_f(ea[k]);
+        f[4 + k] = to_f(ec[k]);
+    }
+}
+template <typename T>
+__device__ __forceinline__ void store8_a8(T* p, const float* f) {
+    uint2 a, c;
+    T* ea = reinterpret_cast<T*>(&a);
+    T* ec = reinterpret_cast<T*>(&c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        ea[k] = from_f<T>(f[k]);
+        ec[k] = from_f<T>(f[4 + k]);
+    }
+    reinterpret_cast<uint2*>(p)[0] = a;
+    reinterpret_cast<uint2*>(p)[1] = c;
+}
+
+constexpr int kFixKeys = 256;  // keys per k_fix_keys workgroup
+
+// Part A updates of key head kh: dV (and dvmul) and dbias of the bias-class-0 keys,
+// read-modify-write on what the MFMA dK/dV kernel stored; D/8 lanes per key row.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_fix_keys(GradDev G) {
+    const PassDev& P = G.f;
+    constexpr int LPR = D / 8, R = 256 / LPR;
+    const int kh = blockIdx.y, b = blockIdx.z;
+    const int rep = P.heads / G.hk, h0 = kh * rep;
+    __shared__ float sU[D];
+    __shared__ float sWC[2];
+    const int tid = threadIdx.x;
+    if (tid < D + 2) {
+        float a = 0.f;
+        for (int hh = 0; hh < rep; ++hh) a += G.ws_part[((int64_t)b * P.heads + h0 + hh) * (D + 2) + tid];
+        if (tid < D) sU[tid] = a;
+        else sWC[tid - D] = a;
+    }
+    __syncthreads();
+    if (sWC[1] == 0.f) return;  // no fully-masked row in the group
+    const int slot = tid / LPR, c0 = (tid % LPR) * 8;
+    float u[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) u[e] = sU[c0 + e];
+    for (int jj = slot; jj < kFixKeys; jj += R) {
+        const int j = blockIdx.x * kFixKeys + jj;
+        const bool ok = j < P.nk && (!P.bias.ok() || bias_class(P.bias.scalar(b, h0, j)) == 0);
+        float dot = 0.f;
+        if (ok) {
+            float v[8], m[8], g[8];
+            load8(P.v.row<T>(b, h0, j) + c0, v);
+            if (P.vmul.ok()) load8(P.vmul.row<T>(b, h0, j) + c0, m);
+            T* dv = G.dv.wrow<T>(b, h0, j) + c0;
+            load8_a8(dv, g);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                dot += u[e] * (P.vmul.ok() ? round_to<T>(v[e] * m[e]) : v[e]);
+                g[e] += P.vmul.ok() ? u[e] * m[e] : u[e];
+            }
+            store8_a8(dv, g);
+            if (P.vmul.ok()) {
+                T* dm = G.dvmul.wrow<T>(b, h0, j) + c0;
+                load8_a8(dm, g);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) g[e] += u[e] * v[e];
+                store8_a8(dm, g);
+            }
+        }
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+        if (ok && c0 == 0 && G.dbias.ok()) *G.dbias.wrow<float>(b, h0, j) += dot - sWC[0];
+    }
+}
+
+// Part B, query side: dQ of the fully-masked kept rows through their unmasked bias-class-1
+// keys (one lane per row).
+template <typename T, int D>
+__global__ __launch_bounds__(kSimtRows) void k_fix_rows_b(GradDev G) {
+    const PassDev& P = G.f;
+    __shared__ float sK[kSimtKT][D];
+    __shared__ float sV[kSimtKT][D];
+    __shared__ float sB[kSimtKT];
+    __shared__ uint8_t sKM[kSimtKT];
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int kh = h / (P.heads / G.hk);
+    if (G.ws_kcnt[2 * ((int64_t)b * G.hk + kh) + 1] == 0) return;
+    const int i = blockIdx.x * kSimtRows + threadIdx.x;
+    const int64_t r = ((int64_t)b * P.heads + h) * P.nq + i;
+    const bool dg = i < P.nq && degenerate_row(G, r) && P.qm.keep(b, i);
+    if (!__syncthreads_or(dg)) return;
+    const float Dp = dg ? G.ws_D[r] : 0.f;
+    const float ic = dg ? G.ws_invc[r] : 0.f;
+    float q[D], go[D], dq[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        q[d] = dg ? to_f(P.q.row<T>(b, h, i)[d]) : 0.f;
+        go[d] = dg ? to_f(G.dout.row<T>(b, h, i)[d]) : 0.f;
+        dq[d] = 0.f;
+    }
+    const int i_last = min(P.nq, (int)(blockIdx.x + 1) * kSimtRows) - 1;
+    const int jend = P.causal ? min(P.nk, i_last + 1) : P.nk;
+    for (int j0 = 0; j0 < jend; j0 += kSimtKT) {
+        simt_stage_keys<T, D>(P, b, h, j0, sK, sV, sB, sKM);
+        __syncthreads();
+        const int cnt = min(kSimtKT, jend - j0);
+        bool any = false;
+        for (int jj = 0; jj < cnt; ++jj) any |= bias_class(sB[jj]) == 1 && sKM[jj];
+        if (any && dg) {
+            for (int jj = 0; jj < cnt; ++jj) {
+                const int j = j0 + jj;
+                if (bias_class(sB[jj]) != 1 || !sKM[jj] || (P.causal && j > i)) continue;
+                float s = 0.f, dp = 0.f;
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    s += q[d] * sK[jj][d];
+                    dp += go[d] * sV[jj][d];
+                }
+                const float y = softclamp_f(s * P.scale, P.softclamp);
+                const float g = ic * (dp - Dp) * softclamp_grad(y, P.softclamp) * P.scale;
+#pragma unroll
+                for (int d = 0; d < D; ++d) dq[d] += g * sK[jj][d];
+            }
+        }
+        __syncthreads();
+    }
+    if (!dg) return;
+    T* o = G.dq.wrow<T>(b, h, i);
+    for (int d = 0; d < D; ++d) o[d] = from_f<T>(to_f(o[d]) + dq[d]);
+}
+
+// Part B, key side: dK, dV (dvmul) and dbias of the unmasked bias-class-1 keys from the
+// fully-masked kept rows of every query head of the group (one lane per key).
+template <typename T, int D>
+__global__ __launch_bounds__(kSimtRows) void k_fix_keys_b(GradDev G) {
+    const PassDev& P = G.f;
+    __shared__ float sQ[kSimtKT][D];
+    __shared__ float sO[kSimtKT][D];
+    __shared__ float sL[kSimtKT], sI[kSimtKT], sD[kSimtKT];
+    const int b = blockIdx.z, kh = blockIdx.y;
+    if (G.ws_kcnt[2 * ((int64_t)b * G.hk + kh) + 1] == 0) return;
+    const int rep = P.heads / G.hk, h0 = kh * rep;
+    const int j = blockIdx.x * kSimtRows + threadIdx.x;
+    const bool mine = j < P.nk && P.km.keep(b, j) && bias_class(P.bias.scalar(b, h0, j)) == 1;
+    if (!__syncthreads_or(mine)) return;
+    float kk[D], vv[D], dk[D], dv[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        float kv = 0.f, v = 0.f;
+        if (mine) {
+            kv = to_f(P.k.row<T>(b, h0, j)[d]);
+            v = to_f(P.v.row<T>(b, h0, j)[d]);
+            if (P.vmul.ok()) v = round_to<T>(v * to_f(P.vmul.row<T>(b, h0, j)[d]));
+        }
+        kk[d] = kv;
+        vv[d] = v;
+        dk[d] = 0.f;
+        dv[d] = 0.f;
+    }
+    float dbias = 0.f;
+    const int j_first = blockIdx.x * kSimtRows;
+    for (int h = h0; h < h0 + rep; ++h) {
+        if (G.ws_part[((int64_t)b * P.heads + h) * (D + 2) + D + 1] == 0.f) continue;
+        for (int i0 = 0; i0 < P.nq; i0 += kSimtKT) {
+            const int cnt = min(kSimtKT, P.nq - i0);
+            if (P.causal && i0 + cnt - 1 < j_first) continue;  // every row precedes these keys
+            for (int ii = threadIdx.x; ii < kSimtKT; ii += blockDim.x) {
+                const int i = i0 + ii;
+                const int64_t r = ((int64_t)b * P.heads + h) * P.nq + i;
+                const bool dg = i < P.nq && degenerate_row(G, r) && P.qm.keep(b, i);
+                sL[ii] = dg ? 1.f : 0.f;
+                sI[ii] = dg ? G.ws_invc[r] : 0.f;
+                sD[ii] = dg ? G.ws_D[r] : 0.f;
+            }
+            __syncthreads();
+            bool any = false;
+            for (int ii = 0; ii < cnt; ++ii) any |= sL[ii] != 0.f;
+            if (any) {
+                for (int e = threadIdx.x; e < kSimtKT * D; e += blockDim.x) {
+                    const int ii = e / D, d = e % D, i = i0 + ii;
+                    const bool ok = i < P.nq;
+                    sQ[ii][d] = ok ? to_f(P.q.row<T>(b, h, i)[d]) : 0.f;
+                    sO[ii][d] = ok ? to_f(G.dout.row<T>(b, h, i)[d]) : 0.f;
+                }
+            }
+            __syncthreads();
+            if (any && mine) {
+                for (int ii = 0; ii < cnt; ++ii) {
+                    if (sL[ii] == 0.f || (P.causal && j > i0 + ii)) continue;
+                    float s = 0.f, dp = 0.f;
+#pragma unroll
+                    for (int d = 0; d < D; ++d) {
+                        s += sQ[ii][d] * kk[d];
+                        dp += sO[ii][d] * vv[d];
+                    }
+                    const float y = softclamp_f(s * P.scale, P.softclamp);
+                    const float ds = sI[ii] * (dp - sD[ii]);
+                    const float g = ds * softclamp_grad(y, P.softclamp) * P.scale;
+                    dbias += ds;
+#pragma unroll
+                    for (int d = 0; d < D; ++d) {
+                        dv[d] += sI[ii] * sO[ii][d];
+                        dk[d] += g * sQ[ii][d];
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (!mine) return;
+    {
+        T* o = G.dk.wrow<T>(b, h0, j);
+        for (int d = 0; d < D; ++d) o[d] = from_f<T>(to_f(o[d]) + dk[d]);
+    }
+    {
+        T* o = G.dv.wrow<T>(b, h0, j);
+        const T* mul = P.vmul.ok() ? P.vmul.row<T>(b, h0, j) : nullptr;
+        for (int d = 0; d < D; ++d) o[d] = from_f<T>(to_f(o[d]) + (mul ? dv[d] * to_f(mul[d]) : dv[d]));
+    }
+    if (P.vmul.ok()) {
+        T* o = G.dvmul.wrow<T>(b, h0, j);
+        const T* v = P.v.row<T>(b, h0, j);
+        for (int d = 0; d < D; ++d) o[d] = from_f<T>(to_f(o[d]) + dv[d] * to_f(v[d]));
+    }
+    if (G.dbias.ok()) *G.dbias.wrow<float>(b, h0, j) += dbias;
+}
+
+// ---------------------------------------------------------------------------------------
 // launchers
 
 template <typename T, int D>
@@ -435,10 +873,9 @@ static void launch_simt_fwd_t(const PassDev& P, hipStream_t s) {
     hipLaunchKernelGGL((k_simt_fwd<T, D>), grid, dim3(kSimtRows), 0, s, P);
 }
 template <typename T, int D>
-static void launch_simt_fixup_t(const PassDev& P, hipStream_t s) {
-    dim3 grid((P.nq + kSimtRows - 1) / kSimtRows, P.heads, P.batch);
-    ProfScope ps("simt_fixup", s);
-    hipLaunchKernelGGL((k_simt_fixup<T, D>), grid, dim3(kSimtRows), 0, s, P);
+static void launch_fwd_fixup_t(const PassDev& P, hipStream_t s) {
+    ProfScope ps("fwd_fixup", s);
+    hipLaunchKernelGGL((k_fwd_fixup<T, D>), dim3(P.heads, P.batch), dim3(kFixThreads), 0, s, P);
 }
 template <typename T, int D>
 static void launch_simt_bwd_t(const GradDev& G, hipStream_t s, bool pre, bool dq, bool dkv) {
@@ -479,16 +916,8 @@ static void launch_simt_bwd_t(const GradDev& G, hipStream_t s, bool pre, bool dq
 }
 
 template <typename T>
-static void simt_fwd_d(const PassDev& P, hipStream_t s, bool fixup) {
+static void simt_fwd_d(const PassDev& P, hipStream_t s) {
     const int d = P.dim;
-    if (fixup) {
-        if (d <= 16) launch_simt_fixup_t<T, 16>(P, s);
-        else if (d <= 32) launch_simt_fixup_t<T, 32>(P, s);
-        else if (d <= 64) launch_simt_fixup_t<T, 64>(P, s);
-        else if (d <= 128) launch_simt_fixup_t<T, 128>(P, s);
-        else launch_simt_fixup_t<T, 256>(P, s);
-        return;
-    }
     if (d <= 16) launch_simt_fwd_t<T, 16>(P, s);
     else if (d <= 32) launch_simt_fwd_t<T, 32>(P, s);
     else if (d <= 64) launch_simt_fwd_t<T, 64>(P, s);
@@ -506,15 +935,47 @@ static void simt_bwd_d(const GradDev& G, hipStream_t s, bool pre, bool dq, bool 
     else launch_simt_bwd_t<T, 256>(G, s, pre, dq, dkv);
 }
 
-void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s) {
-    if (dtype == PA_F32) simt_fwd_d<float>(P, s, false);
-    else if (dtype == PA_F16) simt_fwd_d<f16>(P, s, false);
-    else simt_fwd_d<bf16>(P, s, false);
+template <typename T, int D>
+static void launch_mask_fixups_t(const GradDev& G, hipStream_t s) {
+    const PassDev& P = G.f;
+    {
+        ProfScope ps("fix_rows", s);
+        hipLaunchKernelGGL((k_fix_rows<T, D>), dim3(P.heads, P.batch), dim3(kFixThreads), 0, s, G);
+    }
+    {
+        ProfScope ps("fix_keys", s);
+        const dim3 grid((P.nk + kFixKeys - 1) / kFixKeys, G.hk, P.batch);
+        hipLaunchKernelGGL((k_fix_keys<T, D>), grid, dim3(256), 0, s, G);
+    }
+    if (P.bias.ok()) {  // part B needs keys of bias class 1
+        ProfScope ps("fix_part_b", s);
+        const dim3 qgrid((P.nq + kSimtRows - 1) / kSimtRows, P.heads, P.batch);
+        const dim3 kgrid((P.nk + kSimtRows - 1) / kSimtRows, G.hk, P.batch);
+        hipLaunchKernelGGL((k_fix_rows_b<T, D>), qgrid, dim3(kSimtRows), 0, s, G);
+        hipLaunchKernelGGL((k_fix_keys_b<T, D>), kgrid, dim3(kSimtRows), 0, s, G);
+    }
 }
-void launch_simt_fixup(const PassDev& P, int dtype, hipStream_t s) {
-    if (dtype == PA_F32) simt_fwd_d<float>(P, s, true);
-    else if (dtype == PA_F16) simt_fwd_d<f16>(P, s, true);
-    else simt_fwd_d<bf16>(P, s, true);
+
+void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, hipStream_t s) {
+    ProfScope ps("key_terms", s);
+    hipLaunchKernelGGL(k_key_terms, dim3(G.hk, G.f.batch), dim3(256), 0, s, G, kterm, nkp, kcnt);
+}
+
+void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s) {
+    const bool d64 = G.f.dim == 64;
+    if (dtype == PA_F16) d64 ? launch_mask_fixups_t<f16, 64>(G, s) : launch_mask_fixups_t<f16, 128>(G, s);
+    else d64 ? launch_mask_fixups_t<bf16, 64>(G, s) : launch_mask_fixups_t<bf16, 128>(G, s);
+}
+
+void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s) {
+    if (dtype == PA_F32) simt_fwd_d<float>(P, s);
+    else if (dtype == PA_F16) simt_fwd_d<f16>(P, s);
+    else simt_fwd_d<bf16>(P, s);
+}
+void launch_fwd_fixup(const PassDev& P, int dtype, hipStream_t s) {
+    const bool d64 = P.dim == 64;
+    if (dtype == PA_F16) d64 ? launch_fwd_fixup_t<f16, 64>(P, s) : launch_fwd_fixup_t<f16, 128>(P, s);
+    else d64 ? launch_fwd_fixup_t<bf16, 64>(P, s) : launch_fwd_fixup_t<bf16, 128>(P, s);
 }
 void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool dq, bool dkv) {
     if (dtype == PA_F32) simt_bwd_d<float>(G, s, pre, dq, dkv);

@@ -115,6 +115,55 @@ def test_pass_masks_and_degenerate_rows(dtype, causal):
           f"masks {dtype} causal={causal}")
 
 
+@param("dtype", (torch.bfloat16, torch.float16))
+@param("d", (64, 128))
+@param("n", (150, 256))
+@param("causal", (False, True))
+@param("gqa", (False, True))
+def test_pass_masked_mfma_head_dims(dtype, d, n, causal, gqa):
+    """Masked passes at the MFMA head dims (the backward's normal rows on the MFMA kernels, the
+    fully-masked rows added by the fix-ups), forward and all gradients:
+    * leading keys masked: causal rows 0-2 fully masked (class-1 keys all masked ones);
+    * batch 1, keys 3-5 biased to -finfo.max (bias class 1): causal rows 3-5 fully masked with
+      unmasked class-1 keys; non-causal, every other key of batch 1 masked as well, so every
+      row of batch 1 is fully masked the same way;
+    * a -inf bias entry (class 2) and query-masked rows (uniform over the bias-class-0 keys);
+    * gqa: 4 query heads over 2 key heads with a value multiplier (a middle chain level).
+    n = 150 leaves a key count that is not a multiple of 4 (row-padded key terms)."""
+    B, H, HK = 2, 4, (2 if gqa else 4)
+    q = randn((B, H, n, d), dtype, 31)
+    k, v = (randn((B, HK, n, d), dtype, s) for s in (32, 33))
+    vmul = randn((B, HK, n, d), dtype, 34) if gqa else None
+    bias = torch.log(torch.arange(1, n + 1).float())[None, None].repeat(B, HK, 1)
+    bias = bias + randn((B, HK, n), torch.float32, 35)
+    fmax = torch.finfo(torch.float32).max
+    km = torch.ones(B, n, dtype=torch.bool)
+    qm = torch.ones(B, n, dtype=torch.bool)
+    km[:, :3] = False
+    km[0, n // 2:n // 2 + 20] = False
+    bias[1, :, 3:6] = -fmax
+    bias[0, 0, 10] = -float("inf")
+    qm[0, -7:] = False
+    if not causal:
+        km[1, 6:] = False
+    res = run_pass(q, k, v, vmul=vmul, bias=bias, key_mask=km, query_mask=qm, causal=causal)
+    check(res, dtype, f"masked mfma {dtype} d={d} n={n} causal={causal} gqa={gqa}")
+
+
+@param("causal", (False, True))
+def test_pass_masked_mfma_key_mask_only(causal):
+    """A key mask with no bias (the first pass of a masked chain): the key mask becomes the
+    MFMA kernels' only key term; batch 1 masks every key (every row fully masked)."""
+    dtype, n = torch.bfloat16, 200
+    q, k, v = (randn((2, 4, n, 64), dtype, s) for s in (41, 42, 43))
+    km = torch.ones(2, n, dtype=torch.bool)
+    km[0, ::5] = False
+    km[0, :2] = False
+    km[1] = False
+    check(run_pass(q, k, v, key_mask=km, causal=causal), dtype,
+          f"masked mfma key mask only causal={causal}")
+
+
 @param("dtype", (torch.float32, torch.bfloat16))
 def test_pass_cross_lengths(dtype):
     """Different query and key lengths (contexts), causal with a top-left aligned mask."""
