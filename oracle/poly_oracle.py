@@ -8,6 +8,8 @@ import it, and only as the checker (or the timed CPU baseline); the product path
 Contents and what pins each function (see tests/test_oracle.py):
   reference_poly_attention   poly_attention.py:48-116  -- brute_order2 (pair-softmax closed
                              form, fp64), per-pass SDPA with a float bias, gradcheck
+  order2_rows                the same for chosen query rows of one long slice (chunked pass 1)
+                             -- equal to reference_poly_attention and its autograd dq1
   attn_pass                  one level: n_poly_attention.py:237-261 + :272-275 -- SDPA,
                              brute force, the finite-fill class semantics of masked rows
   n_poly_core                n_poly_attention.py:233-313 -- brute_order3 / brute_order_n
@@ -193,6 +195,50 @@ def n_poly_core(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs_full: Se
     s12 = add_key_bias(lse_full, scores[0])  # :307
     out = einsum("b h i j, b h j d -> b h i d", s12.softmax(dim=-1), msg_full)  # :311-313
     return out, lses, msgs
+
+
+def order2_rows(q1: Tensor, q2: Tensor, q3: Tensor, v3: Tensor, rows: Tensor,
+                dout_rows: Optional[Tensor] = None, causal: bool = True,
+                softclamp_value: Optional[float] = None, chunk: int = 1024):
+    """reference_poly_attention (poly_attention.py:48-116, no cache, no masks) for one
+    (batch, head) slice at lengths where the N x N score matrix does not fit: pass 1 runs over
+    every pass-1 row in chunks of ``chunk`` rows (its msg / lse23 feed every pass-2 key), pass 2
+    only for the query rows ``rows``.  q* / v3: [N, d].  Returns (out[rows], msg, lse23) and,
+    with the upstream gradient of those rows, also dq1[rows] (the pass-2 score gradient, which
+    involves only the row itself: dS = P (dP - rowsum(dO * O)), dq1 = scale * dS q2 through the
+    softclamp's derivative)."""
+    n, d = q1.shape
+    scale = d ** -0.5
+    mask_value = -torch.finfo(q1.dtype).max
+    msg = torch.empty_like(v3)
+    lse23 = torch.empty(n, dtype=q1.dtype)
+    for i0 in range(0, n, chunk):
+        i1 = min(n, i0 + chunk)
+        kend = i1 if causal else n
+        sim = (q2[i0:i1] @ q3[:kend].T) * scale
+        if exists(softclamp_value):
+            sim = softclamp(sim, softclamp_value)
+        if causal:
+            later = torch.arange(kend)[None, :] > torch.arange(i0, i1)[:, None]
+            sim = sim.masked_fill(later, mask_value)
+        lse23[i0:i1] = sim.logsumexp(dim=-1)
+        msg[i0:i1] = sim.softmax(dim=-1) @ v3[:kend]
+    raw = (q1[rows] @ q2.T) * scale
+    sim = softclamp(raw, softclamp_value) if exists(softclamp_value) else raw
+    if causal:
+        sim = sim.masked_fill(torch.arange(n)[None, :] > rows[:, None], mask_value)
+    sim = sim + lse23[None, :]
+    attn = sim.softmax(dim=-1)
+    out = attn @ msg
+    if dout_rows is None:
+        return out, msg, lse23
+    dsim = attn * (dout_rows @ msg.T - (dout_rows * out).sum(-1, keepdim=True))
+    if exists(softclamp_value):
+        dsim = dsim * (1 - torch.tanh(raw / softclamp_value) ** 2)
+    if causal:
+        dsim = dsim.masked_fill(torch.arange(n)[None, :] > rows[:, None], 0.0)
+    dq1 = (dsim @ q2) * scale
+    return out, msg, lse23, dq1
 
 
 # ---------------------------------------------------------------------------------------

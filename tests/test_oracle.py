@@ -38,6 +38,33 @@ def test_order2_matches_pair_softmax(causal, softclamp, n):
     np.testing.assert_allclose(out.numpy(), ref, rtol=1e-10, atol=1e-10)
 
 
+@param("causal", (False, True))
+@param("softclamp", (None, 3.0))
+def test_order2_rows_equals_full_core_and_its_dq1(causal, softclamp):
+    """The chunked row-restricted form used at long lengths: out, msg, lse23 and dq1 of chosen
+    rows equal reference_poly_attention and its autograd (chunks that do not divide N), and
+    the brute-force pair softmax."""
+    n, d = 37, 8
+    q1, q2, q3, v3 = (rnd(n, d, seed=40 + s) for s in range(4))
+    rows = torch.tensor([0, 5, 17, 36])
+    dout = rnd(len(rows), d, seed=45)
+    out, msg, lse23, dq1 = O.order2_rows(q1, q2, q3, v3, rows, dout_rows=dout, causal=causal,
+                                         softclamp_value=softclamp, chunk=10)
+    q = [t[None, None].clone().requires_grad_() for t in (q1, q2, q3, v3)]
+    ref, lse_r, msg_r = O.reference_poly_attention(q[0], q[1], q[1], q[2], q[3], causal=causal,
+                                                   softclamp_value=softclamp)
+    g = torch.zeros_like(ref)
+    g[0, 0, rows] = dout
+    ref.backward(g)
+    torch.testing.assert_close(out, ref[0, 0, rows].detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(msg, msg_r[0, 0].detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(lse23, lse_r[0, 0].detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(dq1, q[0].grad[0, 0, rows], rtol=1e-10, atol=1e-10)
+    brute = O.brute_order2(q1[None, None], q2[None, None], q3[None, None], v3[None, None],
+                           causal=causal, softclamp_value=softclamp)
+    np.testing.assert_allclose(out.numpy(), brute[0, 0, rows.numpy()], rtol=1e-10, atol=1e-10)
+
+
 def test_order2_brute_force_detects_dropped_bias():
     # planting a mistake in the oracle (no lse bias in pass 2) must break the pin
     q1, q2, q3, v3 = (rnd(1, 2, 6, 8, seed=10 + s) for s in range(4))
