@@ -767,7 +767,7 @@ def main():
                 "traffic": measured_traffic(dominant), "avg_ms": round(avg_ms, 4)}
     log(f"[bench] kernels: {kernels}")
 
-    module_ms = None
+    module_ms = module_epi_ms = None
     module_kernels = None
     if not args.no_module:
         module_ms = time_steps(lambda: module_step(m, x, dx), max(3, args.steps // 2), 2)
@@ -786,6 +786,15 @@ def main():
                 rec["GB_per_s"] = round(moved / (t / n_l / 1e3) / 1e9, 1)
             module_kernels[k] = rec
         log(f"[bench] module kernels {module_kernels}")
+        # the same module with the root-value / gate epilogue (fused into pass 2)
+        from poly_attention import PolyAttention
+
+        torch.manual_seed(0)
+        me = PolyAttention(dim=DIM, heads=H, dim_head=DH, causal=True, multiply_root_value=True,
+                           attn_gate=True).to(dev, torch.bfloat16)
+        module_epi_ms = time_steps(lambda: module_step(me, x, dx), max(3, args.steps // 2), 2)
+        log(f"[bench] module with root value + gate fwd+bwd {module_epi_ms:.3f} ms/step")
+        del me
     masked = None
     if not args.no_masked:
         masked = masked_core_bench(qs, dout, max(3, args.steps // 2), 2)
@@ -847,6 +856,7 @@ def main():
         "kernels": kernels,
         "masked_core": masked,
         "module_ms_per_step": round(module_ms, 4) if module_ms else None,
+        "module_root_value_gate_ms_per_step": round(module_epi_ms, 4) if module_epi_ms else None,
         "module_kernels": module_kernels,
         "cpu_baseline": cpu,
         "decode": decode,

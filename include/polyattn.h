@@ -10,7 +10,9 @@
  *   pa_attn_pass_fwd   one level of reference_poly_attention / NPolyAttention scores+aggregation
  *                      (poly_attention/poly_attention.py:48-116, n_poly_attention.py:233-313);
  *                      the Triton launch it stands in for is _poly_flash_fwd_kernel
- *                      (flash_poly_attention.py:12-154, launched at :347 and :365).
+ *                      (flash_poly_attention.py:12-154, launched at :347 and :365); with
+ *                      pa_pass.epi also the modules' root-value / gate epilogue
+ *                      (poly_attention.py:342-351, n_poly_attention.py:315-326).
  *   pa_attn_pass_bwd   the backward of one level (flash_poly_attention.py:156-316, launched at
  *                      :409 and :429 inside PolyFlashAttention.backward :386-446).
  *   pa_poly_decode     the cached single-token step of Order2PolyAttention.forward
@@ -48,7 +50,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 4
+#define PA_ABI_VERSION 5
 #define PA_MAX_ORDER 8
 
 /* status codes (0 = success, negative = failure) */
@@ -88,6 +90,25 @@ typedef struct pa_mask {
     int64_t sb, sn;
 } pa_mask;
 
+/* pa_epilogue.flags */
+#define PA_EPI_ROOT_SIGMOID 1   /* the root factor is sigmoid(root) (use_root_value_as_attn_gate) */
+
+/* The modules' epilogue of the final level, applied where the pass stores its output
+ * (replaces the element-wise tail of poly_attention.py:342-351 and n_poly_attention.py:
+ * 315-326):
+ *   y = round(round(r * out) * round(sigmoid(gate))),   r = root, or round(sigmoid(root))
+ * with every product and sigmoid rounded to the pass dtype in the order torch evaluates
+ * `v2 * out` then `out * gates.sigmoid()`; an absent root or gate drops its factor.  The pass
+ * still writes `out` (the backward needs it).  In the backward (pa_pass_grad) `dout` is then
+ * the gradient reaching y, and droot / dgate receive the epilogue's input gradients (droot
+ * summed over the heads sharing one root head). */
+typedef struct pa_epilogue {
+    pa_view root;         /* optional [B, hr, nq, dim], dtype of q; hr divides heads */
+    pa_view gate;         /* optional [B, heads, nq, dim] */
+    pa_view y;            /* [B, heads, nq, dim] */
+    int32_t flags;        /* PA_EPI_* */
+} pa_epilogue;
+
 /* One attention pass (one level of the poly chain). */
 typedef struct pa_pass {
     int32_t batch, heads, nq, nk, dim;
@@ -102,13 +123,14 @@ typedef struct pa_pass {
     pa_mask query_mask;   /* optional [B, nq] */
     pa_view out;          /* [B, heads, nq, dim], dtype of q */
     pa_view lse;          /* [B, heads, nq], PA_F32 */
+    const pa_epilogue* epi;  /* optional module epilogue (NULL: none) */
 } pa_pass;
 
 /* Backward of one pass.  In the backward the key-side tensors (k, v, vmul, bias) must share
  * one head count hk; their gradients are summed over the heads/hk query heads of a group. */
 typedef struct pa_pass_grad {
     pa_pass fwd;          /* forward description, with out and lse as written by the forward */
-    pa_view dout;         /* [B, heads, nq, dim] */
+    pa_view dout;         /* [B, heads, nq, dim]; with fwd.epi the gradient of the epilogue's y */
     pa_view dlse;         /* optional fp32 [B, heads, nq]: gradient reaching lse */
     pa_view dq, dk, dv;   /* dq like q; dk, dv like k, v */
     pa_view dvmul;        /* required iff fwd.vmul is given */
@@ -116,6 +138,8 @@ typedef struct pa_pass_grad {
     int32_t accumulate;   /* PA_ACC_* bits */
     void*   workspace;
     size_t  workspace_bytes;
+    pa_view droot;        /* with fwd.epi: required iff it has a root; like root */
+    pa_view dgate;        /* with fwd.epi: required iff it has a gate; like gate */
 } pa_pass_grad;
 
 /* One level of a cached single-token decode step (see pa_poly_decode). */
@@ -273,7 +297,7 @@ const char* pa_strerror(int status);
 int         pa_last_hip_error(void);   /* hipError_t of the last PA_EHIP on this thread */
 /* sizeof of the ABI structs, for binding checks: 0 pa_view, 1 pa_mask, 2 pa_pass,
  * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode, 6 pa_prologue_item, 7 pa_prologue,
- * 8 pa_rmsnorm, 9 pa_linear, 10 pa_linear_out; 0 for other values */
+ * 8 pa_rmsnorm, 9 pa_linear, 10 pa_linear_out, 11 pa_epilogue; 0 for other values */
 size_t      pa_struct_size(int which);
 
 /* Kernel timing (no counterpart in the reference: a measurement facility for benchmarks).

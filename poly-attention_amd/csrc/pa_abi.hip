@@ -96,6 +96,14 @@ int validate_pass(const pa_pass* p) {
     PA_TRY(check_view(p->out, p->heads, true, T));
     PA_TRY(check_view(p->lse, p->heads, true, PA_F32));
     if (p->out.heads != p->heads || p->lse.heads != p->heads) return PA_EINVAL;
+    if (p->epi) {
+        const pa_epilogue* e = p->epi;
+        PA_TRY(check_view(e->root, p->heads, false, T));
+        PA_TRY(check_view(e->gate, p->heads, false, T));
+        PA_TRY(check_view(e->y, p->heads, true, T));
+        if (e->y.heads != p->heads || (e->gate.ptr && e->gate.heads != p->heads)) return PA_EINVAL;
+        if (e->flags & ~PA_EPI_ROOT_SIGMOID) return PA_EINVAL;
+    }
     return PA_OK;
 }
 
@@ -119,6 +127,12 @@ PassDev to_passdev(const pa_pass* p) {
     P.lse = to_dview(p->lse, p->heads);
     P.km = to_dmask(p->key_mask);
     P.qm = to_dmask(p->query_mask);
+    const pa_view none = {};
+    const pa_epilogue* e = p->epi;
+    P.er = to_dview(e ? e->root : none, p->heads);
+    P.eg = to_dview(e ? e->gate : none, p->heads);
+    P.ey = to_dview(e ? e->y : none, p->heads);
+    P.eflags = e ? e->flags : 0;
     return P;
 }
 
@@ -140,11 +154,15 @@ bool pass_masked(const pa_pass& f) {
 // key-term row stride: whole 16-byte chunks
 int key_term_stride(const pa_pass& f) { return (f.nk + 3) & ~3; }
 
-// [D | lse | 1/c1] per query row; masked passes add the key term (with a key mask), the
-// per-head fully-masked-row sums and the per-key-head bias-class counts
+size_t elem_bytes(int dtype) { return dtype == PA_F32 ? 4 : 2; }
+
+// [D | lse | 1/c1] per query row; with an epilogue the gradient reaching the pass output;
+// masked passes add the key term (with a key mask), the per-head fully-masked-row sums and
+// the per-key-head bias-class counts
 size_t bwd_ws_bytes(const pa_pass& f) {
     const size_t rows = (size_t)f.batch * f.heads * f.nq;
     size_t n = 3 * align256(rows * sizeof(float));
+    if (f.epi) n += align256(rows * f.dim * elem_bytes(f.q.dtype));
     if (pass_masked(f)) {
         const size_t kheads = (size_t)f.batch * f.k.heads;
         if (f.key_mask.ptr) n += align256(kheads * key_term_stride(f) * sizeof(float));
@@ -189,6 +207,7 @@ size_t pa_struct_size(int which) {
         case 8: return sizeof(pa_rmsnorm);
         case 9: return sizeof(pa_linear);
         case 10: return sizeof(pa_linear_out);
+        case 11: return sizeof(pa_epilogue);
         default: return 0;
     }
 }
@@ -279,6 +298,12 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
     if (g->dvmul.ptr && g->dvmul.heads != hk) return PA_EINVAL;
     if (g->dbias.ptr && g->dbias.heads != hk) return PA_EINVAL;
     if (g->dlse.ptr && g->dlse.heads != H) return PA_EINVAL;
+    if (p->epi) {
+        PA_TRY(check_view(g->droot, H, p->epi->root.ptr != nullptr, T));
+        PA_TRY(check_view(g->dgate, H, p->epi->gate.ptr != nullptr, T));
+        if (g->droot.ptr && g->droot.heads != p->epi->root.heads) return PA_EINVAL;
+        if (g->dgate.ptr && g->dgate.heads != H) return PA_EINVAL;
+    }
     const size_t need = bwd_ws_bytes(*p);
     if (!g->workspace || g->workspace_bytes < need) return PA_EWORKSPACE;
 
@@ -298,8 +323,27 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
     G.ws_D = reinterpret_cast<float*>(ws);
     G.ws_lse = reinterpret_cast<float*>(ws + align256(rows * sizeof(float)));
     G.ws_invc = reinterpret_cast<float*>(ws + 2 * align256(rows * sizeof(float)));
+    ws += 3 * align256(rows * sizeof(float));
+    const pa_view none = {};
+    G.droot = to_dview(p->epi ? g->droot : none, H);
+    G.dgate = to_dview(p->epi ? g->dgate : none, H);
 
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (p->epi) {
+        // the epilogue's gradients, and the gradient reaching the pass output (dO) in the
+        // workspace, which the pass backward then reads as its dout
+        char* dO = ws;
+        ws += align256(rows * p->dim * elem_bytes(T));
+        const int hr = p->epi->root.ptr ? p->epi->root.heads : H;
+        launch_epi_bwd(G, dO, hr, T, s);
+        DView& d = G.dout;
+        d.p = dO;
+        d.sn = p->dim;
+        d.sh = (int64_t)p->nq * p->dim;
+        d.sb = (int64_t)H * d.sh;
+        d.hdiv = 1;
+        d.dtype = T;
+    }
     G.fused_pre = 0;
     G.seeds = 0;
     G.ws_kcnt = nullptr;
@@ -307,7 +351,7 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
     if (mfma_bwd_supported(G, T) && pass_masked(*p)) {
         // normal rows on the MFMA kernels with the key mask folded into the key bias; the
         // preprocess marks fully-masked rows (lse = +inf), whose part the fix-ups add
-        char* w = ws + 3 * align256(rows * sizeof(float));
+        char* w = ws;
         float* kterm = nullptr;
         const int nkp = key_term_stride(*p);
         if (p->key_mask.ptr) {

@@ -73,11 +73,14 @@ struct PassDev {
     int32_t causal, flags;
     DView q, k, v, vmul, bias, out, lse;
     DMask km, qm;
+    DView er, eg, ey;  // module epilogue: root, gate, y (ey absent: no epilogue)
+    int32_t eflags;    // PA_EPI_*
 };
 
 struct GradDev {
     PassDev f;
     DView dout, dlse, dq, dk, dv, dvmul, dbias;
+    DView droot, dgate;    // epilogue input gradients (with f.ey)
     int32_t accumulate;
     int32_t hk;            // key-side head count (k, v, vmul, bias share it)
     float* ws_D;           // [B, heads, nq]  rowsum(dO * O) - dlse
@@ -91,6 +94,26 @@ struct GradDev {
     float* ws_part;          // [B, heads, dim + 2]: over the fully-masked rows of a head,
                              // sum dO / c1, sum D / c1 and their number
 };
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+
+// The module epilogue of one output element o (already rounded to T) from its raw root and
+// gate values, in torch's order: t = round(r * o) with r = root or round(sigmoid(root)),
+// y = round(t * round(sigmoid(gate))); an absent factor is skipped.
+template <typename T>
+__device__ __forceinline__ float epi_combine(float o, float root, float gate, bool has_r,
+                                             bool has_g, bool sig) {
+    float t = o;
+    if (has_r) t = round_to<T>((sig ? round_to<T>(sigmoid_f(root)) : root) * t);
+    if (has_g) t = round_to<T>(t * round_to<T>(sigmoid_f(gate)));
+    return t;
+}
+template <typename T>
+__device__ __forceinline__ float epi_y(const PassDev& P, int b, int h, int64_t i, int d, float o) {
+    const float r = P.er.ok() ? to_f(P.er.row<T>(b, h, i)[d]) : 0.f;
+    const float g = P.eg.ok() ? to_f(P.eg.row<T>(b, h, i)[d]) : 0.f;
+    return epi_combine<T>(o, r, g, P.er.ok(), P.eg.ok(), (P.eflags & PA_EPI_ROOT_SIGMOID) != 0);
+}
 
 // class of a bias value in the finite-fill arithmetic: 0 normal, 1 = -FLT_MAX, 2 = -inf
 __device__ __forceinline__ int bias_class(float x) {

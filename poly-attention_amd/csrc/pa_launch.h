@@ -17,6 +17,9 @@ struct ProfScope {
 
 // generic (one lane per row) kernels: every dtype, head dim <= 256, every mask feature
 void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s);
+// the epilogue backward: dO (contiguous [B, heads, nq, dim]) and G.droot / G.dgate from the
+// gradient of y in G.dout; hr = the root's head count (the pass head count without a root)
+void launch_epi_bwd(const GradDev& G, void* dO, int hr, int dtype, hipStream_t s);
 // finish the fully-masked rows of an MFMA forward (head dim 64 or 128)
 void launch_fwd_fixup(const PassDev& P, int dtype, hipStream_t s);
 void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool dq, bool dkv);

@@ -103,6 +103,40 @@ __device__ __forceinline__ KeySide<T> key_side(const PassDev& P, int b, int h) {
     return s;
 }
 
+// The module epilogue (pa_pass.epi) at one lane's output store: the lane holds 4 * NG outputs
+// of row qi, 4 consecutive columns from d = (k / 4) * 32 + (k % 4) * 8 + 4 * hh for k < NG,
+// rounded and packed in o[k].  Every root and gate word is loaded before any is used: the
+// store is the kernel's tail, where a load per element would serialise on memory latency.
+template <typename T, int NG>
+__device__ __forceinline__ void epi_store_lane(const PassDev& P, int b, int h, int qi, int hh,
+                                               const u32x2_t (&o)[NG]) {
+    const bool has_r = P.er.ok(), has_g = P.eg.ok();
+    const bool sig = (P.eflags & PA_EPI_ROOT_SIGMOID) != 0;
+    const T* rrow = has_r ? P.er.row<T>(b, h, qi) : nullptr;
+    const T* grow = has_g ? P.eg.row<T>(b, h, qi) : nullptr;
+    u32x2_t r[NG], g[NG];
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+        const int d = (k / 4) * 32 + (k % 4) * 8 + 4 * hh;
+        r[k] = has_r ? *reinterpret_cast<const u32x2_t*>(rrow + d) : o[k];
+        g[k] = has_g ? *reinterpret_cast<const u32x2_t*>(grow + d) : o[k];
+    }
+    T* yrow = P.ey.wrow<T>(b, h, qi);
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+        const int d = (k / 4) * 32 + (k % 4) * 8 + 4 * hh;
+        const T* o4 = reinterpret_cast<const T*>(&o[k]);
+        const T* r4 = reinterpret_cast<const T*>(&r[k]);
+        const T* g4 = reinterpret_cast<const T*>(&g[k]);
+        u32x2_t y4;
+        T* y = reinterpret_cast<T*>(&y4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            y[e] = from_f<T>(epi_combine<T>(to_f(o4[e]), to_f(r4[e]), to_f(g4[e]), has_r, has_g, sig));
+        *reinterpret_cast<u32x2_t*>(yrow + d) = y4;
+    }
+}
+
 // Registers holding one K tile and one V tile (+ key bias) between global load and LDS store.
 template <int D, int KB>
 struct FwdStage {
@@ -431,17 +465,19 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
     const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
     const float inv = degenerate ? 0.f : 1.f / l;
     T* orow = P.out.wrow<T>(b, h, qi);
+    u32x2_t pk[D / 8];
 #pragma unroll
     for (int x = 0; x < D / 32; ++x) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d = x * 32 + 8 * g + 4 * wv.hh;
-            u32x2_t pk;
-            pk[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
-            pk[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
-            *reinterpret_cast<u32x2_t*>(orow + d) = pk;
+            u32x2_t& p = pk[4 * x + g];
+            p[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
+            p[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
+            *reinterpret_cast<u32x2_t*>(orow + d) = p;
         }
     }
+    if (P.ey.ok()) epi_store_lane<T, D / 8>(P, b, h, qi, wv.hh, pk);
     if (wv.hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
 }
 
@@ -787,17 +823,19 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
             const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
             const float inv = degenerate ? 0.f : 1.f / l;
             T* orow = P.out.wrow<T>(b, h, qi);
+            u32x2_t pk[D / 8];
 #pragma unroll
             for (int x = 0; x < D / 32; ++x) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int d = x * 32 + 8 * g + 4 * hh;
-                    u32x2_t pk;
-                    pk[0] = pack2<T>(v.o[x][4 * g] * inv, v.o[x][4 * g + 1] * inv);
-                    pk[1] = pack2<T>(v.o[x][4 * g + 2] * inv, v.o[x][4 * g + 3] * inv);
-                    *reinterpret_cast<u32x2_t*>(orow + d) = pk;
+                    u32x2_t& p = pk[4 * x + g];
+                    p[0] = pack2<T>(v.o[x][4 * g] * inv, v.o[x][4 * g + 1] * inv);
+                    p[1] = pack2<T>(v.o[x][4 * g + 2] * inv, v.o[x][4 * g + 3] * inv);
+                    *reinterpret_cast<u32x2_t*>(orow + d) = p;
                 }
             }
+            if (P.ey.ok()) epi_store_lane<T, D / 8>(P, b, h, qi, hh, pk);
             if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (v.m + log2f(l)) * kLn2;
         }
     }
@@ -1040,17 +1078,19 @@ __global__ __launch_bounds__(kPpThreads, 1) void k_mfma_fwd_pp(PassDev P) {
     const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
     const float inv = degenerate ? 0.f : 1.f / l;
     T* orow = P.out.wrow<T>(b, h, qi);
+    u32x2_t ow[D / 8];
 #pragma unroll
     for (int x = 0; x < D / 32; ++x) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d = x * 32 + 8 * g + 4 * hh;
-            u32x2_t o2;
+            u32x2_t& o2 = ow[4 * x + g];
             o2[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
             o2[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
             *reinterpret_cast<u32x2_t*>(orow + d) = o2;
         }
     }
+    if (P.ey.ok()) epi_store_lane<T, D / 8>(P, b, h, qi, hh, ow);
     if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
 }
 
@@ -1067,6 +1107,9 @@ bool mfma_fwd_supported(const PassDev& P, int dtype) {
     if (!aligned_rows_host(P.q, 8) || !aligned_rows_host(P.k, 8) || !aligned_rows_host(P.v, 8)) return false;
     if (P.vmul.ok() && !aligned_rows_host(P.vmul, 8)) return false;
     if (!aligned_rows_host(P.out, 4)) return false;
+    // the epilogue's root / gate / y rows travel in 8-byte words
+    for (const DView* e : {&P.er, &P.eg, &P.ey})
+        if (e->ok() && !aligned_rows_host(*e, 4)) return false;
     return true;
 }
 

@@ -5,6 +5,8 @@
 // fp32 arithmetic.  They run whenever the MFMA kernels do not cover a request (fp32 data,
 // head dims other than 64/128).  The same file holds the kernels that finish the fully-masked
 // rows of the MFMA forward and backward kernels (k_fwd_fixup, the k_fix_* kernels).
+#include <algorithm>
+
 #include "pa_common.h"
 #include "pa_launch.h"
 
@@ -73,6 +75,10 @@ __device__ void simt_write_row(const PassDev& P, int b, int h, int i, const floa
                                float lse) {
     T* o = P.out.wrow<T>(b, h, i);
     for (int d = 0; d < P.dim; ++d) o[d] = from_f<T>(acc[d] * inv);
+    if (P.ey.ok()) {
+        T* y = P.ey.wrow<T>(b, h, i);
+        for (int d = 0; d < P.dim; ++d) y[d] = from_f<T>(epi_y<T>(P, b, h, i, d, round_to<T>(acc[d] * inv)));
+    }
     *P.lse.wrow<float>(b, h, i) = lse;
 }
 
@@ -234,7 +240,11 @@ __global__ __launch_bounds__(kFixThreads) void k_fwd_fixup(PassDev P) {
             const float inv = c1 > 0 ? 1.f / (float)c1 : NAN;
             T* o = P.out.wrow<T>(b, h, r);
 #pragma unroll
-            for (int e = 0; e < E; ++e) o[lane + 64 * e] = from_f<T>(sum[e] * inv);
+            for (int e = 0; e < E; ++e) {
+                const int d = lane + 64 * e;
+                o[d] = from_f<T>(sum[e] * inv);
+                if (P.ey.ok()) P.ey.wrow<T>(b, h, r)[d] = from_f<T>(epi_y<T>(P, b, h, r, d, round_to<T>(sum[e] * inv)));
+            }
             if (lane == 0) *P.lse.wrow<float>(b, h, r) = c1 > 0 ? -FLT_MAX : -INFINITY;
         }
     }
@@ -864,6 +874,76 @@ __global__ __launch_bounds__(kSimtRows) void k_fix_keys_b(GradDev G) {
 }
 
 // ---------------------------------------------------------------------------------------
+// the module epilogue's backward (torch's autograd of y = round(round(r * o) * g'),
+// g' = round(sigmoid(gate)), r = root or round(sigmoid(root)), each step rounded as torch
+// rounds its intermediate tensors):
+//   gt = round(dy * g'), dgate = round(round(dy * t) * (1 - g') * g')        (t = round(r * o))
+//   dO = round(gt * r),  droot = sum over the heads sharing the root of round(gt * o)
+//                                (times (1 - r) * r for a sigmoid root)
+// Grid (row chunks, root head, batch); a thread takes W consecutive elements of one row of
+// the root's [B, hr, nq, dim] (the pass's without a root) and the rep query heads sharing it.
+
+template <typename T, int W>
+struct alignas(sizeof(T) * W) EpiVec {
+    T v[W];
+};
+
+template <typename T, int W>
+__global__ __launch_bounds__(256) void k_epi_bwd(GradDev G, T* dO, int hr) {
+    using V = EpiVec<T, W>;
+    const PassDev& P = G.f;
+    const int rep = P.heads / hr;
+    const int rh = blockIdx.y, b = blockIdx.z;
+    const int cpr = P.dim / W;  // chunks per row
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= P.nq * cpr) return;
+    const int i = c / cpr, d = (c % cpr) * W;
+    const bool has_r = P.er.ok(), has_g = P.eg.ok(), sig = (P.eflags & PA_EPI_ROOT_SIGMOID) != 0;
+    float rp[W], dr[W];
+    V rv;
+    if (has_r) rv = *reinterpret_cast<const V*>(P.er.row<T>(b, rh * rep, i) + d);
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+        rp[e] = has_r ? to_f(rv.v[e]) : 1.f;
+        if (has_r && sig) rp[e] = round_to<T>(sigmoid_f(rp[e]));
+        dr[e] = 0.f;
+    }
+    for (int k = 0; k < rep; ++k) {
+        const int h = rh * rep + k;
+        const V ov = *reinterpret_cast<const V*>(P.out.row<T>(b, h, i) + d);
+        const V yv = *reinterpret_cast<const V*>(G.dout.row<T>(b, h, i) + d);
+        V gv;
+        if (has_g) gv = *reinterpret_cast<const V*>(P.eg.row<T>(b, h, i) + d);
+        V go, dg;
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+            const float o = to_f(ov.v[e]), dy = to_f(yv.v[e]);
+            float gt = dy;
+            if (has_g) {
+                const float gp = round_to<T>(sigmoid_f(to_f(gv.v[e])));
+                const float t = has_r ? round_to<T>(rp[e] * o) : o;
+                gt = round_to<T>(dy * gp);
+                dg.v[e] = from_f<T>(round_to<T>(dy * t) * (1.f - gp) * gp);
+            }
+            float g_o = gt;
+            if (has_r) {
+                g_o = round_to<T>(gt * rp[e]);
+                dr[e] += round_to<T>(gt * o);
+            }
+            go.v[e] = from_f<T>(g_o);
+        }
+        *reinterpret_cast<V*>(dO + (((int64_t)b * P.heads + h) * P.nq + i) * P.dim + d) = go;
+        if (has_g) *reinterpret_cast<V*>(G.dgate.wrow<T>(b, h, i) + d) = dg;
+    }
+    if (has_r) {
+        V out;
+#pragma unroll
+        for (int e = 0; e < W; ++e) out.v[e] = from_f<T>(sig ? dr[e] * (1.f - rp[e]) * rp[e] : dr[e]);
+        *reinterpret_cast<V*>(G.droot.wrow<T>(b, rh * rep, i) + d) = out;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // launchers
 
 template <typename T, int D>
@@ -954,6 +1034,27 @@ static void launch_mask_fixups_t(const GradDev& G, hipStream_t s) {
         hipLaunchKernelGGL((k_fix_rows_b<T, D>), qgrid, dim3(kSimtRows), 0, s, G);
         hipLaunchKernelGGL((k_fix_keys_b<T, D>), kgrid, dim3(kSimtRows), 0, s, G);
     }
+}
+
+template <typename T>
+static void launch_epi_bwd_t(const GradDev& G, T* dO, int hr, hipStream_t s) {
+    const PassDev& P = G.f;
+    auto rows4 = [](const DView& v) {
+        return !v.ok() || ((uintptr_t)v.p % 16 == 0 && v.sb % 4 == 0 && v.sh % 4 == 0 && v.sn % 4 == 0);
+    };
+    const bool vec = P.dim % 4 == 0 && rows4(P.out) && rows4(G.dout) && rows4(P.er) &&
+                     rows4(P.eg) && rows4(G.droot) && rows4(G.dgate);
+    const int w = vec ? 4 : 1;
+    const dim3 grid((unsigned)(((int64_t)P.nq * (P.dim / w) + 255) / 256), hr, P.batch);
+    if (vec) hipLaunchKernelGGL((k_epi_bwd<T, 4>), grid, dim3(256), 0, s, G, dO, hr);
+    else hipLaunchKernelGGL((k_epi_bwd<T, 1>), grid, dim3(256), 0, s, G, dO, hr);
+}
+
+void launch_epi_bwd(const GradDev& G, void* dO, int hr, int dtype, hipStream_t s) {
+    ProfScope ps("epi_bwd", s);
+    if (dtype == PA_F32) launch_epi_bwd_t<float>(G, (float*)dO, hr, s);
+    else if (dtype == PA_F16) launch_epi_bwd_t<f16>(G, (f16*)dO, hr, s);
+    else launch_epi_bwd_t<bf16>(G, (bf16*)dO, hr, s);
 }
 
 void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, hipStream_t s) {

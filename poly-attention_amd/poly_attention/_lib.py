@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolyattn.so"
 
-PA_ABI_VERSION = 4
+PA_ABI_VERSION = 5
 PA_MAX_ORDER = 8
 
 PA_OK = 0
@@ -30,6 +30,7 @@ PA_DECODE_SCRATCH_BYTES = 16 << 20
 
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 PA_FLAG_MAY_DEGENERATE = 1
+PA_EPI_ROOT_SIGMOID = 1
 PA_ACC_DQ, PA_ACC_DK, PA_ACC_DV, PA_ACC_DVMUL, PA_ACC_DBIAS = 1, 2, 4, 8, 16
 
 DTYPE_CODE = {torch.float32: PA_F32, torch.float16: PA_F16, torch.bfloat16: PA_BF16}
@@ -71,6 +72,10 @@ class PaMask(ctypes.Structure):
     _fields_ = [("ptr", c_void_p), ("sb", c_int64), ("sn", c_int64)]
 
 
+class PaEpilogue(ctypes.Structure):
+    _fields_ = [("root", PaView), ("gate", PaView), ("y", PaView), ("flags", c_int32)]
+
+
 class PaPass(ctypes.Structure):
     _fields_ = [
         ("batch", c_int32),
@@ -91,6 +96,7 @@ class PaPass(ctypes.Structure):
         ("query_mask", PaMask),
         ("out", PaView),
         ("lse", PaView),
+        ("epi", c_void_p),
     ]
 
 
@@ -107,6 +113,8 @@ class PaPassGrad(ctypes.Structure):
         ("accumulate", c_int32),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("droot", PaView),
+        ("dgate", PaView),
     ]
 
 
@@ -235,7 +243,7 @@ class PaKernelTime(ctypes.Structure):
 
 
 STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode, PaPrologueItem,
-           PaPrologue, PaRmsNorm, PaLinear, PaLinearOut)
+           PaPrologue, PaRmsNorm, PaLinear, PaLinearOut, PaEpilogue)
 
 
 class PolyAttnError(RuntimeError):

@@ -27,8 +27,10 @@ from torch import Tensor
 from . import _lib
 from ._lib import (
     DTYPE_CODE,
+    PA_EPI_ROOT_SIGMOID,
     PA_FLAG_MAY_DEGENERATE,
     PaDecode,
+    PaEpilogue,
     PaMask,
     PaPass,
     PaPassGrad,
@@ -101,8 +103,17 @@ def _stream(t: Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def _epilogue_struct(epilogue, y) -> PaEpilogue:
+    """epilogue = (root or None, gate or None, root_sigmoid); y its output buffer."""
+    root, gate, root_sigmoid = epilogue
+    e = PaEpilogue()
+    e.root, e.gate, e.y = _view(root), _view(gate), _view(y)
+    e.flags = PA_EPI_ROOT_SIGMOID if root_sigmoid else 0
+    return e
+
+
 def _pass_struct(q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal, softclamp, scale,
-                 may_degenerate) -> PaPass:
+                 may_degenerate, epi: Optional[PaEpilogue] = None) -> PaPass:
     p = PaPass()
     p.batch, p.heads, p.nq, p.dim = q.shape[0], out.shape[1], q.shape[2], q.shape[3]
     p.nk = k.shape[2]
@@ -114,6 +125,7 @@ def _pass_struct(q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal, so
     p.vmul, p.bias = _view(vmul), _view(bias)
     p.key_mask, p.query_mask = _mask(key_mask), _mask(query_mask)
     p.out, p.lse = _view(out), _view(lse)
+    p.epi = ctypes.addressof(epi) if epi is not None else None
     return p
 
 
@@ -142,7 +154,9 @@ def _check_pass_inputs(q, k, v, vmul, bias, key_mask, query_mask):
 
 
 def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale,
-                 may_degenerate) -> tuple[Tensor, Tensor]:
+                 may_degenerate, epilogue=None):
+    """One pass forward: (out, lse), and with ``epilogue`` = (root, gate, root_sigmoid) the
+    modules' gated output y as a third result (computed where the kernel stores out)."""
     lib = _lib.load()
     q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
     vmul = _inner_contig(vmul) if vmul is not None else None
@@ -152,11 +166,15 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
     H = _pass_heads(q, k, v, vmul, bias)
     out = _empty_heads((B, H, nq, d), q)
     lse = torch.empty(B, H, nq, dtype=torch.float32, device=q.device)
+    y = epi = None
+    if epilogue is not None:
+        y = _empty_heads((B, H, nq, d), q)
+        epi = _epilogue_struct(epilogue, y)
     p = _pass_struct(q, k, v, vmul, bias, km, qm, out, lse, causal, softclamp, scale,
-                     may_degenerate or km is not None or qm is not None)
+                     may_degenerate or km is not None or qm is not None, epi)
     with _device(q):
         _lib.check(lib.pa_attn_pass_fwd(ctypes.byref(p), _stream(q)), "pa_attn_pass_fwd")
-    return out, lse
+    return (out, lse) if epilogue is None else (out, lse, y)
 
 
 def _out_buffer(buf: Optional[Tensor], like: Tensor) -> Tensor:
@@ -169,11 +187,12 @@ def _out_buffer(buf: Optional[Tensor], like: Tensor) -> Tensor:
 def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal,
                  softclamp, scale, may_degenerate, dq_into: Optional[Tensor] = None,
                  dq_out: Optional[Tensor] = None, dk_out: Optional[Tensor] = None,
-                 dv_out: Optional[Tensor] = None):
+                 dv_out: Optional[Tensor] = None, epilogue=None):
     """One pass backward.  ``dq_into``: a gradient buffer of q's shape that the query gradient
     is added into (PA_ACC_DQ) instead of a new tensor.  ``dq_out`` / ``dk_out`` / ``dv_out``:
     buffers (any strided view of the right shape) that the gradients are written to instead
-    of new tensors."""
+    of new tensors.  With ``epilogue`` (as in the forward) ``dout`` is the gradient of y and
+    the gradients of root and gate follow the other five."""
     lib = _lib.load()
     q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
     vmul = _inner_contig(vmul) if vmul is not None else None
@@ -208,6 +227,14 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
     g.dq, g.dk, g.dv = _view(dq), _view(dk), _view(dv)
     g.dvmul, g.dbias = _view(dvmul), _view(dbias)
     g.accumulate = accumulate
+    droot = dgate = epi = None
+    if epilogue is not None:
+        root, gate, _ = epilogue
+        droot = _empty_heads(root.shape, root) if root is not None else None
+        dgate = _empty_heads(gate.shape, gate) if gate is not None else None
+        epi = _epilogue_struct(epilogue, out)  # y is not read by the backward
+        g.fwd.epi = ctypes.addressof(epi)
+        g.droot, g.dgate = _view(droot), _view(dgate)
     ws_bytes = lib.pa_attn_pass_bwd_workspace(ctypes.byref(g))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     g.workspace, g.workspace_bytes = ws.data_ptr(), ws_bytes
@@ -215,6 +242,8 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
         _lib.check(lib.pa_attn_pass_bwd(ctypes.byref(g), _stream(q)), "pa_attn_pass_bwd")
     if dbias is not None and bias is not None and dbias.dtype != bias.dtype:
         dbias = dbias.to(bias.dtype)
+    if epilogue is not None:
+        return dq, dk, dv, dvmul, dbias, droot, dgate
     return dq, dk, dv, dvmul, dbias
 
 
@@ -885,24 +914,26 @@ def _split_heads(t: Tensor, heads, d: int):
 # the order-n chain
 
 
-def order2_forward(q1, q2, q3, v3, key_mask, causal, softclamp, scale):
+def order2_forward(q1, q2, q3, v3, key_mask, causal, softclamp, scale, epilogue=None):
     """The two forward passes of the order-2 chain (poly_attention.py:48-116 with q2 as both
     the pass-1 queries and the pass-2 keys); ``key_mask`` masks the keys of both passes.
-    Returns (out, lse, lse23, msg)."""
+    Returns (out, lse, lse23, msg), and with ``epilogue`` = (root, gate, root_sigmoid) the
+    modules' gated output y (computed in pass 2's store) as a fifth result."""
     degenerate = key_mask is not None
     msg, lse23 = pass_fwd_raw(q2, q3, v3, None, None, key_mask, None, causal, softclamp, scale,
                               degenerate)
-    out, lse = pass_fwd_raw(q1, q2, msg, None, lse23, key_mask, None, causal, softclamp, scale,
-                            degenerate)
-    return out, lse, lse23, msg
+    res = pass_fwd_raw(q1, q2, msg, None, lse23, key_mask, None, causal, softclamp, scale,
+                       degenerate, epilogue)
+    return (res[0], res[1], lse23, msg) + tuple(res[2:])
 
 
 def order2_backward(saved, key_mask, cfg, slots, dout, dlse=None, dlse23_ext=None,
-                    dmsg_ext=None):
+                    dmsg_ext=None, epilogue=None):
     """The two pass backwards of ``order2_forward``, back to back: pass 2's key gradient of
     q2 is the buffer that pass 1's query gradient of q2 is accumulated into (no separate
     add).  ``saved`` = (q1, q2, q3, v3, msg, lse23, out, lse); ``slots`` the head-split
-    gradient slots of q1..v3 (or Nones).  Returns (dq1, dq2, dq3, dv3)."""
+    gradient slots of q1..v3 (or Nones).  Returns (dq1, dq2, dq3, dv3); with ``epilogue``
+    (as in the forward) ``dout`` is the gradient of y and (droot, dgate) follow."""
     q1, q2, q3, v3, msg, lse23, out, lse = saved
     causal, softclamp, scale = cfg
     degenerate = key_mask is not None
@@ -912,9 +943,10 @@ def order2_backward(saved, key_mask, cfg, slots, dout, dlse=None, dlse23_ext=Non
     # its gradient buffer
     dq1_out, dq2_out, dq3_out, dv3_out = (claim_slot(r, t) for r, t in
                                           zip(slots, (q1, q2, q3, v3)))
-    dq1, dq2, dmsg, _, dlse23 = pass_bwd_raw(dout, dlse, q1, q2, msg, None, lse23, key_mask,
-                                             None, out, lse, causal, softclamp, scale,
-                                             degenerate, dq_out=dq1_out, dk_out=dq2_out)
+    res = pass_bwd_raw(dout, dlse, q1, q2, msg, None, lse23, key_mask, None, out, lse, causal,
+                       softclamp, scale, degenerate, dq_out=dq1_out, dk_out=dq2_out,
+                       epilogue=epilogue)
+    dq1, dq2, dmsg, _, dlse23 = res[:5]
     if dmsg_ext is not None:
         dmsg = dmsg + dmsg_ext
     if dlse23_ext is not None:
@@ -922,27 +954,68 @@ def order2_backward(saved, key_mask, cfg, slots, dout, dlse=None, dlse23_ext=Non
     _, dq3, dv3, _, _ = pass_bwd_raw(dmsg, dlse23, q2, q3, v3, None, None, key_mask, None, msg,
                                      lse23, causal, softclamp, scale, degenerate, dq_into=dq2,
                                      dk_out=dq3_out, dv_out=dv3_out)
-    return dq1, dq2, dq3, dv3
+    return (dq1, dq2, dq3, dv3) + tuple(res[5:])
 
 
 class _Order2Chain(torch.autograd.Function):
     """The order-2 chain (poly_attention.py:48-116) as one autograd node
-    (``order2_forward`` / ``order2_backward``)."""
+    (``order2_forward`` / ``order2_backward``), with the modules' root-value / gate epilogue
+    (poly_attention.py:342-351) fused into pass 2 when root or gate is given: the first
+    output is then the gated y."""
 
     @staticmethod
-    def forward(ctx, q1, q2, q3, v3, causal, softclamp, scale):
-        out, lse, lse23, msg = order2_forward(q1, q2, q3, v3, None, causal, softclamp, scale)
-        ctx.save_for_backward(q1, q2, q3, v3, msg, lse23, out, lse)
+    def forward(ctx, q1, q2, q3, v3, root, gate, causal, softclamp, scale, root_sigmoid):
+        epi = (root, gate, root_sigmoid) if root is not None or gate is not None else None
+        res = order2_forward(q1, q2, q3, v3, None, causal, softclamp, scale, epi)
+        out, lse, lse23, msg = res[:4]
+        ctx.save_for_backward(q1, q2, q3, v3, msg, lse23, out, lse, root, gate)
         ctx.cfg = (causal, softclamp, scale)
+        ctx.root_sigmoid = root_sigmoid
         ctx.slots = [slot_ref(t) for t in (q1, q2, q3, v3)]
         ctx.set_materialize_grads(False)
-        return out, lse, lse23, msg
+        return (res[4] if epi is not None else out), lse, lse23, msg
 
     @staticmethod
     def backward(ctx, dout, dlse, dlse23_ext, dmsg_ext):
-        grads = order2_backward(ctx.saved_tensors, None, ctx.cfg, ctx.slots, dout, dlse,
-                                dlse23_ext, dmsg_ext)
-        return (*grads, None, None, None)
+        *saved, root, gate = ctx.saved_tensors
+        epi = (root, gate, ctx.root_sigmoid) if root is not None or gate is not None else None
+        grads = order2_backward(saved, None, ctx.cfg, ctx.slots, dout, dlse, dlse23_ext,
+                                dmsg_ext, epi)
+        droot, dgate = grads[4:] if epi is not None else (None, None)
+        return (*grads[:4], droot, dgate, None, None, None, None)
+
+
+def apply_epilogue(out: Tensor, epilogue) -> Tensor:
+    """The modules' epilogue in torch (poly_attention.py:342-351, n_poly_attention.py:315-326),
+    where it is not fused into the final pass; the root may be at fewer heads (repeated)."""
+    root, gate, root_sigmoid = epilogue
+    if root is not None:
+        if root.shape[1] != out.shape[1]:
+            root = root.repeat_interleave(out.shape[1] // root.shape[1], dim=1)
+        out = (root.sigmoid() if root_sigmoid else root) * out
+    if gate is not None:
+        out = out * gate.sigmoid()
+    return out
+
+
+def _epilogue_fusable(epilogue, q1, heads) -> bool:
+    root, gate, _ = epilogue
+    shape = (q1.shape[0], heads, q1.shape[2], q1.shape[3])
+    for t in (root, gate):
+        if t is None:
+            continue
+        if t.dtype != q1.dtype or t.stride(-1) != 1 or t.device != q1.device:
+            return False
+        # the kernels move root / gate rows in 8-byte words
+        if t.data_ptr() % 16 != 0 or any(st % 4 != 0 for st in t.stride()[:3]):
+            return False
+    if gate is not None and tuple(gate.shape) != shape:
+        return False
+    if root is not None:
+        r = root.shape
+        if (r[0], r[2], r[3]) != (shape[0], shape[2], shape[3]) or heads % r[1] != 0:
+            return False
+    return True
 
 
 def _chain_fusable(q_left, q_right, vs, query_mask, key_masks, may_degenerate) -> bool:
@@ -963,20 +1036,31 @@ def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence
                causal: bool, softclamp: Optional[float], scale: float,
                query_mask: Optional[Tensor] = None,
                key_masks: Optional[Sequence[Optional[Tensor]]] = None,
-               may_degenerate: bool = False):
+               may_degenerate: bool = False, epilogue=None):
     """Order-n poly attention through HIP passes.
 
     q_left[l] . q_right[l] are the scores of level l (l = 0 is q1 . q2); vs are the values
     v_3 .. v_{n+1}.  Returns (out, lses, msgs) with lses / msgs ordered deepest level first
-    (the reference's cache order, n_poly_attention.py:268-305).
+    (the reference's cache order, n_poly_attention.py:268-305).  ``epilogue`` = (root, gate,
+    root_sigmoid): the modules' root-value / gate epilogue applied to out (fused into the
+    final pass on the order-2 chain's path, else in torch).
     """
     n = len(q_left)
     assert len(q_right) == n and len(vs) == n - 1 and n >= 2
     key_masks = list(key_masks) if key_masks is not None else [None] * n
+    if epilogue is not None and epilogue[0] is None and epilogue[1] is None:
+        epilogue = None
     if _chain_fusable(q_left, q_right, vs, query_mask, key_masks, may_degenerate):
-        out, _, lse23, msg = _Order2Chain.apply(q_left[0], q_left[1], q_right[1], vs[0],
-                                                bool(causal), float(softclamp or 0.0),
-                                                float(scale))
+        root = gate = None
+        root_sigmoid = False
+        fuse = epilogue is not None and _epilogue_fusable(epilogue, q_left[0], q_left[0].shape[1])
+        if fuse:
+            root, gate, root_sigmoid = epilogue
+        out, _, lse23, msg = _Order2Chain.apply(q_left[0], q_left[1], q_right[1], vs[0], root,
+                                                gate, bool(causal), float(softclamp or 0.0),
+                                                float(scale), bool(root_sigmoid))
+        if epilogue is not None and not fuse:
+            out = apply_epilogue(out, epilogue)
         return out, [lse23], [msg]
     may_degenerate = may_degenerate or query_mask is not None or any(
         m is not None for m in key_masks)
@@ -1001,6 +1085,8 @@ def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence
             msg_next, lse_next = o, lse
         else:
             out = o
+    if epilogue is not None:
+        out = apply_epilogue(out, epilogue)
     return out, lses, msgs
 
 

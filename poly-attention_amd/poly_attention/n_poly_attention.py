@@ -210,6 +210,12 @@ class NPolyAttention(Module):
 
         qs = (q1, *qs_rest)
 
+        # the root-value / gate epilogue (n_poly_attention.py:315-326): fused into the final
+        # pass on the HIP path's order-2 chain, else the torch element-wise tail below
+        epilogue = (root_value if self.multiply_root_value else None,
+                    gates if self.attn_gate else None, self.use_root_value_as_attn_gate)
+        epilogue_done = False
+
         if isinstance(cache, _cache.StaticCache):
             # fixed-capacity cache: norms, rotary and appends fused into the decode step
             out = _static_decode_step(self, qs, vs_for_aggregation, mask, context_mask,
@@ -227,20 +233,19 @@ class NPolyAttention(Module):
             if self._use_fused(q1):
                 out, new_cache = self._fused_core(q1, qs_rest, vs_for_aggregation, mask,
                                                   context_mask, rotary_pos_emb, cache,
-                                                  return_cache)
-                if exists(root_value) and self.is_gqa:
-                    root_value = repeat_kv(root_value, self.num_rep)
+                                                  return_cache, epilogue)
+                epilogue_done = True
             else:
                 out, new_cache, root_value = self._eager_core(q1, qs_rest, vs_for_aggregation,
                                                               root_value, mask, context_mask,
                                                               rotary_pos_emb, cache, device)
 
-        if self.multiply_root_value:
+        if self.multiply_root_value and not epilogue_done:
             if self.use_root_value_as_attn_gate:
                 root_value = root_value.sigmoid()
             out = root_value * out
 
-        if self.attn_gate:
+        if self.attn_gate and not epilogue_done:
             out = out * gates.sigmoid()
 
         out = self._proj(self.to_out, self.merge_heads(out))
@@ -337,8 +342,9 @@ class NPolyAttention(Module):
         return out, new_cache, root_value
 
     def _fused_core(self, q1, qs_rest, vs, mask, context_mask, rotary_pos_emb, cache,
-                    return_cache):
-        """The order-n chain on the HIP kernels; qs_rest / vs stay at kv_heads."""
+                    return_cache, epilogue):
+        """The order-n chain on the HIP kernels (qs_rest / vs stay at kv_heads), with the
+        module epilogue applied: fused into the final pass on the order-2 chain's path."""
         from . import _ops
 
         order = self.order
@@ -357,7 +363,8 @@ class NPolyAttention(Module):
                 q_left, q_right = (list(t) for t in zip(*rotated))
             out, lses, msgs = _ops.poly_chain(q_left, q_right, list(vs), causal=self.causal,
                                               softclamp=self.softclamp_value, scale=self.scale,
-                                              query_mask=mask, key_masks=list(context_mask))
+                                              query_mask=mask, key_masks=list(context_mask),
+                                              epilogue=epilogue)
             new_cache = None
             if return_cache:
                 new_cache = (
@@ -381,15 +388,17 @@ class NPolyAttention(Module):
             t.requires_grad for t in (q1, *qs_rest, *vs, *c_qs, *c_vs, *c_lses, *c_msgs))
         masked = exists(mask) or any(exists(m) for m in context_mask)
         if needs_grad or masked:
-            return self._fused_step_autograd(q_left, q_right, vs_cache, c_lses, c_msgs, rep,
-                                             qs_cache, mask, context_mask)
+            out, new_cache = self._fused_step_autograd(q_left, q_right, vs_cache, c_lses, c_msgs,
+                                                       rep, qs_cache, mask, context_mask)
+            return _ops.apply_epilogue(out, epilogue), new_cache
 
         lses_full = [_cache.reserve(l, l[:, :, :1], -1) for l in c_lses]
         msgs_full = [_cache.reserve(m, m[:, :, :1], -2) for m in c_msgs]
         out = _ops.poly_decode_step(q_left, q_right, vs_cache, msgs_full, lses_full,
                                     kv_heads=self.kv_heads, heads=self.heads,
                                     softclamp=self.softclamp_value, scale=self.scale)
-        return out, (tuple(qs_cache), tuple(vs_cache), tuple(lses_full), tuple(msgs_full))
+        return _ops.apply_epilogue(out, epilogue), (tuple(qs_cache), tuple(vs_cache),
+                                                     tuple(lses_full), tuple(msgs_full))
 
     def _fused_step_autograd(self, q_left, q_right, vs_cache, c_lses, c_msgs, rep, qs_cache,
                              mask=None, context_mask=None):

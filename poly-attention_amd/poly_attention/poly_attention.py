@@ -372,6 +372,12 @@ class Order2PolyAttention(Module):
             q3, v3 = kv2
             qs = (q1, q2, q3)
 
+        # the root-value / gate epilogue (poly_attention.py:342-351): fused into the final
+        # pass on the HIP path, else the torch element-wise tail below
+        epilogue = (v2 if self.multiply_root_value else None,
+                    gates if self.attn_gate else None, self.use_root_value_as_attn_gate)
+        epilogue_done = False
+
         if isinstance(cache, _cache.StaticCache):
             # fixed-capacity cache: norms, rotary and appends fused into the decode step
             out = _static_decode_step(self, qs, (v3,), mask, context_mask, rotary_pos_emb,
@@ -393,20 +399,20 @@ class Order2PolyAttention(Module):
 
             if self._use_fused(q1):
                 out, new_cache = self._fused_core(q1, q2, q3, v3, mask, context_mask,
-                                                  rotary_pos_emb, cache, return_cache)
-                v2 = repeat_kv(v2, self.num_rep) if self.is_gqa else v2
+                                                  rotary_pos_emb, cache, return_cache, epilogue)
+                epilogue_done = True
             else:
                 out, new_cache, v2 = self._eager_core(q1, q2, q3, v2, v3, mask, context_mask,
                                                       rotary_pos_emb, cache, return_cache)
 
         # elementwise multiply root values
 
-        if self.multiply_root_value:
+        if self.multiply_root_value and not epilogue_done:
             if self.use_root_value_as_attn_gate:
                 v2 = v2.sigmoid()
             out = v2 * out
 
-        if self.attn_gate:
+        if self.attn_gate and not epilogue_done:
             out = out * gates.sigmoid()
 
         out = self._proj(self.to_out, self.merge_heads(out))
@@ -453,8 +459,9 @@ class Order2PolyAttention(Module):
         return out, new_cache, v2
 
     def _fused_core(self, q1, q2, q3, v3, mask, context_mask, rotary_pos_emb, cache,
-                    return_cache):
-        """The attention core on the HIP kernels; q2 / q3 / v3 stay at kv_heads."""
+                    return_cache, epilogue):
+        """The attention core on the HIP kernels (q2 / q3 / v3 stay at kv_heads), with the
+        module epilogue applied: fused into pass 2 on the order-2 chain's path."""
         from . import _ops
 
         rep = self.num_rep if self.is_gqa else 1
@@ -470,7 +477,7 @@ class Order2PolyAttention(Module):
             out, lses, msgs = _ops.poly_chain(
                 [q1r, q2r_left], [q2r_right, q3r], [v3], causal=self.causal,
                 softclamp=self.softclamp_value, scale=self.scale, query_mask=mask,
-                key_masks=list(context_mask))
+                key_masks=list(context_mask), epilogue=epilogue)
             new_cache = None
             if return_cache:
                 lse23 = repeat_kv(lses[0][:, :, :, None], rep)[..., 0]
@@ -507,6 +514,7 @@ class Order2PolyAttention(Module):
                                     key_mask=key_mask1, query_mask=mask,
                                     softclamp=self.softclamp_value, scale=self.scale,
                                     may_degenerate=True)
+            out = _ops.apply_epilogue(out, epilogue)
             return out, (q2_cache, q3_cache, v3_cache, lse23_full, msg_full)
 
         lse23_full = _cache.reserve(clse23, clse23[:, :, :1], -1)
@@ -515,4 +523,5 @@ class Order2PolyAttention(Module):
             [q1r, q2_left], [q2_right, q3_full], [v3_cache], [msg_full], [lse23_full],
             kv_heads=self.kv_heads, heads=self.heads, softclamp=self.softclamp_value,
             scale=self.scale)
-        return out, (q2_cache, q3_cache, v3_cache, lse23_full, msg_full)
+        return _ops.apply_epilogue(out, epilogue), (q2_cache, q3_cache, v3_cache, lse23_full,
+                                                     msg_full)

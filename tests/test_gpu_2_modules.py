@@ -66,6 +66,11 @@ ORDER2_CFGS = [
     dict(heads=4, dim_head=32, causal=True, multiply_root_value=True, attn_gate=True,
          use_rotary_embed=True, prenorm=True),
     dict(heads=4, kv_heads=1, dim_head=64, causal=False, shared_kv=True),
+    # the epilogue fused into pass 2 at the MFMA head dim: GQA root, sigmoid root, shared kv
+    dict(heads=8, kv_heads=2, dim_head=64, causal=True, multiply_root_value=True, attn_gate=True),
+    dict(heads=4, dim_head=64, causal=False, multiply_root_value=True,
+         use_root_value_as_attn_gate=True, attn_gate=True),
+    dict(heads=4, kv_heads=2, dim_head=64, causal=True, shared_kv=True, multiply_root_value=True),
 ]
 
 
@@ -112,6 +117,76 @@ def test_order2_module_e2e(cfg, masked, seq_len):
     assert_parity(out, ref, torch.float32, f"{what} out")
     assert_parity(xg.grad, xo.grad, torch.float32, f"{what} dx")
     _check_param_grads(m, params, what)
+
+
+@param("order", (2, 3))
+@param("gate_root", (False, True))
+def test_npoly_module_epilogue_e2e(order, gate_root):
+    """NPolyAttention's root value / gate (n_poly_attention.py:315-326): fused into the final
+    pass at order 2, torch element-wise at order 3; fwd, dx and parameter gradients."""
+    from poly_attention import NPolyAttention
+
+    d = dev()
+    torch.manual_seed(9)
+    cfg = dict(heads=4, dim_head=64, causal=True, order=order, multiply_root_value=True,
+               use_root_value_as_attn_gate=gate_root, attn_gate=True)
+    m = NPolyAttention(dim=64, use_flash_kernel=True, **cfg).to(d)
+    x = torch.randn(2, 40, 64)
+    xg = x.to(d).requires_grad_()
+    out = m(xg)
+    params = _grad_params(m)
+    xo = x.clone().requires_grad_()
+    ref = O.npoly_forward(params, cfg, xo)
+    dout = torch.randn_like(ref)
+    out.backward(dout.to(d))
+    ref.backward(dout)
+    what = f"npoly epilogue order={order} sigmoid root={gate_root}"
+    assert_parity(out, ref, torch.float32, f"{what} out")
+    assert_parity(xg.grad, xo.grad, torch.float32, f"{what} dx")
+    _check_param_grads(m, params, what)
+
+
+@param("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@param("root_heads,root_sigmoid,gate", ((8, False, True), (2, False, True), (8, True, True),
+                                        (8, False, False), (None, False, True)))
+def test_fused_epilogue_equals_torch_tail(dtype, root_heads, root_sigmoid, gate):
+    """The order-2 chain with the epilogue fused into pass 2 against the same chain followed
+    by torch's element-wise tail (poly_attention.py:342-351) on the same kernels: y, and the
+    gradients of q1..v3, root and gate.  Same roundings in the same order, so the bound is
+    one storage rounding (tol 0) in bf16 / f16; fp32 allows for the sigmoid's last bit and
+    the order of the GQA root's head sum (tol 1e-5)."""
+    from poly_attention import _ops
+
+    d = dev()
+    B, H, N, D = 2, 8, 160, 64
+    gen = torch.Generator().manual_seed(5)
+
+    def rnd(*s):
+        return torch.randn(*s, generator=gen).to(dtype).to(d)
+
+    q1, q2, q3, v3 = (rnd(B, H, N, D) for _ in range(4))
+    root = rnd(B, root_heads, N, D) if root_heads else None
+    gt = rnd(B, H, N, D) if gate else None
+    dy = rnd(B, H, N, D)
+    leaves = [t.requires_grad_() for t in (q1, q2, q3, v3, root, gt) if t is not None]
+    epi = (root, gt, root_sigmoid)
+    y, _, _, _ = _ops._Order2Chain.apply(q1, q2, q3, v3, root, gt, True, 0.0, D ** -0.5,
+                                         root_sigmoid)
+    y.backward(dy)
+    fused = [y.detach()] + [t.grad for t in leaves]
+    for t in leaves:
+        t.grad = None
+    out, _, _, _ = _ops._Order2Chain.apply(q1, q2, q3, v3, None, None, True, 0.0, D ** -0.5,
+                                           False)
+    ref = _ops.apply_epilogue(out, epi)
+    ref.backward(dy)
+    torch.cuda.synchronize()
+    names = ["y", "dq1", "dq2", "dq3", "dv3"] + (["droot"] if root is not None else []) + \
+        (["dgate"] if gate else [])
+    what = f"fused epilogue {dtype} root_heads={root_heads} sigmoid={root_sigmoid} gate={gate}"
+    for name, a, b in zip(names, fused, [ref.detach()] + [t.grad for t in leaves]):
+        assert_parity(a, b.float().cpu(), dtype, f"{what} {name}",
+                      tol=1e-5 if dtype == torch.float32 else 0.0, grad=name != "y")
 
 
 @param("order", (2, 3, 4))
