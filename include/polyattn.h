@@ -212,6 +212,12 @@ typedef struct pa_prologue {
     const int32_t* n_dev;       /* device: the step's n (positions after the append), or NULL */
     int32_t*       overflow;    /* device int32 [1] set to 1 when the position is outside
                                  * [0, capacity), or NULL */
+    /* Without angles: the angles of a rotary module's own positions (poly_attention.py:302-304,
+     * n_poly_attention.py:224-229 through rotary-embedding-torch's get_seq_pos / forward),
+     * a[f] = p * inv_freq[f / 2] in fp32 with p = round(round(pos) / interp), both roundings to
+     * the items' dtype (the rotated tensor's), pos the position written.  NULL: no such rotary. */
+    const float*   inv_freq;    /* [rot_dim / 2] */
+    float          interp;      /* interpolate_factor (1: none) */
     pa_prologue_item items[2 * PA_MAX_ORDER];
 } pa_prologue;
 

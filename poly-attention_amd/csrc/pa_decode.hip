@@ -720,6 +720,8 @@ struct ProDev {
     int32_t adt;
     const int32_t* n_dev;
     int32_t* overflow;
+    const float* inv_freq;  // angles from the position (when angles is null)
+    float interp;
     ProItemDev it[2 * PA_MAX_ORDER];
 };
 
@@ -757,19 +759,21 @@ __global__ __launch_bounds__(kProThreads) void k_dec_prologue(ProDev P) {
             x[e] = round_to<T>((x[e] * r) * w);
         }
     }
-    if (I.rotate && P.angles) {
+    const int64_t pos = P.n_dev ? (int64_t)*P.n_dev - 1 : (int64_t)P.pos;
+    if (I.rotate && (P.angles || P.inv_freq)) {
+        // the rotary module's own position, rounded as its get_seq_pos builds it
+        const float pt = P.angles ? 0.f : round_to<T>(round_to<T>((float)pos) / P.interp);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int d = lane + 64 * e;
             const float partner = __shfl_xor(x[e], 1);  // feature d ^ 1 (same 64-block)
             if (d < P.rot_dim) {
-                const float a = load_any(P.angles, P.adt, d);
+                const float a = P.angles ? load_any(P.angles, P.adt, d) : pt * P.inv_freq[d >> 1];
                 const float rot = (d & 1) ? partner : -partner;
                 x[e] = round_to<T>(x[e] * cosf(a) + rot * sinf(a));
             }
         }
     }
-    const int64_t pos = P.n_dev ? (int64_t)*P.n_dev - 1 : (int64_t)P.pos;
     const bool in_range = pos >= 0 && pos < P.capacity;
     const bool to_cache = I.cache.ok() && in_range;
     if (!in_range && P.overflow && row == 0 && lane == 0) *P.overflow = 1;
@@ -787,8 +791,10 @@ int launch_prologue(const pa_prologue* p, hipStream_t s) {
     if (p->batch < 1 || p->dim < 1 || p->count < 1 || p->count > 2 * PA_MAX_ORDER)
         return PA_EINVAL;
     if (p->dim > 256) return PA_EUNSUPPORTED;
-    if (p->angles && (p->rot_dim < 0 || p->rot_dim > p->dim || p->rot_dim % 2 != 0))
+    const bool rotary = p->angles || p->inv_freq;
+    if (rotary && (p->rot_dim < 0 || p->rot_dim > p->dim || p->rot_dim % 2 != 0))
         return PA_EINVAL;
+    if (!p->angles && p->inv_freq && !(p->interp > 0.f)) return PA_EINVAL;
     if (p->angles && p->angles_dtype != PA_F32 && p->angles_dtype != PA_F16 && p->angles_dtype != PA_BF16)
         return PA_EINVAL;
     const int T = p->items[0].src.dtype;
@@ -798,13 +804,15 @@ int launch_prologue(const pa_prologue* p, hipStream_t s) {
     P.dim = p->dim;
     P.count = p->count;
     P.capacity = p->capacity;
-    P.rot_dim = p->angles ? p->rot_dim : 0;
+    P.rot_dim = rotary ? p->rot_dim : 0;
     P.pos = p->pos;
     P.eps = p->eps;
     P.angles = p->angles;
     P.adt = p->angles_dtype;
     P.n_dev = p->n_dev;
     P.overflow = p->overflow;
+    P.inv_freq = p->angles ? nullptr : p->inv_freq;
+    P.interp = p->interp;
     int rows = 0;
     for (int k = 0; k < p->count; ++k) {
         const pa_prologue_item& it = p->items[k];

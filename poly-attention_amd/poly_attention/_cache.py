@@ -125,6 +125,13 @@ class StaticCache:
     holding the same positions), which the caller advances once per decode step, after
     every layer ran (``StaticCache.advance_counter``): one device add per token instead of
     one per layer.  Without it each cache owns its count and advances it itself.
+
+    With a module's own rotary embedding (``use_rotary_embed=True`` and no external
+    ``rotary_pos_emb``) the module's tuple cache holds its keys unrotated and rotates the whole
+    cache at every step (poly_attention.py:302-304); a StaticCache holds them rotated at their
+    positions instead, each rotated once as it is appended, which gives the same scores.  The
+    positions copied in from the tuple cache are rotated in place at the first such step
+    (``rotate_prefix``), which must run eagerly, before any graph capture.
     """
 
     def __init__(self, cache, capacity: int, counter: Tensor | None = None):
@@ -138,6 +145,8 @@ class StaticCache:
         if capacity <= n:
             raise ValueError(f"capacity {capacity} must exceed the {n} cached positions")
         self.capacity = int(capacity)
+        self.prefix = n                 # positions copied from the tuple cache
+        self.keys_rotated = False       # those positions rotated by a module's own rotary
 
         def grow(t: Tensor) -> Tensor:
             shape = list(t.shape)
@@ -162,6 +171,21 @@ class StaticCache:
             _set_host_count(self.n_step, n + 1)
         # set to 1 by the prologue kernel when a step's position is past the capacity
         self.overflow = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def rotate_prefix(self, rotary) -> None:
+        """Rotate the keys of the positions copied from the tuple cache in place, as the
+        module's rotary rotates cached keys (rotate_queries_with_cached_keys: position j for
+        key j), once."""
+        if self.keys_rotated:
+            return
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("StaticCache with the module's own rotary: run one eager step "
+                               "before capturing decode steps (the cached prefix is rotated "
+                               "once, in place, at the first step)")
+        for q in self.qs:
+            head = q.narrow(2, 0, self.prefix)
+            head.copy_(rotary.rotate_queries_or_keys(head))
+        self.keys_rotated = True
 
     def host_step(self):
         """The next step's n as the host knows it, or None once graph replays (or a counter

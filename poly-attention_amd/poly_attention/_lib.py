@@ -172,6 +172,8 @@ class PaPrologue(ctypes.Structure):
         ("pos", c_int32),
         ("n_dev", c_void_p),
         ("overflow", c_void_p),
+        ("inv_freq", c_void_p),
+        ("interp", c_float),
         ("items", PaPrologueItem * (2 * PA_MAX_ORDER)),
     ]
 

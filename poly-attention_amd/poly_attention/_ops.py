@@ -1180,12 +1180,15 @@ def poly_decode_step(q_new: Sequence[Tensor], k_caches: Sequence[Tensor],
 
 
 def decode_prologue(items, *, eps: float, angles: Optional[Tensor], n_dev: Tensor,
-                    capacity: int, overflow: Optional[Tensor] = None) -> None:
+                    capacity: int, overflow: Optional[Tensor] = None,
+                    inv_freq: Optional[Tensor] = None, interp: float = 1.0) -> None:
     """The q norms, rotary embedding and cache appends of one decode step, one launch
     (pa_decode_prologue).  ``items``: (src [B, h, 1, d], norm weight or None, rotate,
     out [B, h, 1, d] or None, cache [B, h, capacity, d] or None) per tensor; ``angles`` is
-    the [rot_dim] rotary angle row of the new position (fp32, f16 or bf16); the cache
-    position, n - 1, is read from ``n_dev`` (device int32 [1], the step's n) on the device."""
+    the [rot_dim] rotary angle row of the new position (fp32, f16 or bf16), or ``inv_freq``
+    (fp32 [rot_dim / 2]) a rotary module's frequencies, whose angles the kernel forms from
+    the position (with ``interp`` its interpolate_factor); the cache position, n - 1, is read
+    from ``n_dev`` (device int32 [1], the step's n) on the device."""
     lib = _lib.load()
     src0 = items[0][0]
     B, _, _, d = src0.shape
@@ -1200,6 +1203,10 @@ def decode_prologue(items, *, eps: float, angles: Optional[Tensor], n_dev: Tenso
         a = a.contiguous()
         keep.append(a)
         P.angles, P.angles_dtype, P.rot_dim = a.data_ptr(), DTYPE_CODE[a.dtype], a.numel()
+    elif inv_freq is not None:
+        f = inv_freq.detach().to(torch.float32).contiguous()
+        keep.append(f)
+        P.inv_freq, P.rot_dim, P.interp = f.data_ptr(), 2 * f.numel(), float(interp)
     assert n_dev.dtype == torch.int32 and n_dev.is_cuda and n_dev.numel() == 1
     P.n_dev = n_dev.data_ptr()
     if overflow is not None:

@@ -89,10 +89,7 @@ def _static_decode_step(module, qs, vs, mask, context_mask, rotary_pos_emb,
         raise ValueError("a StaticCache step takes exactly one new token")
     if exists(mask) or any(exists(m) for m in context_mask):
         raise NotImplementedError("masks are not supported with a StaticCache")
-    if not exists(rotary_pos_emb) and exists(module.rotary_emb):
-        raise NotImplementedError(
-            "the module's own rotary re-rotates the whole cache every step; pass external "
-            "rotary_pos_emb with a StaticCache")
+    module_rotary = not exists(rotary_pos_emb) and exists(module.rotary_emb)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (*qs, *vs)):
         raise RuntimeError("StaticCache decode is inference-only: run it under torch.no_grad()")
     if len(cache.qs) != order or len(cache.vs) != order - 1:
@@ -116,16 +113,24 @@ def _static_decode_step(module, qs, vs, mask, context_mask, rotary_pos_emb,
         if rotary_pos_emb.dim() not in (1, 2):
             raise NotImplementedError("rotary_pos_emb must be [positions, dim] or [dim]")
         angles = rotary_pos_emb if rotary_pos_emb.dim() == 1 else rotary_pos_emb[-1]
+    if module_rotary:
+        # the module's own rotary (poly_attention.py:302-304, n_poly_attention.py:224-229)
+        # rotates every cached key at its position on every step; the StaticCache keeps its
+        # keys rotated instead, each once, as the prologue appends it
+        cache.rotate_prefix(module.rotary_emb)
     q_left = [torch.empty(q.shape[0], q.shape[1], 1, q.shape[3], dtype=dt, device=q.device)
               for q in qs[:-1]]
     items = []
     for i, (q, norm) in enumerate(zip(qs, norms)):
         w = norm.weight if norm.weight is not None else torch.ones(q.shape[-1], device=q.device)
-        items.append((q, w, angles is not None, q_left[i] if i < order else None,
+        items.append((q, w, angles is not None or module_rotary, q_left[i] if i < order else None,
                       cache.qs[i - 1] if i >= 1 else None))
     items += [(v, None, False, None, buf) for v, buf in zip(vs, cache.vs)]
+    rot = module.rotary_emb if module_rotary else None
     _ops.decode_prologue(items, eps=eps, angles=angles, n_dev=cache.n_step,
-                         capacity=cache.capacity, overflow=cache.overflow)
+                         capacity=cache.capacity, overflow=cache.overflow,
+                         inv_freq=rot.freqs if rot is not None else None,
+                         interp=rot.interpolate_factor if rot is not None else 1.0)
     out = _ops.poly_decode_step(q_left, cache.qs, cache.vs, cache.msgs, cache.lses,
                                 kv_heads=module.kv_heads, heads=module.heads,
                                 softclamp=module.softclamp_value, scale=module.scale,

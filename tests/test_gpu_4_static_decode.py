@@ -135,6 +135,91 @@ def test_static_cache_stepwise_equals_parallel(order, kv_heads, dtype):
     assert q_cache.shape[2] == n
 
 
+@param("order", (2, 3))
+@param("dtype", (torch.float32, torch.bfloat16))
+def test_static_cache_with_module_rotary(order, dtype):
+    """The module's own rotary (use_rotary_embed=True, no external rotary_pos_emb): the tuple
+    cache rotates every cached key each step (poly_attention.py:302-304); the StaticCache holds
+    its keys rotated once, at the append (the prefix copied from the tuple cache rotated at the
+    first step).  Steps equal the oracle's parallel forward and the tuple-cache steps; then one
+    step captured into a HIP graph replays the eager steps of a twin cache."""
+    from poly_attention import NPolyAttention, Order2PolyAttention, StaticCache
+
+    d = dev()
+    torch.manual_seed(16)
+    cfg = dict(heads=4, kv_heads=2, dim_head=64, causal=True, use_rotary_embed=True)
+    if order == 2:
+        m, fwd = Order2PolyAttention(dim=64, **cfg), O.order2_forward
+    else:
+        cfg = dict(cfg, order=order)
+        m, fwd = NPolyAttention(dim=64, **cfg), O.npoly_forward
+    m = m.to(d, dtype).eval()
+    n, n0 = 12, 5
+    x = torch.randn(2, n + 4, 64).to(dtype)
+    params = {k: v.float().cpu() for k, v in m.state_dict().items()}
+    ref = fwd(params, cfg, x[:, :n].float())
+    with torch.no_grad():
+        out0, cache = m(x[:, :n0].to(d), return_cache=True)
+        sc = StaticCache(cache, capacity=n + 6)
+        twin = StaticCache(cache, capacity=n + 6)
+        outs = [out0]
+        for i in range(n0, n):
+            xi = x[:, i:i + 1].to(d)
+            o, _ = m(xi, cache=sc, return_cache=True)
+            o_t, cache = m(xi, return_cache=True, cache=cache)
+            m(xi, cache=twin, return_cache=True)
+            assert_parity(o, o_t, dtype, f"module rotary static vs tuple step {i} order={order}")
+            outs.append(o)
+        assert_parity(torch.cat(outs, dim=1), ref, dtype,
+                      f"module rotary static stepwise order={order} {dtype}")
+        # capture one step (the prefix is already rotated) and replay it per token
+        xb = x[:, n:n + 1].to(d).clone()
+        graph_sc = StaticCache(cache, capacity=n + 6)
+        m(xb, cache=graph_sc, return_cache=True)  # eager: rotates graph_sc's prefix
+        _, cache = m(xb, return_cache=True, cache=cache)  # the tuple cache at the same step
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            warm = StaticCache(cache, capacity=n + 6)
+            m(xb, cache=warm, return_cache=True)
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(graph):
+            out_g, _ = m(xb, cache=graph_sc, return_cache=True)
+        torch.cuda.synchronize()
+        for i in range(n + 1, n + 4):
+            xb.copy_(x[:, i:i + 1].to(d))
+            graph.replay()
+            torch.cuda.synchronize()
+            o_t, cache = m(x[:, i:i + 1].to(d), return_cache=True, cache=cache)
+            torch.cuda.synchronize()
+            assert_parity(out_g, o_t, dtype, f"module rotary graph replay at {i} order={order}")
+
+
+def test_prologue_module_rotary_positions_round_in_the_tensor_dtype():
+    """The prologue's angles for a rotary module's own positions: rotary-embedding-torch builds
+    the positions in the rotated tensor's dtype (get_seq_pos), so bf16 positions above 256 are
+    rounded before the fp32 frequency product; the kernel matches the module's rotation of a
+    query at those positions."""
+    from poly_attention import _ops
+    from poly_attention.rotary import RotaryEmbedding
+
+    d = dev()
+    rot = RotaryEmbedding(64).to(d)
+    for pos in (3, 255, 257, 1001, 4097):
+        src = torch.randn(2, 4, 1, 64, device=d).to(torch.bfloat16)
+        out = torch.empty_like(src)
+        n_dev = torch.full((1,), pos + 1, dtype=torch.int32, device=d)
+        _ops.decode_prologue([(src, None, True, out, None)], eps=1e-6, angles=None, n_dev=n_dev,
+                             capacity=pos + 1, inv_freq=rot.freqs, interp=1.0)
+        ref = rot.rotate_queries_or_keys(src, offset=pos)
+        torch.cuda.synchronize()
+        diff = (out.float() - ref.float()).abs()
+        ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -7
+        assert bool((diff <= ulp).all()), f"pos {pos}: max diff {diff.max().item():.3e}"
+        assert (out == ref).float().mean().item() >= 0.97, f"pos {pos}"
+
+
 def test_static_cache_matches_tuple_cache_steps():
     """The fixed-capacity path and the growing-tuple path give the same step outputs and the
     same cache contents (bf16, order 3, GQA)."""
