@@ -24,6 +24,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import platform
 import subprocess
 import sys
@@ -94,6 +95,27 @@ def measured_traffic(family):
     except OSError:
         pass
     return None
+
+
+KERNEL_PROFILE = os.path.join(ROOT, "profiles", "bench_config2_and_decode_kernel_stats.md")
+
+
+def rocprof_avg_ms(family):
+    """The average launch duration of a kernel family in the committed rocprofv3 --stats
+    summary of this workload (calls-weighted over its instantiations), or None."""
+    calls = total = 0.0
+    try:
+        with open(KERNEL_PROFILE) as f:
+            for line in f:
+                cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
+                # mangled names: _ZN2pa<len>k_<family>[_dma]I<template arguments>
+                m = re.match(r"_ZN2pa\d+k_(\w+?)(_dma)?I", cells[0]) if len(cells) == 6 else None
+                if m and m.group(1) == family:
+                    calls += float(cells[1])
+                    total += float(cells[1]) * float(cells[2])
+    except (OSError, ValueError):
+        return None
+    return total / calls / 1e3 if calls else None
 
 
 def achieved_rate(work, avg_ms, unit):
@@ -764,7 +786,15 @@ def main():
     achieved = achieved_rate(work, avg_ms, unit)
     roofline = {"bound": bound, "kernel": dominant, "achieved": round(achieved, 2),
                 "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
-                "traffic": measured_traffic(dominant), "avg_ms": round(avg_ms, 4)}
+                "traffic": measured_traffic(dominant), "avg_ms": round(avg_ms, 4),
+                "timer": "HIP events around each launch of the kernel on its own stream "
+                         "(libpolyattn pa_profile_start/stop), over a second timed region of "
+                         "the same workload"}
+    rp = rocprof_avg_ms(dominant)
+    if rp:
+        # the same figure from the committed rocprofv3 --kernel-trace --stats summary
+        roofline["rocprof_avg_ms"] = round(rp, 4)
+        roofline["rocprof_frac"] = round(achieved_rate(work, rp, unit) / peak, 4)
     log(f"[bench] kernels: {kernels}")
 
     module_ms = module_epi_ms = None
