@@ -291,6 +291,52 @@ def make_vit(dev, dtype, batch):
     return m, img
 
 
+def config1_bench(dev, steps, warmup, cpu):
+    """PolyAttention(dim=512, heads=8, dim_head=64, causal=False) fp32
+    forward on x ~ N(0,1) (1, 1024, 512), random init (seed 0) -- the reference's
+    CPU-runnable case.  GPU: the module forward (fp32 passes on v_mfma_f32_32x32x2_f32);
+    CPU: the oracle's eager module forward (the reference's CPU path restated) at the same
+    shape, median of 5."""
+    from poly_attention import PolyAttention, _lib
+
+    torch.manual_seed(0)
+    m = PolyAttention(dim=512, heads=8, dim_head=64, causal=False)
+    params = {k: v.detach().clone() for k, v in m.state_dict().items()}
+    x = torch.randn(1, 1024, 512, generator=torch.Generator().manual_seed(1))
+    md, xd = m.to(dev), x.to(dev)
+    with torch.no_grad():
+        ms = time_steps(lambda: md(xd), steps, warmup)
+        with _lib.KernelProfile() as prof:
+            for _ in range(5):
+                md(xd)
+    n_l, tot = prof.times.get("mfma_fwd_f32", (0, 0.0))
+    core_flops = 2 * core_flops_fwd(1, 8, 1024, 1024, 64, False)  # two passes per forward
+    res = {"workload": "PolyAttention(512, h8, d64, non-causal) fp32 forward, x (1, 1024, 512)",
+           "ms_per_forward": round(ms, 4),
+           "pass_kernel_avg_ms": round(tot / n_l, 4) if n_l else None,
+           "core_gflop_per_forward": round(core_flops / 1e9, 3)}
+    if n_l:
+        tf = core_flops / 2 / (tot / n_l / 1e3) / 1e12
+        res["pass_tflops"] = round(tf, 2)
+        res["pass_frac_fp32_peak"] = round(tf / PEAK_FP32_TFLOPS, 4)
+    if cpu:
+        import oracle.poly_oracle as O
+
+        torch.set_num_threads(cpu_threads())
+        cfg = dict(heads=8, dim_head=64, causal=False)
+        with torch.no_grad():
+            O.order2_forward(params, cfg, x)
+            t = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                O.order2_forward(params, cfg, x)
+                t.append((time.perf_counter() - t0) * 1e3)
+        # this config's CPU baseline: the oracle's restatement of the reference's CPU path
+        res["cpu_baseline"] = {"ms_per_forward": round(sorted(t)[len(t) // 2], 3),
+                               "kind": "port", "cores": torch.get_num_threads()}
+    return res
+
+
 def vit_bench(dev, steps, warmup, cpu):
     """Config 3 forward, eagerly (one Python call per step; at batch 64 the host issues the
     launches no faster than the GPU runs them) and replayed from a HIP graph captured once
@@ -839,6 +885,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    config1 = config1_bench(dev, max(5, args.steps), args.warmup, cpu=not args.no_cpu)
+    log(f"[bench] config 1 {config1}")
+
     decode = None
     if not args.no_decode:
         decode = decode_bench(dev, args.steps, args.warmup)
@@ -889,6 +938,7 @@ def main():
         "module_root_value_gate_ms_per_step": round(module_epi_ms, 4) if module_epi_ms else None,
         "module_kernels": module_kernels,
         "cpu_baseline": cpu,
+        "config1": config1,
         "decode": decode,
         "vit": vit,
         "decode_order3": lm,

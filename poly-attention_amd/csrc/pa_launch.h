@@ -28,7 +28,10 @@ void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool 
 void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, hipStream_t s);
 void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s);
 
-// MFMA kernels (bf16 / f16, head dim 64 or 128); return false when they do not cover P
+// MFMA kernels (bf16 / f16 / fp32 forward, bf16 / f16 backward; head dim 64 or 128); return
+// false when they do not cover P
+bool mfma_fwd_f32_supported(const PassDev& P);
+void launch_mfma_fwd_f32(const PassDev& P, hipStream_t s);
 bool mfma_fwd_supported(const PassDev& P, int dtype);
 void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s);
 bool mfma_bwd_supported(const GradDev& G, int dtype);

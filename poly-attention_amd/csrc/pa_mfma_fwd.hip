@@ -1101,6 +1101,7 @@ template <int D, bool SOFTCLAMP>
 constexpr int kFwdKB = (D == 64 && !SOFTCLAMP) ? PA_FWD_KB64 : 2;
 
 bool mfma_fwd_supported(const PassDev& P, int dtype) {
+    if (dtype == PA_F32) return mfma_fwd_f32_supported(P);
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
     if (P.dim != 64 && P.dim != 128) return false;
     if (!(P.scale > 0.f)) return false;  // the raw-score running max assumes a positive scale
@@ -1147,6 +1148,10 @@ static void launch_d(const PassDev& P, hipStream_t s) {
 }
 
 void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s) {
+    if (dtype == PA_F32) {
+        launch_mfma_fwd_f32(P, s);
+        return;
+    }
     if (dtype == PA_BF16) {
         if (P.dim == 64) launch_d<bf16, 64>(P, s);
         else launch_d<bf16, 128>(P, s);

@@ -140,6 +140,52 @@ __global__ __launch_bounds__(kSimtRows) void k_simt_fwd(PassDev P) {
     if (row && !degen) simt_write_row<T, D>(P, b, h, i, acc, 1.f / l, (m + log2f(l)) * kLn2);
 }
 
+// 8 consecutive elements to / from fp32: 16-byte aligned rows (the MFMA kernels' loads), and
+// 8-byte aligned rows (their stores) as two 8-byte accesses
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* f) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[k] = to_f(e[k]);
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* f) {  // 32 bytes
+    const float4 a = reinterpret_cast<const float4*>(p)[0], c = reinterpret_cast<const float4*>(p)[1];
+    f[0] = a.x;
+    f[1] = a.y;
+    f[2] = a.z;
+    f[3] = a.w;
+    f[4] = c.x;
+    f[5] = c.y;
+    f[6] = c.z;
+    f[7] = c.w;
+}
+template <typename T>
+__device__ __forceinline__ void load8_a8(const T* p, float* f) {
+    const uint2 a = reinterpret_cast<const uint2*>(p)[0], c = reinterpret_cast<const uint2*>(p)[1];
+    const T* ea = reinterpret_cast<const T*>(&a);
+    const T* ec = reinterpret_cast<const T*>(&c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        f[k] = to_f(ea[k]);
+        f[4 + k] = to_f(ec[k]);
+    }
+}
+template <typename T>
+__device__ __forceinline__ void store8_a8(T* p, const float* f) {
+    uint2 a, c;
+    T* ea = reinterpret_cast<T*>(&a);
+    T* ec = reinterpret_cast<T*>(&c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        ea[k] = from_f<T>(f[k]);
+        ec[k] = from_f<T>(f[4 + k]);
+    }
+    reinterpret_cast<uint2*>(p)[0] = a;
+    reinterpret_cast<uint2*>(p)[1] = c;
+}
+
 constexpr int kFixThreads = 1024;  // per-head reductions: many rows in flight on one CU
 
 // Finish the rows an MFMA forward left fully masked (their lse holds NaN), one workgroup per
@@ -169,16 +215,16 @@ __global__ __launch_bounds__(kFixThreads) void k_fwd_fixup(PassDev P) {
         if (cls == 1 && P.km.keep(b, j)) ++n1;
         if (cls != 0) continue;
         ++n0;
-        const uint4 raw = *reinterpret_cast<const uint4*>(P.v.row<T>(b, h, j) + c0);
-        const T* v8 = reinterpret_cast<const T*>(&raw);
+        float v8[8];
+        load8<T>(P.v.row<T>(b, h, j) + c0, v8);
         if (P.vmul.ok()) {
-            const uint4 mraw = *reinterpret_cast<const uint4*>(P.vmul.row<T>(b, h, j) + c0);
-            const T* m8 = reinterpret_cast<const T*>(&mraw);
+            float m8[8];
+            load8<T>(P.vmul.row<T>(b, h, j) + c0, m8);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] += round_to<T>(to_f(v8[e]) * to_f(m8[e]));
+            for (int e = 0; e < 8; ++e) acc[e] += round_to<T>(v8[e] * m8[e]);
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] += to_f(v8[e]);
+            for (int e = 0; e < 8; ++e) acc[e] += v8[e];
         }
     }
     __shared__ float sS[R][D];
@@ -632,40 +678,6 @@ __global__ __launch_bounds__(kFixThreads) void k_fix_rows(GradDev G) {
     }
 }
 
-// 8 consecutive elements to / from fp32: 16-byte aligned rows (the MFMA kernels' loads), and
-// 8-byte aligned rows (their stores) as two 8-byte accesses
-template <typename T>
-__device__ __forceinline__ void load8(const T* p, float* f) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(p);
-    const T* e = reinterpret_cast<const T*>(&raw);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) f[k] = to_f(e[k]);
-}
-template <typename T>
-__device__ __forceinline__ void load8_a8(const T* p, float* f) {
-    const uint2 a = reinterpret_cast<const uint2*>(p)[0], c = reinterpret_cast<const uint2*>(p)[1];
-    const T* ea = reinterpret_cast<const T*>(&a);
-    const T* ec = reinterpret_cast<const T*>(&c);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        f[k] = to_f(ea[k]);
-        f[4 + k] = to_f(ec[k]);
-    }
-}
-template <typename T>
-__device__ __forceinline__ void store8_a8(T* p, const float* f) {
-    uint2 a, c;
-    T* ea = reinterpret_cast<T*>(&a);
-    T* ec = reinterpret_cast<T*>(&c);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        ea[k] = from_f<T>(f[k]);
-        ec[k] = from_f<T>(f[4 + k]);
-    }
-    reinterpret_cast<uint2*>(p)[0] = a;
-    reinterpret_cast<uint2*>(p)[1] = c;
-}
-
 constexpr int kFixKeys = 256;  // keys per k_fix_keys workgroup
 
 // Part A updates of key head kh: dV (and dvmul) and dbias of the bias-class-0 keys,
@@ -1075,7 +1087,8 @@ void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s) {
 }
 void launch_fwd_fixup(const PassDev& P, int dtype, hipStream_t s) {
     const bool d64 = P.dim == 64;
-    if (dtype == PA_F16) d64 ? launch_fwd_fixup_t<f16, 64>(P, s) : launch_fwd_fixup_t<f16, 128>(P, s);
+    if (dtype == PA_F32) d64 ? launch_fwd_fixup_t<float, 64>(P, s) : launch_fwd_fixup_t<float, 128>(P, s);
+    else if (dtype == PA_F16) d64 ? launch_fwd_fixup_t<f16, 64>(P, s) : launch_fwd_fixup_t<f16, 128>(P, s);
     else d64 ? launch_fwd_fixup_t<bf16, 64>(P, s) : launch_fwd_fixup_t<bf16, 128>(P, s);
 }
 void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool dq, bool dkv) {

@@ -115,7 +115,7 @@ def test_pass_masks_and_degenerate_rows(dtype, causal):
           f"masks {dtype} causal={causal}")
 
 
-@param("dtype", (torch.bfloat16, torch.float16))
+@param("dtype", (torch.bfloat16, torch.float16, torch.float32))
 @param("d", (64, 128))
 @param("n", (150, 256))
 @param("causal", (False, True))
