@@ -32,6 +32,8 @@ void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s);
 // false when they do not cover P
 bool mfma_fwd_f32_supported(const PassDev& P);
 void launch_mfma_fwd_f32(const PassDev& P, hipStream_t s);
+bool mfma_bwd_f32_supported(const GradDev& G);  // unmasked passes
+void launch_mfma_bwd_f32(const GradDev& G, hipStream_t s);
 bool mfma_fwd_supported(const PassDev& P, int dtype);
 void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s);
 bool mfma_bwd_supported(const GradDev& G, int dtype);

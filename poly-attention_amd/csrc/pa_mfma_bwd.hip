@@ -1173,6 +1173,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
 
 bool mfma_bwd_supported(const GradDev& G, int dtype) {
     const PassDev& P = G.f;
+    if (dtype == PA_F32) return mfma_bwd_f32_supported(G);
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
     if (P.dim != 64 && P.dim != 128) return false;
     const DView* loads[] = {&P.q, &P.k, &P.v, &G.dout};
@@ -1215,7 +1216,7 @@ static bool bwd_dq_dma_ok(const GradDev& G) {
 // the O rows of its queries beside dO with 16-byte loads.
 bool mfma_bwd_fuses_pre(const GradDev& G) {
     const PassDev& P = G.f;
-    if (!PA_BWD_DMA || P.vmul.ok()) return false;
+    if (!PA_BWD_DMA || P.vmul.ok() || P.q.dtype == PA_F32) return false;
     if (P.dim != 64 && P.dim != 128) return false;
     return bwd_dq_dma_ok(G) && aligned_rows_host(P.out, 8);
 }
@@ -1265,6 +1266,10 @@ static void launch_bwd_d(const GradDev& G, hipStream_t s) {
 }
 
 void launch_mfma_bwd(const GradDev& G, int dtype, hipStream_t s) {
+    if (dtype == PA_F32) {
+        launch_mfma_bwd_f32(G, s);
+        return;
+    }
     if (dtype == PA_BF16) {
         if (G.f.dim == 64) launch_bwd_d<bf16, 64>(G, s);
         else launch_bwd_d<bf16, 128>(G, s);

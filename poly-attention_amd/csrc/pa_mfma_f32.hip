@@ -1,6 +1,8 @@
-// pa_mfma_f32.hip -- fp32 attention-pass forward on the matrix cores (v_mfma_f32_32x32x2_f32),
-// head dim 64 or 128.
+// pa_mfma_f32.hip -- fp32 attention passes on the matrix cores (v_mfma_f32_32x32x2_f32),
+// head dim 64 or 128: the forward (every pass feature), and the backward of unmasked passes
+// (k_mfma_bwd_f32_dq / k_mfma_bwd_f32_dkv, described at the kernels).
 //
+// Forward:
 // A workgroup of nw waves (1, 2 or 4, chosen by the grid size) owns 32 * nw queries of one
 // (batch, head); each wave owns 32.  Per 32-key tile staged in LDS (K, the effective value
 // v * vmul, the key term):
@@ -191,6 +193,334 @@ __global__ __launch_bounds__(256) void k_mfma_fwd_f32(PassDev P) {
             }
         }
     if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (m + log2f(lt)) * kLn2;
+}
+
+// ---------------------------------------------------------------------------------------
+// backward (unmasked passes; after the row preprocess: ws_lse, ws_D)
+
+// Stage 32 rows [r0, r0 + 32) of two [n, D] fp32 views of (b, h) in LDS (row stride RS)
+// through registers; rows past n read as zero.
+template <int D>
+struct F32Rows {
+    static constexpr int NL = kF32BN * (D / 4) / 64;  // 16-byte loads per thread (one wave)
+    float4 a[NL], c[NL];
+    __device__ __forceinline__ void load(const DView& va, const DView& vc, const DView& vm, int b,
+                                         int h, int r0, int n) {
+        const int nload = kF32BN * (D / 4);
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int e = threadIdx.x + i * (int)blockDim.x;
+            const int rr = e / (D / 4), c4 = (e % (D / 4)) * 4, r = r0 + rr;
+            float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+            if (e < nload && r < n) {
+                x = *reinterpret_cast<const float4*>(va.row<float>(b, h, r) + c4);
+                y = *reinterpret_cast<const float4*>(vc.row<float>(b, h, r) + c4);
+                if (vm.ok()) {  // effective value v * vmul
+                    const float4 mm = *reinterpret_cast<const float4*>(vm.row<float>(b, h, r) + c4);
+                    y.x *= mm.x;
+                    y.y *= mm.y;
+                    y.z *= mm.z;
+                    y.w *= mm.w;
+                }
+            }
+            a[i] = x;
+            c[i] = y;
+        }
+    }
+    __device__ __forceinline__ void store(float* sa, float* sc) const {
+        constexpr int RS = D + 1;
+        const int nload = kF32BN * (D / 4);
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int e = threadIdx.x + i * (int)blockDim.x;
+            if (e < nload) {
+                const int rr = e / (D / 4), c4 = (e % (D / 4)) * 4;
+                float* da = sa + rr * RS + c4;
+                float* dc = sc + rr * RS + c4;
+                da[0] = a[i].x;
+                da[1] = a[i].y;
+                da[2] = a[i].z;
+                da[3] = a[i].w;
+                dc[0] = c[i].x;
+                dc[1] = c[i].y;
+                dc[2] = c[i].z;
+                dc[3] = c[i].w;
+            }
+        }
+    }
+};
+
+__device__ __forceinline__ float key_term_l2(const PassDev& P, int b, int h, int j) {
+    if (j >= P.nk) return -INFINITY;
+    const float x = P.bias.ok() ? P.bias.scalar(b, h, j) : 0.f;
+    return bias_class(x) == 0 ? x * kLog2e : -INFINITY;
+}
+
+// one 4-element group of an output row: value (+ the old value with accumulate)
+__device__ __forceinline__ void store4(float* p, float4 v, bool acc) {
+    if (acc) {
+        const float4 o = *reinterpret_cast<const float4*>(p);
+        v.x += o.x;
+        v.y += o.y;
+        v.z += o.z;
+        v.w += o.w;
+    }
+    *reinterpret_cast<float4*>(p) = v;
+}
+
+// dQ, query-major: per key tile S^T = K Q^T and dP^T = V dO^T (lane = query), dS, then
+// dQ^T += K^T dS^T with dS entering as B from the score registers.
+template <int D>
+__global__ __launch_bounds__(256) void k_mfma_bwd_f32_dq(GradDev G) {
+    constexpr int RS = D + 1;
+    const PassDev& P = G.f;
+    __shared__ float sK[kF32BN * RS];
+    __shared__ float sV[kF32BN * RS];
+    __shared__ float sB[kF32BN];
+    const int nw = blockDim.x >> 6;
+    const int BM = 32 * nw;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const bool causal = P.causal != 0;
+    const int nqb = (P.nq + BM - 1) / BM;
+    int bh, rank;
+    if (causal) block_order<true>(nqb, bh, rank);
+    else block_order<false>(nqb, bh, rank);
+    const int qb = causal ? nqb - 1 - rank : rank;
+    const int h = bh % P.heads, b = bh / P.heads;
+    const int col = lane & 31, hh = lane >> 5;
+    const int q0 = qb * BM + w * 32, qi = q0 + col;
+    const bool qrow = qi < P.nq;
+    float qf[D / 2], of[D / 2];
+    {
+        const float* qr = P.q.row<float>(b, h, qrow ? qi : 0);
+        const float* orr = G.dout.row<float>(b, h, qrow ? qi : 0);
+#pragma unroll
+        for (int s = 0; s < D / 2; ++s) {
+            qf[s] = qrow ? qr[2 * s + hh] : 0.f;
+            of[s] = qrow ? orr[2 * s + hh] : 0.f;
+        }
+    }
+    const int64_t r = ((int64_t)b * P.heads + h) * P.nq + (qrow ? qi : 0);
+    const float lse_l2 = qrow ? G.ws_lse[r] * kLog2e : INFINITY;
+    const float dsum = qrow ? G.ws_D[r] : 0.f;
+    f32x16_t dq[D / 32];
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) dq[x] = zero16();
+    const bool sc = P.softclamp > 0.f;
+    const int kend = causal ? min(P.nk, qb * BM + BM) : P.nk;
+    const int wave_kend = causal ? min(kend, q0 + 32) : kend;
+    F32Rows<D> st;
+    float rb = 0.f;
+    if (kend > 0) {
+        st.load(P.k, P.v, P.vmul, b, h, 0, P.nk);
+        if (tid < kF32BN) rb = key_term_l2(P, b, h, tid);
+    }
+    for (int j0 = 0; j0 < kend; j0 += kF32BN) {
+        st.store(sK, sV);
+        if (tid < kF32BN) sB[tid] = rb;
+        __syncthreads();
+        if (j0 + kF32BN < kend) {
+            st.load(P.k, P.v, P.vmul, b, h, j0 + kF32BN, P.nk);
+            if (tid < kF32BN) rb = key_term_l2(P, b, h, j0 + kF32BN + tid);
+        }
+        if (j0 < wave_kend) {
+            f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+            for (int t = 0; t < D / 2; ++t) {
+                s = mfma_32x32x2(sK[col * RS + 2 * t + hh], qf[t], s);
+                dp = mfma_32x32x2(sV[col * RS + 2 * t + hh], of[t], dp);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int jj = 8 * (i / 4) + 4 * hh + (i % 4);
+                float y = s[i] * P.scale;
+                if (sc) y = softclamp_f(y, P.softclamp);
+                float t = y * kLog2e + sB[jj];
+                if (causal && j0 + jj > qi) t = -INFINITY;
+                const float p = fast_exp2(t - lse_l2);
+                s[i] = p * (dp[i] - dsum) * softclamp_grad(y, P.softclamp) * P.scale;
+            }
+#pragma unroll
+            for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int jj = 8 * (i / 4) + 4 * hh + (i % 4);
+                    dq[x] = mfma_32x32x2(sK[jj * RS + 32 * x + col], s[i], dq[x]);
+                }
+        }
+        __syncthreads();
+    }
+    if (!qrow) return;
+    float* row = G.dq.wrow<float>(b, h, qi);
+    const bool acc = (G.accumulate & PA_ACC_DQ) != 0;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            store4(row + 32 * x + 8 * g + 4 * hh,
+                   make_float4(dq[x][4 * g], dq[x][4 * g + 1], dq[x][4 * g + 2], dq[x][4 * g + 3]), acc);
+}
+
+// dK / dV / dbias, key-major: the wave's 32 keys (K and the effective value in registers as B
+// operands) against the query tiles of every query head of the group: C = Q K^T and
+// dP = dO V^T (lane = key), dV^T += dO^T P and dK^T += Q^T dS with P / dS entering as B.
+template <int D>
+__global__ __launch_bounds__(256) void k_mfma_bwd_f32_dkv(GradDev G) {
+    constexpr int RS = D + 1;
+    const PassDev& P = G.f;
+    __shared__ float sQ[kF32BN * RS];
+    __shared__ float sO[kF32BN * RS];
+    __shared__ float sL[kF32BN], sD[kF32BN];
+    const int nw = blockDim.x >> 6;
+    const int BK = 32 * nw;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const bool causal = P.causal != 0;
+    const int nkb = (P.nk + BK - 1) / BK;
+    int unit, kblk;  // causal: the first key blocks carry the most work
+    if (causal) block_order<true>(nkb, unit, kblk);
+    else block_order<false>(nkb, unit, kblk);
+    const int kh = unit % G.hk, b = unit / G.hk;
+    const int rep = P.heads / G.hk, h0 = kh * rep;
+    const int col = lane & 31, hh = lane >> 5;
+    const int k0 = kblk * BK + w * 32, kj = k0 + col;
+    const bool krow = kj < P.nk;
+    float kf[D / 2], vf[D / 2];
+    {
+        const float* kr = P.k.row<float>(b, h0, krow ? kj : 0);
+        const float* vr = P.v.row<float>(b, h0, krow ? kj : 0);
+        const float* mr = P.vmul.ok() ? P.vmul.row<float>(b, h0, krow ? kj : 0) : nullptr;
+#pragma unroll
+        for (int s = 0; s < D / 2; ++s) {
+            kf[s] = krow ? kr[2 * s + hh] : 0.f;
+            vf[s] = krow ? vr[2 * s + hh] * (mr ? mr[2 * s + hh] : 1.f) : 0.f;
+        }
+    }
+    const float bk = key_term_l2(P, b, h0, kj);  // -inf past nk
+    f32x16_t dk[D / 32], dv[D / 32];
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+        dk[x] = zero16();
+        dv[x] = zero16();
+    }
+    float dbias = 0.f;
+    const bool sc = P.softclamp > 0.f;
+    const int i_start = causal ? (kblk * BK / kF32BN) * kF32BN : 0;
+    const DView none = {nullptr, 0, 0, 0, 1, PA_F32};
+    for (int hr = 0; hr < rep; ++hr) {
+        const int h = h0 + hr;
+        const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
+        F32Rows<D> st;
+        float rl = 0.f, rd = 0.f;
+        auto load_rows = [&](int i0) __attribute__((always_inline)) {
+            st.load(P.q, G.dout, none, b, h, i0, P.nq);
+            if (tid < kF32BN) {
+                const int i = i0 + tid;
+                rl = i < P.nq ? G.ws_lse[row0 + i] * kLog2e : INFINITY;
+                rd = i < P.nq ? G.ws_D[row0 + i] : 0.f;
+            }
+        };
+        if (i_start < P.nq) load_rows(i_start);
+        for (int i0 = i_start; i0 < P.nq; i0 += kF32BN) {
+            st.store(sQ, sO);
+            if (tid < kF32BN) {
+                sL[tid] = rl;
+                sD[tid] = rd;
+            }
+            __syncthreads();
+            if (i0 + kF32BN < P.nq) load_rows(i0 + kF32BN);
+            if (!causal || i0 + kF32BN - 1 >= k0) {  // wave-uniform: some query reaches a key
+                f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+                for (int t = 0; t < D / 2; ++t) {
+                    s = mfma_32x32x2(sQ[col * RS + 2 * t + hh], kf[t], s);
+                    dp = mfma_32x32x2(sO[col * RS + 2 * t + hh], vf[t], dp);
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int ii = 8 * (i / 4) + 4 * hh + (i % 4);
+                    float y = s[i] * P.scale;
+                    if (sc) y = softclamp_f(y, P.softclamp);
+                    float t = y * kLog2e + bk;
+                    if (causal && i0 + ii < kj) t = -INFINITY;
+                    const float p = fast_exp2(t - sL[ii]);
+                    const float ds = p * (dp[i] - sD[ii]);
+                    dbias += ds;
+                    s[i] = p;
+                    dp[i] = ds * softclamp_grad(y, P.softclamp) * P.scale;
+                }
+#pragma unroll
+                for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int ii = 8 * (i / 4) + 4 * hh + (i % 4);
+                        dv[x] = mfma_32x32x2(sO[ii * RS + 32 * x + col], s[i], dv[x]);
+                        dk[x] = mfma_32x32x2(sQ[ii * RS + 32 * x + col], dp[i], dk[x]);
+                    }
+            }
+            __syncthreads();
+        }
+    }
+    dbias = xhalf_sum(dbias);
+    if (!krow) return;
+    const float* mr = P.vmul.ok() ? P.vmul.row<float>(b, h0, kj) : nullptr;
+    const float* vr = P.v.row<float>(b, h0, kj);
+    float* dkr = G.dk.wrow<float>(b, h0, kj);
+    float* dvr = G.dv.wrow<float>(b, h0, kj);
+    float* dmr = mr ? G.dvmul.wrow<float>(b, h0, kj) : nullptr;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * x + 8 * g + 4 * hh;
+            store4(dkr + d, make_float4(dk[x][4 * g], dk[x][4 * g + 1], dk[x][4 * g + 2], dk[x][4 * g + 3]),
+                   (G.accumulate & PA_ACC_DK) != 0);
+            float4 e = make_float4(dv[x][4 * g], dv[x][4 * g + 1], dv[x][4 * g + 2], dv[x][4 * g + 3]);
+            if (mr) {
+                const float4 m4 = *reinterpret_cast<const float4*>(mr + d);
+                const float4 v4 = *reinterpret_cast<const float4*>(vr + d);
+                store4(dmr + d, make_float4(e.x * v4.x, e.y * v4.y, e.z * v4.z, e.w * v4.w),
+                       (G.accumulate & PA_ACC_DVMUL) != 0);
+                e = make_float4(e.x * m4.x, e.y * m4.y, e.z * m4.z, e.w * m4.w);
+            }
+            store4(dvr + d, e, (G.accumulate & PA_ACC_DV) != 0);
+        }
+    if (hh == 0 && G.dbias.ok()) {
+        float* o = G.dbias.wrow<float>(b, h0, kj);
+        *o = dbias + ((G.accumulate & PA_ACC_DBIAS) ? *o : 0.f);
+    }
+}
+
+bool mfma_bwd_f32_supported(const GradDev& G) {
+    const PassDev& P = G.f;
+    if (P.dim != 64 && P.dim != 128) return false;
+    if (P.km.p || P.qm.p || (P.flags & PA_FLAG_MAY_DEGENERATE)) return false;
+    for (const DView* v : {&P.q, &P.k, &P.v, &G.dout, &G.dq, &G.dk, &G.dv})
+        if (!aligned_rows_host(*v, 4)) return false;
+    if (P.vmul.ok() && (!aligned_rows_host(P.vmul, 4) || !aligned_rows_host(G.dvmul, 4))) return false;
+    return true;
+}
+
+void launch_mfma_bwd_f32(const GradDev& G, hipStream_t s) {
+    const PassDev& P = G.f;
+    auto waves = [](int64_t units, int n) {
+        int nw = 4;
+        while (nw > 1 && units * ((n + 32 * nw - 1) / (32 * nw)) < 512) nw >>= 1;
+        return nw;
+    };
+    {
+        const int nw = waves((int64_t)P.batch * P.heads, P.nq);
+        const dim3 grid(P.batch * P.heads * ((P.nq + 32 * nw - 1) / (32 * nw)));
+        ProfScope ps("mfma_bwd_f32_dq", s);
+        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dq<64>), grid, dim3(64 * nw), 0, s, G);
+        else hipLaunchKernelGGL((k_mfma_bwd_f32_dq<128>), grid, dim3(64 * nw), 0, s, G);
+    }
+    {
+        const int nw = waves((int64_t)P.batch * G.hk, P.nk);
+        const dim3 grid(P.batch * G.hk * ((P.nk + 32 * nw - 1) / (32 * nw)));
+        ProfScope ps("mfma_bwd_f32_dkv", s);
+        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dkv<64>), grid, dim3(64 * nw), 0, s, G);
+        else hipLaunchKernelGGL((k_mfma_bwd_f32_dkv<128>), grid, dim3(64 * nw), 0, s, G);
+    }
 }
 
 bool mfma_fwd_f32_supported(const PassDev& P) {
