@@ -124,6 +124,11 @@ typedef struct pa_pass {
     pa_view out;          /* [B, heads, nq, dim], dtype of q */
     pa_view lse;          /* [B, heads, nq], PA_F32 */
     const pa_epilogue* epi;  /* optional module epilogue (NULL: none) */
+    /* Optional forward workspace of pa_attn_pass_fwd_workspace() bytes (ignored by the
+     * backward): with it a key-masked pass folds its key mask into a per-key term and takes
+     * the faster forward kernel; without it the results are the same. */
+    void*   workspace;
+    size_t  workspace_bytes;
 } pa_pass;
 
 /* Backward of one pass.  In the backward the key-side tensors (k, v, vmul, bias) must share
@@ -319,6 +324,7 @@ int pa_profile_start(void);
 int pa_profile_stop(pa_kernel_time* out, int capacity, int* count);
 
 int    pa_attn_pass_fwd(const pa_pass* p, void* stream);
+size_t pa_attn_pass_fwd_workspace(const pa_pass* p);   /* 0: the forward takes none */
 size_t pa_attn_pass_bwd_workspace(const pa_pass_grad* g);
 int    pa_attn_pass_bwd(const pa_pass_grad* g, void* stream);
 size_t pa_poly_decode_workspace(const pa_decode* d);

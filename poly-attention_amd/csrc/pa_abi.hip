@@ -156,6 +156,17 @@ int key_term_stride(const pa_pass& f) { return (f.nk + 3) & ~3; }
 
 size_t elem_bytes(int dtype) { return dtype == PA_F32 ? 4 : 2; }
 
+// forward workspace: the per-key term (and the bias-class counts written with it) of a
+// key-masked 16-bit pass on the MFMA kernels, whose key bias it then is
+size_t fwd_ws_bytes(const pa_pass& f) {
+    if (!f.key_mask.ptr || (f.q.dtype != PA_BF16 && f.q.dtype != PA_F16)) return 0;
+    if (f.dim != 64 && f.dim != 128) return 0;
+    if (f.bias.ptr && f.bias.heads != f.k.heads) return 0;  // one key term per key head
+    const size_t kheads = (size_t)f.batch * f.k.heads;
+    return align256(kheads * key_term_stride(f) * sizeof(float)) +
+           align256(kheads * 2 * sizeof(int32_t));
+}
+
 // [D | lse | 1/c1] per query row; with an epilogue the gradient reaching the pass output;
 // masked passes add the key term (with a key mask), the per-head fully-masked-row sums and
 // the per-key-head bias-class counts
@@ -253,13 +264,35 @@ int pa_profile_stop(pa_kernel_time* out, int capacity, int* count) {
     return status;
 }
 
+size_t pa_attn_pass_fwd_workspace(const pa_pass* p) { return p ? fwd_ws_bytes(*p) : 0; }
+
 int pa_attn_pass_fwd(const pa_pass* p, void* stream) {
     PA_TRY(validate_pass(p));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const PassDev P = to_passdev(p);
     const int T = p->q.dtype;
     if (mfma_fwd_supported(P, T)) {
-        launch_mfma_fwd(P, T, s);
+        const size_t need = fwd_ws_bytes(*p);
+        if (need && p->workspace && p->workspace_bytes >= need) {
+            // the key mask folded into a per-key term read as the key bias (the
+            // direct-to-LDS kernel has no key-mask path); fully-masked rows as before
+            const int hk = p->k.heads, nkp = key_term_stride(*p);
+            char* w = static_cast<char*>(p->workspace);
+            float* kterm = reinterpret_cast<float*>(w);
+            int32_t* kcnt = reinterpret_cast<int32_t*>(
+                w + align256((size_t)p->batch * hk * nkp * sizeof(float)));
+            GradDev G = {};  // the key-term kernel reads f and hk only
+            G.f = P;
+            G.hk = hk;
+            launch_key_terms(G, kterm, nkp, kcnt, s);
+            PassDev Pm = P;
+            Pm.bias = DView{reinterpret_cast<char*>(kterm), (int64_t)hk * nkp, nkp, 1,
+                            p->heads / hk, PA_F32};
+            Pm.km.p = nullptr;
+            launch_mfma_fwd(Pm, T, s);
+        } else {
+            launch_mfma_fwd(P, T, s);
+        }
         const bool may_degenerate = (p->flags & PA_FLAG_MAY_DEGENERATE) || p->key_mask.ptr ||
                                     p->query_mask.ptr;
         if (may_degenerate) launch_fwd_fixup(P, T, s);

@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "pa_profile_start",
     "pa_profile_stop",
     "pa_attn_pass_fwd",
+    "pa_attn_pass_fwd_workspace",
     "pa_attn_pass_bwd_workspace",
     "pa_attn_pass_bwd",
     "pa_poly_decode_workspace",
@@ -97,6 +98,8 @@ class PaPass(ctypes.Structure):
         ("out", PaView),
         ("lse", PaView),
         ("epi", c_void_p),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
     ]
 
 
@@ -277,6 +280,8 @@ def _configure(lib) -> None:
     lib.pa_profile_stop.argtypes = [ctypes.POINTER(PaKernelTime), c_int, ctypes.POINTER(c_int)]
     lib.pa_attn_pass_fwd.restype = c_int
     lib.pa_attn_pass_fwd.argtypes = [ctypes.POINTER(PaPass), c_void_p]
+    lib.pa_attn_pass_fwd_workspace.restype = c_size_t
+    lib.pa_attn_pass_fwd_workspace.argtypes = [ctypes.POINTER(PaPass)]
     lib.pa_attn_pass_bwd_workspace.restype = c_size_t
     lib.pa_attn_pass_bwd_workspace.argtypes = [ctypes.POINTER(PaPassGrad)]
     lib.pa_attn_pass_bwd.restype = c_int

@@ -172,6 +172,12 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
         epi = _epilogue_struct(epilogue, y)
     p = _pass_struct(q, k, v, vmul, bias, km, qm, out, lse, causal, softclamp, scale,
                      may_degenerate or km is not None or qm is not None, epi)
+    ws = None
+    if km is not None:  # a key-masked pass takes the faster kernel with a workspace
+        ws_bytes = lib.pa_attn_pass_fwd_workspace(ctypes.byref(p))
+        if ws_bytes:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+            p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
     with _device(q):
         _lib.check(lib.pa_attn_pass_fwd(ctypes.byref(p), _stream(q)), "pa_attn_pass_fwd")
     return (out, lse) if epilogue is None else (out, lse, y)

@@ -164,6 +164,50 @@ def test_pass_masked_mfma_key_mask_only(causal):
           f"masked mfma key mask only causal={causal}")
 
 
+@param("causal", (False, True))
+def test_pass_key_masked_forward_with_and_without_workspace(causal):
+    """pa_attn_pass_fwd on a key-masked bf16 pass: with its optional workspace the key mask
+    becomes a per-key term and the direct-to-LDS kernel runs; without it the register-staged
+    kernel reads the mask.  The same outputs up to the two kernels' different rounding points
+    (P enters its MFMA in bf16 in both, summed in a different order: 1e-2 here, below the
+    oracle bound both meet) and lse (the direct-to-LDS kernel sums the rounded P, as its PV
+    product uses them: 2e-3), fully-masked rows included."""
+    import ctypes
+
+    from poly_attention import _lib, _ops
+
+    d = dev()
+    lib = _lib.load()
+    n = 256
+    q, k, v = (randn((2, 4, n, 64), torch.bfloat16, s).to(d) for s in (51, 52, 53))
+    bias = (randn((2, 4, n), torch.float32, 54) + 3.0).to(d)
+    km = torch.ones(2, n, dtype=torch.bool)
+    km[0, :3] = False
+    km[1, n // 3:] = False
+    km8 = km.to(d).to(torch.uint8)
+    results = []
+    for use_ws in (False, True):
+        out = torch.empty_like(q)
+        lse = torch.empty(2, 4, n, dtype=torch.float32, device=d)
+        p = _ops._pass_struct(q, k, v, None, bias, km8, None, out, lse, causal, 0.0, 64 ** -0.5,
+                              True)
+        ws = None
+        if use_ws:
+            nbytes = lib.pa_attn_pass_fwd_workspace(ctypes.byref(p))
+            assert nbytes > 0
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=d)
+            p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+        _lib.check(lib.pa_attn_pass_fwd(ctypes.byref(p), torch.cuda.current_stream().cuda_stream),
+                   "pa_attn_pass_fwd")
+        torch.cuda.synchronize()
+        results.append((out, lse))
+    (o0, l0), (o1, l1) = results
+    assert_parity(o1, o0.float(), torch.bfloat16, f"key-masked fwd, workspace vs none causal={causal}",
+                  tol=1e-2)
+    assert_parity(l1, l0, torch.float32, f"key-masked lse, workspace vs none causal={causal}",
+                  tol=2e-3)
+
+
 @param("dtype", (torch.float32, torch.bfloat16))
 def test_pass_cross_lengths(dtype):
     """Different query and key lengths (contexts), causal with a top-left aligned mask."""
