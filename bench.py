@@ -322,7 +322,7 @@ def config1_bench(dev, steps, warmup, cpu):
     if cpu:
         import oracle.poly_oracle as O
 
-        torch.set_num_threads(cpu_threads())
+        torch.set_num_threads(cpu_threads()[0])
         cfg = dict(heads=8, dim_head=64, causal=False)
         with torch.no_grad():
             O.order2_forward(params, cfg, x)
@@ -732,6 +732,25 @@ def cpu_model() -> str:
     return max(names, key=len) if names else (platform.processor() or "unknown")
 
 
+def cpu_identity() -> dict:
+    """CPU family / model / stepping and clock from /proc/cpuinfo: on hosts whose model name
+    is only "AMD EPYC" (virtualised), these identify the generation (family 25 = Zen 3 / 4,
+    26 = Zen 5)."""
+    info = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if not ln.strip():
+                    break  # the first processor's block
+                k, _, v = ln.partition(":")
+                k = k.strip()
+                if k in ("cpu family", "model", "stepping", "cpu MHz", "cache size"):
+                    info[k.replace(" ", "_")] = v.strip()
+    except OSError:
+        pass
+    return info
+
+
 def cpu_baseline(max_seconds=20.0):
     import oracle.poly_oracle as O
 
@@ -767,6 +786,7 @@ def cpu_baseline(max_seconds=20.0):
         "host_cpus": total,
         "usable_cpus": usable,
         "cpu_model": cpu_name,
+        "cpu_identity": cpu_identity(),
         "threads_reason": "torch threads = CPUs this process may use, capped by OMP_NUM_THREADS "
                           "(the box's per-GPU CPU share)",
         "kind": "port",
