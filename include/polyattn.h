@@ -345,6 +345,11 @@ int    pa_poly_decode(const pa_decode* d, void* stream);
 int    pa_poly_decode_noalloc(const pa_decode* d, void* stream);
 int    pa_decode_prologue(const pa_prologue* p, void* stream);
 int    pa_rmsnorm_fwd(const pa_rmsnorm* r, void* stream);
+/* Up to PA_RMS_MAX_ITEMS forwards of one dtype and dim (no rotary angles) in one launch: the
+ * q/k norms of a layer (poly_attention.py:271, n_poly_attention.py:188) when no gradient is
+ * needed (inference, prefill). */
+#define PA_RMS_MAX_ITEMS 4
+int    pa_rmsnorm_fwd_many(const pa_rmsnorm* items, int count, void* stream);
 size_t pa_rmsnorm_bwd_workspace(const pa_rmsnorm* r);
 int    pa_rmsnorm_bwd(const pa_rmsnorm* r, void* stream);
 int    pa_linear_small(const pa_linear* l, void* stream);

@@ -459,6 +459,12 @@ int pa_rmsnorm_fwd(const pa_rmsnorm* r, void* stream) {
     return finish_launch();
 }
 
+int pa_rmsnorm_fwd_many(const pa_rmsnorm* items, int count, void* stream) {
+    const int st = launch_rms_fwd_many(items, count, static_cast<hipStream_t>(stream));
+    if (st != PA_OK) return st;
+    return finish_launch();
+}
+
 size_t pa_rmsnorm_bwd_workspace(const pa_rmsnorm* r) {
     if (!r) return 0;
     return rms_bwd_workspace(r);

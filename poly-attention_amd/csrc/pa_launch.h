@@ -49,6 +49,7 @@ int launch_decode(const pa_decode* d, hipStream_t s);
 int launch_decode_noalloc(const pa_decode* d, hipStream_t s, int* hip_err);
 int launch_prologue(const pa_prologue* p, hipStream_t s);
 int launch_rms_fwd(const pa_rmsnorm* p, hipStream_t s);
+int launch_rms_fwd_many(const pa_rmsnorm* items, int count, hipStream_t s);
 size_t rms_bwd_workspace(const pa_rmsnorm* p);
 int launch_rms_bwd(const pa_rmsnorm* p, hipStream_t s);
 int launch_linear_small(const pa_linear* l, hipStream_t s);

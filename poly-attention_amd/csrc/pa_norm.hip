@@ -4,6 +4,8 @@
 // reads a whole row with 16-byte loads, reduces with DPP inside the row group, and writes the
 // row back; the backward writes dx and accumulates the weight gradient per workgroup into a
 // fixed partial row, summed afterwards in a fixed order (deterministic, no atomics).
+#include <algorithm>
+
 #include "pa_common.h"
 #include "pa_launch.h"
 
@@ -144,7 +146,7 @@ __device__ __forceinline__ uint32_t rstd_index(const RmsDev& R, uint32_t b, uint
 // y = round(x * rsqrt(mean(x^2) + eps) * w); rstd saved per row.  Each row group handles
 // kRmsU rows per pass, their loads issued together (memory-level parallelism).
 template <typename T, int LPR, bool ROPE>
-__global__ __launch_bounds__(kRmsThreads) void k_rms_fwd(RmsDev R) {
+__device__ __forceinline__ void rms_fwd_rows(const RmsDev& R) {
     constexpr int E = RVec<T>::n;
     constexpr int RPB = kRmsThreads / LPR;  // row groups per block
     const int sub = threadIdx.x % LPR, rg = threadIdx.x / LPR;
@@ -187,6 +189,21 @@ __global__ __launch_bounds__(kRmsThreads) void k_rms_fwd(RmsDev R) {
             if (sub == 0) R.rstd[rstd_index(R, b[u], h[u], i[u])] = rs;
         }
     }
+}
+
+template <typename T, int LPR, bool ROPE>
+__global__ __launch_bounds__(kRmsThreads) void k_rms_fwd(RmsDev R) {
+    rms_fwd_rows<T, LPR, ROPE>(R);
+}
+
+// several norms in one launch (pa_rmsnorm_fwd_many): blockIdx.y selects the tensor
+struct RmsMany {
+    RmsDev it[PA_RMS_MAX_ITEMS];
+};
+
+template <typename T, int LPR>
+__global__ __launch_bounds__(kRmsThreads) void k_rms_fwd_many(RmsMany M) {
+    rms_fwd_rows<T, LPR, false>(M.it[blockIdx.y]);
 }
 
 // dx = rstd * (g - xhat * mean(g * xhat)), g = dy * w, xhat = x * rstd; the block's weight
@@ -382,6 +399,37 @@ int launch_rms_fwd(const pa_rmsnorm* p, hipStream_t s) {
     if (p->x.dtype == PA_F32) rms_launch<float>(R, false, s);
     else if (p->x.dtype == PA_F16) rms_launch<f16>(R, false, s);
     else rms_launch<bf16>(R, false, s);
+    return PA_OK;
+}
+
+int launch_rms_fwd_many(const pa_rmsnorm* items, int count, hipStream_t s) {
+    if (!items || count < 1 || count > PA_RMS_MAX_ITEMS) return PA_EINVAL;
+    RmsMany M;
+    int blocks = 1;
+    for (int k = 0; k < count; ++k) {
+        const pa_rmsnorm* p = items + k;
+        if (p->angles) return PA_EUNSUPPORTED;  // rotary: one pa_rmsnorm_fwd per tensor
+        if (p->x.dtype != items[0].x.dtype || p->dim != items[0].dim) return PA_EINVAL;
+        const int st = rms_setup(p, M.it[k], false);
+        if (st != PA_OK) return st;
+        blocks = std::max(blocks, rms_blocks(M.it[k]));
+    }
+    const dim3 grid(blocks, count);
+    ProfScope ps("rms_fwd_many", s);
+#define PA_RMS_MANY(T)                                                                        \
+    switch (M.it[0].lpr) {                                                                    \
+        case 1: hipLaunchKernelGGL((k_rms_fwd_many<T, 1>), grid, dim3(kRmsThreads), 0, s, M); break;   \
+        case 2: hipLaunchKernelGGL((k_rms_fwd_many<T, 2>), grid, dim3(kRmsThreads), 0, s, M); break;   \
+        case 4: hipLaunchKernelGGL((k_rms_fwd_many<T, 4>), grid, dim3(kRmsThreads), 0, s, M); break;   \
+        case 8: hipLaunchKernelGGL((k_rms_fwd_many<T, 8>), grid, dim3(kRmsThreads), 0, s, M); break;   \
+        case 16: hipLaunchKernelGGL((k_rms_fwd_many<T, 16>), grid, dim3(kRmsThreads), 0, s, M); break; \
+        case 32: hipLaunchKernelGGL((k_rms_fwd_many<T, 32>), grid, dim3(kRmsThreads), 0, s, M); break; \
+        default: hipLaunchKernelGGL((k_rms_fwd_many<T, 64>), grid, dim3(kRmsThreads), 0, s, M); break; \
+    }
+    if (items[0].x.dtype == PA_F32) { PA_RMS_MANY(float) }
+    else if (items[0].x.dtype == PA_F16) { PA_RMS_MANY(f16) }
+    else { PA_RMS_MANY(bf16) }
+#undef PA_RMS_MANY
     return PA_OK;
 }
 

@@ -32,6 +32,7 @@ PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 PA_FLAG_MAY_DEGENERATE = 1
 PA_EPI_ROOT_SIGMOID = 1
 PA_ACC_DQ, PA_ACC_DK, PA_ACC_DV, PA_ACC_DVMUL, PA_ACC_DBIAS = 1, 2, 4, 8, 16
+PA_RMS_MAX_ITEMS = 4
 
 DTYPE_CODE = {torch.float32: PA_F32, torch.float16: PA_F16, torch.bfloat16: PA_BF16}
 
@@ -52,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "pa_poly_decode_noalloc",
     "pa_decode_prologue",
     "pa_rmsnorm_fwd",
+    "pa_rmsnorm_fwd_many",
     "pa_rmsnorm_bwd_workspace",
     "pa_rmsnorm_bwd",
     "pa_linear_small",
@@ -296,6 +298,8 @@ def _configure(lib) -> None:
     lib.pa_decode_prologue.argtypes = [ctypes.POINTER(PaPrologue), c_void_p]
     lib.pa_rmsnorm_fwd.restype = c_int
     lib.pa_rmsnorm_fwd.argtypes = [ctypes.POINTER(PaRmsNorm), c_void_p]
+    lib.pa_rmsnorm_fwd_many.restype = c_int
+    lib.pa_rmsnorm_fwd_many.argtypes = [ctypes.POINTER(PaRmsNorm), c_int, c_void_p]
     lib.pa_rmsnorm_bwd_workspace.restype = c_size_t
     lib.pa_rmsnorm_bwd_workspace.argtypes = [ctypes.POINTER(PaRmsNorm)]
     lib.pa_rmsnorm_bwd.restype = c_int

@@ -534,6 +534,30 @@ def rms_norm(x: Tensor, weight: Optional[Tensor], eps: Optional[float],
     return rms_norm_op(x, weight, float(eps), angles)[0]
 
 
+def rms_norm_many(xs: Sequence[Tensor], weights: Sequence[Optional[Tensor]],
+                  eps: Sequence[Optional[float]]) -> list[Tensor]:
+    """torch.nn.RMSNorm of up to PA_RMS_MAX_ITEMS [B, H, N, d] CUDA tensors of one dtype and d
+    in one launch (pa_rmsnorm_fwd_many), without autograd: the q/k norms of a layer when no
+    gradient is needed.  The caller checks rms_supported for each (no rotary angles)."""
+    lib = _lib.load()
+    n = len(xs)
+    assert 1 <= n <= _lib.PA_RMS_MAX_ITEMS
+    items = (PaRmsNorm * n)()
+    ys, keep = [], []
+    for k, (x, w, e) in enumerate(zip(xs, weights, eps)):
+        x = _aligned16(x)
+        y = _empty_heads(x.shape, x)
+        rstd = torch.empty(x.shape[:3], dtype=torch.float32, device=x.device)
+        r = _rms_struct(x, w, torch.finfo(torch.float32).eps if e is None else float(e))
+        r.y, r.rstd = _view(y), rstd.data_ptr()
+        items[k] = r
+        ys.append(y)
+        keep += [x, rstd]
+    with _device(xs[0]):
+        _lib.check(lib.pa_rmsnorm_fwd_many(items, n, _stream(xs[0])), "pa_rmsnorm_fwd_many")
+    return ys
+
+
 # ---------------------------------------------------------------------------------------
 # projections of a single-token decode step
 

@@ -50,7 +50,11 @@ def _q_norms(module, norms, qs, rotary_pos_emb=None):
     """The per-head q/k RMSNorms (poly_attention.py:271, n_poly_attention.py:188), then the
     external rotary when given (:275-276, :190-191): on the fused GPU path through pa_rmsnorm
     (forward and backward, the rotation inside the same kernel), else torch.nn.RMSNorm and
-    apply_rotary_emb."""
+    apply_rotary_emb.  Without gradients and rotary the norms of a layer go out in one launch
+    (pa_rmsnorm_fwd_many)."""
+    many = _q_norms_one_launch(module, norms, qs, rotary_pos_emb)
+    if many is not None:
+        return many
     out = []
     for norm, q in zip(norms, qs):
         if (module._use_fused(q) and isinstance(norm, RMSNorm)
@@ -67,6 +71,32 @@ def _q_norms(module, norms, qs, rotary_pos_emb=None):
         q = norm(q)
         out.append(apply_rotary_emb(rotary_pos_emb, q) if exists(rotary_pos_emb) else q)
     return tuple(out)
+
+
+def _q_norms_one_launch(module, norms, qs, rotary_pos_emb):
+    """The norms of ``qs`` in one pa_rmsnorm_fwd_many launch when that applies: the fused GPU
+    path, no gradient, no rotary, not under torch.compile, every norm an RMSNorm over the
+    head dim of a tensor pa_rmsnorm takes, one dtype and head dim.  Else None."""
+    from . import _lib, _ops
+
+    if exists(rotary_pos_emb) or not 1 <= len(qs) <= _lib.PA_RMS_MAX_ITEMS:
+        return None
+    if torch.compiler.is_compiling():
+        return None
+    weights = [getattr(n, "weight", None) for n in norms]
+    if torch.is_grad_enabled() and (any(q.requires_grad for q in qs) or
+                                    any(w is not None and w.requires_grad for w in weights)):
+        return None
+    q0 = qs[0]
+    for norm, q in zip(norms, qs):
+        if not (isinstance(norm, RMSNorm) and module._use_fused(q)
+                and tuple(norm.normalized_shape) == (q.shape[-1],)):
+            return None
+        if q.dtype != q0.dtype or q.shape[-1] != q0.shape[-1] or q.device != q0.device:
+            return None
+        if not _ops.rms_supported(q, norm.weight):
+            return None
+    return tuple(_ops.rms_norm_many(qs, weights, [n.eps for n in norms]))
 
 
 def _static_decode_step(module, qs, vs, mask, context_mask, rotary_pos_emb,

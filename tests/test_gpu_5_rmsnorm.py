@@ -189,3 +189,32 @@ def test_module_grads_with_fused_norms(order, rotary):
     assert_parity(xg.grad, xr.grad, torch.float32, f"{what} dx")
     for name, p in m.named_parameters():
         assert_parity(p.grad, params[name].grad, torch.float32, f"{what} d{name}")
+
+
+@param("dtype", (torch.bfloat16, torch.float32))
+def test_rmsnorm_many_one_launch(dtype):
+    """pa_rmsnorm_fwd_many: the q/k norms of a layer in one launch, without autograd (three
+    head-split views of one projection, different weights and eps, and a contiguous tensor
+    of another shape): each output bit-identical to pa_rmsnorm_fwd's, and torch.nn.RMSNorm's
+    within one rounding."""
+    from poly_attention import _ops
+
+    d = dev()
+    g = torch.Generator().manual_seed(31)
+    proj = (torch.randn(2, 65, 3 * 16 * 64, generator=g) * 3).to(dtype).to(d)
+    heads = proj.view(2, 65, 3, 16, 64).permute(2, 0, 3, 1, 4)  # 3 x [B, H, N, d] views
+    xs = [heads[0], heads[1], heads[2], (torch.randn(1, 4, 7, 64, generator=g)).to(dtype).to(d)]
+    ws = [(torch.rand(64, generator=g) + 0.5).to(dtype).to(d) for _ in xs]
+    eps = [None, 1e-6, 1e-5, None]
+    with torch.no_grad():
+        ys = _ops.rms_norm_many(xs, ws, eps)
+        for x, w, e, y in zip(xs, ws, eps, ys):
+            one = _ops.rms_norm(x, w, e)
+            assert torch.equal(y, one)
+            ref = torch.nn.functional.rms_norm(x, (64,), w, e)
+            if dtype == torch.float32:
+                assert_parity(y, ref, dtype, "rms_norm_many fp32", tol=1e-5)
+            else:  # one rounding apart at most
+                diff = (y.float() - ref.float()).abs()
+                ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -7
+                assert bool((diff <= ulp).all()), diff.max().item()
