@@ -150,6 +150,28 @@ def test_pass_masked_mfma_head_dims(dtype, d, n, causal, gqa):
     check(res, dtype, f"masked mfma {dtype} d={d} n={n} causal={causal} gqa={gqa}")
 
 
+@param("dtype", (torch.bfloat16, torch.float32))
+@param("causal", (False, True))
+@param("softclamp", (None, 5.0))
+def test_pass_masked_mfma_cross_lengths_softclamp(dtype, causal, softclamp):
+    """Masks at the MFMA head dim with 96 queries over 200 keys (contexts), softclamp on the
+    scores, a key bias with -finfo.max entries and GQA: the key term, the fully-masked-row
+    fix-ups and the causal limits with nq != nk."""
+    nq, nk = 96, 200
+    q = randn((2, 4, nq, 64), dtype, 61)
+    k, v = (randn((2, 2, nk, 64), dtype, s) for s in (62, 63))
+    bias = randn((2, 2, nk), torch.float32, 64) + 2.0
+    bias[0, :, 2:4] = -torch.finfo(torch.float32).max
+    km = torch.ones(2, nk, dtype=torch.bool)
+    km[0, :2] = False
+    km[1, 50:120] = False
+    qm = torch.ones(2, nq, dtype=torch.bool)
+    qm[1, :5] = False
+    res = run_pass(q, k, v, bias=bias, key_mask=km, query_mask=qm, causal=causal,
+                   softclamp=softclamp)
+    check(res, dtype, f"masked cross {dtype} causal={causal} sc={softclamp}")
+
+
 @param("causal", (False, True))
 def test_pass_masked_mfma_key_mask_only(causal):
     """A key mask with no bias (the first pass of a masked chain): the key mask becomes the
