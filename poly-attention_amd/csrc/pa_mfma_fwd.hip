@@ -844,6 +844,132 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
 // The direct-to-LDS kernel addresses K / V with 32-bit byte offsets up to the end of the last
 // tile and reads the key bias as one contiguous row; other cases take the register-staged
 // kernel.
+// ---------------------------------------------------------------------------------------
+// Short passes (nq, nk <= 64, head dim 64, not causal, no value multiplier or key mask: the
+// PolyViT shape): one (batch, head) unit per wave, kShortUnits units per workgroup.  Such a
+// pass is one key tile per unit and a few microseconds of dependent latency (loads, 16 MFMAs,
+// softmax, 16 MFMAs, store); what sets the time is how many units run at once.  The general
+// kernels' 256-query workgroups (three LDS stages, up to 256 VGPRs per lane) fit two or three
+// per CU, so 1024 units took two rounds; here each wave stages only its own K and V^T tile
+// (18 KB) and works on it alone -- no workgroup barrier, a wave may finish independently.
+
+constexpr int kShortUnits = 4;
+
+template <typename T, bool SOFTCLAMP, bool HAS_BIAS>
+__global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
+    constexpr int D = 64, KB = 2;
+    using TL = FwdTile<D, KB>;
+    constexpr int BN = TL::BN;
+    using W = FwdWave<T, D, KB, false, SOFTCLAMP, HAS_BIAS>;
+    typedef typename W::frag frag;
+    __shared__ __attribute__((aligned(16))) T sK[kShortUnits][BN * TL::KS];
+    __shared__ __attribute__((aligned(16))) T sVt[kShortUnits][D * TL::VS];
+    __shared__ __attribute__((aligned(16))) float sB[kShortUnits][BN];
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int unit = blockIdx.x * kShortUnits + w;
+    if (unit >= P.batch * P.heads) return;  // whole waves; nothing below synchronises waves
+    const int h = unit % P.heads, b = unit / P.heads;
+    T* Ks = sK[w];
+    T* Vt = sVt[w];
+    float* Bk = sB[w];
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+    const int hh = lane >> 5, kcol = lane & 31;
+
+    // the Q^T fragments of both 32-query blocks (lane (q, hh): Q[q][c*16 + 8*hh .. +7]), issued
+    // with the key loads below: one memory round trip per unit
+    u32x4_t qraw[2][D / 16];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int qi = 32 * u + kcol;
+        const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+            qraw[u][c] = qi < P.nq ? *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh) : zero;
+    }
+
+    // this unit's keys: K row-major, V transposed (4-key x 8-dim blocks), the key term
+    for (int blk = lane; blk < TL::BLOCKS; blk += 64) {
+        const int rg = blk / (D / 8), cc = blk % (D / 8);
+        u32x4_t kw[4], vw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int j = rg * 4 + r;
+            kw[r] = j < P.nk ? *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h, j) + cc * 8) : zero;
+            vw[r] = j < P.nk ? *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h, j) + cc * 8) : zero;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) *reinterpret_cast<u32x4_t*>(Ks + (rg * 4 + r) * TL::KS + cc * 8) = kw[r];
+        store_block_transposed(vw, reinterpret_cast<uint16_t*>(Vt + (cc * 8) * TL::VS + rg * 4), TL::VS);
+    }
+    if (HAS_BIAS) {
+        for (int j = lane; j < BN; j += 64) {
+            float t = -INFINITY;
+            if (j < P.nk) {
+                const float x = P.bias.scalar(b, h, j);
+                t = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
+            }
+            Bk[j] = t;
+        }
+    }
+    // one wave's LDS operations complete in order: wait for the writes, fence the compiler
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {  // the unit's two 32-query blocks
+        W wv;
+        wv.hh = hh;
+        wv.kcol = kcol;
+        wv.q0 = 32 * u;
+        wv.qi = wv.q0 + wv.kcol;
+        wv.nk = P.nk;
+        wv.sl2 = P.scale * kLog2e;
+        wv.cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
+        wv.cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
+        wv.m = -INFINITY;
+        wv.l = 0.f;
+        const int qi = wv.qi;
+        if (wv.q0 >= P.nq) break;  // wave-uniform
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) wv.qf[c] = __builtin_bit_cast(frag, qraw[u][c]);
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x) wv.o[x] = zero16();
+        f32x16_t s[KB];
+        wv.scores(Ks, s);
+        wv.mask_edges(s, 0);
+        wv.settle(wv.logits(s, Bk));
+        u32x4_t pk[KB][2];
+        frag vf[KB][2][D / 32];
+        wv.load_v(Vt, vf);
+        wv.l += wv.probs(s, wv.m == -INFINITY ? 0.f : wv.m, pk);
+        wv.pv(vf, pk);
+
+        const float l = xhalf_sum(wv.l);
+        if (qi < P.nq) {
+            const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
+            const float inv = degenerate ? 0.f : 1.f / l;
+            T* orow = P.out.wrow<T>(b, h, qi);
+            u32x2_t ow[D / 8];
+#pragma unroll
+            for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    u32x2_t& o2 = ow[4 * x + g];
+                    o2[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
+                    o2[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
+                    *reinterpret_cast<u32x2_t*>(orow + x * 32 + 8 * g + 4 * wv.hh) = o2;
+                }
+            if (P.ey.ok()) epi_store_lane<T, D / 8>(P, b, h, qi, wv.hh, ow);
+            if (wv.hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
+        }
+    }
+}
+
+#ifndef PA_FWD_SHORT
+#define PA_FWD_SHORT 1  // the short-pass kernel where it applies
+#endif
+
 static bool dma_ok(const PassDev& P, int bn) {
     const int64_t rows = (int64_t)P.nk + 2 * bn;
     const int64_t span = std::max(P.k.sn, P.v.sn) * rows * 2;
@@ -1116,6 +1242,15 @@ bool mfma_fwd_supported(const PassDev& P, int dtype) {
 
 template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_t(const PassDev& P, hipStream_t s) {
+    if constexpr (D == 64 && !C && !V) {
+        if (PA_FWD_SHORT && P.nq <= 64 && P.nk <= 64 && !P.km.p) {
+            const int units = P.batch * P.heads;
+            ProfScope ps("mfma_fwd_short", s);
+            hipLaunchKernelGGL((k_mfma_fwd_short<T, S, B>), dim3((units + kShortUnits - 1) / kShortUnits),
+                               dim3(kFwdThreads), 0, s, P);
+            return;
+        }
+    }
     constexpr int KB = kFwdKB<D, S>;
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     dim3 grid(nqb * P.heads * P.batch);

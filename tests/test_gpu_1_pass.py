@@ -230,6 +230,25 @@ def test_pass_key_masked_forward_with_and_without_workspace(causal):
                   tol=2e-3)
 
 
+@param("dtype", (torch.bfloat16, torch.float16))
+@param("nq,nk", ((64, 64), (17, 50), (64, 1), (33, 64)))
+@param("softclamp", (None, 5.0))
+def test_pass_short_sequences(dtype, nq, nk, softclamp):
+    """Short non-causal passes at head dim 64 (nq, nk <= 64: the PolyViT shape, one unit per
+    wave): a key bias with a -finfo.max entry, a query-masked row, GQA, forward and all
+    gradients."""
+    q = randn((2, 8, nq, 64), dtype, 71)
+    k, v = (randn((2, 2, nk, 64), dtype, s) for s in (72, 73))
+    bias = randn((2, 2, nk), torch.float32, 74) + 1.0
+    bias[1, 0, 0] = -torch.finfo(torch.float32).max
+    qm = torch.ones(2, nq, dtype=torch.bool)
+    qm[0, nq // 2] = False
+    check(run_pass(q, k, v, bias=bias, query_mask=qm, causal=False, softclamp=softclamp), dtype,
+          f"short {dtype} nq={nq} nk={nk} sc={softclamp}")
+    check(run_pass(q, k, v, causal=False, softclamp=softclamp), dtype,
+          f"short {dtype} nq={nq} nk={nk} sc={softclamp} no bias")
+
+
 @param("dtype", (torch.float32, torch.bfloat16))
 def test_pass_cross_lengths(dtype):
     """Different query and key lengths (contexts), causal with a top-left aligned mask."""
