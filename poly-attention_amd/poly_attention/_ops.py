@@ -153,10 +153,48 @@ def _check_pass_inputs(q, k, v, vmul, bias, key_mask, query_mask):
 # one pass: raw calls
 
 
+def _padded_dim(q: Tensor) -> Optional[int]:
+    """The MFMA head dim (64 or 128) a CUDA pass of another head dim up to 128 is run at, its
+    features zero-padded: the padded features add nothing to any score, and the padded value
+    features are zero (the scale stays the caller's), so out, lse and every gradient are the
+    unpadded pass's.  None when the pass runs as it is."""
+    d = q.shape[-1]
+    if not q.is_cuda or d in (64, 128) or d > 128:
+        return None
+    return 64 if d < 64 else 128
+
+
+def _pad(t: Optional[Tensor], dp: int) -> Optional[Tensor]:
+    return None if t is None else torch.nn.functional.pad(t, (0, dp - t.shape[-1]))
+
+
+def _unpad(t: Tensor, d: int, like: Tensor, buf: Optional[Tensor] = None) -> Tensor:
+    """The first d features of t, in ``buf`` or in a new tensor laid out as an unpadded call
+    lays out its result for an input like ``like``."""
+    if buf is None:
+        buf = _empty_heads((*t.shape[:3], d), _inner_contig(like))
+    buf.copy_(t[..., :d])
+    return buf
+
+
+def _padded_epilogue(epilogue, dp):
+    if epilogue is None:
+        return None
+    root, gate, root_sigmoid = epilogue
+    return _pad(root, dp), _pad(gate, dp), root_sigmoid
+
+
 def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale,
                  may_degenerate, epilogue=None):
     """One pass forward: (out, lse), and with ``epilogue`` = (root, gate, root_sigmoid) the
     modules' gated output y as a third result (computed where the kernel stores out)."""
+    dp = _padded_dim(q)
+    if dp is not None:
+        d = q.shape[-1]
+        res = pass_fwd_raw(_pad(q, dp), _pad(k, dp), _pad(v, dp), _pad(vmul, dp), bias,
+                           key_mask, query_mask, causal, softclamp, scale, may_degenerate,
+                           _padded_epilogue(epilogue, dp))
+        return tuple(t if i == 1 else _unpad(t, d, q) for i, t in enumerate(res))
     lib = _lib.load()
     q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
     vmul = _inner_contig(vmul) if vmul is not None else None
@@ -199,6 +237,28 @@ def pass_bwd_raw(dout, dlse, q, k, v, vmul, bias, key_mask, query_mask, out, lse
     buffers (any strided view of the right shape) that the gradients are written to instead
     of new tensors.  With ``epilogue`` (as in the forward) ``dout`` is the gradient of y and
     the gradients of root and gate follow the other five."""
+    dp = _padded_dim(q)
+    if dp is not None:
+        d = q.shape[-1]
+        res = pass_bwd_raw(_pad(_inner_contig(dout), dp), dlse, _pad(q, dp), _pad(k, dp),
+                           _pad(v, dp), _pad(vmul, dp), bias, key_mask, query_mask,
+                           _pad(out, dp), lse, causal, softclamp, scale, may_degenerate,
+                           epilogue=_padded_epilogue(epilogue, dp))
+        dq, dk, dv, dvmul, dbias = res[:5]
+        if dq_into is not None:
+            dq_into.add_(dq[..., :d])
+            dq = dq_into
+        else:  # at the pass head count when q has fewer heads (the caller sums them)
+            dq = _unpad(dq, d, q, dq_out if dq.shape[1] == q.shape[1] else None)
+        dk = _unpad(dk, d, k, dk_out)
+        dv = _unpad(dv, d, v, dv_out)
+        dvmul = _unpad(dvmul, d, vmul) if dvmul is not None else None
+        extra = ()
+        if epilogue is not None:
+            droot, dgate = res[5:]
+            extra = (_unpad(droot, d, epilogue[0]) if droot is not None else None,
+                     _unpad(dgate, d, epilogue[1]) if dgate is not None else None)
+        return (dq, dk, dv, dvmul, dbias) + extra
     lib = _lib.load()
     q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
     vmul = _inner_contig(vmul) if vmul is not None else None
