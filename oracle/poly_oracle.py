@@ -19,6 +19,10 @@ Contents and what pins each function (see tests/test_oracle.py):
   polyvit_forward            poly_vit.py:19-101 (PolyViT forward, functional) -- the position
                              table and the patch order pinned by closed forms / direct pixel
                              indexing, the composition by the drop-in module on the CPU
+  attention_residual         poly_transformer.py:17-56 -- closed forms (one layer: identity,
+                             zero query: layer mean, a dominant query: one-hot selection)
+  polytransformer_forward    poly_transformer.py:60-150 (PolyTransformer forward, functional)
+                             -- the composition by the drop-in module on the CPU in float64
   rotary_*                   rotary-embedding-torch's RoPE (absent here; parity unpinned for
                              the pair layout, pinned by rotation properties)
   brute_* / masked_pass_classes   independent float64 closed forms used as pins
@@ -477,6 +481,49 @@ def polyvit_forward(p: dict, cfg: dict, img: Tensor) -> Tensor:
         x = F.linear(h, pf["3.weight"], pf["3.bias"]) + x
     x = F.layer_norm(x, (dim,), p["transformer.norm.weight"], p["transformer.norm.bias"])
     return F.linear(x.mean(dim=1), p["linear_head.weight"])
+
+
+def attention_residual(p: dict, outputs: Sequence[Tensor]) -> list[Tensor]:
+    """AttentionResidual.forward (poly_transformer.py:29-56): for each pseudo-query q_j (a row
+    of ``p['pseudo_queries']``) the mix sum_l w_jl h_l of the block outputs h_1..h_L, with
+    w_j. = softmax over l of <q_j, RMSNorm(h_l)> / sqrt(dim) at every position; written as
+    explicit sums over the layer list."""
+    dim = outputs[0].shape[-1]
+    keys = [_rms(h, p["norm_keys.weight"]) for h in outputs]
+    mixes = []
+    for q in p["pseudo_queries"]:
+        logits = torch.stack([(k * q).sum(-1) * dim ** -0.5 for k in keys])  # [L, ...]
+        w = torch.softmax(logits, dim=0)
+        mixes.append(sum(w[l][..., None] * h for l, h in enumerate(outputs)))
+    return mixes
+
+
+def polytransformer_forward(p: dict, cfg: dict, x: Tensor, mask=None) -> Tensor:
+    """PolyTransformer.forward (poly_transformer.py:106-150) with FeedForward (:60-70) and
+    the block layout of :91-104; ``p`` the module's state_dict, ``cfg`` its constructor
+    arguments. Returns the output and the list of block outputs."""
+    depth, deep = cfg["depth"], cfg.get("deep_cross_attention", False)
+    acfg = dict(heads=cfg.get("heads", 8), dim_head=cfg.get("dim_head", 64),
+                causal=cfg.get("causal", False))
+    outputs, contexts = [], None
+    for i in range(depth):
+        pl = _sub(p, f"layers.{i}.")
+        ctx = None
+        if contexts is not None:
+            ctx = tuple(_rms(c, pl[f"1.{j}.weight"]) for j, c in enumerate(contexts))
+        x = order2_forward(_sub(pl, "2."), acfg, _rms(x, pl["0.weight"]), context=ctx,
+                           mask=mask) + x
+        h = F.gelu(F.linear(_rms(x, pl["3.0.weight"]), pl["3.1.weight"], pl["3.1.bias"]))
+        x = F.linear(h, pl["3.3.weight"], pl["3.3.bias"]) + x
+        outputs.append(x)
+        mixes = attention_residual(_sub(p, f"attn_residuals.{i}."), outputs)
+        if deep and i < depth - 1:
+            x, contexts = mixes[0], tuple(mixes[1:])
+        else:
+            x = mixes[0]
+    if cfg.get("norm_out", False):
+        x = _rms(x, p["norm_out.weight"])
+    return x, outputs
 
 
 # ---------------------------------------------------------------------------------------

@@ -242,3 +242,53 @@ def test_polyvit_oracle_matches_module_on_cpu(order):
         want = m(img)
         got = O.polyvit_forward(m.state_dict(), cfg, img)
     torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10)
+
+
+def test_attention_residual_closed_forms():
+    """The layer mix against what its formula fixes: one layer -> that layer (weights 1); a
+    zero pseudo-query -> the plain mean over layers; a pseudo-query far along one layer's
+    normalised direction -> that layer alone (the softmax saturates), the others not."""
+    torch.manual_seed(8)
+    dim = 32
+    hs = [torch.randn(2, 5, dim, dtype=torch.float64) for _ in range(3)]
+    w = 1 + 0.2 * torch.randn(dim, dtype=torch.float64)
+    p = {"norm_keys.weight": w, "pseudo_queries": torch.zeros(2, dim, dtype=torch.float64)}
+    assert torch.allclose(O.attention_residual(p, hs[:1])[0], hs[0], atol=1e-14)
+    mean = (hs[0] + hs[1] + hs[2]) / 3
+    for m in O.attention_residual(p, hs):
+        assert torch.allclose(m, mean, atol=1e-14)
+    # one position, a query aligned with layer 1's normalised key: weight -> 1 on layer 1
+    one = [h[:1, :1] for h in hs]
+    k1 = F.rms_norm(one[1], (dim,), w, None)[0, 0]
+    p["pseudo_queries"] = torch.stack([k1 * 400.0, -k1 * 400.0])
+    sel, anti = O.attention_residual(p, one)
+    assert torch.allclose(sel, one[1], atol=1e-9)
+    assert not torch.allclose(anti, one[1], atol=1e-3)
+
+
+@pytest.mark.parametrize("deep_cross_attention", (False, True))
+@pytest.mark.parametrize("causal", (False, True))
+def test_polytransformer_oracle_matches_module_on_cpu(deep_cross_attention, causal):
+    """The oracle's PolyTransformer forward against the drop-in module's CPU (eager) path in
+    float64 on the same state dict, with a query mask (the reference test's shapes,
+    poly-attention tests:405-424), the block outputs included."""
+    from poly_attention import PolyTransformer
+
+    cfg = dict(dim=64, depth=3, heads=4, dim_head=16, causal=causal,
+               deep_cross_attention=deep_cross_attention, norm_out=True)
+    torch.manual_seed(4)
+    m = PolyTransformer(**cfg).double().eval()
+    with torch.no_grad():
+        for n, t in m.named_parameters():
+            if n.endswith("norm_keys.weight") or n.endswith("pseudo_queries"):
+                t.copy_(torch.randn_like(t) * 0.5 + (1.0 if n.endswith("weight") else 0.0))
+    x = torch.randn(2, 16, 64, dtype=torch.float64)
+    mask = torch.ones(2, 16, dtype=torch.bool)
+    mask[:, 8:] = False
+    for mk in (None, mask):
+        with torch.no_grad():
+            want, want_h = m(x, mask=mk, return_layer_hiddens=True)
+            got, got_h = O.polytransformer_forward(m.state_dict(), cfg, x, mask=mk)
+        torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10)
+        for a, b in zip(got_h, want_h):
+            torch.testing.assert_close(a, b, rtol=1e-10, atol=1e-10)
