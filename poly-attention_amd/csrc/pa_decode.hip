@@ -44,6 +44,7 @@ __device__ __forceinline__ int step_n(const DecodeDev& D) {
 
 constexpr int kDecThreads = 256;
 constexpr int kDecHB = 4;      // grouped kernel: level heads scored per pass over a chunk's K rows
+constexpr int kDecVH = 4;      // grouped kernel: level heads per sweep over a chunk's value rows
 constexpr int kDecRows = 8;    // rows in flight per row group (streaming kernel: heads x rows)
 constexpr float kDecTau = 8.f;  // lazy-rescale headroom of the partial's running max (log2 units)
 constexpr int kDecChunkWork = 4096;  // level heads per KV group x positions of one chunk, at most
@@ -283,16 +284,17 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_partial(DecodeDev D) {
 //      each row group of LPR lanes reads whole K rows (16 bytes per lane, kDecU rows in
 //      flight) and adds the score of every level head of the group;
 //   2. per head: max, p = 2^(s - max) in place, and the sum, over the chunk;
-//   3. per head: the values (times vmul for middle levels) are streamed with one FMA per
-//      element, reduced over the row groups and written as the chunk record (m, l, sum p v).
-template <typename T, int LPR>
+//   3. the values (times vmul for middle levels) of kDecVH heads at a time are streamed
+//      together, one FMA per element, reduced over the row groups and written as the
+//      chunk records (m, l, sum p v).
+template <typename T, int LPR, bool VM>
 __global__ __launch_bounds__(kDecThreads) void k_dec_partial_grp(DecodeDev D) {
     constexpr int E = Vec16<T>::n;
     constexpr int KG = kDecThreads / LPR;
     constexpr int kDecU = kDecRows;
     __shared__ float s_sc[kDecChunkWork];
     __shared__ float s_ml[kDecMaxHeadsPerGroup][2];
-    __shared__ float s_acc[kDecThreads / 64][256];
+    __shared__ float s_acc[kDecThreads / 64][kDecVH][256];
 
     const int c = blockIdx.x, bg = blockIdx.y, t = blockIdx.z;
     const int b = bg / D.kv_heads, g = bg % D.kv_heads;
@@ -393,60 +395,85 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_partial_grp(DecodeDev D) {
     }
     __syncthreads();
 
-    // 3. values
-    const bool has_vmul = L.vmul.ok();
-    for (int hh = 0; hh < rep; ++hh) {
-        const int h = h0 + hh;
-        const T* vbase = L.v.row<T>(b, h, 0) + d0;
-        const T* mbase = has_vmul ? L.vmul.row<T>(b, h, 0) + d0 : nullptr;
-        const int64_t vsn = L.v.sn, msn = L.vmul.sn;
-        const float* p = s_sc + hh * C;
-        float acc[E];
+    // 3. values: the heads of the group in sweeps of kDecVH over the chunk's rows, VU rows per
+    // row group and head in flight (one pipeline drain and one record write-out per sweep).
+    // VM: some level of the launch has a value multiplier, whose rows then share the budget
+    // of loads in flight (four rows without one, one with: the kernel stays within 128 VGPRs,
+    // four waves per SIMD)
+    constexpr int VU = VM ? 1 : 4;
+    const bool has_vmul = VM && L.vmul.ok();
+    const int64_t vsn = L.v.sn, msn = L.vmul.sn;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    auto raw16 = [&](const T* q) __attribute__((always_inline)) -> u32x4 {
+        return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q));
+    };
+    for (int hb0 = 0; hb0 < rep; hb0 += kDecVH) {
+        const int nh = min(kDecVH, rep - hb0);
+        const T* vbase[kDecVH];
+        const T* mbase[kDecVH];
+        float acc[kDecVH][E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[e] = 0.f;
-        for (int jl0 = kg; jl0 < cnt; jl0 += KG * kDecU) {
-            float vf[kDecU][E];
+        for (int hh = 0; hh < kDecVH; ++hh) {
+            const int h = h0 + hb0 + (hh < nh ? hh : 0);
+            vbase[hh] = L.v.row<T>(b, h, 0) + d0;
+            mbase[hh] = has_vmul ? L.vmul.row<T>(b, h, 0) + d0 : nullptr;
 #pragma unroll
-            for (int u = 0; u < kDecU; ++u) {
+            for (int e = 0; e < E; ++e) acc[hh][e] = 0.f;
+        }
+        for (int jl0 = kg; jl0 < cnt; jl0 += KG * VU) {
+            u32x4 vr[kDecVH][VU], mr[kDecVH][VU];
+#pragma unroll
+            for (int u = 0; u < VU; ++u) {
                 const int jl = jl0 + u * KG;
-                if (jl < cnt && dok) {
-                    load16<T>(vbase + (j_begin + jl) * vsn, vf[u]);
-                    if (has_vmul) {
-                        float mf[E];
-                        load16<T>(mbase + (j_begin + jl) * msn, mf);
+                const int64_t j = j_begin + (jl < cnt ? jl : 0);
 #pragma unroll
-                        for (int e = 0; e < E; ++e) vf[u][e] = round_to<T>(vf[u][e] * mf[e]);
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < E; ++e) vf[u][e] = 0.f;
+                for (int hh = 0; hh < kDecVH; ++hh) {
+                    const bool ok = jl < cnt && dok && hh < nh;
+                    vr[hh][u] = ok ? raw16(vbase[hh] + j * vsn) : u32x4{0u, 0u, 0u, 0u};
+                    mr[hh][u] = (ok && has_vmul) ? raw16(mbase[hh] + j * msn) : u32x4{0u, 0u, 0u, 0u};
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kDecU; ++u) {
+            for (int u = 0; u < VU; ++u) {
                 const int jl = jl0 + u * KG;
-                const float pj = jl < cnt ? p[jl] : 0.f;
 #pragma unroll
-                for (int e = 0; e < E; ++e) acc[e] += pj * vf[u][e];
+                for (int hh = 0; hh < kDecVH; ++hh) {
+                    if (hh >= nh) break;
+                    const float pj = jl < cnt ? s_sc[(hb0 + hh) * C + jl] : 0.f;
+                    const T* ve = reinterpret_cast<const T*>(&vr[hh][u]);
+                    const T* me = reinterpret_cast<const T*>(&mr[hh][u]);
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        float v = to_f(ve[e]);
+                        if (has_vmul) v = round_to<T>(v * to_f(me[e]));
+                        acc[hh][e] += pj * v;
+                    }
+                }
             }
         }
-        for (int off = LPR; off < 64; off <<= 1)
 #pragma unroll
-            for (int e = 0; e < E; ++e) acc[e] += __shfl_xor(acc[e], off);
-        if (lane < LPR && dok)
+        for (int hh = 0; hh < kDecVH; ++hh) {
+            if (hh >= nh) break;
+            for (int off = LPR; off < 64; off <<= 1)
 #pragma unroll
-            for (int e = 0; e < E; ++e) s_acc[wave][d0 + e] = acc[e];
-        __syncthreads();
-        float* rec = L.ws + (((int64_t)b * L.heads + h) * D.nchunks + c) * D.rec;
-        for (int x = tid; x < D.dim; x += kDecThreads) {
-            float a = 0.f;
+                for (int e = 0; e < E; ++e) acc[hh][e] += __shfl_xor(acc[hh][e], off);
+            if (lane < LPR && dok)
 #pragma unroll
-            for (int w2 = 0; w2 < kDecThreads / 64; ++w2) a += s_acc[w2][x];
-            rec[2 + x] = a;
+                for (int e = 0; e < E; ++e) s_acc[wave][hh][d0 + e] = acc[hh][e];
         }
-        if (tid == 0) {
-            rec[0] = s_ml[hh][0];
-            rec[1] = s_ml[hh][1];
+        __syncthreads();
+        for (int hh = 0; hh < nh; ++hh) {
+            float* rec = L.ws + (((int64_t)b * L.heads + h0 + hb0 + hh) * D.nchunks + c) * D.rec;
+            for (int x = tid; x < D.dim; x += kDecThreads) {
+                float a = 0.f;
+#pragma unroll
+                for (int w2 = 0; w2 < kDecThreads / 64; ++w2) a += s_acc[w2][hh][x];
+                rec[2 + x] = a;
+            }
+            if (tid == 0) {
+                rec[0] = s_ml[hb0 + hh][0];
+                rec[1] = s_ml[hb0 + hh][1];
+            }
         }
         __syncthreads();
     }
@@ -903,17 +930,25 @@ static void launch_partial_h(const DecodeDev& D, dim3 grid, hipStream_t s) {
     }
 }
 
+template <typename T, bool VM>
+static void launch_partial_grp_v(const DecodeDev& D, dim3 grid, hipStream_t s) {
+    switch (D.lpr) {
+        case 1: hipLaunchKernelGGL((k_dec_partial_grp<T, 1, VM>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 2: hipLaunchKernelGGL((k_dec_partial_grp<T, 2, VM>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 4: hipLaunchKernelGGL((k_dec_partial_grp<T, 4, VM>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 8: hipLaunchKernelGGL((k_dec_partial_grp<T, 8, VM>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 16: hipLaunchKernelGGL((k_dec_partial_grp<T, 16, VM>), grid, dim3(kDecThreads), 0, s, D); break;
+        case 32: hipLaunchKernelGGL((k_dec_partial_grp<T, 32, VM>), grid, dim3(kDecThreads), 0, s, D); break;
+        default: hipLaunchKernelGGL((k_dec_partial_grp<T, 64, VM>), grid, dim3(kDecThreads), 0, s, D); break;
+    }
+}
+
 template <typename T>
 static void launch_partial_grp(const DecodeDev& D, dim3 grid, hipStream_t s) {
-    switch (D.lpr) {
-        case 1: hipLaunchKernelGGL((k_dec_partial_grp<T, 1>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 2: hipLaunchKernelGGL((k_dec_partial_grp<T, 2>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 4: hipLaunchKernelGGL((k_dec_partial_grp<T, 4>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 8: hipLaunchKernelGGL((k_dec_partial_grp<T, 8>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 16: hipLaunchKernelGGL((k_dec_partial_grp<T, 16>), grid, dim3(kDecThreads), 0, s, D); break;
-        case 32: hipLaunchKernelGGL((k_dec_partial_grp<T, 32>), grid, dim3(kDecThreads), 0, s, D); break;
-        default: hipLaunchKernelGGL((k_dec_partial_grp<T, 64>), grid, dim3(kDecThreads), 0, s, D); break;
-    }
+    bool vm = false;
+    for (int t = 0; t < D.order; ++t) vm = vm || D.L[t].vmul.ok();
+    if (vm) launch_partial_grp_v<T, true>(D, grid, s);
+    else launch_partial_grp_v<T, false>(D, grid, s);
 }
 
 // by the largest level head count per KV group: one or two heads stream in one pass (K, values

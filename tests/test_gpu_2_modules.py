@@ -237,7 +237,7 @@ def test_contexts_and_context_masks_e2e():
 
 
 @param("order", (2, 3))
-@param("kv_heads", (2, 4))
+@param("kv_heads", (1, 2, 4))
 @param("use_rotary_embed", (False, True))
 def test_kv_cache_stepwise_equals_parallel(order, kv_heads, use_rotary_embed):
     """Prefill with return_cache, then single-token steps through the decode kernel; the

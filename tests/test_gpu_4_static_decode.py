@@ -101,7 +101,7 @@ def _module(order, kv_heads, d, dtype):
 
 
 @param("order", (2, 3))
-@param("kv_heads", (2, 4))
+@param("kv_heads", (1, 2, 4))
 @param("dtype", (torch.float32, torch.bfloat16))
 def test_static_cache_stepwise_equals_parallel(order, kv_heads, dtype):
     """Prefill with return_cache, move the cache into a StaticCache, then single-token steps
