@@ -19,7 +19,11 @@
 
 namespace pa {
 
-constexpr int kLinThreads = 256;
+// eight waves per workgroup: x is staged once per eight output features.  Staging it per four
+// cost more L2 traffic than the weights themselves at decode shapes (an 8-layer order-3 decode
+// step at batch 8, dim 1024: 0.898 -> 0.866 ms); sixteen leave too few or unevenly spread
+// workgroups for outputs of 1024 - 6144 features.
+constexpr int kLinThreads = 512;
 constexpr int kLinMaxRows = 16;
 constexpr int kLinMaxLds = 64 * 1024;  // bytes of staged x rows
 
