@@ -543,7 +543,9 @@ __device__ __forceinline__ void dec_finish(const DecodeDev& D, const DecLevelDev
         if (L.lse.ok()) {
             for (int r = 0; r < L.lse_rep; ++r)
                 store_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep + r, slot), lse_v);
-            stored = load_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep, slot));
+            // the value the slot now holds (its dtype's rounding), without reading it back
+            stored = L.lse.dtype == PA_F32 ? lse_v
+                     : L.lse.dtype == PA_F16 ? (float)(f16)lse_v : (float)(bf16)lse_v;
         }
         s_lse2[hh] = stored;  // the value the next level's cached bias will hold
     }
