@@ -246,7 +246,8 @@ typedef struct pa_rmsnorm {
     const void* weight;         /* [dim] or NULL (no affine weight) */
     int32_t     weight_dtype;   /* PA_F32 / PA_F16 / PA_BF16 */
     pa_view     y;              /* forward output (same dtype as x) */
-    float*      rstd;           /* [batch * heads * n] fp32: written by the forward, read by the backward */
+    float*      rstd;           /* [batch * heads * n] fp32: written by the forward, read by the backward;
+                                 * NULL in a forward whose backward never runs (not written) */
     pa_view     dy, dx;         /* backward: upstream gradient and input gradient */
     float*      dweight;        /* backward: [dim] fp32 weight gradient, or NULL */
     void*       workspace;

@@ -186,7 +186,7 @@ __device__ __forceinline__ void rms_fwd_rows(const RmsDev& R) {
                 }
                 store_row<T>(R.y.at<T>(b[u], h[u], i[u]) + d0, y);
             }
-            if (sub == 0) R.rstd[rstd_index(R, b[u], h[u], i[u])] = rs;
+            if (sub == 0 && R.rstd) R.rstd[rstd_index(R, b[u], h[u], i[u])] = rs;
         }
     }
 }
@@ -318,7 +318,7 @@ static int rms_setup(const pa_rmsnorm* p, RmsDev& R, bool bwd) {
     if (!view_ok(p->x)) return PA_EINVAL;
     if (!bwd && !view_ok(p->y)) return PA_EINVAL;
     if (bwd && (!view_ok(p->dy) || !view_ok(p->dx))) return PA_EINVAL;
-    if (!p->rstd) return PA_EINVAL;
+    if (bwd && !p->rstd) return PA_EINVAL;  // the forward writes it only when given
     if (p->weight && p->weight_dtype != PA_F32 && p->weight_dtype != PA_F16 &&
         p->weight_dtype != PA_BF16)
         return PA_EINVAL;

@@ -607,12 +607,11 @@ def rms_norm_many(xs: Sequence[Tensor], weights: Sequence[Optional[Tensor]],
     for k, (x, w, e) in enumerate(zip(xs, weights, eps)):
         x = _aligned16(x)
         y = _empty_heads(x.shape, x)
-        rstd = torch.empty(x.shape[:3], dtype=torch.float32, device=x.device)
         r = _rms_struct(x, w, torch.finfo(torch.float32).eps if e is None else float(e))
-        r.y, r.rstd = _view(y), rstd.data_ptr()
+        r.y = _view(y)  # no rstd: nothing runs backward through these norms
         items[k] = r
         ys.append(y)
-        keep += [x, rstd]
+        keep.append(x)
     with _device(xs[0]):
         _lib.check(lib.pa_rmsnorm_fwd_many(items, n, _stream(xs[0])), "pa_rmsnorm_fwd_many")
     return ys

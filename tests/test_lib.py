@@ -143,7 +143,10 @@ def test_rmsnorm_rejects_invalid():
     r.x.sb = r.x.sh = r.x.sn = 64
     assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # no output view
     r.y = r.x
-    assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # no rstd
+    r.dy = r.dx = r.x
+    # rstd is optional in the forward (not written without it), required by the backward
+    assert lib.pa_rmsnorm_bwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # no rstd
+    r.dy = r.dx = _lib.PaView()
     r.y, r.rstd = r.x, 0x2000
     r.angles, r.rot_dim, r.angles_dtype = 0x4000, 63, _lib.PA_F32
     assert lib.pa_rmsnorm_fwd(ctypes.byref(r), None) == _lib.PA_EINVAL  # odd rot_dim
