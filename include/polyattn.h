@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 5
+#define PA_ABI_VERSION 6
 #define PA_MAX_ORDER 8
 
 /* status codes (0 = success, negative = failure) */
@@ -109,6 +109,25 @@ typedef struct pa_epilogue {
     int32_t flags;        /* PA_EPI_* */
 } pa_epilogue;
 
+/* pa_qk_norm.flags */
+#define PA_NORM_Q 1   /* normalise the queries */
+#define PA_NORM_K 2   /* normalise the keys */
+
+/* RMSNorms of a pass's queries and / or keys, applied as the kernel loads them instead of by
+ * a separate norm kernel (the modules' q norms, poly_attention.py:196-200,271, when nothing
+ * else reads the normalised tensors):
+ *   x <- round(x * rsqrt(mean(x^2) + eps) * w)
+ * with pa_rmsnorm_fwd's arithmetic and summation order (bit-identical results).  Forward
+ * only, where the short-pass kernel runs: head dim 64, nq and nk <= 64, not causal, no value
+ * multiplier or key mask, bf16 / f16 with weights of the same dtype; PA_EUNSUPPORTED
+ * otherwise. */
+typedef struct pa_qk_norm {
+    const void* q_weight;   /* [dim] with PA_NORM_Q */
+    const void* k_weight;   /* [dim] with PA_NORM_K */
+    float       q_eps, k_eps;
+    int32_t     flags;      /* PA_NORM_* */
+} pa_qk_norm;
+
 /* One attention pass (one level of the poly chain). */
 typedef struct pa_pass {
     int32_t batch, heads, nq, nk, dim;
@@ -129,6 +148,7 @@ typedef struct pa_pass {
      * the faster forward kernel; without it the results are the same. */
     void*   workspace;
     size_t  workspace_bytes;
+    const pa_qk_norm* norm;  /* optional q / k norms on load (NULL: none; forward only) */
 } pa_pass;
 
 /* Backward of one pass.  In the backward the key-side tensors (k, v, vmul, bias) must share
@@ -309,7 +329,8 @@ const char* pa_strerror(int status);
 int         pa_last_hip_error(void);   /* hipError_t of the last PA_EHIP on this thread */
 /* sizeof of the ABI structs, for binding checks: 0 pa_view, 1 pa_mask, 2 pa_pass,
  * 3 pa_pass_grad, 4 pa_decode_level, 5 pa_decode, 6 pa_prologue_item, 7 pa_prologue,
- * 8 pa_rmsnorm, 9 pa_linear, 10 pa_linear_out, 11 pa_epilogue; 0 for other values */
+ * 8 pa_rmsnorm, 9 pa_linear, 10 pa_linear_out, 11 pa_epilogue, 12 pa_qk_norm; 0 for other
+ * values */
 size_t      pa_struct_size(int which);
 
 /* Kernel timing (no counterpart in the reference: a measurement facility for benchmarks).

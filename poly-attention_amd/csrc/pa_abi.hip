@@ -133,6 +133,12 @@ PassDev to_passdev(const pa_pass* p) {
     P.eg = to_dview(e ? e->gate : none, p->heads);
     P.ey = to_dview(e ? e->y : none, p->heads);
     P.eflags = e ? e->flags : 0;
+    const pa_qk_norm* n = p->norm;
+    P.nflags = n ? n->flags : 0;
+    P.qnw = n ? n->q_weight : nullptr;
+    P.knw = n ? n->k_weight : nullptr;
+    P.qeps = n ? n->q_eps : 0.f;
+    P.keps = n ? n->k_eps : 0.f;
     return P;
 }
 
@@ -219,6 +225,7 @@ size_t pa_struct_size(int which) {
         case 9: return sizeof(pa_linear);
         case 10: return sizeof(pa_linear_out);
         case 11: return sizeof(pa_epilogue);
+        case 12: return sizeof(pa_qk_norm);
         default: return 0;
     }
 }
@@ -271,6 +278,15 @@ int pa_attn_pass_fwd(const pa_pass* p, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const PassDev P = to_passdev(p);
     const int T = p->q.dtype;
+    if (P.nflags) {
+        // q / k norms on load: only where the short-pass kernel runs
+        const pa_qk_norm* n = p->norm;
+        if (n->flags & ~(PA_NORM_Q | PA_NORM_K)) return PA_EINVAL;
+        if (((n->flags & PA_NORM_Q) && (!n->q_weight || (uintptr_t)n->q_weight % 16)) ||
+            ((n->flags & PA_NORM_K) && (!n->k_weight || (uintptr_t)n->k_weight % 16)))
+            return PA_EINVAL;
+        if (!mfma_fwd_supported(P, T) || !mfma_fwd_short_applies(P, T)) return PA_EUNSUPPORTED;
+    }
     if (mfma_fwd_supported(P, T)) {
         const size_t need = fwd_ws_bytes(*p);
         if (need && p->workspace && p->workspace_bytes >= need) {
@@ -311,6 +327,7 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
     if (!g) return PA_EINVAL;
     const pa_pass* p = &g->fwd;
     PA_TRY(validate_pass(p));
+    if (p->norm && p->norm->flags) return PA_EUNSUPPORTED;  // forward only
     const int T = p->q.dtype;
     const int H = p->heads;
     const int hk = p->k.heads;

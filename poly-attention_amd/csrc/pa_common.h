@@ -75,6 +75,11 @@ struct PassDev {
     DMask km, qm;
     DView er, eg, ey;  // module epilogue: root, gate, y (ey absent: no epilogue)
     int32_t eflags;    // PA_EPI_*
+    // RMSNorm of the queries / keys on load (PA_NORM_* in nflags; weights of the pass dtype)
+    const void* qnw;
+    const void* knw;
+    float qeps, keps;
+    int32_t nflags;
 };
 
 struct GradDev {

@@ -35,6 +35,9 @@ void launch_mfma_fwd_f32(const PassDev& P, hipStream_t s);
 bool mfma_bwd_f32_supported(const GradDev& G);  // unmasked passes
 void launch_mfma_bwd_f32(const GradDev& G, hipStream_t s);
 bool mfma_fwd_supported(const PassDev& P, int dtype);
+// the short-pass kernel takes this pass (head dim 64, nq, nk <= 64, not causal, no value
+// multiplier or key mask, 16-bit)
+bool mfma_fwd_short_applies(const PassDev& P, int dtype);
 void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s);
 bool mfma_bwd_supported(const GradDev& G, int dtype);
 bool mfma_bwd_fuses_pre(const GradDev& G);

@@ -855,6 +855,33 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
 
 constexpr int kShortUnits = 4;
 
+template <typename T>
+__device__ __forceinline__ void unpack8(const u32x4_t& r, float (&out)[8]) {
+    const T* e = reinterpret_cast<const T*>(&r);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = to_f(e[i]);
+}
+// y = (x * rs) * w in fp32, each product rounded to fp32 before the caller's conversion to T,
+// as pa_rmsnorm_fwd computes it.  The empty asm operand makes the fp32 product a value of its
+// own: otherwise the second product and the conversion to f16 become one mixed-precision FMA
+// (v_fma_mixlo_f16, a single rounding), which differs from the norm kernel in rare cases.
+__device__ __forceinline__ void norm_scale(const float (&x)[8], float rs, const float (&w)[8],
+                                           float (&y)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        y[e] = (x[e] * rs) * w[e];
+        asm volatile("" : "+v"(y[e]));
+    }
+}
+template <typename T>
+__device__ __forceinline__ u32x4_t pack8(const float (&v)[8]) {
+    u32x4_t r;
+    T* e = reinterpret_cast<T*>(&r);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = from_f<T>(v[i]);
+    return r;
+}
+
 template <typename T, bool SOFTCLAMP, bool HAS_BIAS>
 __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     constexpr int D = 64, KB = 2;
@@ -887,7 +914,42 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
             qraw[u][c] = qi < P.nq ? *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh) : zero;
     }
 
-    // this unit's keys: K row-major, V transposed (4-key x 8-dim blocks), the key term
+    // optional RMSNorm of the queries, bit-identical to pa_rmsnorm_fwd: lane (q, hh) holds row
+    // q's feature chunks 2c + hh (8 features each), the partner half lane ^ 32 the others; the
+    // chunk sums combine as that kernel's butterfly over its 8 lanes does: chunk pairs first,
+    // then (t0 + t1) + (t2 + t3)
+    if (P.nflags & PA_NORM_Q) {
+        float wq[D / 16][8];
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+            unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P.qnw) + c * 16 + 8 * hh), wq[c]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float x[D / 16][8], t[D / 16];
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) {
+                unpack8<T>(qraw[u][c], x[c]);
+                float sc = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sc += x[c][e] * x[c][e];
+                t[c] = sc + __shfl_xor(sc, 32);
+            }
+            const float rs = rsqrtf(((t[0] + t[1]) + (t[2] + t[3])) * (1.f / D) + P.qeps);
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) {
+                float y[8];
+                norm_scale(x[c], rs, wq[c], y);
+                qraw[u][c] = pack8<T>(y);
+            }
+        }
+    }
+
+    // this unit's keys: K row-major, V transposed (4-key x 8-dim blocks), the key term; with
+    // PA_NORM_K the K rows are normalised on the way (a row's 8 chunks sit in 8 consecutive
+    // lanes, summed by pa_rmsnorm_fwd's butterfly)
+    float wk[8];
+    if (P.nflags & PA_NORM_K)
+        unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P.knw) + (lane % (D / 8)) * 8), wk);
     for (int blk = lane; blk < TL::BLOCKS; blk += 64) {
         const int rg = blk / (D / 8), cc = blk % (D / 8);
         u32x4_t kw[4], vw[4];
@@ -896,6 +958,22 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
             const int j = rg * 4 + r;
             kw[r] = j < P.nk ? *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h, j) + cc * 8) : zero;
             vw[r] = j < P.nk ? *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h, j) + cc * 8) : zero;
+        }
+        if (P.nflags & PA_NORM_K) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float x[8];
+                unpack8<T>(kw[r], x);
+                float sc = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sc += x[e] * x[e];
+#pragma unroll
+                for (int off = 1; off < D / 8; off <<= 1) sc += __shfl_xor(sc, off);
+                const float rs = rsqrtf(sc * (1.f / D) + P.keps);
+                float y[8];
+                norm_scale(x, rs, wk, y);
+                kw[r] = pack8<T>(y);
+            }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) *reinterpret_cast<u32x4_t*>(Ks + (rg * 4 + r) * TL::KS + cc * 8) = kw[r];
@@ -1240,10 +1318,15 @@ bool mfma_fwd_supported(const PassDev& P, int dtype) {
     return true;
 }
 
+bool mfma_fwd_short_applies(const PassDev& P, int dtype) {
+    return PA_FWD_SHORT && (dtype == PA_BF16 || dtype == PA_F16) && P.dim == 64 && !P.causal &&
+           !P.vmul.ok() && P.nq <= 64 && P.nk <= 64 && !P.km.p;
+}
+
 template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_t(const PassDev& P, hipStream_t s) {
     if constexpr (D == 64 && !C && !V) {
-        if (PA_FWD_SHORT && P.nq <= 64 && P.nk <= 64 && !P.km.p) {
+        if (mfma_fwd_short_applies(P, sizeof(T) == 2 ? PA_BF16 : PA_F32)) {
             const int units = P.batch * P.heads;
             ProfScope ps("mfma_fwd_short", s);
             hipLaunchKernelGGL((k_mfma_fwd_short<T, S, B>), dim3((units + kShortUnits - 1) / kShortUnits),

@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolyattn.so"
 
-PA_ABI_VERSION = 5
+PA_ABI_VERSION = 6
 PA_MAX_ORDER = 8
 
 PA_OK = 0
@@ -31,6 +31,8 @@ PA_DECODE_SCRATCH_BYTES = 16 << 20
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 PA_FLAG_MAY_DEGENERATE = 1
 PA_EPI_ROOT_SIGMOID = 1
+PA_NORM_Q = 1
+PA_NORM_K = 2
 PA_ACC_DQ, PA_ACC_DK, PA_ACC_DV, PA_ACC_DVMUL, PA_ACC_DBIAS = 1, 2, 4, 8, 16
 PA_RMS_MAX_ITEMS = 4
 
@@ -79,6 +81,11 @@ class PaEpilogue(ctypes.Structure):
     _fields_ = [("root", PaView), ("gate", PaView), ("y", PaView), ("flags", c_int32)]
 
 
+class PaQkNorm(ctypes.Structure):
+    _fields_ = [("q_weight", c_void_p), ("k_weight", c_void_p), ("q_eps", c_float),
+                ("k_eps", c_float), ("flags", c_int32)]
+
+
 class PaPass(ctypes.Structure):
     _fields_ = [
         ("batch", c_int32),
@@ -102,6 +109,7 @@ class PaPass(ctypes.Structure):
         ("epi", c_void_p),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("norm", c_void_p),
     ]
 
 
@@ -250,7 +258,7 @@ class PaKernelTime(ctypes.Structure):
 
 
 STRUCTS = (PaView, PaMask, PaPass, PaPassGrad, PaDecodeLevel, PaDecode, PaPrologueItem,
-           PaPrologue, PaRmsNorm, PaLinear, PaLinearOut, PaEpilogue)
+           PaPrologue, PaRmsNorm, PaLinear, PaLinearOut, PaEpilogue, PaQkNorm)
 
 
 class PolyAttnError(RuntimeError):

@@ -29,11 +29,14 @@ from ._lib import (
     DTYPE_CODE,
     PA_EPI_ROOT_SIGMOID,
     PA_FLAG_MAY_DEGENERATE,
+    PA_NORM_K,
+    PA_NORM_Q,
     PaDecode,
     PaEpilogue,
     PaMask,
     PaPass,
     PaPassGrad,
+    PaQkNorm,
     PaRmsNorm,
     PaView,
 )
@@ -112,6 +115,35 @@ def _epilogue_struct(epilogue, y) -> PaEpilogue:
     return e
 
 
+def _qk_norm_struct(qk_norm) -> PaQkNorm:
+    """qk_norm = (q norm, k norm), each (weight, eps) or None: RMSNorms applied on load."""
+    qn, kn = qk_norm
+    n = PaQkNorm()
+    if qn is not None:
+        n.q_weight, n.q_eps, n.flags = qn[0].data_ptr(), float(qn[1]), n.flags | PA_NORM_Q
+    if kn is not None:
+        n.k_weight, n.k_eps, n.flags = kn[0].data_ptr(), float(kn[1]), n.flags | PA_NORM_K
+    return n
+
+
+def qk_norms_fusable(q1: Tensor, q2: Tensor, q3: Tensor, v3: Tensor, weights, causal: bool) -> bool:
+    """The order-2 chain can normalise its q1 / q2 / q3 as the passes load them (the short-pass
+    kernel's q / k norms): 16-bit CUDA tensors of head dim 64 and at most 64 positions, not
+    causal, every norm weight a contiguous, 16-byte aligned [64] tensor of that dtype, rows
+    aligned for the MFMA kernels."""
+    ts = (q1, q2, q3, v3)
+    dt = q1.dtype
+    if dt not in (torch.bfloat16, torch.float16) or causal:
+        return False
+    if any(not t.is_cuda or t.dtype != dt or t.dim() != 4 or t.shape[-1] != 64 or
+           t.shape[2] > 64 or t.stride(-1) != 1 for t in ts):
+        return False
+    if any(t.data_ptr() % 16 or any(st % 8 for st in t.stride()[:3]) for t in ts):
+        return False
+    return all(w is not None and w.dtype == dt and w.is_contiguous() and w.numel() == 64
+               and w.data_ptr() % 16 == 0 for w in weights)
+
+
 def _pass_struct(q, k, v, vmul, bias, key_mask, query_mask, out, lse, causal, softclamp, scale,
                  may_degenerate, epi: Optional[PaEpilogue] = None) -> PaPass:
     p = PaPass()
@@ -185,11 +217,15 @@ def _padded_epilogue(epilogue, dp):
 
 
 def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale,
-                 may_degenerate, epilogue=None):
+                 may_degenerate, epilogue=None, qk_norm=None):
     """One pass forward: (out, lse), and with ``epilogue`` = (root, gate, root_sigmoid) the
-    modules' gated output y as a third result (computed where the kernel stores out)."""
+    modules' gated output y as a third result (computed where the kernel stores out).
+    ``qk_norm`` = (q norm, k norm), each (weight, eps) or None: RMSNorms of q and k applied
+    as the kernel loads them (where the short-pass kernel runs, see qk_norms_fusable)."""
     dp = _padded_dim(q)
     if dp is not None:
+        assert qk_norm is None, "q / k norms on load need head dim 64"
+
         d = q.shape[-1]
         res = pass_fwd_raw(_pad(q, dp), _pad(k, dp), _pad(v, dp), _pad(vmul, dp), bias,
                            key_mask, query_mask, causal, softclamp, scale, may_degenerate,
@@ -210,6 +246,10 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
         epi = _epilogue_struct(epilogue, y)
     p = _pass_struct(q, k, v, vmul, bias, km, qm, out, lse, causal, softclamp, scale,
                      may_degenerate or km is not None or qm is not None, epi)
+    norm = None
+    if qk_norm is not None:
+        norm = _qk_norm_struct(qk_norm)
+        p.norm = ctypes.addressof(norm)
     ws = None
     if km is not None:  # a key-masked pass takes the faster kernel with a workspace
         ws_bytes = lib.pa_attn_pass_fwd_workspace(ctypes.byref(p))
@@ -1003,16 +1043,20 @@ def _split_heads(t: Tensor, heads, d: int):
 # the order-n chain
 
 
-def order2_forward(q1, q2, q3, v3, key_mask, causal, softclamp, scale, epilogue=None):
+def order2_forward(q1, q2, q3, v3, key_mask, causal, softclamp, scale, epilogue=None,
+                   norms=None):
     """The two forward passes of the order-2 chain (poly_attention.py:48-116 with q2 as both
     the pass-1 queries and the pass-2 keys); ``key_mask`` masks the keys of both passes.
     Returns (out, lse, lse23, msg), and with ``epilogue`` = (root, gate, root_sigmoid) the
-    modules' gated output y (computed in pass 2's store) as a fifth result."""
+    modules' gated output y (computed in pass 2's store) as a fifth result.  ``norms`` =
+    ((w1, eps1), (w2, eps2), (w3, eps3)): q1, q2, q3 are raw and the passes apply their
+    RMSNorms on load (qk_norms_fusable; no gradient)."""
     degenerate = key_mask is not None
+    n1, n2, n3 = norms if norms is not None else (None, None, None)
     msg, lse23 = pass_fwd_raw(q2, q3, v3, None, None, key_mask, None, causal, softclamp, scale,
-                              degenerate)
+                              degenerate, qk_norm=(n2, n3) if norms is not None else None)
     res = pass_fwd_raw(q1, q2, msg, None, lse23, key_mask, None, causal, softclamp, scale,
-                       degenerate, epilogue)
+                       degenerate, epilogue, qk_norm=(n1, n2) if norms is not None else None)
     return (res[0], res[1], lse23, msg) + tuple(res[2:])
 
 
@@ -1125,20 +1169,32 @@ def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence
                causal: bool, softclamp: Optional[float], scale: float,
                query_mask: Optional[Tensor] = None,
                key_masks: Optional[Sequence[Optional[Tensor]]] = None,
-               may_degenerate: bool = False, epilogue=None):
+               may_degenerate: bool = False, epilogue=None, qk_norms=None):
     """Order-n poly attention through HIP passes.
 
     q_left[l] . q_right[l] are the scores of level l (l = 0 is q1 . q2); vs are the values
     v_3 .. v_{n+1}.  Returns (out, lses, msgs) with lses / msgs ordered deepest level first
     (the reference's cache order, n_poly_attention.py:268-305).  ``epilogue`` = (root, gate,
     root_sigmoid): the modules' root-value / gate epilogue applied to out (fused into the
-    final pass on the order-2 chain's path, else in torch).
+    final pass on the order-2 chain's path, else in torch).  ``qk_norms`` = the (weight, eps)
+    RMSNorms of q1, q2, q3 of an order-2 chain whose inputs are not normalised yet: applied as
+    the passes load them (no gradient; the caller checks qk_norms_fusable).
     """
     n = len(q_left)
     assert len(q_right) == n and len(vs) == n - 1 and n >= 2
     key_masks = list(key_masks) if key_masks is not None else [None] * n
     if epilogue is not None and epilogue[0] is None and epilogue[1] is None:
         epilogue = None
+    if qk_norms is not None:
+        assert n == 2 and q_right[0] is q_left[1] and query_mask is None and not may_degenerate
+        assert all(m is None for m in key_masks)
+        fuse = epilogue is not None and _epilogue_fusable(epilogue, q_left[0], q_left[0].shape[1])
+        res = order2_forward(q_left[0], q_left[1], q_right[1], vs[0], None, bool(causal),
+                             softclamp, float(scale), epilogue if fuse else None, norms=qk_norms)
+        out = res[4] if fuse else res[0]
+        if epilogue is not None and not fuse:
+            out = apply_epilogue(out, epilogue)
+        return out, [res[2]], [res[3]]
     if _chain_fusable(q_left, q_right, vs, query_mask, key_masks, may_degenerate):
         root = gate = None
         root_sigmoid = False

@@ -420,8 +420,12 @@ class Order2PolyAttention(Module):
             new_cache = cache
             v2 = repeat_kv(v2, self.num_rep) if self.is_gqa and exists(v2) else v2
         else:
-            # the q norms and the external rotary (fused into one kernel on the GPU path)
-            qs = _q_norms(self, self.q_norms, qs, rotary_pos_emb)
+            # the q norms and the external rotary (fused into one kernel on the GPU path), or
+            # the norms applied by the attention passes as they load q1 / q2 / q3
+            norms_on_load = self._norms_on_load(qs, v3, mask, context_mask, rotary_pos_emb,
+                                                cache, return_cache)
+            if norms_on_load is None:
+                qs = _q_norms(self, self.q_norms, qs, rotary_pos_emb)
 
             q1, q2, q3 = qs
 
@@ -434,7 +438,8 @@ class Order2PolyAttention(Module):
 
             if self._use_fused(q1):
                 out, new_cache = self._fused_core(q1, q2, q3, v3, mask, context_mask,
-                                                  rotary_pos_emb, cache, return_cache, epilogue)
+                                                  rotary_pos_emb, cache, return_cache, epilogue,
+                                                  norms_on_load)
                 epilogue_done = True
             else:
                 out, new_cache, v2 = self._eager_core(q1, q2, q3, v2, v3, mask, context_mask,
@@ -493,10 +498,38 @@ class Order2PolyAttention(Module):
             new_cache = (q2_cache, q3_cache, v3_cache, lse23_full, msg_full)
         return out, new_cache, v2
 
+    def _norms_on_load(self, qs, v3, mask, context_mask, rotary_pos_emb, cache, return_cache):
+        """The q norms (poly_attention.py:196-200,271) to be applied by the attention passes
+        as they load q1 / q2 / q3 rather than by a norm kernel whose outputs they read back:
+        no gradient, cache, rotary or mask, and the short-pass kernel's shapes (head dim 64,
+        at most 64 positions, not causal: PolyViT's attention).  ((weight, eps) x 3) or None."""
+        from . import _ops
+
+        if exists(cache) or return_cache or exists(rotary_pos_emb) or exists(self.rotary_emb):
+            return None
+        if exists(mask) or any(exists(m) for m in context_mask):
+            return None
+        if torch.compiler.is_compiling() or not self._use_fused(qs[0]):
+            return None
+        norms = self.q_norms
+        weights = [getattr(n, "weight", None) for n in norms]
+        if not all(isinstance(n, RMSNorm) and tuple(n.normalized_shape) == (q.shape[-1],)
+                   for n, q in zip(norms, qs)):
+            return None
+        if torch.is_grad_enabled() and (any(t.requires_grad for t in (*qs, v3)) or
+                                        any(w is not None and w.requires_grad for w in weights)):
+            return None
+        if not _ops.qk_norms_fusable(*qs, v3, weights, self.causal):
+            return None
+        # torch's RMSNorm without eps uses the fp32 epsilon for 16-bit inputs
+        return tuple((w, n.eps if n.eps is not None else torch.finfo(torch.float32).eps)
+                     for w, n in zip(weights, norms))
+
     def _fused_core(self, q1, q2, q3, v3, mask, context_mask, rotary_pos_emb, cache,
-                    return_cache, epilogue):
+                    return_cache, epilogue, qk_norms=None):
         """The attention core on the HIP kernels (q2 / q3 / v3 stay at kv_heads), with the
-        module epilogue applied: fused into pass 2 on the order-2 chain's path."""
+        module epilogue applied: fused into pass 2 on the order-2 chain's path.  ``qk_norms``:
+        q1 / q2 / q3 are not normalised yet and the passes apply these norms on load."""
         from . import _ops
 
         rep = self.num_rep if self.is_gqa else 1
@@ -512,7 +545,7 @@ class Order2PolyAttention(Module):
             out, lses, msgs = _ops.poly_chain(
                 [q1r, q2r_left], [q2r_right, q3r], [v3], causal=self.causal,
                 softclamp=self.softclamp_value, scale=self.scale, query_mask=mask,
-                key_masks=list(context_mask), epilogue=epilogue)
+                key_masks=list(context_mask), epilogue=epilogue, qk_norms=qk_norms)
             new_cache = None
             if return_cache:
                 lse23 = repeat_kv(lses[0][:, :, :, None], rep)[..., 0]
