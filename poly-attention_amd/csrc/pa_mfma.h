@@ -53,6 +53,18 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, t2));
 }
 
+// the two T packed in a 32-bit word (lo = first) as floats, in registers (element access
+// through a T pointer into a packed register array makes the compiler spill the array to
+// scratch memory)
+template <typename T>
+__device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef T t2 __attribute__((ext_vector_type(2)));
+    const f2 f = __builtin_convertvector(__builtin_bit_cast(t2, w), f2);
+    lo = f[0];
+    hi = f[1];
+}
+
 // max / sum with the lane 32 apart (the other half of a 32x32 accumulator column) through
 // v_permlane32_swap: lane l ends up with {x[l], x[l ^ 32]} in the two results
 __device__ __forceinline__ float xhalf_max(float x) {

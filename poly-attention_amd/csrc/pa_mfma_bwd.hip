@@ -942,10 +942,15 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
 #pragma unroll
             for (int c = 0; c < D / 16; ++c) {
                 const u32x4_t orow = *reinterpret_cast<const u32x4_t*>(P.out.row<T>(b, h, qi) + c * 16 + 8 * hh);
-                const T* oe = reinterpret_cast<const T*>(&orow);
-                const T* ge = reinterpret_cast<const T*>(&of[c]);
+                const u32x4_t grow = __builtin_bit_cast(u32x4_t, of[c]);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) part += to_f(oe[e]) * to_f(ge[e]);
+                for (int e = 0; e < 4; ++e) {
+                    float o0, o1, g0, g1;
+                    unpack2<T>(orow[e], o0, o1);
+                    unpack2<T>(grow[e], g0, g1);
+                    part += o0 * g0;
+                    part += o1 * g1;
+                }
             }
         }
         const float dsum = xhalf_sum(part);

@@ -125,14 +125,16 @@ __device__ __forceinline__ void epi_store_lane(const PassDev& P, int b, int h, i
 #pragma unroll
     for (int k = 0; k < NG; ++k) {
         const int d = (k / 4) * 32 + (k % 4) * 8 + 4 * hh;
-        const T* o4 = reinterpret_cast<const T*>(&o[k]);
-        const T* r4 = reinterpret_cast<const T*>(&r[k]);
-        const T* g4 = reinterpret_cast<const T*>(&g[k]);
         u32x2_t y4;
-        T* y = reinterpret_cast<T*>(&y4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            y[e] = from_f<T>(epi_combine<T>(to_f(o4[e]), to_f(r4[e]), to_f(g4[e]), has_r, has_g, sig));
+        for (int w = 0; w < 2; ++w) {
+            float o0, o1, r0, r1, g0, g1;
+            unpack2<T>(o[k][w], o0, o1);
+            unpack2<T>(r[k][w], r0, r1);
+            unpack2<T>(g[k][w], g0, g1);
+            y4[w] = pack2<T>(epi_combine<T>(o0, r0, g0, has_r, has_g, sig),
+                             epi_combine<T>(o1, r1, g1, has_r, has_g, sig));
+        }
         *reinterpret_cast<u32x2_t*>(yrow + d) = y4;
     }
 }
@@ -857,9 +859,8 @@ constexpr int kShortUnits = 4;
 
 template <typename T>
 __device__ __forceinline__ void unpack8(const u32x4_t& r, float (&out)[8]) {
-    const T* e = reinterpret_cast<const T*>(&r);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = to_f(e[i]);
+    for (int i = 0; i < 4; ++i) unpack2<T>(r[i], out[2 * i], out[2 * i + 1]);
 }
 // y = (x * rs) * w in fp32, each product rounded to fp32 before the caller's conversion to T,
 // as pa_rmsnorm_fwd computes it.  The empty asm operand makes the fp32 product a value of its
@@ -876,9 +877,8 @@ __device__ __forceinline__ void norm_scale(const float (&x)[8], float rs, const 
 template <typename T>
 __device__ __forceinline__ u32x4_t pack8(const float (&v)[8]) {
     u32x4_t r;
-    T* e = reinterpret_cast<T*>(&r);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = from_f<T>(v[i]);
+    for (int i = 0; i < 4; ++i) r[i] = pack2<T>(v[2 * i], v[2 * i + 1]);
     return r;
 }
 
@@ -902,17 +902,42 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     const u32x4_t zero = {0u, 0u, 0u, 0u};
     const int hh = lane >> 5, kcol = lane & 31;
 
-    // the Q^T fragments of both 32-query blocks (lane (q, hh): Q[q][c*16 + 8*hh .. +7]), issued
-    // with the key loads below: one memory round trip per unit
+    // Every global load of the unit is issued before the first wait (one memory round trip):
+    // the Q^T fragments of both 32-query blocks, the K and V rows of both 4-key x 8-dim block
+    // rounds, the key bias.  Rows past nq / nk are read from the last row (no branch around a
+    // load) and replaced by zeros afterwards.
+    static_assert(TL::BLOCKS % 64 == 0 && BN == 64, "short-pass tile");
+    constexpr int NR = TL::BLOCKS / 64;  // block rounds per lane
     u32x4_t qraw[2][D / 16];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const int qi = 32 * u + kcol;
-        const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
+        const T* qrow = P.q.row<T>(b, h, min(32 * u + kcol, P.nq - 1));
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c)
-            qraw[u][c] = qi < P.nq ? *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh) : zero;
+        for (int c = 0; c < D / 16; ++c) qraw[u][c] = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
     }
+    u32x4_t kw[NR][4], vw[NR][4];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int blk = lane + 64 * i, rg = blk / (D / 8), cc = blk % (D / 8);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int j = min(rg * 4 + r, P.nk - 1);
+            kw[i][r] = *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h, j) + cc * 8);
+            vw[i][r] = *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h, j) + cc * 8);
+        }
+    }
+    float braw = 0.f;  // lane j's key bias (BN = 64 keys, one per lane)
+    if (HAS_BIAS) braw = P.bias.scalar(b, h, min(lane, P.nk - 1));
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        if (32 * u + kcol >= P.nq)
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) qraw[u][c] = zero;
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if ((lane + 64 * i) / (D / 8) * 4 + r >= P.nk) kw[i][r] = vw[i][r] = zero;
 
     // optional RMSNorm of the queries, bit-identical to pa_rmsnorm_fwd: lane (q, hh) holds row
     // q's feature chunks 2c + hh (8 features each), the partner half lane ^ 32 the others; the
@@ -944,26 +969,18 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
         }
     }
 
-    // this unit's keys: K row-major, V transposed (4-key x 8-dim blocks), the key term; with
-    // PA_NORM_K the K rows are normalised on the way (a row's 8 chunks sit in 8 consecutive
-    // lanes, summed by pa_rmsnorm_fwd's butterfly)
-    float wk[8];
-    if (P.nflags & PA_NORM_K)
+    // this unit's keys into LDS: K row-major, V transposed (4-key x 8-dim blocks), the key
+    // term; with PA_NORM_K the K rows are normalised on the way (a row's 8 chunks sit in 8
+    // consecutive lanes, summed by pa_rmsnorm_fwd's butterfly)
+    if (P.nflags & PA_NORM_K) {
+        float wk[8];
         unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P.knw) + (lane % (D / 8)) * 8), wk);
-    for (int blk = lane; blk < TL::BLOCKS; blk += 64) {
-        const int rg = blk / (D / 8), cc = blk % (D / 8);
-        u32x4_t kw[4], vw[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int j = rg * 4 + r;
-            kw[r] = j < P.nk ? *reinterpret_cast<const u32x4_t*>(P.k.row<T>(b, h, j) + cc * 8) : zero;
-            vw[r] = j < P.nk ? *reinterpret_cast<const u32x4_t*>(P.v.row<T>(b, h, j) + cc * 8) : zero;
-        }
-        if (P.nflags & PA_NORM_K) {
+        for (int i = 0; i < NR; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float x[8];
-                unpack8<T>(kw[r], x);
+                unpack8<T>(kw[i][r], x);
                 float sc = 0.f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) sc += x[e] * x[e];
@@ -972,23 +989,17 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
                 const float rs = rsqrtf(sc * (1.f / D) + P.keps);
                 float y[8];
                 norm_scale(x, rs, wk, y);
-                kw[r] = pack8<T>(y);
+                kw[i][r] = pack8<T>(y);
             }
-        }
+    }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) *reinterpret_cast<u32x4_t*>(Ks + (rg * 4 + r) * TL::KS + cc * 8) = kw[r];
-        store_block_transposed(vw, reinterpret_cast<uint16_t*>(Vt + (cc * 8) * TL::VS + rg * 4), TL::VS);
+    for (int i = 0; i < NR; ++i) {
+        const int blk = lane + 64 * i, rg = blk / (D / 8), cc = blk % (D / 8);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) *reinterpret_cast<u32x4_t*>(Ks + (rg * 4 + r) * TL::KS + cc * 8) = kw[i][r];
+        store_block_transposed(vw[i], reinterpret_cast<uint16_t*>(Vt + (cc * 8) * TL::VS + rg * 4), TL::VS);
     }
-    if (HAS_BIAS) {
-        for (int j = lane; j < BN; j += 64) {
-            float t = -INFINITY;
-            if (j < P.nk) {
-                const float x = P.bias.scalar(b, h, j);
-                t = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
-            }
-            Bk[j] = t;
-        }
-    }
+    if (HAS_BIAS) Bk[lane] = lane < P.nk && bias_class(braw) == 0 ? braw * kLog2e : -INFINITY;
     // one wave's LDS operations complete in order: wait for the writes, fence the compiler
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
