@@ -855,7 +855,16 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
 // per CU, so 1024 units took two rounds; here each wave stages only its own K and V^T tile
 // (18 KB) and works on it alone -- no workgroup barrier, a wave may finish independently.
 
-constexpr int kShortUnits = 4;
+constexpr int kShortUnits = 4;  // waves per workgroup
+#ifndef PA_FWD_SHORT_SPLIT
+#define PA_FWD_SHORT_SPLIT 2
+#endif
+// waves per unit: each takes 2 / kShortSplit of the unit's two 32-query blocks and stages the
+// unit's K / V^T tile itself.  With 2 (two waves per SIMD at PolyViT's 1024 units, the second
+// K / V read of a unit served by L2) the pass took 16.5 against 17.5 us event-timed, PolyViT
+// 1.130 against 1.144 ms.
+constexpr int kShortSplit = PA_FWD_SHORT_SPLIT;
+static_assert(kShortSplit == 1 || kShortSplit == 2, "short-pass split");
 
 template <typename T>
 __device__ __forceinline__ void unpack8(const u32x4_t& r, float (&out)[8]) {
@@ -893,8 +902,11 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     __shared__ __attribute__((aligned(16))) T sVt[kShortUnits][D * TL::VS];
     __shared__ __attribute__((aligned(16))) float sB[kShortUnits][BN];
     const int lane = threadIdx.x & 63, w = wave_id();
-    const int unit = blockIdx.x * kShortUnits + w;
-    if (unit >= P.batch * P.heads) return;  // whole waves; nothing below synchronises waves
+    constexpr int QPW = 2 / kShortSplit;  // 32-query blocks per wave
+    const int task = blockIdx.x * kShortUnits + w;
+    const int unit = task / kShortSplit, qb0 = (task % kShortSplit) * QPW;
+    // whole waves; nothing below synchronises waves
+    if (unit >= P.batch * P.heads || 32 * qb0 >= P.nq) return;
     const int h = unit % P.heads, b = unit / P.heads;
     T* Ks = sK[w];
     T* Vt = sVt[w];
@@ -908,10 +920,10 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     // load) and replaced by zeros afterwards.
     static_assert(TL::BLOCKS % 64 == 0 && BN == 64, "short-pass tile");
     constexpr int NR = TL::BLOCKS / 64;  // block rounds per lane
-    u32x4_t qraw[2][D / 16];
+    u32x4_t qraw[QPW][D / 16];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const T* qrow = P.q.row<T>(b, h, min(32 * u + kcol, P.nq - 1));
+    for (int u = 0; u < QPW; ++u) {
+        const T* qrow = P.q.row<T>(b, h, min(32 * (qb0 + u) + kcol, P.nq - 1));
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) qraw[u][c] = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
     }
@@ -929,8 +941,8 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     float braw = 0.f;  // lane j's key bias (BN = 64 keys, one per lane)
     if (HAS_BIAS) braw = P.bias.scalar(b, h, min(lane, P.nk - 1));
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-        if (32 * u + kcol >= P.nq)
+    for (int u = 0; u < QPW; ++u)
+        if (32 * (qb0 + u) + kcol >= P.nq)
 #pragma unroll
             for (int c = 0; c < D / 16; ++c) qraw[u][c] = zero;
 #pragma unroll
@@ -949,7 +961,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
         for (int c = 0; c < D / 16; ++c)
             unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P.qnw) + c * 16 + 8 * hh), wq[c]);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < QPW; ++u) {
             float x[D / 16][8], t[D / 16];
 #pragma unroll
             for (int c = 0; c < D / 16; ++c) {
@@ -1006,11 +1018,11 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     asm volatile("" ::: "memory");
 
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {  // the unit's two 32-query blocks
+    for (int u = 0; u < QPW; ++u) {  // this wave's 32-query blocks
         W wv;
         wv.hh = hh;
         wv.kcol = kcol;
-        wv.q0 = 32 * u;
+        wv.q0 = 32 * (qb0 + u);
         wv.qi = wv.q0 + wv.kcol;
         wv.nk = P.nk;
         wv.sl2 = P.scale * kLog2e;
@@ -1340,7 +1352,8 @@ static void launch_t(const PassDev& P, hipStream_t s) {
         if (mfma_fwd_short_applies(P, sizeof(T) == 2 ? PA_BF16 : PA_F32)) {
             const int units = P.batch * P.heads;
             ProfScope ps("mfma_fwd_short", s);
-            hipLaunchKernelGGL((k_mfma_fwd_short<T, S, B>), dim3((units + kShortUnits - 1) / kShortUnits),
+            hipLaunchKernelGGL((k_mfma_fwd_short<T, S, B>),
+                               dim3((units * kShortSplit + kShortUnits - 1) / kShortUnits),
                                dim3(kFwdThreads), 0, s, P);
             return;
         }
