@@ -13,6 +13,9 @@
  *                      (flash_poly_attention.py:12-154, launched at :347 and :365); with
  *                      pa_pass.epi also the modules' root-value / gate epilogue
  *                      (poly_attention.py:342-351, n_poly_attention.py:315-326).
+ *   pa_poly_order2_fwd both levels of the order-2 chain (poly_attention.py:48-116: the two
+ *                      _poly_flash_fwd_kernel launches at flash_poly_attention.py:347 and
+ *                      :365), in one launch where both are short passes.
  *   pa_attn_pass_bwd   the backward of one level (flash_poly_attention.py:156-316, launched at
  *                      :409 and :429 inside PolyFlashAttention.backward :386-446).
  *   pa_poly_decode     the cached single-token step of Order2PolyAttention.forward
@@ -50,7 +53,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 6
+#define PA_ABI_VERSION 7
 #define PA_MAX_ORDER 8
 
 /* status codes (0 = success, negative = failure) */
@@ -349,6 +352,16 @@ int    pa_attn_pass_fwd(const pa_pass* p, void* stream);
 size_t pa_attn_pass_fwd_workspace(const pa_pass* p);   /* 0: the forward takes none */
 size_t pa_attn_pass_bwd_workspace(const pa_pass_grad* g);
 int    pa_attn_pass_bwd(const pa_pass_grad* g, void* stream);
+
+/* The two forward passes of an order-2 chain, in order: `second`'s keys, values and key bias
+ * must be `first`'s queries, output and lse (the same views; second->nk == first->nq), else
+ * PA_EINVAL.  Where both are short passes of the same heads (head dim 64, nq and nk <= 64, not
+ * causal, bf16 / f16, no masks, value multiplier or first-pass bias / epilogue, both
+ * softclamped or neither; with norms on load, second's key norm the same weight and eps as
+ * first's query norm) one kernel runs both: the first pass's output and lse reach the second
+ * through on-chip memory (they are still written), and every result has the bits of the two
+ * pa_attn_pass_fwd calls it replaces.  Otherwise it makes those two calls. */
+int    pa_poly_order2_fwd(const pa_pass* first, const pa_pass* second, void* stream);
 size_t pa_poly_decode_workspace(const pa_decode* d);
 int    pa_poly_decode(const pa_decode* d, void* stream);
 

@@ -273,20 +273,25 @@ int pa_profile_stop(pa_kernel_time* out, int capacity, int* count) {
 
 size_t pa_attn_pass_fwd_workspace(const pa_pass* p) { return p ? fwd_ws_bytes(*p) : 0; }
 
+// q / k norms on load: valid flags and weights, and only where the short-pass kernel runs
+static int check_norm(const pa_pass* p, const PassDev& P) {
+    if (!P.nflags) return PA_OK;
+    const pa_qk_norm* n = p->norm;
+    if (n->flags & ~(PA_NORM_Q | PA_NORM_K)) return PA_EINVAL;
+    if (((n->flags & PA_NORM_Q) && (!n->q_weight || (uintptr_t)n->q_weight % 16)) ||
+        ((n->flags & PA_NORM_K) && (!n->k_weight || (uintptr_t)n->k_weight % 16)))
+        return PA_EINVAL;
+    const int T = p->q.dtype;
+    if (!mfma_fwd_supported(P, T) || !mfma_fwd_short_applies(P, T)) return PA_EUNSUPPORTED;
+    return PA_OK;
+}
+
 int pa_attn_pass_fwd(const pa_pass* p, void* stream) {
     PA_TRY(validate_pass(p));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const PassDev P = to_passdev(p);
     const int T = p->q.dtype;
-    if (P.nflags) {
-        // q / k norms on load: only where the short-pass kernel runs
-        const pa_qk_norm* n = p->norm;
-        if (n->flags & ~(PA_NORM_Q | PA_NORM_K)) return PA_EINVAL;
-        if (((n->flags & PA_NORM_Q) && (!n->q_weight || (uintptr_t)n->q_weight % 16)) ||
-            ((n->flags & PA_NORM_K) && (!n->k_weight || (uintptr_t)n->k_weight % 16)))
-            return PA_EINVAL;
-        if (!mfma_fwd_supported(P, T) || !mfma_fwd_short_applies(P, T)) return PA_EUNSUPPORTED;
-    }
+    PA_TRY(check_norm(p, P));
     if (mfma_fwd_supported(P, T)) {
         const size_t need = fwd_ws_bytes(*p);
         if (need && p->workspace && p->workspace_bytes >= need) {
@@ -316,6 +321,32 @@ int pa_attn_pass_fwd(const pa_pass* p, void* stream) {
         launch_simt_fwd(P, T, s);
     }
     return finish_launch();
+}
+
+static bool same_view(const pa_view& a, const pa_view& b) {
+    return a.ptr == b.ptr && a.sb == b.sb && a.sh == b.sh && a.sn == b.sn && a.heads == b.heads &&
+           a.dtype == b.dtype;
+}
+
+int pa_poly_order2_fwd(const pa_pass* first, const pa_pass* second, void* stream) {
+    PA_TRY(validate_pass(first));
+    PA_TRY(validate_pass(second));
+    // the chain: the second pass's keys, values and key term are the first's queries, output
+    // and lse
+    if (!same_view(second->k, first->q) || !same_view(second->v, first->out) ||
+        !same_view(second->bias, first->lse) || second->nk != first->nq)
+        return PA_EINVAL;
+    const PassDev P1 = to_passdev(first), P2 = to_passdev(second);
+    PA_TRY(check_norm(first, P1));
+    PA_TRY(check_norm(second, P2));
+    const int T = first->q.dtype;
+    const bool degenerate = ((first->flags | second->flags) & PA_FLAG_MAY_DEGENERATE) != 0;
+    if (!degenerate && second->q.dtype == T && mfma_order2_short_applies(P1, P2, T)) {
+        launch_order2_short(P1, P2, T, static_cast<hipStream_t>(stream));
+        return finish_launch();
+    }
+    PA_TRY(pa_attn_pass_fwd(first, stream));
+    return pa_attn_pass_fwd(second, stream);
 }
 
 size_t pa_attn_pass_bwd_workspace(const pa_pass_grad* g) {

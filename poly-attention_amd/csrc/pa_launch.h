@@ -39,6 +39,10 @@ bool mfma_fwd_supported(const PassDev& P, int dtype);
 // multiplier or key mask, 16-bit)
 bool mfma_fwd_short_applies(const PassDev& P, int dtype);
 void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s);
+// both passes of an order-2 chain in one short-pass launch (pass 2's keys / values / key term
+// are pass 1's queries / output / lse; the caller checks the views)
+bool mfma_order2_short_applies(const PassDev& P1, const PassDev& P2, int dtype);
+void launch_order2_short(const PassDev& P1, const PassDev& P2, int dtype, hipStream_t s);
 bool mfma_bwd_supported(const GradDev& G, int dtype);
 bool mfma_bwd_fuses_pre(const GradDev& G);
 void launch_mfma_bwd(const GradDev& G, int dtype, hipStream_t s);

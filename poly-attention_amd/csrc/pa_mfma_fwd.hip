@@ -107,19 +107,20 @@ __device__ __forceinline__ KeySide<T> key_side(const PassDev& P, int b, int h) {
 // of row qi, 4 consecutive columns from d = (k / 4) * 32 + (k % 4) * 8 + 4 * hh for k < NG,
 // rounded and packed in o[k].  Every root and gate word is loaded before any is used: the
 // store is the kernel's tail, where a load per element would serialise on memory latency.
-template <typename T, int NG>
-__device__ __forceinline__ void epi_store_lane(const PassDev& P, int b, int h, int qi, int hh,
-                                               const u32x2_t (&o)[NG]) {
-    const bool has_r = P.er.ok(), has_g = P.eg.ok();
-    const bool sig = (P.eflags & PA_EPI_ROOT_SIGMOID) != 0;
-    const T* rrow = has_r ? P.er.row<T>(b, h, qi) : nullptr;
-    const T* grow = has_g ? P.eg.row<T>(b, h, qi) : nullptr;
+// The root and gate presence are template arguments: with a run-time choice between a loaded
+// row and the lane's own output the compiler loads through a selected pointer, which puts the
+// output array in scratch memory in every kernel that calls this.
+template <typename T, int NG, bool HR, bool HG>
+__device__ __forceinline__ void epi_store_rows(const PassDev& P, int b, int h, int qi, int hh,
+                                               const u32x2_t (&o)[NG], bool sig) {
     u32x2_t r[NG], g[NG];
 #pragma unroll
     for (int k = 0; k < NG; ++k) {
         const int d = (k / 4) * 32 + (k % 4) * 8 + 4 * hh;
-        r[k] = has_r ? *reinterpret_cast<const u32x2_t*>(rrow + d) : o[k];
-        g[k] = has_g ? *reinterpret_cast<const u32x2_t*>(grow + d) : o[k];
+        if constexpr (HR) r[k] = *reinterpret_cast<const u32x2_t*>(P.er.row<T>(b, h, qi) + d);
+        else r[k] = o[k];
+        if constexpr (HG) g[k] = *reinterpret_cast<const u32x2_t*>(P.eg.row<T>(b, h, qi) + d);
+        else g[k] = o[k];
     }
     T* yrow = P.ey.wrow<T>(b, h, qi);
 #pragma unroll
@@ -132,10 +133,23 @@ __device__ __forceinline__ void epi_store_lane(const PassDev& P, int b, int h, i
             unpack2<T>(o[k][w], o0, o1);
             unpack2<T>(r[k][w], r0, r1);
             unpack2<T>(g[k][w], g0, g1);
-            y4[w] = pack2<T>(epi_combine<T>(o0, r0, g0, has_r, has_g, sig),
-                             epi_combine<T>(o1, r1, g1, has_r, has_g, sig));
+            y4[w] = pack2<T>(epi_combine<T>(o0, r0, g0, HR, HG, sig),
+                             epi_combine<T>(o1, r1, g1, HR, HG, sig));
         }
         *reinterpret_cast<u32x2_t*>(yrow + d) = y4;
+    }
+}
+
+template <typename T, int NG>
+__device__ __forceinline__ void epi_store_lane(const PassDev& P, int b, int h, int qi, int hh,
+                                               const u32x2_t (&o)[NG]) {
+    const bool sig = (P.eflags & PA_EPI_ROOT_SIGMOID) != 0;
+    if (P.er.ok()) {
+        if (P.eg.ok()) epi_store_rows<T, NG, true, true>(P, b, h, qi, hh, o, sig);
+        else epi_store_rows<T, NG, true, false>(P, b, h, qi, hh, o, sig);
+    } else {
+        if (P.eg.ok()) epi_store_rows<T, NG, false, true>(P, b, h, qi, hh, o, sig);
+        else epi_store_rows<T, NG, false, false>(P, b, h, qi, hh, o, sig);
     }
 }
 
@@ -891,13 +905,122 @@ __device__ __forceinline__ u32x4_t pack8(const float (&v)[8]) {
     return r;
 }
 
+// RMSNorm of one 32-row block held as Q^T fragments, bit-identical to pa_rmsnorm_fwd: lane
+// (q, hh) holds row q's feature chunks 2c + hh (8 features each), the partner half lane ^ 32
+// the others; the chunk sums combine as that kernel's butterfly over its 8 lanes does: chunk
+// pairs first, then (t0 + t1) + (t2 + t3)
+template <typename T>
+__device__ __forceinline__ void norm_q_frags(u32x4_t (&q)[4], const void* weight, float eps, int hh) {
+    constexpr int D = 64;
+    float x[D / 16][8], t[D / 16];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        unpack8<T>(q[c], x[c]);
+        float sc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sc += x[c][e] * x[c][e];
+        t[c] = sc + __shfl_xor(sc, 32);
+    }
+    const float rs = rsqrtf(((t[0] + t[1]) + (t[2] + t[3])) * (1.f / D) + eps);
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        float wq[8], y[8];
+        unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(weight) + c * 16 + 8 * hh), wq);
+        norm_scale(x[c], rs, wq, y);
+        q[c] = pack8<T>(y);
+    }
+}
+
+// RMSNorm of a row chunk (8 features) whose row's 8 chunks sit in 8 consecutive lanes, summed
+// by pa_rmsnorm_fwd's butterfly; w = this lane's 8 weights
+template <typename T>
+__device__ __forceinline__ void norm_row_chunk(u32x4_t& k, const float (&w)[8], float eps) {
+    constexpr int D = 64;
+    float x[8];
+    unpack8<T>(k, x);
+    float sc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sc += x[e] * x[e];
+#pragma unroll
+    for (int off = 1; off < D / 8; off <<= 1) sc += __shfl_xor(sc, off);
+    const float rs = rsqrtf(sc * (1.f / D) + eps);
+    float y[8];
+    norm_scale(x, rs, w, y);
+    k = pack8<T>(y);
+}
+
+// One 32-query block (queries q0 .. q0 + 31 as Q^T fragments q) of a short pass against the
+// unit's staged 64-key tile (K row-major, V^T, key term Bk when the pass has one); leaves O,
+// m and l in wv.
+template <typename T, class W>
+__device__ __forceinline__ void short_block(W& wv, const PassDev& P, int q0, int lane,
+                                            const u32x4_t (&q)[4], const T* Ks, const T* Vt,
+                                            const float* Bk, bool softclamp) {
+    constexpr int D = 64, KB = 2;
+    typedef typename W::frag frag;
+    wv.hh = lane >> 5;
+    wv.kcol = lane & 31;
+    wv.q0 = q0;
+    wv.qi = q0 + wv.kcol;
+    wv.nk = P.nk;
+    wv.sl2 = P.scale * kLog2e;
+    wv.cinv = softclamp ? P.scale / P.softclamp : 0.f;
+    wv.cl2 = softclamp ? P.softclamp * kLog2e : 0.f;
+    wv.m = -INFINITY;
+    wv.l = 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) wv.qf[c] = __builtin_bit_cast(frag, q[c]);
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) wv.o[x] = zero16();
+    f32x16_t s[KB];
+    wv.scores(Ks, s);
+    wv.mask_edges(s, 0);
+    wv.settle(wv.logits(s, Bk));
+    u32x4_t pk[KB][2];
+    frag vf[KB][2][D / 32];
+    wv.load_v(Vt, vf);
+    wv.l += wv.probs(s, wv.m == -INFINITY ? 0.f : wv.m, pk);
+    wv.pv(vf, pk);
+}
+
+// The finished block's rows normalised and rounded to T (lane (q, hh): features
+// x*32 + 8g + 4hh .. +3 in ow[4x + g]) and its lse (NaN for a degenerate row); with `store`
+// written to out, lse and the epilogue's y for the rows below nq.  Returns the lse.
+template <typename T, class W>
+__device__ __forceinline__ float short_finish(const W& wv, const PassDev& P, int b, int h,
+                                              bool store, u32x2_t (&ow)[8]) {
+    constexpr int D = 64;
+    const float l = xhalf_sum(wv.l);
+    const int qi = wv.qi;
+    const bool degenerate = !(l > 0.f) || (qi < P.nq && !P.qm.keep(b, qi));
+    const float inv = degenerate ? 0.f : 1.f / l;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            ow[4 * x + g][0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
+            ow[4 * x + g][1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
+        }
+    const float lse = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
+    if (store && qi < P.nq) {
+        T* orow = P.out.wrow<T>(b, h, qi);
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<u32x2_t*>(orow + x * 32 + 8 * g + 4 * wv.hh) = ow[4 * x + g];
+        if (P.ey.ok()) epi_store_lane<T, D / 8>(P, b, h, qi, wv.hh, ow);
+        if (wv.hh == 0) *P.lse.wrow<float>(b, h, qi) = lse;
+    }
+    return lse;
+}
+
 template <typename T, bool SOFTCLAMP, bool HAS_BIAS>
 __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     constexpr int D = 64, KB = 2;
     using TL = FwdTile<D, KB>;
     constexpr int BN = TL::BN;
     using W = FwdWave<T, D, KB, false, SOFTCLAMP, HAS_BIAS>;
-    typedef typename W::frag frag;
     __shared__ __attribute__((aligned(16))) T sK[kShortUnits][BN * TL::KS];
     __shared__ __attribute__((aligned(16))) T sVt[kShortUnits][D * TL::VS];
     __shared__ __attribute__((aligned(16))) float sB[kShortUnits][BN];
@@ -915,9 +1038,9 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     const int hh = lane >> 5, kcol = lane & 31;
 
     // Every global load of the unit is issued before the first wait (one memory round trip):
-    // the Q^T fragments of both 32-query blocks, the K and V rows of both 4-key x 8-dim block
-    // rounds, the key bias.  Rows past nq / nk are read from the last row (no branch around a
-    // load) and replaced by zeros afterwards.
+    // the Q^T fragments of the wave's 32-query blocks, the K and V rows of both 4-key x 8-dim
+    // block rounds, the key bias.  Rows past nq / nk are read from the last row (no branch
+    // around a load) and replaced by zeros afterwards.
     static_assert(TL::BLOCKS % 64 == 0 && BN == 64, "short-pass tile");
     constexpr int NR = TL::BLOCKS / 64;  // block rounds per lane
     u32x4_t qraw[QPW][D / 16];
@@ -951,59 +1074,20 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
         for (int r = 0; r < 4; ++r)
             if ((lane + 64 * i) / (D / 8) * 4 + r >= P.nk) kw[i][r] = vw[i][r] = zero;
 
-    // optional RMSNorm of the queries, bit-identical to pa_rmsnorm_fwd: lane (q, hh) holds row
-    // q's feature chunks 2c + hh (8 features each), the partner half lane ^ 32 the others; the
-    // chunk sums combine as that kernel's butterfly over its 8 lanes does: chunk pairs first,
-    // then (t0 + t1) + (t2 + t3)
-    if (P.nflags & PA_NORM_Q) {
-        float wq[D / 16][8];
+    // optional RMSNorms of the queries and keys
+    if (P.nflags & PA_NORM_Q)
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c)
-            unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P.qnw) + c * 16 + 8 * hh), wq[c]);
-#pragma unroll
-        for (int u = 0; u < QPW; ++u) {
-            float x[D / 16][8], t[D / 16];
-#pragma unroll
-            for (int c = 0; c < D / 16; ++c) {
-                unpack8<T>(qraw[u][c], x[c]);
-                float sc = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) sc += x[c][e] * x[c][e];
-                t[c] = sc + __shfl_xor(sc, 32);
-            }
-            const float rs = rsqrtf(((t[0] + t[1]) + (t[2] + t[3])) * (1.f / D) + P.qeps);
-#pragma unroll
-            for (int c = 0; c < D / 16; ++c) {
-                float y[8];
-                norm_scale(x[c], rs, wq[c], y);
-                qraw[u][c] = pack8<T>(y);
-            }
-        }
-    }
-
-    // this unit's keys into LDS: K row-major, V transposed (4-key x 8-dim blocks), the key
-    // term; with PA_NORM_K the K rows are normalised on the way (a row's 8 chunks sit in 8
-    // consecutive lanes, summed by pa_rmsnorm_fwd's butterfly)
+        for (int u = 0; u < QPW; ++u) norm_q_frags<T>(qraw[u], P.qnw, P.qeps, hh);
     if (P.nflags & PA_NORM_K) {
         float wk[8];
         unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P.knw) + (lane % (D / 8)) * 8), wk);
 #pragma unroll
         for (int i = 0; i < NR; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float x[8];
-                unpack8<T>(kw[i][r], x);
-                float sc = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) sc += x[e] * x[e];
-#pragma unroll
-                for (int off = 1; off < D / 8; off <<= 1) sc += __shfl_xor(sc, off);
-                const float rs = rsqrtf(sc * (1.f / D) + P.keps);
-                float y[8];
-                norm_scale(x, rs, wk, y);
-                kw[i][r] = pack8<T>(y);
-            }
+            for (int r = 0; r < 4; ++r) norm_row_chunk<T>(kw[i][r], wk, P.keps);
     }
+
+    // this unit's keys into LDS: K row-major, V transposed (4-key x 8-dim blocks), the key term
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
         const int blk = lane + 64 * i, rg = blk / (D / 8), cc = blk % (D / 8);
@@ -1019,51 +1103,135 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
 
 #pragma unroll
     for (int u = 0; u < QPW; ++u) {  // this wave's 32-query blocks
+        if (32 * (qb0 + u) >= P.nq) break;  // wave-uniform
         W wv;
-        wv.hh = hh;
-        wv.kcol = kcol;
-        wv.q0 = 32 * (qb0 + u);
-        wv.qi = wv.q0 + wv.kcol;
-        wv.nk = P.nk;
-        wv.sl2 = P.scale * kLog2e;
-        wv.cinv = SOFTCLAMP ? P.scale / P.softclamp : 0.f;
-        wv.cl2 = SOFTCLAMP ? P.softclamp * kLog2e : 0.f;
-        wv.m = -INFINITY;
-        wv.l = 0.f;
-        const int qi = wv.qi;
-        if (wv.q0 >= P.nq) break;  // wave-uniform
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) wv.qf[c] = __builtin_bit_cast(frag, qraw[u][c]);
-#pragma unroll
-        for (int x = 0; x < D / 32; ++x) wv.o[x] = zero16();
-        f32x16_t s[KB];
-        wv.scores(Ks, s);
-        wv.mask_edges(s, 0);
-        wv.settle(wv.logits(s, Bk));
-        u32x4_t pk[KB][2];
-        frag vf[KB][2][D / 32];
-        wv.load_v(Vt, vf);
-        wv.l += wv.probs(s, wv.m == -INFINITY ? 0.f : wv.m, pk);
-        wv.pv(vf, pk);
+        short_block<T>(wv, P, 32 * (qb0 + u), lane, qraw[u], Ks, Vt, Bk, SOFTCLAMP);
+        u32x2_t ow[D / 8];
+        short_finish<T>(wv, P, b, h, true, ow);
+    }
+}
 
-        const float l = xhalf_sum(wv.l);
-        if (qi < P.nq) {
-            const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
-            const float inv = degenerate ? 0.f : 1.f / l;
-            T* orow = P.out.wrow<T>(b, h, qi);
-            u32x2_t ow[D / 8];
+// ---------------------------------------------------------------------------------------
+// Both passes of an order-2 chain in one launch, where each is a short pass of the same heads
+// and the second pass's keys, values and key bias are the first pass's queries, output and
+// lse (the chain's q2, msg and lse23; poly_attention.py:48-116):
+//   pass 1: msg = attn(q2, q3, v3), lse23;   pass 2: out = attn(q1, q2, msg; key bias lse23).
+// Two waves per (batch, head) unit, one per 32-row block p: each loads its rows of q2 and q1
+// and its half of pass 1's K / V rows in one memory round trip, normalises q2 once for both
+// passes (its pass-1 query norm is the pass-2 key norm), stages its half of pass 1's K / V^T
+// tile and of pass 2's K tile, runs pass 1 for its q2 block, hands the rounded msg rows and
+// their lse (as the key term) to pass 2's V^T tile in LDS -- also storing them as pass 1's
+// outputs -- and runs pass 2 for its q1 block.  A unit's two waves meet at two workgroup
+// barriers, which every wave reaches: a padding unit recomputes the last unit and stores
+// nothing.  Per unit it reads q1, q2, q3, v3 once (32 KB at the PolyViT shape) and writes
+// msg, lse23 and out, where the two launches read 48 KB; the results are the two passes'
+// bits.
+
+constexpr int kO2Units = kShortUnits / 2;  // units per workgroup
+
+template <typename T, bool SOFTCLAMP>
+__global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_order2_short(PassDev P1, PassDev P2) {
+    constexpr int D = 64, KB = 2;
+    using TL = FwdTile<D, KB>;
+    constexpr int BN = TL::BN;
+    static_assert(BN == 64 && kShortUnits == 4, "order-2 short tile");
+    using W1 = FwdWave<T, D, KB, false, SOFTCLAMP, false>;
+    using W2 = FwdWave<T, D, KB, false, SOFTCLAMP, true>;
+    __shared__ __attribute__((aligned(16))) T sK1[kO2Units][BN * TL::KS];
+    __shared__ __attribute__((aligned(16))) T sVt1[kO2Units][D * TL::VS];
+    __shared__ __attribute__((aligned(16))) T sK2[kO2Units][BN * TL::KS];
+    __shared__ __attribute__((aligned(16))) T sVt2[kO2Units][D * TL::VS];
+    __shared__ __attribute__((aligned(16))) float sB2[kO2Units][BN];
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int units = P1.batch * P1.heads;
+    const int slot = w >> 1, p = w & 1;  // unit slot in the workgroup, 32-row block
+    const int task = blockIdx.x * kO2Units + slot;
+    const bool live = task < units;
+    const int unit = live ? task : units - 1;
+    const int h = unit % P1.heads, b = unit / P1.heads;
+    const int hh = lane >> 5, kcol = lane & 31, row = 32 * p + kcol;
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+    const int n2 = P1.nq;  // q2 rows: pass 1's queries, pass 2's keys
+
+    // loads: q2 and q1 rows of block p as Q^T fragments, pass 1's K / V rows 32p .. 32p + 31
+    // as 4-key x 8-dim blocks (one per lane); rows past the end read from the last row, zeroed
+    const int rg = lane / (D / 8) + 8 * p, cc = lane % (D / 8);
+    u32x4_t q2r[D / 16], q1r[D / 16], kw[4], vw[4];
+    {
+        const T* r2 = P1.q.row<T>(b, h, min(row, n2 - 1));
+        const T* r1 = P2.q.row<T>(b, h, min(row, P2.nq - 1));
 #pragma unroll
-            for (int x = 0; x < D / 32; ++x)
+        for (int c = 0; c < D / 16; ++c) q2r[c] = *reinterpret_cast<const u32x4_t*>(r2 + c * 16 + 8 * hh);
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    u32x2_t& o2 = ow[4 * x + g];
-                    o2[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
-                    o2[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
-                    *reinterpret_cast<u32x2_t*>(orow + x * 32 + 8 * g + 4 * wv.hh) = o2;
-                }
-            if (P.ey.ok()) epi_store_lane<T, D / 8>(P, b, h, qi, wv.hh, ow);
-            if (wv.hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
+        for (int c = 0; c < D / 16; ++c) q1r[c] = *reinterpret_cast<const u32x4_t*>(r1 + c * 16 + 8 * hh);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int j = min(rg * 4 + r, P1.nk - 1);
+            kw[r] = *reinterpret_cast<const u32x4_t*>(P1.k.row<T>(b, h, j) + cc * 8);
+            vw[r] = *reinterpret_cast<const u32x4_t*>(P1.v.row<T>(b, h, j) + cc * 8);
         }
+    }
+    if (row >= n2)
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) q2r[c] = zero;
+    if (row >= P2.nq)
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) q1r[c] = zero;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (rg * 4 + r >= P1.nk) kw[r] = vw[r] = zero;
+
+    if (P1.nflags & PA_NORM_Q) norm_q_frags<T>(q2r, P1.qnw, P1.qeps, hh);
+    if (P2.nflags & PA_NORM_Q) norm_q_frags<T>(q1r, P2.qnw, P2.qeps, hh);
+    if (P1.nflags & PA_NORM_K) {
+        float wk[8];
+        unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P1.knw) + cc * 8), wk);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) norm_row_chunk<T>(kw[r], wk, P1.keps);
+    }
+
+    // stage: pass 1's K rows / V^T columns of this block, pass 2's K rows (normalised q2)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) *reinterpret_cast<u32x4_t*>(sK1[slot] + (rg * 4 + r) * TL::KS + cc * 8) = kw[r];
+    store_block_transposed(vw, reinterpret_cast<uint16_t*>(sVt1[slot] + (cc * 8) * TL::VS + rg * 4), TL::VS);
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+        *reinterpret_cast<u32x4_t*>(sK2[slot] + row * TL::KS + c * 16 + 8 * hh) = q2r[c];
+    __syncthreads();
+
+    // pass 1 for q2 block p; its rounded msg rows and lse become pass 2's values and key term
+    u32x2_t ow[D / 8];
+    float lse = 0.f;
+    const bool run1 = 32 * p < n2;  // wave-uniform
+    if (run1) {
+        W1 wv;
+        short_block<T>(wv, P1, 32 * p, lane, q2r, sK1[slot], sVt1[slot], nullptr, SOFTCLAMP);
+        lse = short_finish<T>(wv, P1, b, h, live, ow);
+    }
+    {
+        const bool keep = run1 && row < n2;
+        uint16_t* vt = reinterpret_cast<uint16_t*>(sVt2[slot]);
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int e2 = 0; e2 < 2; ++e2) {
+                    const uint32_t wd = keep ? ow[4 * x + g][e2] : 0u;
+                    const int d = x * 32 + 8 * g + 4 * hh + 2 * e2;
+                    vt[d * TL::VS + row] = (uint16_t)(wd & 0xffffu);
+                    vt[(d + 1) * TL::VS + row] = (uint16_t)(wd >> 16);
+                }
+        if (hh == 0) sB2[slot][row] = keep && bias_class(lse) == 0 ? lse * kLog2e : -INFINITY;
+    }
+    __syncthreads();
+
+    // pass 2 for q1 block p
+    if (32 * p < P2.nq) {
+        W2 wv;
+        short_block<T>(wv, P2, 32 * p, lane, q1r, sK2[slot], sVt2[slot], sB2[slot], SOFTCLAMP);
+        u32x2_t ow2[D / 8];
+        short_finish<T>(wv, P2, b, h, live, ow2);
     }
 }
 
@@ -1401,6 +1569,35 @@ void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s) {
         if (P.dim == 64) launch_d<f16, 64>(P, s);
         else launch_d<f16, 128>(P, s);
     }
+}
+
+bool mfma_order2_short_applies(const PassDev& P1, const PassDev& P2, int dtype) {
+    if (!(dtype == PA_BF16 || dtype == PA_F16)) return false;
+    if (!mfma_fwd_supported(P1, dtype) || !mfma_fwd_supported(P2, dtype)) return false;
+    if (!mfma_fwd_short_applies(P1, dtype) || !mfma_fwd_short_applies(P2, dtype)) return false;
+    if (P1.batch != P2.batch || P1.heads != P2.heads || P2.nk != P1.nq) return false;
+    if ((P1.softclamp > 0.f) != (P2.softclamp > 0.f)) return false;
+    // pass 1 has no key term and no epilogue; no query masks
+    if (P1.bias.ok() || P1.ey.ok() || P1.qm.p || P2.qm.p) return false;
+    // q2 is normalised once: pass 2's key norm must be pass 1's query norm
+    const bool nq1 = (P1.nflags & PA_NORM_Q) != 0, nk2 = (P2.nflags & PA_NORM_K) != 0;
+    if (nq1 != nk2) return false;
+    if (nq1 && (P1.qnw != P2.knw || P1.qeps != P2.keps)) return false;
+    return true;
+}
+
+template <typename T>
+static void launch_o2(const PassDev& P1, const PassDev& P2, hipStream_t s) {
+    const int units = P1.batch * P1.heads;
+    const dim3 grid((units + kO2Units - 1) / kO2Units);
+    ProfScope ps("mfma_order2_short", s);
+    if (P1.softclamp > 0.f) hipLaunchKernelGGL((k_mfma_order2_short<T, true>), grid, dim3(kFwdThreads), 0, s, P1, P2);
+    else hipLaunchKernelGGL((k_mfma_order2_short<T, false>), grid, dim3(kFwdThreads), 0, s, P1, P2);
+}
+
+void launch_order2_short(const PassDev& P1, const PassDev& P2, int dtype, hipStream_t s) {
+    if (dtype == PA_BF16) launch_o2<bf16>(P1, P2, s);
+    else launch_o2<f16>(P1, P2, s);
 }
 
 }  // namespace pa

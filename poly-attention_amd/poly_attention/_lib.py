@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolyattn.so"
 
-PA_ABI_VERSION = 6
+PA_ABI_VERSION = 7
 PA_MAX_ORDER = 8
 
 PA_OK = 0
@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "pa_attn_pass_fwd_workspace",
     "pa_attn_pass_bwd_workspace",
     "pa_attn_pass_bwd",
+    "pa_poly_order2_fwd",
     "pa_poly_decode_workspace",
     "pa_poly_decode",
     "pa_poly_decode_noalloc",
@@ -296,6 +297,8 @@ def _configure(lib) -> None:
     lib.pa_attn_pass_bwd_workspace.argtypes = [ctypes.POINTER(PaPassGrad)]
     lib.pa_attn_pass_bwd.restype = c_int
     lib.pa_attn_pass_bwd.argtypes = [ctypes.POINTER(PaPassGrad), c_void_p]
+    lib.pa_poly_order2_fwd.restype = c_int
+    lib.pa_poly_order2_fwd.argtypes = [ctypes.POINTER(PaPass), ctypes.POINTER(PaPass), c_void_p]
     lib.pa_poly_decode_workspace.restype = c_size_t
     lib.pa_poly_decode_workspace.argtypes = [ctypes.POINTER(PaDecode)]
     lib.pa_poly_decode.restype = c_int

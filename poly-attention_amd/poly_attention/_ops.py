@@ -231,6 +231,18 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
                            key_mask, query_mask, causal, softclamp, scale, may_degenerate,
                            _padded_epilogue(epilogue, dp))
         return tuple(t if i == 1 else _unpad(t, d, q) for i, t in enumerate(res))
+    p, res, _keep = _pass_prepare(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp,
+                                  scale, may_degenerate, epilogue, qk_norm)
+    with _device(q):
+        _lib.check(_lib.load().pa_attn_pass_fwd(ctypes.byref(p), _stream(q)), "pa_attn_pass_fwd")
+    return res
+
+
+def _pass_prepare(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, scale,
+                  may_degenerate, epilogue=None, qk_norm=None):
+    """The pa_pass of one forward pass over unpadded inputs with its outputs allocated:
+    (struct, results, keep), results as pass_fwd_raw returns them and ``keep`` what the
+    struct points at, to be held until the launch."""
     lib = _lib.load()
     q, k, v = _inner_contig(q), _inner_contig(k), _inner_contig(v)
     vmul = _inner_contig(vmul) if vmul is not None else None
@@ -256,9 +268,8 @@ def pass_fwd_raw(q, k, v, vmul, bias, key_mask, query_mask, causal, softclamp, s
         if ws_bytes:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
             p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
-    with _device(q):
-        _lib.check(lib.pa_attn_pass_fwd(ctypes.byref(p), _stream(q)), "pa_attn_pass_fwd")
-    return (out, lse) if epilogue is None else (out, lse, y)
+    res = (out, lse) if epilogue is None else (out, lse, y)
+    return p, res, (q, k, v, vmul, bias, km, qm, epi, norm, ws, epilogue)
 
 
 def _out_buffer(buf: Optional[Tensor], like: Tensor) -> Tensor:
@@ -1053,6 +1064,19 @@ def order2_forward(q1, q2, q3, v3, key_mask, causal, softclamp, scale, epilogue=
     RMSNorms on load (qk_norms_fusable; no gradient)."""
     degenerate = key_mask is not None
     n1, n2, n3 = norms if norms is not None else (None, None, None)
+    if key_mask is None and _padded_dim(q2) is None:
+        # both passes through pa_poly_order2_fwd: one launch where both are short passes
+        q2 = _inner_contig(q2)
+        p1, (msg, lse23), keep1 = _pass_prepare(
+            q2, q3, v3, None, None, None, None, causal, softclamp, scale, False,
+            qk_norm=(n2, n3) if norms is not None else None)
+        p2, res, keep2 = _pass_prepare(
+            q1, q2, msg, None, lse23, None, None, causal, softclamp, scale, False, epilogue,
+            qk_norm=(n1, n2) if norms is not None else None)
+        with _device(q2):
+            _lib.check(_lib.load().pa_poly_order2_fwd(ctypes.byref(p1), ctypes.byref(p2),
+                                                      _stream(q2)), "pa_poly_order2_fwd")
+        return (res[0], res[1], lse23, msg) + tuple(res[2:])
     msg, lse23 = pass_fwd_raw(q2, q3, v3, None, None, key_mask, None, causal, softclamp, scale,
                               degenerate, qk_norm=(n2, n3) if norms is not None else None)
     res = pass_fwd_raw(q1, q2, msg, None, lse23, key_mask, None, causal, softclamp, scale,

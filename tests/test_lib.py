@@ -89,6 +89,27 @@ def test_pass_fwd_rejects_invalid_arguments(breakage):
     assert lib.pa_attn_pass_fwd(ctypes.byref(p), None) == want
 
 
+@pytest.mark.parametrize("breakage", ["null", "keys", "values", "bias", "nk"])
+def test_order2_fwd_rejects_passes_that_do_not_chain(breakage):
+    """pa_poly_order2_fwd takes the second pass's keys, values and key bias to be the first
+    pass's queries, output and lse; anything else is refused before a launch."""
+    lib = _lib.load()
+    if breakage == "null":
+        assert lib.pa_poly_order2_fwd(None, None, None) == _lib.PA_EINVAL
+        return
+    a, c = _valid_pass(), _valid_pass()
+    c.k, c.v, c.bias, c.nk = a.q, a.out, a.lse, a.nq
+    if breakage == "keys":
+        c.k.ptr = c.k.ptr + 4096
+    elif breakage == "values":
+        c.v.sn = 128
+    elif breakage == "bias":
+        c.bias = _lib.PaView()
+    elif breakage == "nk":
+        c.nk = a.nq + 1
+    assert lib.pa_poly_order2_fwd(ctypes.byref(a), ctypes.byref(c), None) == _lib.PA_EINVAL
+
+
 def test_pass_bwd_rejects_missing_workspace():
     lib = _lib.load()
     g = _lib.PaPassGrad()
