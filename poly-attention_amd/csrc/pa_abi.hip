@@ -300,12 +300,10 @@ int pa_attn_pass_fwd(const pa_pass* p, void* stream) {
             const int hk = p->k.heads, nkp = key_term_stride(*p);
             char* w = static_cast<char*>(p->workspace);
             float* kterm = reinterpret_cast<float*>(w);
-            int32_t* kcnt = reinterpret_cast<int32_t*>(
-                w + align256((size_t)p->batch * hk * nkp * sizeof(float)));
             GradDev G = {};  // the key-term kernel reads f and hk only
             G.f = P;
             G.hk = hk;
-            launch_key_terms(G, kterm, nkp, kcnt, s);
+            launch_key_terms(G, kterm, nkp, nullptr, s);  // the key counts serve the backward
             PassDev Pm = P;
             Pm.bias = DView{reinterpret_cast<char*>(kterm), (int64_t)hk * nkp, nkp, 1,
                             p->heads / hk, PA_F32};

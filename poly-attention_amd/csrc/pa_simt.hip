@@ -590,28 +590,44 @@ __global__ __launch_bounds__(kSimtRows) void k_simt_bwd_dkv(GradDev G) {
 // on each bias-class-0 key j.  Part B is a plain loop over the rare (row, key) pairs.
 
 // Per (b, key head): the count of bias-class-0 keys and of unmasked bias-class-1 keys (part
-// B exists only where the latter is nonzero), and (with kterm) the per-key term the MFMA
-// kernels read as their bias, rows of stride nkp.
-__global__ __launch_bounds__(256) void k_key_terms(GradDev G, float* kterm, int nkp,
-                                                   int32_t* kcnt) {
+// B exists only where the latter is nonzero; with kcnt), and (with kterm) the per-key term the
+// MFMA kernels read as their bias, rows of stride nkp.  A workgroup walks a key row in rounds
+// of kKeyTermThreads x kKeyTermPer keys, every load of a round issued before its first use (the
+// key-mask bytes may alias the key-term stores, so a loop mixing them would load one key at
+// a time); at 4096 keys that is one round instead of 16 dependent steps.
+constexpr int kKeyTermThreads = 1024, kKeyTermPer = 4;
+__global__ __launch_bounds__(kKeyTermThreads) void k_key_terms(GradDev G, float* kterm, int nkp,
+                                                               int32_t* kcnt) {
     const PassDev& P = G.f;
     const int kh = blockIdx.x, b = blockIdx.y;
     const int h0 = kh * (P.heads / G.hk);
     int c0 = 0, c1 = 0;
-    for (int j = threadIdx.x; j < P.nk; j += blockDim.x) {
-        const float x = P.bias.ok() ? P.bias.scalar(b, h0, j) : 0.f;
-        const int cls = bias_class(x);
-        const bool kept = P.km.keep(b, j);
-        c0 += cls == 0;
-        c1 += cls == 1 && kept;
-        if (kterm) kterm[((int64_t)b * G.hk + kh) * nkp + j] = kept ? x : -INFINITY;
+    for (int j0 = 0; j0 < P.nk; j0 += kKeyTermThreads * kKeyTermPer) {
+        float x[kKeyTermPer];
+        bool kept[kKeyTermPer];
+#pragma unroll
+        for (int u = 0; u < kKeyTermPer; ++u) {
+            const int j = j0 + u * kKeyTermThreads + (int)threadIdx.x;
+            x[u] = (j < P.nk && P.bias.ok()) ? P.bias.scalar(b, h0, j) : 0.f;
+            kept[u] = j < P.nk && P.km.keep(b, j);
+        }
+#pragma unroll
+        for (int u = 0; u < kKeyTermPer; ++u) {
+            const int j = j0 + u * kKeyTermThreads + (int)threadIdx.x;
+            if (j >= P.nk) break;
+            const int cls = bias_class(x[u]);
+            c0 += cls == 0;
+            c1 += cls == 1 && kept[u];
+            if (kterm) kterm[((int64_t)b * G.hk + kh) * nkp + j] = kept[u] ? x[u] : -INFINITY;
+        }
     }
+    if (!kcnt) return;  // whole workgroup: the forward needs only the key term
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         c0 += __shfl_xor(c0, off);
         c1 += __shfl_xor(c1, off);
     }
-    __shared__ int s0[4], s1[4];
+    __shared__ int s0[kKeyTermThreads / 64], s1[kKeyTermThreads / 64];
     const int w = threadIdx.x / 64;
     if (threadIdx.x % 64 == 0) {
         s0[w] = c0;
@@ -642,6 +658,15 @@ __global__ __launch_bounds__(kFixThreads) void k_fix_rows(GradDev G) {
     const int h = blockIdx.x, b = blockIdx.y;
     const int slot = threadIdx.x / LPR, c0 = (threadIdx.x % LPR) * 8;
     const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
+    float* part = G.ws_part + ((int64_t)b * P.heads + h) * (D + 2);
+    // most heads hold no fully-masked row (lse = +inf): one coalesced scan decides, and the
+    // row-slot loop below runs only where one exists
+    bool any = false;
+    for (int i = threadIdx.x; i < P.nq; i += kFixThreads) any |= G.ws_lse[row0 + i] == INFINITY;
+    if (!__syncthreads_or(any)) {
+        if (threadIdx.x < D + 2) part[threadIdx.x] = 0.f;
+        return;
+    }
     float u[8], wsum = 0.f, cnt = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) u[e] = 0.f;
@@ -665,7 +690,6 @@ __global__ __launch_bounds__(kFixThreads) void k_fix_rows(GradDev G) {
         sC[slot] = cnt;
     }
     __syncthreads();
-    float* part = G.ws_part + ((int64_t)b * P.heads + h) * (D + 2);
     if (threadIdx.x < D) {
         float a = 0.f;
         for (int r = 0; r < R; ++r) a += sU[r][threadIdx.x];
@@ -1071,7 +1095,8 @@ void launch_epi_bwd(const GradDev& G, void* dO, int hr, int dtype, hipStream_t s
 
 void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, hipStream_t s) {
     ProfScope ps("key_terms", s);
-    hipLaunchKernelGGL(k_key_terms, dim3(G.hk, G.f.batch), dim3(256), 0, s, G, kterm, nkp, kcnt);
+    hipLaunchKernelGGL(k_key_terms, dim3(G.hk, G.f.batch), dim3(kKeyTermThreads), 0, s, G, kterm,
+                       nkp, kcnt);
 }
 
 void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s) {
