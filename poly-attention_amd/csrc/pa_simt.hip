@@ -9,6 +9,7 @@
 
 #include "pa_common.h"
 #include "pa_launch.h"
+#include "pa_mfma.h"
 
 namespace pa {
 
@@ -188,6 +189,46 @@ __device__ __forceinline__ void store8_a8(T* p, const float* f) {
 
 constexpr int kFixThreads = 1024;  // per-head reductions: many rows in flight on one CU
 
+// S0 of k_fwd_fixup, one slot's share (key rows slot, slot + R, ...): its key rows four at a
+// time, each round's loads issued unconditionally (rows past the end read the last row and
+// count for nothing) before the first is used -- a load per dependent step took 27 us at 4096
+// keys; eight at a time measured the same.  VM: the values are v * vmul, rounded to T.
+template <typename T, int D, bool VM>
+__device__ __forceinline__ void fixup_s0(const PassDev& P, int b, int h, int slot, int c0,
+                                         float (&acc)[8], int& n0, int& n1) {
+    constexpr int R = kFixThreads / (D / 8), kFixU = 4;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    for (int j0 = slot; j0 < P.nk; j0 += R * kFixU) {
+        int cls[kFixU];
+        float v8[kFixU][8], m8[VM ? kFixU : 1][8];
+        // the classes first: a key bias load sits behind a branch, whose join waits for every
+        // load issued before it
+#pragma unroll
+        for (int u = 0; u < kFixU; ++u) {
+            const int j = j0 + u * R;
+            cls[u] = j >= P.nk ? -1 : P.bias.ok() ? bias_class(P.bias.scalar(b, h, j)) : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kFixU; ++u) {
+            const int jc = min(j0 + u * R, P.nk - 1);
+            load8<T>(P.v.row<T>(b, h, jc) + c0, v8[u]);
+            if constexpr (VM) load8<T>(P.vmul.row<T>(b, h, jc) + c0, m8[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kFixU; ++u) {
+            if (cls[u] == 1 && P.km.keep(b, j0 + u * R)) ++n1;
+            if (cls[u] != 0) continue;
+            ++n0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if constexpr (VM) acc[e] += round_to<T>(v8[u][e] * m8[u][e]);
+                else acc[e] += v8[u][e];
+            }
+        }
+    }
+}
+
 // Finish the rows an MFMA forward left fully masked (their lse holds NaN), one workgroup per
 // (b, query head).  Every key of bias class 0 is masked for such a row (else the row would
 // hold a normal entry), so its class-1 entries are all bias-class-0 keys plus its own
@@ -206,27 +247,9 @@ __global__ __launch_bounds__(kFixThreads) void k_fwd_fixup(PassDev P) {
     // S0 and the counts of bias-class-0 and unmasked bias-class-1 keys
     const int slot = tid / LPR, c0 = (tid % LPR) * 8;
     float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
     int n0 = 0, n1 = 0;
-#pragma unroll 4
-    for (int j = slot; j < P.nk; j += R) {
-        const int cls = P.bias.ok() ? bias_class(P.bias.scalar(b, h, j)) : 0;
-        if (cls == 1 && P.km.keep(b, j)) ++n1;
-        if (cls != 0) continue;
-        ++n0;
-        float v8[8];
-        load8<T>(P.v.row<T>(b, h, j) + c0, v8);
-        if (P.vmul.ok()) {
-            float m8[8];
-            load8<T>(P.vmul.row<T>(b, h, j) + c0, m8);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] += round_to<T>(v8[e] * m8[e]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] += v8[e];
-        }
-    }
+    if (P.vmul.ok()) fixup_s0<T, D, true>(P, b, h, slot, c0, acc, n0, n1);
+    else fixup_s0<T, D, false>(P, b, h, slot, c0, acc, n0, n1);
     __shared__ float sS[R][D];
     __shared__ int sN[R][2];
     __shared__ float sT[D];
@@ -249,6 +272,42 @@ __global__ __launch_bounds__(kFixThreads) void k_fwd_fixup(PassDev P) {
     }
     __syncthreads();
     const int N0 = sCnt[0], N1 = sCnt[1];
+
+    if constexpr (sizeof(T) == 2) {
+        if (N1 == 0 && !P.ey.ok()) {
+            // no unmasked bias-class-1 key: every fully-masked row is S0 / N0.  Round it once,
+            // then each thread finds its rows (their lse loaded before any store) and copies it
+            constexpr int RB = 8;
+            __shared__ __attribute__((aligned(16))) uint32_t sRow[D / 2];
+            if (tid < D / 2) {
+                const float inv = N0 > 0 ? 1.f / (float)N0 : NAN;
+                float y0 = sT[2 * tid] * inv, y1 = sT[2 * tid + 1] * inv;
+                asm volatile("" : "+v"(y0), "+v"(y1));  // round the fp32 products, then convert
+                sRow[tid] = pack2<T>(y0, y1);
+            }
+            __syncthreads();
+            const float fill = N0 > 0 ? -FLT_MAX : -INFINITY;
+            for (int i0 = tid; i0 < P.nq; i0 += kFixThreads * RB) {
+                bool dg[RB];
+#pragma unroll
+                for (int u = 0; u < RB; ++u) {
+                    const int i = i0 + u * kFixThreads;
+                    dg[u] = i < P.nq && isnan(*P.lse.row<float>(b, h, i));
+                }
+#pragma unroll
+                for (int u = 0; u < RB; ++u) {
+                    if (!dg[u]) continue;
+                    const int i = i0 + u * kFixThreads;
+                    T* o = P.out.wrow<T>(b, h, i);
+#pragma unroll
+                    for (int c = 0; c < D / 4; ++c)
+                        *reinterpret_cast<u32x2_t*>(o + 4 * c) = *reinterpret_cast<const u32x2_t*>(&sRow[2 * c]);
+                    *P.lse.wrow<float>(b, h, i) = fill;
+                }
+            }
+            return;
+        }
+    }
 
     // each wave finds its fully-masked rows 64 at a time and writes them, lanes as columns
     const int w = tid / 64, lane = tid % 64;
