@@ -483,7 +483,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_partial_grp(DecodeDev D) {
 // the merged state of the cached positions, part the raw q.k of the new position, vnew its
 // value and bnew its bias (the deeper level's step results).
 template <typename T>
-__device__ __forceinline__ void dec_finish(const DecodeDev& D, const DecLevelDev& L, int b, int h,
+__device__ __forceinline__ float dec_finish(const DecodeDev& D, const DecLevelDev& L, int b, int h,
                                            int hh, int lane, bool final_level, int n, float mm,
                                            float ll, float (&acc)[4], float part,
                                            const float (&vnew)[4], float bnew, float* s_msg2,
@@ -538,17 +538,19 @@ __device__ __forceinline__ void dec_finish(const DecodeDev& D, const DecLevelDev
         for (int r = 0; r < L.out_rep; ++r) L.out.wrow<T>(b, h * L.out_rep + r, slot)[d] = from_f<T>(o);
         s_msg2[hh * dim + d] = round_to<T>(o);
     }
+    // the value the lse slot now holds (its dtype's rounding; every lane computes it), which
+    // the next level's cached bias will hold
+    float stored = lse_v;
+    if (L.lse.ok())
+        stored = L.lse.dtype == PA_F32 ? lse_v
+                 : L.lse.dtype == PA_F16 ? (float)(f16)lse_v : (float)(bf16)lse_v;
     if (lane == 0) {
-        float stored = lse_v;
-        if (L.lse.ok()) {
+        if (L.lse.ok())
             for (int r = 0; r < L.lse_rep; ++r)
                 store_any(L.lse.p, L.lse.dtype, L.lse.idx(b, h * L.lse_rep + r, slot), lse_v);
-            // the value the slot now holds (its dtype's rounding), without reading it back
-            stored = L.lse.dtype == PA_F32 ? lse_v
-                     : L.lse.dtype == PA_F16 ? (float)(f16)lse_v : (float)(bf16)lse_v;
-        }
-        s_lse2[hh] = stored;  // the value the next level's cached bias will hold
+        s_lse2[hh] = stored;
     }
+    return stored;
 }
 
 // merge the chunk partials of one (level, head): running max, sum and sum p v.  The chunk
@@ -670,7 +672,40 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_combine(DecodeDev D) {
     }
     __syncthreads();
 
-    // phase 2: the levels in order
+    // phase 2: the levels in order.  With one level head per KV group at every level (no GQA)
+    // the chain is one wave's work: the deeper level's result stays in that wave (each lane
+    // reads back only the features it wrote itself; the lse, uniform, is returned to every
+    // lane), with no workgroup barrier or LDS copy per level.
+    bool single = nitems <= nfit;
+    for (int t = 0; t < D.order; ++t) single = single && D.L[t].rep == 1;
+    if (single) {
+        if (wave != 0) return;  // no barrier below
+        float vprev[4] = {0.f, 0.f, 0.f, 0.f}, lprev = 0.f;
+        for (int t = 0; t < D.order; ++t) {
+            const DecLevelDev& L = D.L[t];
+            const bool deepest = (t == 0), final_level = (t == D.order - 1);
+            const float* st = s_st + t * ist;  // item t: level t's only head
+            float acc[4], vnew[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = lane + 64 * e;
+                acc[e] = d < dim ? st[4 + d] : 0.f;
+                const float vr = d < dim ? st[4 + dim + d] : 0.f;
+                vnew[e] = d >= dim ? 0.f
+                          : deepest ? vr
+                          : final_level ? vprev[e]
+                          : round_to<T>(vr * vprev[e]);
+            }
+            lprev = dec_finish<T>(D, L, b, g, 0, lane, final_level, n, st[0], st[1], acc, st[2],
+                                  vnew, deepest ? 0.f : lprev, s_msg2, s_lse2);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {  // this lane's own features of the result
+                const int d = lane + 64 * e;
+                vprev[e] = d < dim ? s_msg2[d] : 0.f;
+            }
+        }
+        return;
+    }
     int prev_rep = 1, base = 0;
     for (int t = 0; t < D.order; ++t) {
         const DecLevelDev& L = D.L[t];
