@@ -26,9 +26,105 @@
 namespace pa {
 
 constexpr int kF32BN = 32;  // keys per tile
+#ifndef PA_F32_SPLIT
+#define PA_F32_SPLIT 1  // small grids: the forward split over the keys (k_mfma_fwd_f32_split)
+#endif
 
 __device__ __forceinline__ f32x16_t mfma_32x32x2(float a, float b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// One wave's online-softmax state for its 32 queries: O^T accumulators, the running max (log2
+// units, shared by the lane pair) and the lane's partial sum.
+template <int D>
+struct F32Acc {
+    f32x16_t o[D / 32];
+    float m, l;
+};
+
+// One 32-key tile (rows j0 .. j0 + 31 staged at sK / sV with row stride D + 1, key term sB):
+// S^T = K Q^T, the softmax update, O^T += V^T P^T.
+template <int D>
+__device__ __forceinline__ void f32_tile(F32Acc<D>& a, const float (&qf)[D / 2], const float* sK,
+                                         const float* sV, const float* sB, int j0, int qi, int col,
+                                         int hh, const PassDev& P, bool sc, bool causal) {
+    constexpr int RS = D + 1;
+    f32x16_t s = zero16();
+#pragma unroll
+    for (int st = 0; st < D / 2; ++st) s = mfma_32x32x2(sK[col * RS + 2 * st + hh], qf[st], s);
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int jj = 8 * (r / 4) + 4 * hh + (r % 4);
+        float y = s[r] * P.scale;
+        if (sc) y = softclamp_f(y, P.softclamp);
+        float t = y * kLog2e + sB[jj];
+        if (causal && j0 + jj > qi) t = -INFINITY;
+        s[r] = t;
+        tmax = fmaxf(tmax, t);
+    }
+    const float mnew = fmaxf(a.m, xhalf_max(tmax));
+    if (mnew > a.m) {
+        const float c = a.m == -INFINITY ? 0.f : fast_exp2(a.m - mnew);
+        a.l *= c;
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) a.o[x][r] *= c;
+        a.m = mnew;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float p = a.m == -INFINITY ? 0.f : fast_exp2(s[r] - a.m);
+        s[r] = p;
+        a.l += p;
+    }
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int jj = 8 * (r / 4) + 4 * hh + (r % 4);
+            a.o[x] = mfma_32x32x2(sV[jj * RS + 32 * x + col], s[r], a.o[x]);
+        }
+}
+
+// The 32 queries' outputs, lse (NaN for a row left fully masked, for k_fwd_fixup) and the
+// module epilogue.
+template <int D>
+__device__ __forceinline__ void f32_store(const F32Acc<D>& a, const PassDev& P, int b, int h,
+                                          int qi, int hh) {
+    const float lt = xhalf_sum(a.l);
+    if (qi >= P.nq) return;
+    const bool degenerate = !(lt > 0.f) || !P.qm.keep(b, qi);
+    const float inv = degenerate ? 0.f : 1.f / lt;
+    float* orow = P.out.wrow<float>(b, h, qi);
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * x + 8 * g + 4 * hh;
+            const float4 v = make_float4(a.o[x][4 * g] * inv, a.o[x][4 * g + 1] * inv,
+                                         a.o[x][4 * g + 2] * inv, a.o[x][4 * g + 3] * inv);
+            *reinterpret_cast<float4*>(orow + d) = v;
+            if (P.ey.ok()) {
+                float* yrow = P.ey.wrow<float>(b, h, qi);
+                yrow[d] = epi_y<float>(P, b, h, qi, d, v.x);
+                yrow[d + 1] = epi_y<float>(P, b, h, qi, d + 1, v.y);
+                yrow[d + 2] = epi_y<float>(P, b, h, qi, d + 2, v.z);
+                yrow[d + 3] = epi_y<float>(P, b, h, qi, d + 3, v.w);
+            }
+        }
+    if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (a.m + log2f(lt)) * kLn2;
+}
+
+// Q[qi][2s + hh] of the lane's query (zeros past the last query)
+template <int D>
+__device__ __forceinline__ void f32_load_q(const PassDev& P, int b, int h, int qi, int hh,
+                                           float (&qf)[D / 2]) {
+    const bool qrow = qi < P.nq;
+    const float* qr = P.q.row<float>(b, h, qrow ? qi : 0);
+#pragma unroll
+    for (int s = 0; s < D / 2; ++s) qf[s] = qrow ? qr[2 * s + hh] : 0.f;
 }
 
 template <int D>
@@ -51,18 +147,14 @@ __global__ __launch_bounds__(256) void k_mfma_fwd_f32(PassDev P) {
     const int col = lane & 31, hh = lane >> 5;
     const int q0 = qb * BM + w * 32;
     const int qi = q0 + col;
-    const bool qrow = qi < P.nq;
 
     float qf[D / 2];  // Q[qi][2s + hh]
-    {
-        const float* qr = P.q.row<float>(b, h, qrow ? qi : 0);
+    f32_load_q<D>(P, b, h, qi, hh, qf);
+    F32Acc<D> a;
 #pragma unroll
-        for (int s = 0; s < D / 2; ++s) qf[s] = qrow ? qr[2 * s + hh] : 0.f;
-    }
-    f32x16_t o[D / 32];
-#pragma unroll
-    for (int x = 0; x < D / 32; ++x) o[x] = zero16();
-    float m = -INFINITY, l = 0.f;  // running max (log2 units, shared by the lane pair), partial sum
+    for (int x = 0; x < D / 32; ++x) a.o[x] = zero16();
+    a.m = -INFINITY;
+    a.l = 0.f;
 
     const bool sc = P.softclamp > 0.f, has_vmul = P.vmul.ok(), has_bias = P.bias.ok();
     const int kend = causal ? min(P.nk, qb * BM + BM) : P.nk;
@@ -129,70 +221,147 @@ __global__ __launch_bounds__(256) void k_mfma_fwd_f32(PassDev P) {
         store_tile();
         __syncthreads();
         if (j0 + kF32BN < kend) load_tile(j0 + kF32BN);
-        if (j0 < wave_kend) {  // wave-uniform: the causal limit of this wave's queries
-            f32x16_t s = zero16();
-#pragma unroll
-            for (int st = 0; st < D / 2; ++st) s = mfma_32x32x2(sK[col * RS + 2 * st + hh], qf[st], s);
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int jj = 8 * (r / 4) + 4 * hh + (r % 4);
-                float y = s[r] * P.scale;
-                if (sc) y = softclamp_f(y, P.softclamp);
-                float t = y * kLog2e + sB[jj];
-                if (causal && j0 + jj > qi) t = -INFINITY;
-                s[r] = t;
-                tmax = fmaxf(tmax, t);
-            }
-            const float mnew = fmaxf(m, xhalf_max(tmax));
-            if (mnew > m) {
-                const float c = m == -INFINITY ? 0.f : fast_exp2(m - mnew);
-                l *= c;
-#pragma unroll
-                for (int x = 0; x < D / 32; ++x)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[x][r] *= c;
-                m = mnew;
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = m == -INFINITY ? 0.f : fast_exp2(s[r] - m);
-                s[r] = p;
-                l += p;
-            }
-#pragma unroll
-            for (int x = 0; x < D / 32; ++x)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int jj = 8 * (r / 4) + 4 * hh + (r % 4);
-                    o[x] = mfma_32x32x2(sV[jj * RS + 32 * x + col], s[r], o[x]);
-                }
-        }
+        if (j0 < wave_kend)  // wave-uniform: the causal limit of this wave's queries
+            f32_tile<D>(a, qf, sK, sV, sB, j0, qi, col, hh, P, sc, causal);
         __syncthreads();
     }
+    f32_store<D>(a, P, b, h, qi, hh);  // no barriers below
+}
 
-    const float lt = xhalf_sum(l);
-    if (!qrow) return;  // no barriers below
-    const bool degenerate = !(lt > 0.f) || !P.qm.keep(b, qi);
-    const float inv = degenerate ? 0.f : 1.f / lt;
-    float* orow = P.out.wrow<float>(b, h, qi);
+// Split over the keys, for grids too small to occupy the chip (config 1: 8 heads x 1024
+// queries is 256 blocks of 32 queries): NS waves share one 32-query block, wave w taking key
+// tiles w, w + NS, ...  Each wave stages its own tiles in its own LDS region (wave-level order
+// only: a wave's LDS operations complete in order), keeps its own softmax state, and after a
+// workgroup barrier leaves (m, l, O) in its region; wave 0 merges the NS states (scaled by
+// 2^(m_w - max m)) and stores.
+template <int D, int NS>
+__global__ __launch_bounds__(64 * NS) void k_mfma_fwd_f32_split(PassDev P) {
+    constexpr int RS = D + 1;
+    constexpr int TILE = 2 * kF32BN * RS + kF32BN;  // K, V rows and the key term
+    static_assert(TILE >= (D / 32) * 16 * 64 + 2 * 64, "a wave's region holds its state");
+    __shared__ float sT[NS][TILE];
+    const int lane = threadIdx.x & 63, w = wave_id();
+    float* sK = sT[w];
+    float* sV = sK + kF32BN * RS;
+    float* sB = sV + kF32BN * RS;
+    const bool causal = P.causal != 0;
+    const int nqb = (P.nq + 31) / 32;
+    int bh, rank;
+    if (causal) block_order<true>(nqb, bh, rank);
+    else block_order<false>(nqb, bh, rank);
+    const int qb = causal ? nqb - 1 - rank : rank;
+    const int h = bh % P.heads, b = bh / P.heads;
+    const int col = lane & 31, hh = lane >> 5;
+    const int q0 = qb * 32, qi = q0 + col;
+
+    float qf[D / 2];
+    f32_load_q<D>(P, b, h, qi, hh, qf);
+    F32Acc<D> a;
 #pragma unroll
-    for (int x = 0; x < D / 32; ++x)
+    for (int x = 0; x < D / 32; ++x) a.o[x] = zero16();
+    a.m = -INFINITY;
+    a.l = 0.f;
+    const bool sc = P.softclamp > 0.f, has_vmul = P.vmul.ok(), has_bias = P.bias.ok();
+    const int kend = causal ? min(P.nk, q0 + 32) : P.nk;
+
+    constexpr int NL = kF32BN * (D / 4) / 64;  // 16-byte loads per lane and tensor
+    float4 rk[NL], rv[NL];
+    float rb = 0.f;
+    auto load_tile = [&](int j0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d = 32 * x + 8 * g + 4 * hh;
-            const float4 v = make_float4(o[x][4 * g] * inv, o[x][4 * g + 1] * inv,
-                                         o[x][4 * g + 2] * inv, o[x][4 * g + 3] * inv);
-            *reinterpret_cast<float4*>(orow + d) = v;
-            if (P.ey.ok()) {
-                float* yrow = P.ey.wrow<float>(b, h, qi);
-                yrow[d] = epi_y<float>(P, b, h, qi, d, v.x);
-                yrow[d + 1] = epi_y<float>(P, b, h, qi, d + 1, v.y);
-                yrow[d + 2] = epi_y<float>(P, b, h, qi, d + 2, v.z);
-                yrow[d + 3] = epi_y<float>(P, b, h, qi, d + 3, v.w);
+        for (int i = 0; i < NL; ++i) {
+            const int e = lane + 64 * i, jj = e / (D / 4), c4 = (e % (D / 4)) * 4, j = j0 + jj;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (j < P.nk) {
+                kv = *reinterpret_cast<const float4*>(P.k.row<float>(b, h, j) + c4);
+                vv = *reinterpret_cast<const float4*>(P.v.row<float>(b, h, j) + c4);
+                if (has_vmul) {
+                    const float4 mm = *reinterpret_cast<const float4*>(P.vmul.row<float>(b, h, j) + c4);
+                    vv.x *= mm.x;
+                    vv.y *= mm.y;
+                    vv.z *= mm.z;
+                    vv.w *= mm.w;
+                }
+            }
+            rk[i] = kv;
+            rv[i] = vv;
+        }
+        if (lane < kF32BN) {
+            const int j = j0 + lane;
+            rb = -INFINITY;
+            if (j < P.nk && P.km.keep(b, j)) {
+                const float x = has_bias ? P.bias.scalar(b, h, j) : 0.f;
+                rb = bias_class(x) == 0 ? x * kLog2e : -INFINITY;
             }
         }
-    if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (m + log2f(lt)) * kLn2;
+    };
+    auto store_tile = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int e = lane + 64 * i, jj = e / (D / 4), c4 = (e % (D / 4)) * 4;
+            float* dk = sK + jj * RS + c4;
+            float* dv = sV + jj * RS + c4;
+            dk[0] = rk[i].x;
+            dk[1] = rk[i].y;
+            dk[2] = rk[i].z;
+            dk[3] = rk[i].w;
+            dv[0] = rv[i].x;
+            dv[1] = rv[i].y;
+            dv[2] = rv[i].z;
+            dv[3] = rv[i].w;
+        }
+        if (lane < kF32BN) sB[lane] = rb;
+    };
+    // a wave's own LDS writes before its reads (and its reads before the next tile's writes)
+    auto wave_sync = []() __attribute__((always_inline)) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+    };
+
+    const int ntiles = (kend + kF32BN - 1) / kF32BN;
+    if (w < ntiles) load_tile(w * kF32BN);
+    for (int t = w; t < ntiles; t += NS) {  // wave-uniform
+        wave_sync();
+        store_tile();
+        wave_sync();
+        if (t + NS < ntiles) load_tile((t + NS) * kF32BN);
+        f32_tile<D>(a, qf, sK, sV, sB, t * kF32BN, qi, col, hh, P, sc, causal);
+    }
+
+    // every wave's state into its region, then wave 0 merges
+    __syncthreads();
+    {
+        float* so = sT[w];
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) so[(x * 16 + r) * 64 + lane] = a.o[x][r];
+        so[(D / 32) * 16 * 64 + lane] = a.m;
+        so[(D / 32) * 16 * 64 + 64 + lane] = a.l;
+    }
+    __syncthreads();
+    if (w != 0) return;  // no barriers below
+    float mt = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < NS; ++v) mt = fmaxf(mt, sT[v][(D / 32) * 16 * 64 + lane]);
+    F32Acc<D> r;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) r.o[x] = zero16();
+    r.m = mt;
+    r.l = 0.f;
+#pragma unroll
+    for (int v = 0; v < NS; ++v) {
+        const float* so = sT[v];
+        const float mv = so[(D / 32) * 16 * 64 + lane];
+        const float c = mv == -INFINITY ? 0.f : fast_exp2(mv - mt);
+        r.l += so[(D / 32) * 16 * 64 + 64 + lane] * c;
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) r.o[x][q] += so[(x * 16 + q) * 64 + lane] * c;
+    }
+    f32_store<D>(r, P, b, h, qi, hh);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -532,8 +701,18 @@ bool mfma_fwd_f32_supported(const PassDev& P) {
 }
 
 void launch_mfma_fwd_f32(const PassDev& P, hipStream_t s) {
-    // waves per workgroup: the most that still give the grid two workgroups per CU
     const int units = P.batch * P.heads;
+    // grids of fewer than 512 blocks of 32 queries leave most of the chip idle: split the keys
+    // of a block over 4 waves (the kernel's 332-512 registers allow one wave per SIMD), when
+    // there are that many key tiles
+    const int blocks32 = units * ((P.nq + 31) / 32), tiles = (P.nk + kF32BN - 1) / kF32BN;
+    if (PA_F32_SPLIT && blocks32 < 512 && tiles >= 4) {
+        ProfScope ps("mfma_fwd_f32", s);
+        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_fwd_f32_split<64, 4>), dim3(blocks32), dim3(64 * 4), 0, s, P);
+        else hipLaunchKernelGGL((k_mfma_fwd_f32_split<128, 4>), dim3(blocks32), dim3(64 * 4), 0, s, P);
+        return;
+    }
+    // waves per workgroup: the most that still give the grid two workgroups per CU
     int nw = 4;
     while (nw > 1 && (int64_t)units * ((P.nq + 32 * nw - 1) / (32 * nw)) < 512) nw >>= 1;
     const dim3 grid(units * ((P.nq + 32 * nw - 1) / (32 * nw)));
