@@ -269,3 +269,16 @@ def test_pass_multi_block_causal_grids(heads, n, d):
     bias = bias + randn((1, heads, n), torch.float32, 24)
     check(run_pass(q, k, v, causal=True), dtype, f"grid h={heads} n={n} d={d}")
     check(run_pass(q, k, v, bias=bias, causal=True), dtype, f"grid h={heads} n={n} d={d} bias")
+
+
+@param("B,H", ((4, 8), (4, 16)))
+@param("causal", (False, True))
+def test_f32_forward_multiwave_workgroups(B, H, causal):
+    """fp32 forwards whose grids take two (4 x 8 heads) and four (4 x 16) 32-query waves per
+    workgroup sharing each key tile; smaller grids split the keys over the waves instead, and
+    the other tests cover those."""
+    q = randn((B, H, 1024, 64), torch.float32, 81)
+    k = randn((B, H, 1024, 64), torch.float32, 82)
+    v = randn((B, H, 1024, 64), torch.float32, 83)
+    check(run_pass(q, k, v, causal=causal, grads=False), torch.float32,
+          f"fp32 multi-wave B={B} H={H} causal={causal}")
