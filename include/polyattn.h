@@ -71,6 +71,9 @@ extern "C" {
 
 /* pa_pass.flags */
 #define PA_FLAG_MAY_DEGENERATE 1   /* masks or -FLT_MAX biases may leave rows fully masked */
+#define PA_FLAG_DISCARD_OUT    4   /* pa_poly_order2_fwd, first pass: the caller does not read its
+                                      out and lse, which the one-launch path then leaves unwritten
+                                      (the buffers are still required) */
 /* pa_pass_grad.accumulate bits: add into the gradient buffer instead of overwriting it */
 #define PA_ACC_DQ    1
 #define PA_ACC_DK    2

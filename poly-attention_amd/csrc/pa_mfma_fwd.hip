@@ -1206,7 +1206,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_order2_short(PassDev P1
     if (run1) {
         W1 wv;
         short_block<T>(wv, P1, 32 * p, lane, q2r, sK1[slot], sVt1[slot], nullptr, SOFTCLAMP);
-        lse = short_finish<T>(wv, P1, b, h, live, ow);
+        lse = short_finish<T>(wv, P1, b, h, live && !(P1.flags & PA_FLAG_DISCARD_OUT), ow);
     }
     {
         const bool keep = run1 && row < n2;

@@ -30,6 +30,7 @@ PA_DECODE_SCRATCH_BYTES = 16 << 20
 
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 PA_FLAG_MAY_DEGENERATE = 1
+PA_FLAG_DISCARD_OUT = 4
 PA_EPI_ROOT_SIGMOID = 1
 PA_NORM_Q = 1
 PA_NORM_K = 2

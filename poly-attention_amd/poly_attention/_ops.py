@@ -28,6 +28,7 @@ from . import _lib
 from ._lib import (
     DTYPE_CODE,
     PA_EPI_ROOT_SIGMOID,
+    PA_FLAG_DISCARD_OUT,
     PA_FLAG_MAY_DEGENERATE,
     PA_NORM_K,
     PA_NORM_Q,
@@ -1055,13 +1056,14 @@ def _split_heads(t: Tensor, heads, d: int):
 
 
 def order2_forward(q1, q2, q3, v3, key_mask, causal, softclamp, scale, epilogue=None,
-                   norms=None):
+                   norms=None, keep_inner=True):
     """The two forward passes of the order-2 chain (poly_attention.py:48-116 with q2 as both
     the pass-1 queries and the pass-2 keys); ``key_mask`` masks the keys of both passes.
     Returns (out, lse, lse23, msg), and with ``epilogue`` = (root, gate, root_sigmoid) the
     modules' gated output y (computed in pass 2's store) as a fifth result.  ``norms`` =
     ((w1, eps1), (w2, eps2), (w3, eps3)): q1, q2, q3 are raw and the passes apply their
-    RMSNorms on load (qk_norms_fusable; no gradient)."""
+    RMSNorms on load (qk_norms_fusable; no gradient).  ``keep_inner=False``: the caller does
+    not read lse23 and msg, which the one-launch path then leaves unwritten."""
     degenerate = key_mask is not None
     n1, n2, n3 = norms if norms is not None else (None, None, None)
     if key_mask is None and _padded_dim(q2) is None:
@@ -1073,6 +1075,8 @@ def order2_forward(q1, q2, q3, v3, key_mask, causal, softclamp, scale, epilogue=
         p2, res, keep2 = _pass_prepare(
             q1, q2, msg, None, lse23, None, None, causal, softclamp, scale, False, epilogue,
             qk_norm=(n1, n2) if norms is not None else None)
+        if not keep_inner:
+            p1.flags |= PA_FLAG_DISCARD_OUT
         with _device(q2):
             _lib.check(_lib.load().pa_poly_order2_fwd(ctypes.byref(p1), ctypes.byref(p2),
                                                       _stream(q2)), "pa_poly_order2_fwd")
@@ -1193,7 +1197,8 @@ def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence
                causal: bool, softclamp: Optional[float], scale: float,
                query_mask: Optional[Tensor] = None,
                key_masks: Optional[Sequence[Optional[Tensor]]] = None,
-               may_degenerate: bool = False, epilogue=None, qk_norms=None):
+               may_degenerate: bool = False, epilogue=None, qk_norms=None,
+               keep_levels: bool = True):
     """Order-n poly attention through HIP passes.
 
     q_left[l] . q_right[l] are the scores of level l (l = 0 is q1 . q2); vs are the values
@@ -1202,7 +1207,9 @@ def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence
     root_sigmoid): the modules' root-value / gate epilogue applied to out (fused into the
     final pass on the order-2 chain's path, else in torch).  ``qk_norms`` = the (weight, eps)
     RMSNorms of q1, q2, q3 of an order-2 chain whose inputs are not normalised yet: applied as
-    the passes load them (no gradient; the caller checks qk_norms_fusable).
+    the passes load them (no gradient; the caller checks qk_norms_fusable); with them
+    ``keep_levels=False`` says the caller reads only out: lses and msgs come back as None, and
+    the one-launch path does not write the inner level.
     """
     n = len(q_left)
     assert len(q_right) == n and len(vs) == n - 1 and n >= 2
@@ -1214,11 +1221,12 @@ def poly_chain(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs: Sequence
         assert all(m is None for m in key_masks)
         fuse = epilogue is not None and _epilogue_fusable(epilogue, q_left[0], q_left[0].shape[1])
         res = order2_forward(q_left[0], q_left[1], q_right[1], vs[0], None, bool(causal),
-                             softclamp, float(scale), epilogue if fuse else None, norms=qk_norms)
+                             softclamp, float(scale), epilogue if fuse else None, norms=qk_norms,
+                             keep_inner=keep_levels)
         out = res[4] if fuse else res[0]
         if epilogue is not None and not fuse:
             out = apply_epilogue(out, epilogue)
-        return out, [res[2]], [res[3]]
+        return out, ([res[2]] if keep_levels else None), ([res[3]] if keep_levels else None)
     if _chain_fusable(q_left, q_right, vs, query_mask, key_masks, may_degenerate):
         root = gate = None
         root_sigmoid = False

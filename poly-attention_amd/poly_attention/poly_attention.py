@@ -545,7 +545,8 @@ class Order2PolyAttention(Module):
             out, lses, msgs = _ops.poly_chain(
                 [q1r, q2r_left], [q2r_right, q3r], [v3], causal=self.causal,
                 softclamp=self.softclamp_value, scale=self.scale, query_mask=mask,
-                key_masks=list(context_mask), epilogue=epilogue, qk_norms=qk_norms)
+                key_masks=list(context_mask), epilogue=epilogue, qk_norms=qk_norms,
+                keep_levels=return_cache)
             new_cache = None
             if return_cache:
                 lse23 = repeat_kv(lses[0][:, :, :, None], rep)[..., 0]

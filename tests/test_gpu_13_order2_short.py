@@ -89,3 +89,23 @@ def test_order2_one_launch_with_epilogue(root_sigmoid):
     assert len(got) == len(ref) == 5
     for name, a, b in zip(("out", "lse", "lse23", "msg", "y"), got, ref):
         assert torch.equal(a, b), f"{name}: max diff {(a.float() - b.float()).abs().max().item()}"
+
+
+def test_order2_one_launch_discarding_the_inner_level():
+    """PA_FLAG_DISCARD_OUT on the first pass (the modules' inference path, which reads only
+    out): the one launch skips writing msg and lse23, and out / lse keep their bits."""
+    from poly_attention import _lib, _ops
+
+    d = dev()
+    g = torch.Generator().manual_seed(13)
+    q1, q2, q3, v3 = _views(3, 5, 5, 64, torch.bfloat16, g)
+    ws = [(1 + 0.3 * torch.randn(64, generator=g)).to(torch.bfloat16).to(d) for _ in range(3)]
+    nw = tuple(zip(ws, (1e-6, 1e-6, 1e-6)))
+    with torch.no_grad():
+        ref = _two_calls(q1, q2, q3, v3, None, 0.125, None, nw)
+        with _lib.KernelProfile() as prof:
+            got = _ops.order2_forward(q1, q2, q3, v3, None, False, None, 0.125, norms=nw,
+                                      keep_inner=False)
+    torch.cuda.synchronize()
+    assert prof.times.get("mfma_order2_short", (0, 0.0))[0] == 1, prof.times
+    assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])
