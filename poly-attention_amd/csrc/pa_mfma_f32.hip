@@ -374,11 +374,15 @@ struct F32Rows {
     static constexpr int NL = kF32BN * (D / 4) / 64;  // 16-byte loads per thread (one wave)
     float4 a[NL], c[NL];
     __device__ __forceinline__ void load(const DView& va, const DView& vc, const DView& vm, int b,
-                                         int h, int r0, int n) {
+                                         int h, int r0, int n, int t0 = -1, int ts = 0) {
         const int nload = kF32BN * (D / 4);
+        if (t0 < 0) {  // spread over the workgroup
+            t0 = threadIdx.x;
+            ts = blockDim.x;
+        }
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const int e = threadIdx.x + i * (int)blockDim.x;
+            const int e = t0 + i * ts;
             const int rr = e / (D / 4), c4 = (e % (D / 4)) * 4, r = r0 + rr;
             float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
             if (e < nload && r < n) {
@@ -396,12 +400,16 @@ struct F32Rows {
             c[i] = y;
         }
     }
-    __device__ __forceinline__ void store(float* sa, float* sc) const {
+    __device__ __forceinline__ void store(float* sa, float* sc, int t0 = -1, int ts = 0) const {
         constexpr int RS = D + 1;
         const int nload = kF32BN * (D / 4);
+        if (t0 < 0) {
+            t0 = threadIdx.x;
+            ts = blockDim.x;
+        }
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const int e = threadIdx.x + i * (int)blockDim.x;
+            const int e = t0 + i * ts;
             if (e < nload) {
                 const int rr = e / (D / 4), c4 = (e % (D / 4)) * 4;
                 float* da = sa + rr * RS + c4;
@@ -439,6 +447,79 @@ __device__ __forceinline__ void store4(float* p, float4 v, bool acc) {
 
 // dQ, query-major: per key tile S^T = K Q^T and dP^T = V dO^T (lane = query), dS, then
 // dQ^T += K^T dS^T with dS entering as B from the score registers.
+// dQ of one 32-key tile (rows j0 .. j0 + 31 staged at sK / sV, key term sB): S = Q K^T and
+// dP = dO V^T (lane = query), dS = P (dP - D), dQ^T += K^T dS^T with dS entering as B.
+template <int D>
+__device__ __forceinline__ void f32_dq_tile(f32x16_t (&dq)[D / 32], const float (&qf)[D / 2],
+                                            const float (&of)[D / 2], const float* sK,
+                                            const float* sV, const float* sB, int j0, int qi,
+                                            int col, int hh, const PassDev& P, bool sc,
+                                            bool causal, float lse_l2, float dsum) {
+    constexpr int RS = D + 1;
+    f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+    for (int t = 0; t < D / 2; ++t) {
+        s = mfma_32x32x2(sK[col * RS + 2 * t + hh], qf[t], s);
+        dp = mfma_32x32x2(sV[col * RS + 2 * t + hh], of[t], dp);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int jj = 8 * (i / 4) + 4 * hh + (i % 4);
+        float y = s[i] * P.scale;
+        if (sc) y = softclamp_f(y, P.softclamp);
+        float t = y * kLog2e + sB[jj];
+        if (causal && j0 + jj > qi) t = -INFINITY;
+        const float p = fast_exp2(t - lse_l2);
+        s[i] = p * (dp[i] - dsum) * softclamp_grad(y, P.softclamp) * P.scale;
+    }
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int jj = 8 * (i / 4) + 4 * hh + (i % 4);
+            dq[x] = mfma_32x32x2(sK[jj * RS + 32 * x + col], s[i], dq[x]);
+        }
+}
+
+// dK / dV / dbias of one 32-query tile (rows i0 .. i0 + 31 of Q and dO at sQ / sO, their lse
+// (log2) and D at sL / sD) against the wave's 32 keys (lane = key).
+template <int D>
+__device__ __forceinline__ void f32_dkv_tile(f32x16_t (&dk)[D / 32], f32x16_t (&dv)[D / 32],
+                                             float& dbias, const float (&kf)[D / 2],
+                                             const float (&vf)[D / 2], const float* sQ,
+                                             const float* sO, const float* sL, const float* sD,
+                                             int i0, int kj, int col, int hh, const PassDev& P,
+                                             bool sc, bool causal, float bk) {
+    constexpr int RS = D + 1;
+    f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+    for (int t = 0; t < D / 2; ++t) {
+        s = mfma_32x32x2(sQ[col * RS + 2 * t + hh], kf[t], s);
+        dp = mfma_32x32x2(sO[col * RS + 2 * t + hh], vf[t], dp);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int ii = 8 * (i / 4) + 4 * hh + (i % 4);
+        float y = s[i] * P.scale;
+        if (sc) y = softclamp_f(y, P.softclamp);
+        float t = y * kLog2e + bk;
+        if (causal && i0 + ii < kj) t = -INFINITY;
+        const float p = fast_exp2(t - sL[ii]);
+        const float ds = p * (dp[i] - sD[ii]);
+        dbias += ds;
+        s[i] = p;
+        dp[i] = ds * softclamp_grad(y, P.softclamp) * P.scale;
+    }
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int ii = 8 * (i / 4) + 4 * hh + (i % 4);
+            dv[x] = mfma_32x32x2(sO[ii * RS + 32 * x + col], s[i], dv[x]);
+            dk[x] = mfma_32x32x2(sQ[ii * RS + 32 * x + col], dp[i], dk[x]);
+        }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void k_mfma_bwd_f32_dq(GradDev G) {
     constexpr int RS = D + 1;
@@ -492,31 +573,8 @@ __global__ __launch_bounds__(256) void k_mfma_bwd_f32_dq(GradDev G) {
             st.load(P.k, P.v, P.vmul, b, h, j0 + kF32BN, P.nk);
             if (tid < kF32BN) rb = key_term_l2(P, b, h, j0 + kF32BN + tid);
         }
-        if (j0 < wave_kend) {
-            f32x16_t s = zero16(), dp = zero16();
-#pragma unroll
-            for (int t = 0; t < D / 2; ++t) {
-                s = mfma_32x32x2(sK[col * RS + 2 * t + hh], qf[t], s);
-                dp = mfma_32x32x2(sV[col * RS + 2 * t + hh], of[t], dp);
-            }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int jj = 8 * (i / 4) + 4 * hh + (i % 4);
-                float y = s[i] * P.scale;
-                if (sc) y = softclamp_f(y, P.softclamp);
-                float t = y * kLog2e + sB[jj];
-                if (causal && j0 + jj > qi) t = -INFINITY;
-                const float p = fast_exp2(t - lse_l2);
-                s[i] = p * (dp[i] - dsum) * softclamp_grad(y, P.softclamp) * P.scale;
-            }
-#pragma unroll
-            for (int x = 0; x < D / 32; ++x)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int jj = 8 * (i / 4) + 4 * hh + (i % 4);
-                    dq[x] = mfma_32x32x2(sK[jj * RS + 32 * x + col], s[i], dq[x]);
-                }
-        }
+        if (j0 < wave_kend)
+            f32_dq_tile<D>(dq, qf, of, sK, sV, sB, j0, qi, col, hh, P, sc, causal, lse_l2, dsum);
         __syncthreads();
     }
     if (!qrow) return;
@@ -597,39 +655,242 @@ __global__ __launch_bounds__(256) void k_mfma_bwd_f32_dkv(GradDev G) {
             }
             __syncthreads();
             if (i0 + kF32BN < P.nq) load_rows(i0 + kF32BN);
-            if (!causal || i0 + kF32BN - 1 >= k0) {  // wave-uniform: some query reaches a key
-                f32x16_t s = zero16(), dp = zero16();
-#pragma unroll
-                for (int t = 0; t < D / 2; ++t) {
-                    s = mfma_32x32x2(sQ[col * RS + 2 * t + hh], kf[t], s);
-                    dp = mfma_32x32x2(sO[col * RS + 2 * t + hh], vf[t], dp);
-                }
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int ii = 8 * (i / 4) + 4 * hh + (i % 4);
-                    float y = s[i] * P.scale;
-                    if (sc) y = softclamp_f(y, P.softclamp);
-                    float t = y * kLog2e + bk;
-                    if (causal && i0 + ii < kj) t = -INFINITY;
-                    const float p = fast_exp2(t - sL[ii]);
-                    const float ds = p * (dp[i] - sD[ii]);
-                    dbias += ds;
-                    s[i] = p;
-                    dp[i] = ds * softclamp_grad(y, P.softclamp) * P.scale;
-                }
-#pragma unroll
-                for (int x = 0; x < D / 32; ++x)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int ii = 8 * (i / 4) + 4 * hh + (i % 4);
-                        dv[x] = mfma_32x32x2(sO[ii * RS + 32 * x + col], s[i], dv[x]);
-                        dk[x] = mfma_32x32x2(sQ[ii * RS + 32 * x + col], dp[i], dk[x]);
-                    }
-            }
+            if (!causal || i0 + kF32BN - 1 >= k0)  // wave-uniform: some query reaches a key
+                f32_dkv_tile<D>(dk, dv, dbias, kf, vf, sQ, sO, sL, sD, i0, kj, col, hh, P, sc,
+                                causal, bk);
             __syncthreads();
         }
     }
     dbias = xhalf_sum(dbias);
+    if (!krow) return;
+    const float* mr = P.vmul.ok() ? P.vmul.row<float>(b, h0, kj) : nullptr;
+    const float* vr = P.v.row<float>(b, h0, kj);
+    float* dkr = G.dk.wrow<float>(b, h0, kj);
+    float* dvr = G.dv.wrow<float>(b, h0, kj);
+    float* dmr = mr ? G.dvmul.wrow<float>(b, h0, kj) : nullptr;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * x + 8 * g + 4 * hh;
+            store4(dkr + d, make_float4(dk[x][4 * g], dk[x][4 * g + 1], dk[x][4 * g + 2], dk[x][4 * g + 3]),
+                   (G.accumulate & PA_ACC_DK) != 0);
+            float4 e = make_float4(dv[x][4 * g], dv[x][4 * g + 1], dv[x][4 * g + 2], dv[x][4 * g + 3]);
+            if (mr) {
+                const float4 m4 = *reinterpret_cast<const float4*>(mr + d);
+                const float4 v4 = *reinterpret_cast<const float4*>(vr + d);
+                store4(dmr + d, make_float4(e.x * v4.x, e.y * v4.y, e.z * v4.z, e.w * v4.w),
+                       (G.accumulate & PA_ACC_DVMUL) != 0);
+                e = make_float4(e.x * m4.x, e.y * m4.y, e.z * m4.z, e.w * m4.w);
+            }
+            store4(dvr + d, e, (G.accumulate & PA_ACC_DV) != 0);
+        }
+    if (hh == 0 && G.dbias.ok()) {
+        float* o = G.dbias.wrow<float>(b, h0, kj);
+        *o = dbias + ((G.accumulate & PA_ACC_DBIAS) ? *o : 0.f);
+    }
+}
+
+// The backward split like k_mfma_fwd_f32_split, for grids too small to occupy the chip: NS
+// waves share one 32-row block, each taking every NS-th tile into its own LDS region (wave-level
+// order only); after a workgroup barrier every wave leaves its partial sums in its region and
+// wave 0 adds them in wave order (deterministic) and stores.
+__device__ __forceinline__ void f32_wave_sync() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+}
+
+template <int D, int NS>
+__global__ __launch_bounds__(64 * NS) void k_mfma_bwd_f32_dq_split(GradDev G) {
+    constexpr int RS = D + 1;
+    constexpr int TILE = 2 * kF32BN * RS + kF32BN;
+    static_assert(TILE >= (D / 32) * 16 * 64, "a wave's region holds its partial dQ");
+    const PassDev& P = G.f;
+    __shared__ float sT[NS][TILE];
+    const int lane = threadIdx.x & 63, w = wave_id();
+    float* sK = sT[w];
+    float* sV = sK + kF32BN * RS;
+    float* sB = sV + kF32BN * RS;
+    const bool causal = P.causal != 0;
+    const int nqb = (P.nq + 31) / 32;
+    int bh, rank;
+    if (causal) block_order<true>(nqb, bh, rank);
+    else block_order<false>(nqb, bh, rank);
+    const int qb = causal ? nqb - 1 - rank : rank;
+    const int h = bh % P.heads, b = bh / P.heads;
+    const int col = lane & 31, hh = lane >> 5;
+    const int q0 = qb * 32, qi = q0 + col;
+    const bool qrow = qi < P.nq;
+    float qf[D / 2], of[D / 2];
+    {
+        const float* qr = P.q.row<float>(b, h, qrow ? qi : 0);
+        const float* orr = G.dout.row<float>(b, h, qrow ? qi : 0);
+#pragma unroll
+        for (int t = 0; t < D / 2; ++t) {
+            qf[t] = qrow ? qr[2 * t + hh] : 0.f;
+            of[t] = qrow ? orr[2 * t + hh] : 0.f;
+        }
+    }
+    const int64_t r = ((int64_t)b * P.heads + h) * P.nq + (qrow ? qi : 0);
+    const float lse_l2 = qrow ? G.ws_lse[r] * kLog2e : INFINITY;
+    const float dsum = qrow ? G.ws_D[r] : 0.f;
+    f32x16_t dq[D / 32];
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) dq[x] = zero16();
+    const bool sc = P.softclamp > 0.f;
+    const int kend = causal ? min(P.nk, q0 + 32) : P.nk;
+    const int ntiles = (kend + kF32BN - 1) / kF32BN;
+    F32Rows<D> st;
+    float rb = 0.f;
+    if (w < ntiles) {
+        st.load(P.k, P.v, P.vmul, b, h, w * kF32BN, P.nk, lane, 64);
+        if (lane < kF32BN) rb = key_term_l2(P, b, h, w * kF32BN + lane);
+    }
+    for (int t = w; t < ntiles; t += NS) {  // wave-uniform
+        f32_wave_sync();
+        st.store(sK, sV, lane, 64);
+        if (lane < kF32BN) sB[lane] = rb;
+        f32_wave_sync();
+        if (t + NS < ntiles) {
+            st.load(P.k, P.v, P.vmul, b, h, (t + NS) * kF32BN, P.nk, lane, 64);
+            if (lane < kF32BN) rb = key_term_l2(P, b, h, (t + NS) * kF32BN + lane);
+        }
+        f32_dq_tile<D>(dq, qf, of, sK, sV, sB, t * kF32BN, qi, col, hh, P, sc, causal, lse_l2,
+                       dsum);
+    }
+    __syncthreads();
+    {
+        float* so = sT[w];
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) so[(x * 16 + i) * 64 + lane] = dq[x][i];
+    }
+    __syncthreads();
+    if (w != 0 || !qrow) return;  // no barriers below
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float a = 0.f;
+#pragma unroll
+            for (int v = 0; v < NS; ++v) a += sT[v][(x * 16 + i) * 64 + lane];
+            dq[x][i] = a;
+        }
+    float* row = G.dq.wrow<float>(b, h, qi);
+    const bool acc = (G.accumulate & PA_ACC_DQ) != 0;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            store4(row + 32 * x + 8 * g + 4 * hh,
+                   make_float4(dq[x][4 * g], dq[x][4 * g + 1], dq[x][4 * g + 2], dq[x][4 * g + 3]), acc);
+}
+
+template <int D, int NS>
+__global__ __launch_bounds__(64 * NS) void k_mfma_bwd_f32_dkv_split(GradDev G) {
+    constexpr int RS = D + 1;
+    constexpr int TILE = 2 * kF32BN * RS + 2 * kF32BN;
+    static_assert(TILE >= 2 * (D / 32) * 16 * 64 + 64, "a wave's region holds its partial sums");
+    const PassDev& P = G.f;
+    __shared__ float sT[NS][TILE];
+    const int lane = threadIdx.x & 63, w = wave_id();
+    float* sQ = sT[w];
+    float* sO = sQ + kF32BN * RS;
+    float* sL = sO + kF32BN * RS;
+    float* sD = sL + kF32BN;
+    const bool causal = P.causal != 0;
+    const int nkb = (P.nk + 31) / 32;
+    int unit, kblk;
+    if (causal) block_order<true>(nkb, unit, kblk);
+    else block_order<false>(nkb, unit, kblk);
+    const int kh = unit % G.hk, b = unit / G.hk;
+    const int rep = P.heads / G.hk, h0 = kh * rep;
+    const int col = lane & 31, hh = lane >> 5;
+    const int k0 = kblk * 32, kj = k0 + col;
+    const bool krow = kj < P.nk;
+    float kf[D / 2], vf[D / 2];
+    {
+        const float* kr = P.k.row<float>(b, h0, krow ? kj : 0);
+        const float* vr = P.v.row<float>(b, h0, krow ? kj : 0);
+        const float* mr = P.vmul.ok() ? P.vmul.row<float>(b, h0, krow ? kj : 0) : nullptr;
+#pragma unroll
+        for (int t = 0; t < D / 2; ++t) {
+            kf[t] = krow ? kr[2 * t + hh] : 0.f;
+            vf[t] = krow ? vr[2 * t + hh] * (mr ? mr[2 * t + hh] : 1.f) : 0.f;
+        }
+    }
+    const float bk = key_term_l2(P, b, h0, kj);  // -inf past nk
+    f32x16_t dk[D / 32], dv[D / 32];
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x) {
+        dk[x] = zero16();
+        dv[x] = zero16();
+    }
+    float dbias = 0.f;
+    const bool sc = P.softclamp > 0.f;
+    // the query tiles of every query head of the group, from the block's first reachable tile
+    const int i_start = causal ? k0 : 0;
+    const int ntq = P.nq > i_start ? (P.nq - i_start + kF32BN - 1) / kF32BN : 0;
+    const int ntiles = ntq * rep;
+    const DView none = {nullptr, 0, 0, 0, 1, PA_F32};
+    F32Rows<D> st;
+    float rl = 0.f, rd = 0.f;
+    auto load_rows = [&](int t) __attribute__((always_inline)) {
+        const int h = h0 + t / ntq, i0 = i_start + (t % ntq) * kF32BN;
+        const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
+        st.load(P.q, G.dout, none, b, h, i0, P.nq, lane, 64);
+        if (lane < kF32BN) {
+            const int i = i0 + lane;
+            rl = i < P.nq ? G.ws_lse[row0 + i] * kLog2e : INFINITY;
+            rd = i < P.nq ? G.ws_D[row0 + i] : 0.f;
+        }
+    };
+    if (w < ntiles) load_rows(w);
+    for (int t = w; t < ntiles; t += NS) {  // wave-uniform
+        f32_wave_sync();
+        st.store(sQ, sO, lane, 64);
+        if (lane < kF32BN) {
+            sL[lane] = rl;
+            sD[lane] = rd;
+        }
+        f32_wave_sync();
+        const int i0 = i_start + (t % ntq) * kF32BN;
+        if (t + NS < ntiles) load_rows(t + NS);
+        f32_dkv_tile<D>(dk, dv, dbias, kf, vf, sQ, sO, sL, sD, i0, kj, col, hh, P, sc, causal, bk);
+    }
+    __syncthreads();
+    {
+        float* so = sT[w];
+#pragma unroll
+        for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                so[(x * 16 + i) * 64 + lane] = dk[x][i];
+                so[((D / 32 + x) * 16 + i) * 64 + lane] = dv[x][i];
+            }
+        so[2 * (D / 32) * 16 * 64 + lane] = dbias;
+    }
+    __syncthreads();
+    if (w != 0) return;  // no barriers below
+    float db = 0.f;
+#pragma unroll
+    for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float a = 0.f, c = 0.f;
+#pragma unroll
+            for (int v = 0; v < NS; ++v) {
+                a += sT[v][(x * 16 + i) * 64 + lane];
+                c += sT[v][((D / 32 + x) * 16 + i) * 64 + lane];
+            }
+            dk[x][i] = a;
+            dv[x][i] = c;
+        }
+#pragma unroll
+    for (int v = 0; v < NS; ++v) db += sT[v][2 * (D / 32) * 16 * 64 + lane];
+    dbias = xhalf_sum(db);
     if (!krow) return;
     const float* mr = P.vmul.ok() ? P.vmul.row<float>(b, h0, kj) : nullptr;
     const float* vr = P.v.row<float>(b, h0, kj);
@@ -676,14 +937,25 @@ void launch_mfma_bwd_f32(const GradDev& G, hipStream_t s) {
         while (nw > 1 && units * ((n + 32 * nw - 1) / (32 * nw)) < 512) nw >>= 1;
         return nw;
     };
-    {
+    // grids of fewer than 512 blocks of 32 rows: the tiles of a block split over four waves
+    const int qblocks = P.batch * P.heads * ((P.nq + 31) / 32);
+    const int kblocks = P.batch * G.hk * ((P.nk + 31) / 32);
+    if (PA_F32_SPLIT && qblocks < 512 && (P.nk + kF32BN - 1) / kF32BN >= 4) {
+        ProfScope ps("mfma_bwd_f32_dq", s);
+        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dq_split<64, 4>), dim3(qblocks), dim3(256), 0, s, G);
+        else hipLaunchKernelGGL((k_mfma_bwd_f32_dq_split<128, 4>), dim3(qblocks), dim3(256), 0, s, G);
+    } else {
         const int nw = waves((int64_t)P.batch * P.heads, P.nq);
         const dim3 grid(P.batch * P.heads * ((P.nq + 32 * nw - 1) / (32 * nw)));
         ProfScope ps("mfma_bwd_f32_dq", s);
         if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dq<64>), grid, dim3(64 * nw), 0, s, G);
         else hipLaunchKernelGGL((k_mfma_bwd_f32_dq<128>), grid, dim3(64 * nw), 0, s, G);
     }
-    {
+    if (PA_F32_SPLIT && kblocks < 512 && (P.heads / G.hk) * ((P.nq + kF32BN - 1) / kF32BN) >= 4) {
+        ProfScope ps("mfma_bwd_f32_dkv", s);
+        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dkv_split<64, 4>), dim3(kblocks), dim3(256), 0, s, G);
+        else hipLaunchKernelGGL((k_mfma_bwd_f32_dkv_split<128, 4>), dim3(kblocks), dim3(256), 0, s, G);
+    } else {
         const int nw = waves((int64_t)P.batch * G.hk, P.nk);
         const dim3 grid(P.batch * G.hk * ((P.nk + 32 * nw - 1) / (32 * nw)));
         ProfScope ps("mfma_bwd_f32_dkv", s);
