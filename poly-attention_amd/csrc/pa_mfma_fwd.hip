@@ -12,7 +12,12 @@
 // (and the output is rescaled) only when a tile's max exceeds it by more than kFwdTau, so
 // probabilities stay <= 2^kFwdTau (exact in fp32 and within the input type's exponent range);
 // after the first tiles this almost never happens.  Row sums accumulate the rounded
-// probabilities with v_dot2 (the same values the MFMA consumes).
+// probabilities with v_dot2 (the same values the MFMA consumes).  Without softclamp (and
+// without a bias added to the logits) the direct-to-LDS kernel takes no per-tile max at all:
+// it forms the probabilities against the running max and checks their sum instead
+// (FwdWave::probs_checked), so no reduction sits between the score MFMAs and the
+// exponentials, and it pipelines a wave's two query blocks so that each one's probabilities
+// are formed while the matrix core runs the other's products.
 //
 // Kernels:
 //  * k_mfma_fwd_dma (default): K, V and the key bias travel HBM -> LDS by direct loads,
@@ -20,17 +25,11 @@
 //    key bias is folded into the score accumulators.
 //  * k_mfma_fwd: register-staged loads with a transposing LDS store; the general kernel
 //    (value multiplier, key masks, strided biases, very long rows).
-//  * k_mfma_fwd_pp (PA_FWD_PINGPONG): an 8-wave ping-pong schedule, off by default (slower
-//    than k_mfma_fwd_dma on the measured workloads).
 //
 // Rows whose every key is masked are left with lse = NaN for k_fwd_fixup, which applies the
 // reference's finite-fill semantics to them.  Workgroups are mapped XCD-aware (pa_mfma.h); in
 // causal grids each XCD dispatches the heaviest query blocks of all its heads first.
 //
-// PA_FWD_PIPE = 1 software-pipelines the direct-to-LDS tile loop (scores of tile t+1 beside
-// the softmax of tile t, four LDS stages).  It is off: at two workgroups per CU it is 2-3%
-// faster than the plain loop at two, but the plain loop at three workgroups per CU (three
-// stages fit) is faster still.
 #include <algorithm>
 #include <type_traits>
 
@@ -43,22 +42,21 @@ namespace pa {
 #ifndef PA_FWD_KB64
 #define PA_FWD_KB64 2
 #endif
-#ifndef PA_FWD_PINGPONG
-#define PA_FWD_PINGPONG 0  // 1: head dim 64 without softclamp takes the 8-wave ping-pong kernel
+#ifndef PA_FWD_USPLIT
+#define PA_FWD_USPLIT 1  // QB = 2 with sum-checked probabilities: the two query blocks pipelined
 #endif
 #ifndef PA_FWD_QB64
 #define PA_FWD_QB64 2  // 32-query blocks per wave in the direct-to-LDS kernel at head dim 64
-#endif
-#ifndef PA_FWD_PIPE
-#define PA_FWD_PIPE 0  // 1: software-pipelined tile loop in the direct-to-LDS kernel (QB = 1)
-#endif
-#ifndef PA_FWD_PIPE_NST
-#define PA_FWD_PIPE_NST 4  // LDS stages of the pipelined loop (tiles issued NST - 2 ahead)
 #endif
 
 constexpr int kFwdBM = 128;  // query rows per workgroup
 constexpr int kFwdThreads = 256;
 constexpr float kFwdTau = 8.f;  // lazy-rescale threshold (log2 units)
+// sum-checked probabilities (PLAIN scores): largest tile sum per lane accepted without a max
+constexpr float kFwdSumCap = 8192.f;
+#ifndef PA_FWD_SUMCHECK
+#define PA_FWD_SUMCHECK 1
+#endif
 
 // Key tile of BN = 32 * KB keys: KB accumulator blocks per wave and tile.
 template <int D, int KB>
@@ -345,9 +343,37 @@ struct FwdWave {
         return (lt[0] + lt[1]) + (lt[2] + lt[3]);
     }
 
+    // Probabilities of a tile without a per-tile max (PLAIN scores): they are formed against the
+    // running max m first; a lane whose tile sum is not in [0, kFwdSumCap] -- some probability
+    // above kFwdSumCap, a non-finite value, or m still -inf before the first tile -- makes the
+    // wave take the tile's max, move m (settle) and form them again.  Every probability that
+    // reaches the MFMA is therefore <= kFwdSumCap, and m only ever holds a maximum the lane's
+    // scores reached.  Saves the max reduction (two VALU instructions per four scores) on all
+    // but the rare tiles where the scores rise.
+    __device__ __forceinline__ float probs_checked(f32x16_t (&s)[KB], const float* sB, u32x4_t (&pk)[KB][2]) {
+        float lt = probs(s, m, pk);
+        if (__any(!(lt <= kFwdSumCap))) {
+            keep_branch();
+            settle(logits(s, sB), true);
+            lt = probs(s, m == -INFINITY ? 0.f : m, pk);
+        }
+        return lt;
+    }
+
     // lazy rescale: only when some lane's tile max exceeds its running max by more than
-    // kFwdTau does the running max move (rescaling O and l)
-    __device__ __forceinline__ void settle(float mx) {
+    // kFwdTau (by anything, with `always`) does the running max move (rescaling O and l)
+    __device__ __forceinline__ void settle(float mx, bool always = false) {
+        if (always) {
+            const float m_new = fmaxf(m, mx);
+            const float alpha = (m_new > m) ? fast_exp2(m - m_new) : 1.f;
+            l *= alpha;
+#pragma unroll
+            for (int x = 0; x < D / 32; ++x)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[x][i] *= alpha;
+            m = m_new;
+            return;
+        }
         if (__any(mx > m + kFwdTau)) {
             keep_branch();
             const float m_new = fmaxf(m, mx);
@@ -552,9 +578,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     using W = FwdWave<T, D, KB, CAUSAL, SOFTCLAMP, HAS_BIAS, HAS_BIAS && SOFTCLAMP>;
     using M = Mma<T>;
     typedef typename W::frag frag;
-    // pipelined loop: the scores of tile t+1 are computed beside the softmax of tile t
-    constexpr bool PIPE = PA_FWD_PIPE && QB == 1;
-    constexpr int NSTG = PIPE ? PA_FWD_PIPE_NST : kFwdStages;
+    constexpr int NSTG = kFwdStages;
     __shared__ __attribute__((aligned(16))) T sK[NSTG * TL::ELEMS];
     __shared__ __attribute__((aligned(16))) T sV[NSTG * TL::ELEMS];
     __shared__ __attribute__((aligned(16))) float sBraw[NSTG][BN];  // raw bias bytes
@@ -654,100 +678,6 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     const int ntiles = (kend + BN - 1) / BN;
     const int wave_last = CAUSAL ? (wq0 + 32 * QB - 1) : (1 << 30);
 
-    if constexpr (PIPE) {
-        // Stage of tile t = t % NSTG.  Iteration t computes the scores of tile t+1 (K of stage
-        // t+1), the probabilities of tile t and O += V^T P^T (V of stage t).  At enter(t+1),
-        // every wave has finished iteration t-1, so tile t-1's stage is free: it receives tile
-        // t-1+NSTG = (t+1) + DIST.
-        constexpr int DIST = NSTG - 2;
-        static_assert(DIST >= 1 && DIST <= 2, "pipelined loop: 3 or 4 stages");
-        W& v = wv[0];
-        const int nact = CAUSAL ? min(ntiles, wave_last / BN + 1) : ntiles;
-        auto issue_t = [&](int t) __attribute__((always_inline)) { issue(t * BN, t % NSTG); };
-        auto enter_p = [&](int t) __attribute__((always_inline)) {
-            // tiles issued so far: 0 .. t+DIST-1; those after t may stay in flight
-            if (DIST == 2 && t + 1 < ntiles) wait_vmcnt<NOPS>();
-            else wait_vmcnt<0>();
-            lds_barrier();
-            if (t + DIST < ntiles) issue_t(t + DIST);
-        };
-        auto convert_bias = [&](int stg) __attribute__((always_inline)) {
-            if (HAS_BIAS) {
-                float x;
-                if (bes == 4) x = sBraw[stg][lane];
-                else x = (float)reinterpret_cast<const T*>(&sBraw[stg][0])[lane];
-                sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
-            }
-        };
-        auto scores_of = [&](f32x16_t (&s)[KB], int stg) __attribute__((always_inline)) {
-            const T* K = sK + stg * TL::ELEMS;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                f32x16_t init = zero16();
-                if (FOLD) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float4 bb = *reinterpret_cast<const float4*>(&sBw[w][kb * 32 + 8 * g + 4 * hh]);
-                        init[4 * g] = bb.x;
-                        init[4 * g + 1] = bb.y;
-                        init[4 * g + 2] = bb.z;
-                        init[4 * g + 3] = bb.w;
-                    }
-                }
-                s[kb] = init;
-#pragma unroll
-                for (int c = 0; c < D / 16; ++c)
-                    s[kb] = M::run(ld_frag<T>(K + kb * 32 * D + koff[c]), v.qf[c], s[kb]);
-            }
-        };
-        auto prob_pv = [&](const f32x16_t (&s)[KB], int stg) __attribute__((always_inline)) {
-            const T* V = sV + stg * TL::ELEMS;
-            u32x4_t pk[KB][2];
-            v.l += v.probs(s, v.m == -INFINITY ? 0.f : v.m, pk);
-            frag vf[KB][2][D / 32];
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-                    for (int x = 0; x < D / 32; ++x) {
-                        const T* base = V + (kb * 32 + 16 * t2) * D + voff[x];
-                        const u32x2_t lo = lds_read_tr(base);
-                        const u32x2_t hi = lds_read_tr(base + 8 * D);
-                        const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
-                        vf[kb][t2][x] = __builtin_bit_cast(frag, v4);
-                    }
-            v.pv(vf, pk);
-        };
-        for (int t = 0; t < DIST && t < ntiles; ++t) issue_t(t);
-        f32x16_t s[KB];
-        enter_p(0);
-        convert_bias(0);
-        scores_of(s, 0);
-        if (nact == 1) v.mask_edges_nk(s, 0);
-        v.settle(v.logits(s, sBw[w]));
-        // iteration t (tile t+1 active and not the last: no mask on its scores)
-        auto iter = [&](int t, bool mask_next) __attribute__((always_inline)) {
-            enter_p(t + 1);
-            const int stn = (t + 1) % NSTG;
-            convert_bias(stn);
-            f32x16_t sn[KB];
-            scores_of(sn, stn);
-            prob_pv(s, t % NSTG);
-            if (mask_next) v.mask_edges_nk(sn, (t + 1) * BN);
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) s[kb] = sn[kb];
-            v.settle(v.logits(s, sBw[w]));
-        };
-        int t = 0;
-        for (; t + 2 < nact; ++t) iter(t, false);
-        if (t + 1 < nact) {
-            iter(t, true);
-            ++t;
-        }
-        prob_pv(s, t % NSTG);
-        for (int t2 = nact; t2 < ntiles; ++t2) enter_p(t2);
-    } else {
     issue(0, 0);
     if (ntiles > 1) issue(BN, 1);
 
@@ -775,6 +705,120 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
             else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
             sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
         }
+#if PA_FWD_USPLIT
+        if constexpr (QB == 2 && W::PLAIN && PA_FWD_SUMCHECK) {
+            // The wave's two query blocks in a pipeline: (A) scores of block 0; (B) scores of
+            // block 1 among block 0's probabilities; (C) O += V^T P^T of block 0 among block 1's
+            // probabilities; (D) O += V^T P^T of block 1.  In B and C each MFMA is followed by
+            // the VALU work of four probabilities (scheduling barriers keep the chunks in
+            // order), so the matrix core runs while the wave forms probabilities.
+            frag kf[KB][D / 16];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int c = 0; c < D / 16; ++c) kf[kb][c] = ld_frag<T>(K + kb * 32 * D + koff[c]);
+            f32x16_t s[QB][KB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                f32x16_t init = zero16();
+                if (FOLD) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float4 bb = *reinterpret_cast<const float4*>(&sBw[w][kb * 32 + 8 * g + 4 * hh]);
+                        init[4 * g] = bb.x;
+                        init[4 * g + 1] = bb.y;
+                        init[4 * g + 2] = bb.z;
+                        init[4 * g + 3] = bb.w;
+                    }
+                }
+                s[0][kb] = init;
+                s[1][kb] = init;
+            }
+            // four probabilities of block u (registers 4 (i % 4) .. +3 of key block i / 4) into
+            // the packed operands and the four sum chains
+            auto chunk = [&](int u, int i, float msub, u32x4_t (&pk)[KB][2], float (&lts)[4])
+                             __attribute__((always_inline)) {
+                const int kb = i / 4, r0 = 4 * (i % 4);
+                const float sl2 = wv[u].sl2;
+                const float p0 = fast_exp2(fmaf(s[u][kb][r0], sl2, -msub));
+                const float p1 = fast_exp2(fmaf(s[u][kb][r0 + 1], sl2, -msub));
+                const float p2 = fast_exp2(fmaf(s[u][kb][r0 + 2], sl2, -msub));
+                const float p3 = fast_exp2(fmaf(s[u][kb][r0 + 3], sl2, -msub));
+                const uint32_t w0 = pack2<T>(p0, p1), w1 = pack2<T>(p2, p3);
+                pk[kb][r0 / 8][(r0 % 8) / 2] = w0;
+                pk[kb][r0 / 8][(r0 % 8) / 2 + 1] = w1;
+                lts[(2 * i) % 4] = sum_pair<T>(w0, lts[(2 * i) % 4]);
+                lts[(2 * i + 1) % 4] = sum_pair<T>(w1, lts[(2 * i + 1) % 4]);
+            };
+            // the rare path of a block whose probabilities failed the sum check
+            auto recheck = [&](int u, float lt, u32x4_t (&pk)[KB][2]) __attribute__((always_inline)) {
+                if (__any(!(lt <= kFwdSumCap))) {
+                    keep_branch();
+                    wv[u].settle(wv[u].logits(s[u], sBw[w]), true);
+                    lt = wv[u].probs(s[u], wv[u].m == -INFINITY ? 0.f : wv[u].m, pk);
+                }
+                wv[u].l += lt;
+            };
+            // (A)
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) s[0][kb] = M::run(kf[kb][c], wv[0].qf[c], s[0][kb]);
+            wv[0].mask_edges_nk(s[0], j0);
+            __builtin_amdgcn_sched_barrier(0);
+            // (B)
+            u32x4_t pk0[KB][2];
+            float lt0;
+            {
+                const float msub = wv[0].m;
+                float lts[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < KB * (D / 16); ++i) {
+                    const int c = i / KB, kb = i % KB;
+                    s[1][kb] = M::run(kf[kb][c], wv[1].qf[c], s[1][kb]);
+                    chunk(0, i, msub, pk0, lts);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                lt0 = (lts[0] + lts[1]) + (lts[2] + lts[3]);
+            }
+            frag vf[KB][2][D / 32];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                    for (int x = 0; x < D / 32; ++x) {
+                        const T* base = V + (kb * 32 + 16 * t2) * D + voff[x];
+                        const u32x2_t lo = lds_read_tr(base);
+                        const u32x2_t hi = lds_read_tr(base + 8 * D);
+                        const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
+                        vf[kb][t2][x] = __builtin_bit_cast(frag, v4);
+                    }
+            recheck(0, lt0, pk0);
+            wv[1].mask_edges_nk(s[1], j0);
+            __builtin_amdgcn_sched_barrier(0);
+            // (C)
+            u32x4_t pk1[KB][2];
+            float lt1;
+            {
+                const float msub = wv[1].m;
+                float lts[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < KB * 2 * (D / 32); ++i) {
+                    const int kb = i / (2 * (D / 32)), t2 = (i / (D / 32)) % 2, x = i % (D / 32);
+                    wv[0].o[x] = M::run(vf[kb][t2][x], __builtin_bit_cast(frag, pk0[kb][t2]), wv[0].o[x]);
+                    chunk(1, i, msub, pk1, lts);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                lt1 = (lts[0] + lts[1]) + (lts[2] + lts[3]);
+            }
+            recheck(1, lt1, pk1);
+            // (D)
+            wv[1].pv(vf, pk1);
+            st = st == 2 ? 0 : st + 1;
+            continue;
+        }
+#endif
         f32x16_t s[QB][KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -798,10 +842,11 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
                 for (int u = 0; u < QB; ++u) s[u][kb] = M::run(a, wv[u].qf[c], s[u][kb]);
             }
         }
+        constexpr bool SUMCHK = PA_FWD_SUMCHECK && W::PLAIN;
 #pragma unroll
         for (int u = 0; u < QB; ++u) {
             wv[u].mask_edges_nk(s[u], j0);
-            wv[u].settle(wv[u].logits(s[u], sBw[w]));
+            if (!SUMCHK) wv[u].settle(wv[u].logits(s[u], sBw[w]));
         }
         frag vf[KB][2][D / 32];
 #pragma unroll
@@ -819,7 +864,8 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
 #pragma unroll
         for (int u = 0; u < QB; ++u) {
             u32x4_t pk[KB][2];
-            wv[u].l += wv[u].probs(s[u], wv[u].m == -INFINITY ? 0.f : wv[u].m, pk);
+            if (SUMCHK) wv[u].l += wv[u].probs_checked(s[u], sBw[w], pk);
+            else wv[u].l += wv[u].probs(s[u], wv[u].m == -INFINITY ? 0.f : wv[u].m, pk);
             wv[u].pv(vf, pk);
         }
         st = st == 2 ? 0 : st + 1;
@@ -828,7 +874,6 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
         enter(t);
         st = st == 2 ? 0 : st + 1;
     }
-    }  // !PIPE
 
 #pragma unroll
     for (int u = 0; u < QB; ++u) {
@@ -1253,241 +1298,6 @@ static bool dma_ok(const PassDev& P, int bn) {
     return true;
 }
 
-// ---------------------------------------------------------------------------------------
-// Ping-pong variant (head dim 64, no softclamp, no value multiplier): 8 waves per workgroup
-// in two groups of four, one wave of each group per SIMD.  The tile loop alternates two
-// phases separated by workgroup barriers; in every phase one group issues its MFMAs (scores
-// of tile t and O += V^T P of tile t-1) while the other runs the softmax VALU work of its
-// previous tile, so that each SIMD's matrix core and VALU always have one wave to serve.
-// Group A (waves 0-3) runs MFMA(t) in phase 2t and softmax(t) in phase 2t+1; group B
-// (waves 4-7) runs softmax(t-1) in phase 2t and MFMA(t) in phase 2t+1.  Loads travel HBM ->
-// LDS directly: at phase 2t the group of K_{t+2} (+ key bias) and V_{t+1} is issued, into
-// the stages freed by tile t-1 (three K stages, three V stages).
-
-constexpr int kPpThreads = 512;
-constexpr int kPpBM = 256;  // queries per workgroup (8 waves x 32)
-
-template <typename T, bool CAUSAL, bool HAS_BIAS>
-__global__ __launch_bounds__(kPpThreads, 1) void k_mfma_fwd_pp(PassDev P) {
-    constexpr int D = 64, KB = 2, BN = 64, CPR = D / 8, ELEMS = BN * D;
-    static_assert(BN * CPR == kPpThreads, "one 16-byte chunk per thread and tensor");
-    using W = FwdWave<T, D, KB, CAUSAL, false, HAS_BIAS, false>;  // bias folded into the scores
-    using M = Mma<T>;
-    typedef typename W::frag frag;
-    __shared__ __attribute__((aligned(16))) T sK[3 * ELEMS];
-    __shared__ __attribute__((aligned(16))) T sV[3 * ELEMS];
-    __shared__ __attribute__((aligned(16))) float sBraw[3][BN];
-    __shared__ __attribute__((aligned(16))) float sBw[8][BN];
-
-    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-    const bool grp_a = w < 4;
-    const int nqb = (P.nq + kPpBM - 1) / kPpBM;
-    int bh, rank;
-    block_order<CAUSAL>(nqb, bh, rank);
-    const int qb = CAUSAL ? nqb - 1 - rank : rank;
-    const int h = bh % P.heads, b = bh / P.heads;
-    const int hh = lane >> 5, kcol = lane & 31;
-
-    W wv;
-    wv.hh = hh;
-    wv.kcol = kcol;
-    wv.q0 = qb * kPpBM + w * 32;
-    wv.qi = wv.q0 + kcol;
-    wv.nk = P.nk;
-    wv.sl2 = P.scale * kLog2e;
-    wv.cinv = 0.f;
-    wv.cl2 = 0.f;
-    wv.m = -INFINITY;
-    wv.l = 0.f;
-    {
-        const int qi = wv.qi;
-        const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-            u32x4_t raw = {0u, 0u, 0u, 0u};
-            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
-            wv.qf[c] = __builtin_bit_cast(frag, raw);
-        }
-    }
-#pragma unroll
-    for (int x = 0; x < D / 32; ++x) wv.o[x] = zero16();
-    // retire the (compiler-visible) Q loads before the first direct load
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) wv.qf[c] = opaque(wv.qf[c]);
-
-    const int ksn = (int)P.k.sn, vsn = (int)P.v.sn;
-    const srd_t rk = make_srd(P.k.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * ksn + D) * 2));
-    const srd_t rv = make_srd(P.v.row<T>(b, h, 0), (uint32_t)(((int64_t)(P.nk - 1) * vsn + D) * 2));
-    const int bes = P.bias.dtype == PA_F32 ? 4 : 2;
-    const float bmul = 1.f / P.scale;
-    srd_t rb = {0, 0, 0, 0};
-    if (HAS_BIAS) rb = make_srd(P.bias.p + P.bias.idx(b, h, 0) * bes, (uint32_t)(P.nk * bes));
-    // this thread's chunk of a tile: row tid / CPR, physical chunk tid % CPR
-    uint32_t offk, offv;
-    {
-        const int r = tid / CPR, ph = tid % CPR;
-        offk = (uint32_t)((r * ksn + (ph ^ swz_k<D>(r)) * 8) * 2);
-        offv = (uint32_t)((r * vsn + (ph ^ swz_v<D>(r)) * 8) * 2);
-    }
-    const int bq = BN * bes / 8;  // bias bytes per wave (every wave has lane 0 active)
-    const uint32_t offb = (uint32_t)(w * bq + 16 * lane);
-    const uint32_t lds_k = lds_addr(sK), lds_v = lds_addr(sV), lds_b = lds_addr(&sBraw[0][0]);
-    auto issue_k = [&](int j0, int stage) __attribute__((always_inline)) {
-        dma16(rk, lds_k + (uint32_t)(stage * ELEMS * 2 + w * 64 * 16), offk + (uint32_t)(j0 * ksn * 2));
-        if (HAS_BIAS && 16 * lane < bq)
-            dma16(rb, lds_b + (uint32_t)(stage * BN * 4 + w * bq), offb + (uint32_t)(j0 * bes));
-    };
-    auto issue_v = [&](int j0, int stage) __attribute__((always_inline)) {
-        dma16(rv, lds_v + (uint32_t)(stage * ELEMS * 2 + w * 64 * 16), offv + (uint32_t)(j0 * vsn * 2));
-    };
-
-    int koff[D / 16];
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) koff[c] = kcol * D + (((2 * c + hh) ^ swz_k<D>(kcol)) * 8);
-    int voff[D / 32];
-    {
-        const int g = lane >> 4, j = lane & 15;
-        const int r = 4 * (g >> 1) + (j >> 2);
-#pragma unroll
-        for (int x = 0; x < D / 32; ++x) {
-            const int ch = 4 * x + 2 * (g & 1) + ((j & 3) >> 1);
-            voff[x] = r * D + ((ch ^ swz_v<D>(r)) * 8) + 4 * (j & 1);
-        }
-    }
-
-    const int kend = CAUSAL ? min(P.nk, qb * kPpBM + kPpBM) : P.nk;
-    const int ntiles = (kend + BN - 1) / BN;
-    const int nact = CAUSAL ? min(ntiles, (wv.q0 + 31) / BN + 1) : ntiles;  // this wave's tiles
-    constexpr int KOPS = 1 + (HAS_BIAS ? 1 : 0);  // loads per thread for one K tile (+ bias)
-    // loads per thread in the group issued at even phase 2g: K_{g+2} (+ bias), V_{g+1}
-    auto group_ops = [&](int g) __attribute__((always_inline)) {
-        return (g + 2 < ntiles && g + 2 >= 0 ? KOPS : 0) + (g + 1 < ntiles && g + 1 >= 0 ? 1 : 0);
-    };
-
-    // prologue: group -2 = K_0 (+ bias_0); group -1 = K_1 (+ bias_1), V_0
-    issue_k(0, 0);
-    if (ntiles > 1) issue_k(BN, 1);
-    issue_v(0, 0);
-
-    f32x16_t s[KB];
-    u32x4_t pk[KB][2];
-    // scores S_t of tile t (accumulators seeded with the folded key bias)
-    auto scores_t = [&](int t) __attribute__((always_inline)) {
-        const int st = t % 3;
-        const T* K = sK + st * ELEMS;
-        if (HAS_BIAS) {
-            float x;
-            if (bes == 4) x = sBraw[st][lane];
-            else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
-            sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
-        }
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-            f32x16_t a = zero16();
-            if (HAS_BIAS) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 bb = *reinterpret_cast<const float4*>(&sBw[w][kb * 32 + 8 * g + 4 * hh]);
-                    a[4 * g] = bb.x;
-                    a[4 * g + 1] = bb.y;
-                    a[4 * g + 2] = bb.z;
-                    a[4 * g + 3] = bb.w;
-                }
-            }
-#pragma unroll
-            for (int c = 0; c < D / 16; ++c) a = M::run(ld_frag<T>(K + kb * 32 * D + koff[c]), wv.qf[c], a);
-            s[kb] = a;
-        }
-    };
-    // O += V_t^T P_t
-    auto pv_t = [&](int t) __attribute__((always_inline)) {
-        const T* V = sV + (t % 3) * ELEMS;
-        frag vf[KB][2][D / 32];
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-                for (int x = 0; x < D / 32; ++x) {
-                    const T* base = V + (kb * 32 + 16 * t2) * D + voff[x];
-                    const u32x2_t lo = lds_read_tr(base);
-                    const u32x2_t hi = lds_read_tr(base + 8 * D);
-                    const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
-                    vf[kb][t2][x] = __builtin_bit_cast(frag, v4);
-                }
-        wv.pv(vf, pk);
-    };
-    // softmax of tile t
-    auto softmax_t = [&](int t) __attribute__((always_inline)) {
-        wv.mask_edges_nk(s, t * BN);
-        wv.settle(wv.logits(s, nullptr));
-        wv.l += wv.probs(s, wv.m == -INFINITY ? 0.f : wv.m, pk);
-    };
-    // phase boundaries: even global phase 2e waits for load group e-2, then issues group e
-    auto sync_even = [&](int e) __attribute__((always_inline)) {
-        switch (group_ops(e - 1)) {
-            case 0: wait_vmcnt<0>(); break;
-            case 1: wait_vmcnt<1>(); break;
-            case 2: wait_vmcnt<2>(); break;
-            default: wait_vmcnt<3>(); break;
-        }
-        lds_barrier();
-        if (e + 2 < ntiles) issue_k((e + 2) * BN, (e + 2) % 3);
-        if (e + 1 < ntiles) issue_v((e + 1) * BN, (e + 1) % 3);
-    };
-    // Every wave runs the same sequence "sync, MFMA(t), sync, softmax(t)"; group B starts one
-    // phase later (its first sync is global phase 0), group A ends one phase later.
-    auto sync1 = [&](int t) __attribute__((always_inline)) {
-        if (grp_a) sync_even(t);
-        else lds_barrier();
-    };
-    auto sync2 = [&](int t) __attribute__((always_inline)) {
-        if (grp_a) lds_barrier();
-        else sync_even(t + 1);
-    };
-    if (!grp_a) sync_even(0);
-    // tile 0 (every wave has it)
-    sync1(0);
-    scores_t(0);
-    sync2(0);
-    softmax_t(0);
-    for (int t = 1; t < nact; ++t) {
-        sync1(t);
-        scores_t(t);
-        pv_t(t - 1);
-        sync2(t);
-        softmax_t(t);
-    }
-    sync1(nact);
-    pv_t(nact - 1);
-    sync2(nact);
-    for (int t = nact + 1; t <= ntiles; ++t) {
-        sync1(t);
-        sync2(t);
-    }
-    if (grp_a) sync_even(ntiles + 1);
-
-    const float l = xhalf_sum(wv.l);
-    const int qi = wv.qi;
-    if (qi >= P.nq) return;
-    const bool degenerate = !(l > 0.f) || !P.qm.keep(b, qi);
-    const float inv = degenerate ? 0.f : 1.f / l;
-    T* orow = P.out.wrow<T>(b, h, qi);
-    u32x2_t ow[D / 8];
-#pragma unroll
-    for (int x = 0; x < D / 32; ++x) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d = x * 32 + 8 * g + 4 * hh;
-            u32x2_t& o2 = ow[4 * x + g];
-            o2[0] = pack2<T>(wv.o[x][4 * g] * inv, wv.o[x][4 * g + 1] * inv);
-            o2[1] = pack2<T>(wv.o[x][4 * g + 2] * inv, wv.o[x][4 * g + 3] * inv);
-            *reinterpret_cast<u32x2_t*>(orow + d) = o2;
-        }
-    }
-    if (P.ey.ok()) epi_store_lane<T, D / 8>(P, b, h, qi, hh, ow);
-    if (hh == 0) *P.lse.wrow<float>(b, h, qi) = degenerate ? NAN : (wv.m + log2f(l)) * kLn2;
-}
 
 // ---------------------------------------------------------------------------------------
 
@@ -1530,10 +1340,7 @@ static void launch_t(const PassDev& P, hipStream_t s) {
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     dim3 grid(nqb * P.heads * P.batch);
     ProfScope ps("mfma_fwd", s);
-    if (D == 64 && PA_FWD_PINGPONG && !S && !V && dma_ok(P, 32 * KB)) {
-        const int nqb_pp = (P.nq + kPpBM - 1) / kPpBM;
-        hipLaunchKernelGGL((k_mfma_fwd_pp<T, C, B>), dim3(nqb_pp * P.heads * P.batch), dim3(kPpThreads), 0, s, P);
-    } else if (!V && dma_ok(P, 32 * KB)) {
+    if (!V && dma_ok(P, 32 * KB)) {
         constexpr int QB = (D == 64) ? PA_FWD_QB64 : 1;
         const int nqb2 = (P.nq + kFwdBM * QB - 1) / (kFwdBM * QB);
         hipLaunchKernelGGL((k_mfma_fwd_dma<T, D, KB, QB, C, S, B>), dim3(nqb2 * P.heads * P.batch),
