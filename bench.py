@@ -294,9 +294,9 @@ def make_vit(dev, dtype, batch):
 def config1_bench(dev, steps, warmup, cpu):
     """PolyAttention(dim=512, heads=8, dim_head=64, causal=False) fp32
     forward on x ~ N(0,1) (1, 1024, 512), random init (seed 0) -- the reference's
-    CPU-runnable case.  GPU: the module forward (fp32 passes on v_mfma_f32_32x32x2_f32);
-    CPU: the oracle's eager module forward (the reference's CPU path restated) at the same
-    shape, median of 5."""
+    CPU-runnable case.  GPU: the module forward (fp32 passes on v_mfma_f32_32x32x2_f32), and
+    a training step of the same module with a key padding mask; CPU: the oracle's eager module
+    forward (the reference's CPU path restated) at the same shape, median of 5."""
     from poly_attention import PolyAttention, _lib
 
     torch.manual_seed(0)
@@ -309,7 +309,8 @@ def config1_bench(dev, steps, warmup, cpu):
         with _lib.KernelProfile() as prof:
             for _ in range(5):
                 md(xd)
-    n_l, tot = prof.times.get("mfma_fwd_f32", (0, 0.0))
+    # the fp32 pass: the key-split kernel at this grid (the plain one on other shapes)
+    n_l, tot = prof.times.get("mfma_fwd_f32_split", prof.times.get("mfma_fwd_f32", (0, 0.0)))
     core_flops = 2 * core_flops_fwd(1, 8, 1024, 1024, 64, False)  # two passes per forward
     res = {"workload": "PolyAttention(512, h8, d64, non-causal) fp32 forward, x (1, 1024, 512)",
            "ms_per_forward": round(ms, 4),
@@ -319,6 +320,25 @@ def config1_bench(dev, steps, warmup, cpu):
         tf = core_flops / 2 / (tot / n_l / 1e3) / 1e12
         res["pass_tflops"] = round(tf, 2)
         res["pass_frac_fp32_peak"] = round(tf / PEAK_FP32_TFLOPS, 4)
+    # the same module trained in fp32 with a key padding mask (the last quarter of the keys
+    # masked): masked passes on the fp32 MFMA kernels, forward and backward (the key term and
+    # the fully-masked-row fix-ups around them)
+    mask = torch.ones(1, 1024, dtype=torch.bool, device=dev)
+    mask[:, 768:] = False
+    xg = xd.clone().requires_grad_()
+    gy = torch.randn(1, 1024, 512, generator=torch.Generator().manual_seed(2)).to(dev)
+
+    def masked_step():
+        xg.grad = None
+        md.zero_grad(set_to_none=True)
+        md(xg, mask=mask).backward(gy)
+
+    res["masked_train_ms_per_step"] = round(time_steps(masked_step, steps, warmup), 4)
+    with _lib.KernelProfile() as mprof:
+        for _ in range(3):
+            masked_step()
+    res["masked_train_kernels"] = {k: {"launches_per_step": n // 3, "avg_ms": round(t / n, 4)}
+                                   for k, (n, t) in mprof.times.items()}
     if cpu:
         import oracle.poly_oracle as O
 
@@ -862,6 +882,13 @@ def main():
         roofline["rocprof_avg_ms"] = round(rp, 4)
         roofline["rocprof_frac"] = round(achieved_rate(work, rp, unit) / peak, 4)
     log(f"[bench] kernels: {kernels}")
+    # the shader clock under matrix-core load right after the timed steps (libpolyattn
+    # pa_measure_clock): tells a slower-clocked box apart from a code change
+    gpu_clock = {"ghz": round(_lib.measure_clock(dev), 3),
+                 "how": "s_memtime cycles per 100 MHz s_memrealtime tick over a ~50 us all-CU "
+                        "MFMA probe run right after the timed steps (libpolyattn "
+                        "pa_measure_clock); the bf16 peak of 2.5 PFLOP/s assumes 2.4 GHz"}
+    log(f"[bench] gpu clock under MFMA load {gpu_clock['ghz']} GHz")
 
     module_ms = module_epi_ms = None
     module_kernels = None
@@ -952,6 +979,7 @@ def main():
         "tokens_per_s": round(B * N / (ms / 1e3), 1),
         "flops_per_step": fwd_f + bwd_f,
         "roofline": roofline,
+        "gpu_clock": gpu_clock,
         "kernels": kernels,
         "masked_core": masked,
         "module_ms_per_step": round(module_ms, 4) if module_ms else None,

@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 7
+#define PA_ABI_VERSION 8
 #define PA_MAX_ORDER 8
 
 /* status codes (0 = success, negative = failure) */
@@ -350,6 +350,14 @@ typedef struct pa_kernel_time {
 } pa_kernel_time;
 int pa_profile_start(void);
 int pa_profile_stop(pa_kernel_time* out, int capacity, int* count);
+
+/* Shader clock under matrix-core load (no counterpart in the reference: a measurement facility
+ * for benchmarks, so that a timing can be told apart from a slower-clocked GPU).  Runs a
+ * short kernel of independent MFMA chains on every CU (two waves per SIMD, ~50 us) on
+ * `stream`, waits for it, and returns in *ghz the waves' mean shader-cycle count (s_memtime)
+ * per 100 MHz reference-clock tick (s_memrealtime) over their run, in GHz.  The probe's
+ * counts go through a device array of the library: calls that overlap on one GPU race. */
+int pa_measure_clock(double* ghz, void* stream);
 
 int    pa_attn_pass_fwd(const pa_pass* p, void* stream);
 size_t pa_attn_pass_fwd_workspace(const pa_pass* p);   /* 0: the forward takes none */

@@ -153,6 +153,17 @@ int finish_launch() {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// The MFMA backward of a masked pass runs on the pass without its masks (the key mask folded
+// into the key term, fully-masked rows given lse = +inf and finished by the fix-ups): whether
+// the kernels take that mask-free pass.
+bool mfma_bwd_masked_supported(const GradDev& G, int dtype) {
+    GradDev Gm = G;
+    Gm.f.km.p = nullptr;
+    Gm.f.qm.p = nullptr;
+    Gm.f.flags &= ~PA_FLAG_MAY_DEGENERATE;
+    return mfma_bwd_supported(Gm, dtype);
+}
+
 bool pass_masked(const pa_pass& f) {
     return f.key_mask.ptr || f.query_mask.ptr || (f.flags & PA_FLAG_MAY_DEGENERATE);
 }
@@ -269,6 +280,59 @@ int pa_profile_stop(pa_kernel_time* out, int capacity, int* count) {
     g_prof.clear();
     if (count) *count = n;
     return status;
+}
+
+// ---------------------------------------------------------------------------------------
+// Clock probe: 256 workgroups of 8 waves (two per SIMD), each wave four independent MFMA chains
+// of kClkIters products bracketed by s_memtime (shader cycles) and s_memrealtime (100 MHz).
+// Lanes 0 and 1 of every wave store its two counts (per-lane addresses: vector stores).
+constexpr int kClkWgs = 256, kClkWaves = 8, kClkIters = 768;
+__device__ unsigned long long g_clk[kClkWgs * kClkWaves * 2];
+
+__global__ __launch_bounds__(64 * kClkWaves) void k_clock_probe() {
+    typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+    typedef float f16v __attribute__((ext_vector_type(16)));
+    bf8 a, b;
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (__bf16)(threadIdx.x * 1e-3f);
+        b[i] = (__bf16)(i * 1e-2f);
+    }
+    f16v c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < kClkIters / 4; ++it) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c3, 0, 0, 0);
+    }
+    float sum = 0.f;
+    for (int i = 0; i < 16; ++i) sum += c0[i] + c1[i] + c2[i] + c3[i];
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    const int lane = threadIdx.x & 63, wave = blockIdx.x * kClkWaves + (threadIdx.x >> 6);
+    // (the sum keeps the chains live: it is never NaN for these inputs, so both counts store)
+    if (lane < 2 && !(sum != sum)) g_clk[wave * 2 + lane] = lane == 0 ? t1 - t0 : r1 - r0;
+}
+
+int pa_measure_clock(double* ghz, void* stream) {
+    if (!ghz) return PA_EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<unsigned long long> host(kClkWgs * kClkWaves * 2);
+    hipLaunchKernelGGL(k_clock_probe, dim3(kClkWgs), dim3(64 * kClkWaves), 0, s);
+    if (hipGetLastError() != hipSuccess) return PA_EHIP;
+    if (hipStreamSynchronize(s) != hipSuccess) return PA_EHIP;
+    if (hipMemcpyFromSymbol(host.data(), HIP_SYMBOL(g_clk), host.size() * sizeof(host[0]), 0,
+                            hipMemcpyDeviceToHost) != hipSuccess)
+        return PA_EHIP;
+    double cyc = 0.0, ticks = 0.0;
+    for (int w = 0; w < kClkWgs * kClkWaves; ++w) {
+        cyc += (double)host[2 * w];
+        ticks += (double)host[2 * w + 1];
+    }
+    if (!(ticks > 0.0)) return PA_EHIP;
+    *ghz = cyc / ticks * 0.1;  // cycles per 10 ns tick -> GHz
+    return PA_OK;
 }
 
 size_t pa_attn_pass_fwd_workspace(const pa_pass* p) { return p ? fwd_ws_bytes(*p) : 0; }
@@ -427,7 +491,7 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
     G.seeds = 0;
     G.ws_kcnt = nullptr;
     G.ws_part = nullptr;
-    if (mfma_bwd_supported(G, T) && pass_masked(*p)) {
+    if (pass_masked(*p) && mfma_bwd_masked_supported(G, T)) {
         // normal rows on the MFMA kernels with the key mask folded into the key bias; the
         // preprocess marks fully-masked rows (lse = +inf), whose part the fix-ups add
         char* w = ws;
@@ -455,6 +519,7 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
         }
         Gm.f.km.p = nullptr;
         Gm.f.qm.p = nullptr;
+        Gm.f.flags &= ~PA_FLAG_MAY_DEGENERATE;
         launch_mfma_bwd(Gm, T, s);
         launch_mask_fixups(G, T, s);
     } else if (mfma_bwd_supported(G, T)) {

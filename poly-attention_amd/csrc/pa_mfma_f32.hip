@@ -938,12 +938,13 @@ void launch_mfma_bwd_f32(const GradDev& G, hipStream_t s) {
         return nw;
     };
     // grids of fewer than 512 blocks of 32 rows: the tiles of a block split over four waves
-    const int qblocks = P.batch * P.heads * ((P.nq + 31) / 32);
-    const int kblocks = P.batch * G.hk * ((P.nk + 31) / 32);
+    // (block counts in 64 bits: a product past 2^31 must not wrap into the small-grid test)
+    const int64_t qblocks = (int64_t)P.batch * P.heads * ((P.nq + 31) / 32);
+    const int64_t kblocks = (int64_t)P.batch * G.hk * ((P.nk + 31) / 32);
     if (PA_F32_SPLIT && qblocks < 512 && (P.nk + kF32BN - 1) / kF32BN >= 4) {
-        ProfScope ps("mfma_bwd_f32_dq", s);
-        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dq_split<64, 4>), dim3(qblocks), dim3(256), 0, s, G);
-        else hipLaunchKernelGGL((k_mfma_bwd_f32_dq_split<128, 4>), dim3(qblocks), dim3(256), 0, s, G);
+        ProfScope ps("mfma_bwd_f32_dq_split", s);
+        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dq_split<64, 4>), dim3((uint32_t)qblocks), dim3(256), 0, s, G);
+        else hipLaunchKernelGGL((k_mfma_bwd_f32_dq_split<128, 4>), dim3((uint32_t)qblocks), dim3(256), 0, s, G);
     } else {
         const int nw = waves((int64_t)P.batch * P.heads, P.nq);
         const dim3 grid(P.batch * P.heads * ((P.nq + 32 * nw - 1) / (32 * nw)));
@@ -952,9 +953,9 @@ void launch_mfma_bwd_f32(const GradDev& G, hipStream_t s) {
         else hipLaunchKernelGGL((k_mfma_bwd_f32_dq<128>), grid, dim3(64 * nw), 0, s, G);
     }
     if (PA_F32_SPLIT && kblocks < 512 && (P.heads / G.hk) * ((P.nq + kF32BN - 1) / kF32BN) >= 4) {
-        ProfScope ps("mfma_bwd_f32_dkv", s);
-        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dkv_split<64, 4>), dim3(kblocks), dim3(256), 0, s, G);
-        else hipLaunchKernelGGL((k_mfma_bwd_f32_dkv_split<128, 4>), dim3(kblocks), dim3(256), 0, s, G);
+        ProfScope ps("mfma_bwd_f32_dkv_split", s);
+        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_bwd_f32_dkv_split<64, 4>), dim3((uint32_t)kblocks), dim3(256), 0, s, G);
+        else hipLaunchKernelGGL((k_mfma_bwd_f32_dkv_split<128, 4>), dim3((uint32_t)kblocks), dim3(256), 0, s, G);
     } else {
         const int nw = waves((int64_t)P.batch * G.hk, P.nk);
         const dim3 grid(P.batch * G.hk * ((P.nk + 32 * nw - 1) / (32 * nw)));
@@ -977,11 +978,12 @@ void launch_mfma_fwd_f32(const PassDev& P, hipStream_t s) {
     // grids of fewer than 512 blocks of 32 queries leave most of the chip idle: split the keys
     // of a block over 4 waves (the kernel's 332-512 registers allow one wave per SIMD), when
     // there are that many key tiles
-    const int blocks32 = units * ((P.nq + 31) / 32), tiles = (P.nk + kF32BN - 1) / kF32BN;
+    const int64_t blocks32 = (int64_t)units * ((P.nq + 31) / 32);
+    const int tiles = (P.nk + kF32BN - 1) / kF32BN;
     if (PA_F32_SPLIT && blocks32 < 512 && tiles >= 4) {
-        ProfScope ps("mfma_fwd_f32", s);
-        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_fwd_f32_split<64, 4>), dim3(blocks32), dim3(64 * 4), 0, s, P);
-        else hipLaunchKernelGGL((k_mfma_fwd_f32_split<128, 4>), dim3(blocks32), dim3(64 * 4), 0, s, P);
+        ProfScope ps("mfma_fwd_f32_split", s);
+        if (P.dim == 64) hipLaunchKernelGGL((k_mfma_fwd_f32_split<64, 4>), dim3((uint32_t)blocks32), dim3(64 * 4), 0, s, P);
+        else hipLaunchKernelGGL((k_mfma_fwd_f32_split<128, 4>), dim3((uint32_t)blocks32), dim3(64 * 4), 0, s, P);
         return;
     }
     // waves per workgroup: the most that still give the grid two workgroups per CU

@@ -186,6 +186,16 @@ __device__ __forceinline__ void store8_a8(T* p, const float* f) {
     reinterpret_cast<uint2*>(p)[0] = a;
     reinterpret_cast<uint2*>(p)[1] = c;
 }
+// fp32 rows (16-byte aligned, as the fp32 MFMA kernels require): two 16-byte accesses
+template <>
+__device__ __forceinline__ void load8_a8<float>(const float* p, float* f) {
+    load8<float>(p, f);
+}
+template <>
+__device__ __forceinline__ void store8_a8<float>(float* p, const float* f) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(f[0], f[1], f[2], f[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(f[4], f[5], f[6], f[7]);
+}
 
 constexpr int kFixThreads = 1024;  // per-head reductions: many rows in flight on one CU
 
@@ -733,10 +743,10 @@ __global__ __launch_bounds__(kFixThreads) void k_fix_rows(GradDev G) {
     for (int i = slot; i < P.nq; i += R) {
         if (!degenerate_row(G, row0 + i)) continue;
         const float ic = G.ws_invc[row0 + i];
-        const uint4 raw = *reinterpret_cast<const uint4*>(G.dout.row<T>(b, h, i) + c0);
-        const T* e8 = reinterpret_cast<const T*>(&raw);
+        float g8[8];
+        load8<T>(G.dout.row<T>(b, h, i) + c0, g8);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) u[e] += ic * to_f(e8[e]);
+        for (int e = 0; e < 8; ++e) u[e] += ic * g8[e];
         wsum += ic * G.ws_D[row0 + i];
         cnt += 1.f;
     }
@@ -1160,7 +1170,8 @@ void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, hi
 
 void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s) {
     const bool d64 = G.f.dim == 64;
-    if (dtype == PA_F16) d64 ? launch_mask_fixups_t<f16, 64>(G, s) : launch_mask_fixups_t<f16, 128>(G, s);
+    if (dtype == PA_F32) d64 ? launch_mask_fixups_t<float, 64>(G, s) : launch_mask_fixups_t<float, 128>(G, s);
+    else if (dtype == PA_F16) d64 ? launch_mask_fixups_t<f16, 64>(G, s) : launch_mask_fixups_t<f16, 128>(G, s);
     else d64 ? launch_mask_fixups_t<bf16, 64>(G, s) : launch_mask_fixups_t<bf16, 128>(G, s);
 }
 

@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolyattn.so"
 
-PA_ABI_VERSION = 7
+PA_ABI_VERSION = 8
 PA_MAX_ORDER = 8
 
 PA_OK = 0
@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "pa_struct_size",
     "pa_profile_start",
     "pa_profile_stop",
+    "pa_measure_clock",
     "pa_attn_pass_fwd",
     "pa_attn_pass_fwd_workspace",
     "pa_attn_pass_bwd_workspace",
@@ -290,6 +291,8 @@ def _configure(lib) -> None:
     lib.pa_profile_start.restype = c_int
     lib.pa_profile_stop.restype = c_int
     lib.pa_profile_stop.argtypes = [ctypes.POINTER(PaKernelTime), c_int, ctypes.POINTER(c_int)]
+    lib.pa_measure_clock.restype = c_int
+    lib.pa_measure_clock.argtypes = [ctypes.POINTER(ctypes.c_double), c_void_p]
     lib.pa_attn_pass_fwd.restype = c_int
     lib.pa_attn_pass_fwd.argtypes = [ctypes.POINTER(PaPass), c_void_p]
     lib.pa_attn_pass_fwd_workspace.restype = c_size_t
@@ -384,3 +387,12 @@ class KernelProfile:
         self.times = {buf[i].name.decode(): (buf[i].launches, buf[i].total_ms)
                       for i in range(n.value)}
         return False
+
+
+def measure_clock(device=None) -> float:
+    """The GPU's shader clock in GHz under a short all-CU MFMA load on the current stream of
+    ``device`` (libpolyattn pa_measure_clock): s_memtime cycles per 100 MHz s_memrealtime tick."""
+    ghz = ctypes.c_double(0.0)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    check(load().pa_measure_clock(ctypes.byref(ghz), c_void_p(stream)), "pa_measure_clock")
+    return ghz.value

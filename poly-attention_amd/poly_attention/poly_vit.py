@@ -114,6 +114,15 @@ class PolyViT(Module):
                                        use_flash_kernel=use_flash_kernel)
         self.linear_head = nn.Linear(dim, num_classes, bias=False)
 
+    def _apply(self, fn, recurse=True):
+        # Module casts (.half(), .to(torch.bfloat16), ...) must not round the position table:
+        # the reference keeps it in fp32 and casts it at each forward (poly_vit.py:96), so that
+        # e.g. model.half().float() still adds the exact table.  Only the device follows fn.
+        table = self.pos_embedding
+        out = super()._apply(fn, recurse)
+        self.pos_embedding = table.to(device=self.pos_embedding.device, dtype=torch.float32)
+        return out
+
     def forward(self, img: Tensor) -> Tensor:
         tokens = self.to_patch_embedding(img)
         tokens = tokens + self.pos_embedding.to(img.device, dtype=img.dtype)

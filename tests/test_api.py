@@ -124,6 +124,21 @@ def test_poly_vit(order):  # reference tests:194-211
     assert preds.shape == (2, 10) and not torch.isnan(preds).any()
 
 
+def test_poly_vit_position_table_survives_casts():
+    """The reference keeps the sin-cos table in fp32 and casts it per forward (poly_vit.py:96):
+    module casts must leave the stored table exact (a half round trip would round it)."""
+    from oracle.poly_oracle import posemb_sincos_2d
+
+    vit = PolyViT(image_size=32, patch_size=8, num_classes=10, dim=64, depth=1, heads=4,
+                  mlp_dim=128)
+    exact = posemb_sincos_2d(h=4, w=4, dim=64)
+    assert not torch.equal(exact.half().float(), exact)  # the cast would be visible
+    vit = vit.half().float().to(torch.bfloat16)
+    assert vit.pos_embedding.dtype == torch.float32
+    assert torch.equal(vit.pos_embedding, exact)
+    assert vit.linear_head.weight.dtype == torch.bfloat16  # the rest of the module was cast
+
+
 def test_contexts():  # reference tests:343-370
     attn = PolyAttention(dim=64, heads=4)
     x, c1, c2, c3 = (torch.randn(2, 16, 64) for _ in range(4))

@@ -42,21 +42,29 @@ def run_pass(q, k, v, vmul=None, bias=None, key_mask=None, query_mask=None, caus
                               softclamp=softclamp)
     ref_out, ref_lse = O.attn_pass(*o_in, key_mask=key_mask, query_mask=query_mask,
                                    causal=causal, softclamp_value=softclamp)
-    res = dict(out=(out, ref_out), lse=(lse, ref_lse))
+    res = dict(out=(out, ref_out, None), lse=(lse, ref_lse, None))
     if grads:
         do = randn(ref_out.shape, q.dtype, seed)
         dl = randn(ref_lse.shape, torch.float32, seed + 1)
         torch.autograd.backward((out, lse), (do.to(d), dl.to(d)))
         torch.autograd.backward((ref_out, ref_lse), (do.float(), dl))
-        for name, a, b in zip(("dq", "dk", "dv", "dvmul", "dbias"), g_in, o_in):
+        lp_in = [None] * len(inputs)
+        if q.dtype != torch.float32:
+            # the oracle in the inputs' own precision: the reference's arithmetic at that
+            # precision, whose drift from the fp32 oracle bounds the low-precision gradients
+            lp_in = [t.detach().clone().requires_grad_() if t is not None else None for t in inputs]
+            lp_out, lp_lse = O.attn_pass(*lp_in, key_mask=key_mask, query_mask=query_mask,
+                                         causal=causal, softclamp_value=softclamp)
+            torch.autograd.backward((lp_out, lp_lse), (do, dl.to(lp_lse.dtype)))
+        for name, a, b, c in zip(("dq", "dk", "dv", "dvmul", "dbias"), g_in, o_in, lp_in):
             if a is not None:
-                res[name] = (a.grad, b.grad)
+                res[name] = (a.grad, b.grad, c.grad if c is not None else None)
     torch.cuda.synchronize()
     return res
 
 
 def check(res, dtype, what=""):
-    for name, (got, ref) in res.items():
+    for name, (got, ref, ref_lp) in res.items():
         if name == "lse":  # fp32 in both, from inputs rounded to dtype
             got = got.float().cpu()
             ok = ref.detach() > -1e30
@@ -65,7 +73,7 @@ def check(res, dtype, what=""):
             continue
         # gradients (dbias stored in fp32) are computed from inputs in dtype
         assert_parity(got, ref, dtype, f"{what} {name}", tol=TOL[dtype],
-                      grad=name.startswith("d"))
+                      grad=name.startswith("d"), ref_lp=ref_lp)
 
 
 @param("dtype", (torch.float32, torch.bfloat16, torch.float16))
@@ -129,7 +137,10 @@ def test_pass_masked_mfma_head_dims(dtype, d, n, causal, gqa):
       row of batch 1 is fully masked the same way;
     * a -inf bias entry (class 2) and query-masked rows (uniform over the bias-class-0 keys);
     * gqa: 4 query heads over 2 key heads with a value multiplier (a middle chain level).
-    n = 150 leaves a key count that is not a multiple of 4 (row-padded key terms)."""
+    n = 150 leaves a key count that is not a multiple of 4 (row-padded key terms).  fp32 passes
+    take the fp32 MFMA backward kernels and the same fix-ups (the kernel profile shows them)."""
+    from poly_attention import _lib
+
     B, H, HK = 2, 4, (2 if gqa else 4)
     q = randn((B, H, n, d), dtype, 31)
     k, v = (randn((B, HK, n, d), dtype, s) for s in (32, 33))
@@ -146,8 +157,14 @@ def test_pass_masked_mfma_head_dims(dtype, d, n, causal, gqa):
     qm[0, -7:] = False
     if not causal:
         km[1, 6:] = False
-    res = run_pass(q, k, v, vmul=vmul, bias=bias, key_mask=km, query_mask=qm, causal=causal)
+    with _lib.KernelProfile() as prof:
+        res = run_pass(q, k, v, vmul=vmul, bias=bias, key_mask=km, query_mask=qm, causal=causal)
     check(res, dtype, f"masked mfma {dtype} d={d} n={n} causal={causal} gqa={gqa}")
+    ran = set(prof.times)
+    if dtype == torch.float32:
+        assert any(k.startswith("mfma_bwd_f32_dq") for k in ran), sorted(ran)
+        assert any(k.startswith("mfma_bwd_f32_dkv") for k in ran), sorted(ran)
+    assert "fix_rows" in ran and "fix_keys" in ran, sorted(ran)
 
 
 @param("dtype", (torch.bfloat16, torch.float32))
@@ -282,3 +299,53 @@ def test_f32_forward_multiwave_workgroups(B, H, causal):
     v = randn((B, H, 1024, 64), torch.float32, 83)
     check(run_pass(q, k, v, causal=causal, grads=False), torch.float32,
           f"fp32 multi-wave B={B} H={H} causal={causal}")
+
+
+def _run_profiled(q, k, v, **kw):
+    from poly_attention import _lib
+
+    with _lib.KernelProfile() as prof:
+        res = run_pass(q, k, v, **kw)
+    return res, prof.times
+
+
+SPLIT_KERNELS = ("mfma_fwd_f32_split", "mfma_bwd_f32_dq_split", "mfma_bwd_f32_dkv_split")
+
+
+@param("d", (64, 128))
+@param("causal", (False, True))
+def test_f32_split_kernels_head_dims(d, causal):
+    """fp32 grids of fewer than 512 blocks of 32 rows take the split kernels: the forward's and
+    dQ's key tiles, or dK/dV's query tiles, over four waves whose partial results are merged in
+    wave order.  Head dims 64 and 128 at n = 160 (five tiles per block), against the oracle at
+    1e-4; the kernel profile shows the three split kernels ran."""
+    q, k, v = (randn((1, 3, 160, d), torch.float32, s) for s in (91, 92, 93))
+    res, times = _run_profiled(q, k, v, causal=causal)
+    check(res, torch.float32, f"fp32 split d={d} causal={causal}")
+    for name in SPLIT_KERNELS:
+        assert name in times, f"{name} did not run (kernels: {sorted(times)})"
+
+
+@param("causal", (False, True))
+def test_f32_split_kernels_gqa_bias_vmul(causal):
+    """The split backward of a middle level: 8 query heads over 2 KV heads (dK/dV sums the four
+    heads of a group over its waves), key bias, value multiplier, n = 128."""
+    q = randn((1, 8, 128, 64), torch.float32, 94)
+    k, v, vmul = (randn((1, 2, 128, 64), torch.float32, s) for s in (95, 96, 97))
+    bias = randn((1, 2, 128), torch.float32, 98, scale=2.0)
+    res, times = _run_profiled(q, k, v, vmul=vmul, bias=bias, causal=causal)
+    check(res, torch.float32, f"fp32 split gqa+bias+vmul causal={causal}")
+    for name in SPLIT_KERNELS:
+        assert name in times, f"{name} did not run (kernels: {sorted(times)})"
+
+
+def test_f32_split_kernels_causal_cross_lengths():
+    """Causal with 96 queries over 200 keys (top-left aligned: later keys fully masked for every
+    query) on the split kernels, d = 128, 4 query heads over 2 KV heads (so that dK/dV has the
+    four query tiles per key block its split needs)."""
+    q = randn((1, 4, 96, 128), torch.float32, 99)
+    k, v = (randn((1, 2, 200, 128), torch.float32, s) for s in (100, 101))
+    res, times = _run_profiled(q, k, v, causal=True)
+    check(res, torch.float32, "fp32 split causal 96x200")
+    for name in SPLIT_KERNELS:
+        assert name in times, f"{name} did not run (kernels: {sorted(times)})"

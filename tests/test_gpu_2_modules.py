@@ -43,10 +43,15 @@ def test_flash_poly_attention(dtype, causal, softclamp_value, seq_len):
     out_ref.backward(dout.float())
     out = flash_poly_attention(*g_t, softclamp_value=softclamp_value, is_causal=causal)
     out.backward(dout.to(d))
+    lp_t = [t.clone().requires_grad_() for t in tensors]  # the oracle in the inputs' dtype
+    if dtype != torch.float32:
+        lp, _, _ = O.reference_poly_attention(lp_t[0], lp_t[1], lp_t[1], lp_t[2], lp_t[3],
+                                              softclamp_value=softclamp_value, causal=causal)
+        lp.backward(dout)
     what = f"flash op {dtype} n={seq_len} causal={causal} sc={softclamp_value}"
     assert_parity(out, out_ref, dtype, f"{what} out")
-    for i, (a, b) in enumerate(zip(g_t, o_t)):
-        assert_parity(a.grad, b.grad, dtype, f"{what} grad {i}", grad=True)
+    for i, (a, b, c) in enumerate(zip(g_t, o_t, lp_t)):
+        assert_parity(a.grad, b.grad, dtype, f"{what} grad {i}", grad=True, ref_lp=c.grad)
 
 
 def test_flash_poly_attention_context_mask_disallowed():  # reference tests:541-558
@@ -152,9 +157,14 @@ def test_npoly_module_epilogue_e2e(order, gate_root):
 def test_fused_epilogue_equals_torch_tail(dtype, root_heads, root_sigmoid, gate):
     """The order-2 chain with the epilogue fused into pass 2 against the same chain followed
     by torch's element-wise tail (poly_attention.py:342-351) on the same kernels: y, and the
-    gradients of q1..v3, root and gate.  Same roundings in the same order, so the bound is
-    one storage rounding (tol 0) in bf16 / f16; fp32 allows for the sigmoid's last bit and
-    the order of the GQA root's head sum (tol 1e-5)."""
+    gradients of q1..v3, root and gate.  An implementation-consistency check (the oracle
+    parity of the epilogue is test_order2_module_e2e's and test_gpu_14's): both sides are
+    results stored in bf16 / f16, each rounded on its own, so y is held to two storage
+    roundings of the value (tol 0); the gradients to four roundings of their largest value,
+    since torch's tail also rounds its intermediate products (dy * out, the sigmoid's
+    derivative, a GQA root's per-head terms before their sum) where the fused epilogue keeps
+    them in fp32.  fp32 allows for the sigmoid's last bit and the order of the GQA root's
+    head sum (tol 1e-5)."""
     from poly_attention import _ops
 
     d = dev()
@@ -184,9 +194,14 @@ def test_fused_epilogue_equals_torch_tail(dtype, root_heads, root_sigmoid, gate)
     names = ["y", "dq1", "dq2", "dq3", "dv3"] + (["droot"] if root is not None else []) + \
         (["dgate"] if gate else [])
     what = f"fused epilogue {dtype} root_heads={root_heads} sigmoid={root_sigmoid} gate={gate}"
+    u = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}[dtype]
     for name, a, b in zip(names, fused, [ref.detach()] + [t.grad for t in leaves]):
-        assert_parity(a, b.float().cpu(), dtype, f"{what} {name}",
-                      tol=1e-5 if dtype == torch.float32 else 0.0, grad=name != "y")
+        b = b.float().cpu()
+        if dtype == torch.float32:
+            tol = 1e-5
+        else:
+            tol = 0.0 if name == "y" else 4 * u * b.abs().max().item()
+        assert_parity(a, b, dtype, f"{what} {name}", tol=tol, grad=name != "y", roundings=2)
 
 
 @param("order", (2, 3, 4))

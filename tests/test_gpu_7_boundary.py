@@ -103,10 +103,15 @@ def test_flash_op_mask_masks_keys_of_both_passes(dtype, causal):
     dout = torch.randn(ref.shape).to(dtype)
     out.backward(dout.to(d))
     ref.backward(dout.float())
+    lp_t = [t.clone().requires_grad_() for t in ts]  # the oracle in the inputs' dtype
+    if dtype != torch.float32:
+        lp, _, _ = O.reference_poly_attention(lp_t[0], lp_t[1], lp_t[1], lp_t[2], lp_t[3],
+                                              causal=causal, context_mask=(mask, mask))
+        lp.backward(dout)
     what = f"flash op key mask {dtype} causal={causal}"
     assert_parity(out, ref, dtype, f"{what} out")
-    for i, (a, b) in enumerate(zip(g, o)):
-        assert_parity(a.grad, b.grad, dtype, f"{what} grad {i}", grad=True)
+    for i, (a, b, c) in enumerate(zip(g, o, lp_t)):
+        assert_parity(a.grad, b.grad, dtype, f"{what} grad {i}", grad=True, ref_lp=c.grad)
 
 
 # ---------------------------------------------------------------------------------------
@@ -184,5 +189,10 @@ def test_compile_autocast_module_matches_oracle():
     xo = x.clone().requires_grad_()
     ref = O.order2_forward(params, cfg, xo)
     ref.sum().backward()
+    # the oracle with its weights and input in float16 (a bound at least as loose as
+    # autocast's mixed float16 / fp32 arithmetic)
+    x16 = x.half().requires_grad_()
+    O.order2_forward({k: v.half() for k, v in params.items()}, cfg, x16).float().sum().backward()
     assert_parity(out, ref, torch.float16, "compile+autocast out")
-    assert_parity(xg.grad, xo.grad, torch.float16, "compile+autocast dx", grad=True)
+    assert_parity(xg.grad, xo.grad, torch.float16, "compile+autocast dx", grad=True,
+                  ref_lp=x16.grad)

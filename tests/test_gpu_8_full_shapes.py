@@ -70,11 +70,15 @@ def test_config2_full_length_core_slices():
         ref, _, _ = O.reference_poly_attention(o_in[0], o_in[1], o_in[1], o_in[2], o_in[3],
                                                causal=True)
         ref.backward(dout[b:b + 1, h:h + 1].float())
+        lp_in = [t.detach()[b:b + 1, h:h + 1].cpu().requires_grad_() for t in g_in]  # bf16 oracle
+        lp, _, _ = O.reference_poly_attention(lp_in[0], lp_in[1], lp_in[1], lp_in[2], lp_in[3],
+                                              causal=True)
+        lp.backward(dout[b:b + 1, h:h + 1])
         what = f"config 2 N={N} slice (b={b}, h={h})"
         assert_parity(out[b:b + 1, h:h + 1], ref, torch.bfloat16, f"{what} out")
-        for name, a, r in zip(("dq1", "dq2", "dq3", "dv3"), g_in, o_in):
+        for name, a, r, c in zip(("dq1", "dq2", "dq3", "dv3"), g_in, o_in, lp_in):
             assert_parity(a.grad[b:b + 1, h:h + 1], r.grad, torch.bfloat16, f"{what} {name}",
-                          grad=True)
+                          grad=True, ref_lp=c.grad)
 
 
 def test_config3_polyvit_bf16_forward():
