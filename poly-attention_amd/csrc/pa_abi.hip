@@ -194,7 +194,7 @@ size_t bwd_ws_bytes(const pa_pass& f) {
     if (pass_masked(f)) {
         const size_t kheads = (size_t)f.batch * f.k.heads;
         if (f.key_mask.ptr) n += align256(kheads * key_term_stride(f) * sizeof(float));
-        n += align256((size_t)f.batch * f.heads * (f.dim + 2) * sizeof(float));
+        n += align256((size_t)f.batch * f.heads * fix_row_chunks(f.nq) * (f.dim + 2) * sizeof(float));
         n += align256(kheads * 2 * sizeof(int32_t));
     }
     return n;
@@ -502,7 +502,7 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
             w += align256((size_t)p->batch * hk * nkp * sizeof(float));
         }
         G.ws_part = reinterpret_cast<float*>(w);
-        w += align256((size_t)p->batch * H * (p->dim + 2) * sizeof(float));
+        w += align256((size_t)p->batch * H * fix_row_chunks(p->nq) * (p->dim + 2) * sizeof(float));
         int32_t* kcnt = reinterpret_cast<int32_t*>(w);
         G.ws_kcnt = kcnt;
         launch_key_terms(G, kterm, nkp, kcnt, s);

@@ -96,9 +96,14 @@ struct GradDev {
                            // seeds, -lse/scale (lse*log2e with softclamp) and -D
     // masked passes on the MFMA kernels (null otherwise)
     const int32_t* ws_kcnt;  // [B, hk, 2]: keys of bias class 0 and of bias class 1
-    float* ws_part;          // [B, heads, dim + 2]: over the fully-masked rows of a head,
-                             // sum dO / c1, sum D / c1 and their number
+    float* ws_part;          // [B, heads, chunks, dim + 2]: over the fully-masked rows of a
+                             // chunk of kFixRowChunk rows of a head, sum dO / c1, sum D / c1
+                             // and their number
 };
+
+// rows per partial sum of the masked backward's fully-masked rows (GradDev::ws_part)
+constexpr int kFixRowChunk = 512;
+__host__ __device__ inline int fix_row_chunks(int nq) { return (nq + kFixRowChunk - 1) / kFixRowChunk; }
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
 

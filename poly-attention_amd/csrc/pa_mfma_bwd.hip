@@ -420,9 +420,21 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
     }
     float dbias = 0.f;
 
+    // a key block none of whose keys has a bias-class-0 term (masked keys: padding) receives
+    // nothing from any query: the sweep is skipped and the block's gradients are written as
+    // zero.  Every wave reads the whole block's terms, so all reach the same decision.
+    static_assert(kKvBK == 128, "two keys per lane");
+    bool block_dead = false;
+    if (HAS_BIAS) {
+        const int k0 = kblk * kKvBK;
+        const float y0 = k0 + lane < P.nk ? P.bias.scalar(b, h0, k0 + lane) : -INFINITY;
+        const float y1 = k0 + 64 + lane < P.nk ? P.bias.scalar(b, h0, k0 + 64 + lane) : -INFINITY;
+        block_dead = !__any(bias_class(y0) == 0 || bias_class(y1) == 0);
+    }
+
     const int q_start = CAUSAL ? (kblk * kKvBK / BQ) * BQ : 0;
     const int nt = P.nq > q_start ? (P.nq - q_start + BQ - 1) / BQ : 0;  // tiles per query head
-    const int total = nt * rep;
+    const int total = block_dead ? 0 : nt * rep;
 
     // direct loads: thread tid carries chunk n*256 + tid of a tile: row p / CPR, chunk p % CPR
     const int qsn = (int)P.q.sn, osn = (int)G.dout.sn;
@@ -1053,17 +1065,31 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
         lds_barrier();
         if (t + 2 < ntiles) issue((t + 2) * BN, st == 0 ? 2 : st - 1);
     };
+    // this wave's converted copy of a tile's key terms; true when every one is -inf (masked
+    // keys: every probability of the tile is 0)
+    auto conv_bias = [&](int stg) __attribute__((always_inline)) -> bool {
+        float x;
+        if (bes == 4) x = sBraw[stg][lane];
+        else x = (float)reinterpret_cast<const T*>(&sBraw[stg][0])[lane];
+        const float xw = bias_class(x) == 0 ? x * bmul : -INFINITY;
+        sBw[w][lane] = xw;
+        return !__any(xw != -INFINITY);
+    };
     for (int t = 0; t < nact; ++t) {
-        const int j0 = t * BN;
         enter(t);
+        if (HAS_BIAS) {
+            // tiles of masked keys are passed through (loads and barriers only); the last
+            // active tile is computed even then (its probabilities are 0)
+            bool dead = conv_bias(st);
+            while (dead && t + 1 < nact) {
+                st = st == 2 ? 0 : st + 1;
+                enter(++t);
+                dead = conv_bias(st);
+            }
+        }
+        const int j0 = t * BN;
         const T* Kt = sK + st * ELEMS;
         const T* Vt = sV + st * ELEMS;
-        if (HAS_BIAS) {
-            float x;
-            if (bes == 4) x = sBraw[st][lane];
-            else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
-            sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
-        }
         // the two 32-key blocks in a software pipeline (MFMAs of one beside the VALU of the other)
         auto scores = [&](int kb, f32x16_t& s, f32x16_t& dp) __attribute__((always_inline)) {
             s = zero16();

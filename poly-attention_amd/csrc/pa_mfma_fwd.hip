@@ -703,7 +703,14 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
             float x;
             if (bes == 4) x = sBraw[st][lane];
             else x = (float)reinterpret_cast<const T*>(&sBraw[st][0])[lane];
-            sBw[w][lane] = bias_class(x) == 0 ? x * bmul : -INFINITY;
+            const float xw = bias_class(x) == 0 ? x * bmul : -INFINITY;
+            sBw[w][lane] = xw;
+            // a tile whose every key term is -inf (masked keys: padding) adds nothing to any
+            // row; a row that has seen only such keys keeps m = -inf and l = 0 either way
+            if (!__any(xw != -INFINITY)) {
+                st = st == 2 ? 0 : st + 1;
+                continue;
+            }
         }
 #if PA_FWD_USPLIT
         if constexpr (QB == 2 && W::PLAIN && PA_FWD_SUMCHECK) {

@@ -199,6 +199,22 @@ __device__ __forceinline__ void store8_a8<float>(float* p, const float* f) {
 
 constexpr int kFixThreads = 1024;  // per-head reductions: many rows in flight on one CU
 
+// p[0] + p[S] + p[2 S] + ... (n terms, stride S) in that order, eight loads in flight at a
+// time (partial sums are few; a loop of one load per step waits a round trip per term)
+template <int S>
+__device__ __forceinline__ float ordered_sum(const float* p, int n) {
+    constexpr int U = 8;
+    float a = 0.f;
+    for (int c0 = 0; c0 < n; c0 += U) {
+        float x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = c0 + u < n ? p[(int64_t)(c0 + u) * S] : 0.f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) a += x[u];
+    }
+    return a;
+}
+
 // S0 of k_fwd_fixup, one slot's share (key rows slot, slot + R, ...): its key rows four at a
 // time, each round's loads issued unconditionally (rows past the end read the last row and
 // count for nothing) before the first is used -- a load per dependent step took 27 us at 4096
@@ -423,43 +439,54 @@ __global__ __launch_bounds__(kSimtRows) void k_bwd_pre(GradDev G) {
 
 // The same preprocess for 16-bit types with head dims that are multiples of 8: LPR lanes
 // per row read 16 bytes each (a wave covers 64/LPR whole rows per load), then reduce.
+constexpr int kPreRows = 4;  // rows per lane group of k_bwd_pre_vec, all loads issued first
 template <typename T, int LPR>
 __global__ __launch_bounds__(256) void k_bwd_pre_vec(GradDev G) {
     const PassDev& P = G.f;
-    constexpr int kRows = 256 / LPR;
-    const int64_t total = (int64_t)P.batch * P.heads * P.nq;
-    const int64_t r = (int64_t)blockIdx.x * kRows + threadIdx.x / LPR;
-    const int sub = threadIdx.x % LPR;
-    if (r >= total) return;  // whole LPR-lane groups leave together
-    const int i = (int)(r % P.nq);
-    const int h = (int)((r / P.nq) % P.heads), b = (int)(r / ((int64_t)P.nq * P.heads));
-    const int d0 = sub * 8;
-    float dsum = 0.f;
-    if (d0 < P.dim) {
-        const uint4 ov = *reinterpret_cast<const uint4*>(P.out.row<T>(b, h, i) + d0);
-        const uint4 gv = *reinterpret_cast<const uint4*>(G.dout.row<T>(b, h, i) + d0);
-        const T* oe = reinterpret_cast<const T*>(&ov);
-        const T* ge = reinterpret_cast<const T*>(&gv);
+    constexpr int kRows = 256 / LPR;  // lane groups per workgroup
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int sub = threadIdx.x % LPR, d0 = sub * 8;
+    const int i0 = (int)blockIdx.x * kRows * kPreRows + (int)threadIdx.x / LPR;
+    const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
+    // a lane group takes rows i0, i0 + kRows, ... of (b, h): every load of its rows goes out
+    // before the first is used (one memory round trip per workgroup)
+    uint4 ov[kPreRows], gv[kPreRows];
+    float dl[kPreRows], l[kPreRows];
+#pragma unroll
+    for (int u = 0; u < kPreRows; ++u) {
+        const int i = min(i0 + u * kRows, P.nq - 1);
+        ov[u] = gv[u] = make_uint4(0u, 0u, 0u, 0u);
+        if (d0 < P.dim) {
+            ov[u] = *reinterpret_cast<const uint4*>(P.out.row<T>(b, h, i) + d0);
+            gv[u] = *reinterpret_cast<const uint4*>(G.dout.row<T>(b, h, i) + d0);
+        }
+        dl[u] = G.dlse.ok() ? *G.dlse.row<float>(b, h, i) : 0.f;
+        l[u] = *P.lse.row<float>(b, h, i);
+    }
+#pragma unroll
+    for (int u = 0; u < kPreRows; ++u) {
+        const int i = i0 + u * kRows;
+        const T* oe = reinterpret_cast<const T*>(&ov[u]);
+        const T* ge = reinterpret_cast<const T*>(&gv[u]);
+        float dsum = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) dsum += to_f(oe[e]) * to_f(ge[e]);
-    }
 #pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off);
-    if (sub != 0) return;
-    const float dl = G.dlse.ok() ? *G.dlse.row<float>(b, h, i) : 0.f;
-    const float l = *P.lse.row<float>(b, h, i);
-    float lseb = l, invc = 0.f;
-    if (l > kMaskedThreshold) {
-        dsum -= dl;
-    } else {  // fully-masked row (rare): count its class-1 entries
-        const float c1 = degenerate_count(G, b, h, i);
-        lseb = INFINITY;
-        invc = c1 > 0.f ? 1.f / c1 : 0.f;
-        dsum = c1 > 0.f ? dsum - c1 * dl : 0.f;
+        for (int off = LPR / 2; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off);
+        if (sub != 0 || i >= P.nq) continue;
+        float lseb = l[u], invc = 0.f;
+        if (l[u] > kMaskedThreshold) {
+            dsum -= dl[u];
+        } else {  // fully-masked row (rare): count its class-1 entries
+            const float c1 = degenerate_count(G, b, h, i);
+            lseb = INFINITY;
+            invc = c1 > 0.f ? 1.f / c1 : 0.f;
+            dsum = c1 > 0.f ? dsum - c1 * dl[u] : 0.f;
+        }
+        G.ws_D[row0 + i] = dsum;
+        G.ws_lse[row0 + i] = lseb;
+        G.ws_invc[row0 + i] = invc;
     }
-    G.ws_D[r] = dsum;
-    G.ws_lse[r] = lseb;
-    G.ws_invc[r] = invc;
 }
 
 // probability of entry (i, j) given the row's (lse, 1/c1) and the entry's mask state
@@ -718,20 +745,23 @@ __device__ __forceinline__ bool degenerate_row(const GradDev& G, int64_t r) {
     return G.ws_lse[r] == INFINITY && G.ws_invc[r] > 0.f;
 }
 
-// Part A sums, one workgroup per (b, query head): D/8 lanes per row, 16 bytes of dO each, all
-// rows in flight at once; the row slots are then summed through LDS.
+// Part A sums over the fully-masked rows, one workgroup per (b, query head, chunk of
+// kFixRowChunk rows): D/8 lanes per row, 16 bytes of dO each; each lane group's rows go four
+// at a time with every load issued first (rows that are not fully masked weigh 0); the row
+// slots are then summed through LDS into the chunk's partial row (fixed order: the sums are
+// deterministic).  A chunk without such a row writes zeros after one scan of its lse.
 template <typename T, int D>
-__global__ __launch_bounds__(kFixThreads) void k_fix_rows(GradDev G) {
+__global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
     const PassDev& P = G.f;
-    constexpr int LPR = D / 8, R = kFixThreads / LPR;  // lanes per row, row slots
-    const int h = blockIdx.x, b = blockIdx.y;
+    constexpr int LPR = D / 8, R = 256 / LPR, U = 8;  // lanes per row, row slots, rows per round
+    static_assert(kFixRowChunk % (R * U) == 0, "whole rounds per chunk");
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int slot = threadIdx.x / LPR, c0 = (threadIdx.x % LPR) * 8;
     const int64_t row0 = ((int64_t)b * P.heads + h) * P.nq;
-    float* part = G.ws_part + ((int64_t)b * P.heads + h) * (D + 2);
-    // most heads hold no fully-masked row (lse = +inf): one coalesced scan decides, and the
-    // row-slot loop below runs only where one exists
+    const int i0 = c * kFixRowChunk, i1 = min(P.nq, i0 + kFixRowChunk);
+    float* part = G.ws_part + (((int64_t)b * P.heads + h) * fix_row_chunks(P.nq) + c) * (D + 2);
     bool any = false;
-    for (int i = threadIdx.x; i < P.nq; i += kFixThreads) any |= G.ws_lse[row0 + i] == INFINITY;
+    for (int i = i0 + (int)threadIdx.x; i < i1; i += 256) any |= G.ws_lse[row0 + i] == INFINITY;
     if (!__syncthreads_or(any)) {
         if (threadIdx.x < D + 2) part[threadIdx.x] = 0.f;
         return;
@@ -739,16 +769,23 @@ __global__ __launch_bounds__(kFixThreads) void k_fix_rows(GradDev G) {
     float u[8], wsum = 0.f, cnt = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) u[e] = 0.f;
-#pragma unroll 4
-    for (int i = slot; i < P.nq; i += R) {
-        if (!degenerate_row(G, row0 + i)) continue;
-        const float ic = G.ws_invc[row0 + i];
-        float g8[8];
-        load8<T>(G.dout.row<T>(b, h, i) + c0, g8);
+    for (int ib = i0 + slot; ib < i1; ib += R * U) {
+        float ic[U], dd[U], g8[U][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) u[e] += ic * g8[e];
-        wsum += ic * G.ws_D[row0 + i];
-        cnt += 1.f;
+        for (int k = 0; k < U; ++k) {
+            const int i = min(ib + k * R, i1 - 1);
+            const bool dg = ib + k * R < i1 && degenerate_row(G, row0 + i);
+            ic[k] = dg ? G.ws_invc[row0 + i] : 0.f;
+            dd[k] = G.ws_D[row0 + i];
+            load8<T>(G.dout.row<T>(b, h, i) + c0, g8[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) u[e] += ic[k] * g8[k][e];
+            wsum += ic[k] * dd[k];
+            cnt += ic[k] > 0.f ? 1.f : 0.f;
+        }
     }
     __shared__ float sU[R][D];
     __shared__ float sW[R], sC[R];
@@ -771,14 +808,24 @@ __global__ __launch_bounds__(kFixThreads) void k_fix_rows(GradDev G) {
     }
 }
 
+// The part A sums of query head h over its row chunks (entry e of [sum dO / c1 | sum D / c1 |
+// count]), in chunk order.
+template <int D>
+__device__ __forceinline__ float part_sum(const GradDev& G, int b, int h, int e) {
+    const int C = fix_row_chunks(G.f.nq);
+    return ordered_sum<D + 2>(G.ws_part + ((int64_t)b * G.f.heads + h) * C * (D + 2) + e, C);
+}
+
 constexpr int kFixKeys = 256;  // keys per k_fix_keys workgroup
 
 // Part A updates of key head kh: dV (and dvmul) and dbias of the bias-class-0 keys,
-// read-modify-write on what the MFMA dK/dV kernel stored; D/8 lanes per key row.
+// read-modify-write on what the MFMA dK/dV kernel stored; D/8 lanes per key row, each lane
+// group's keys four at a time with their loads issued first.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_fix_keys(GradDev G) {
     const PassDev& P = G.f;
-    constexpr int LPR = D / 8, R = 256 / LPR;
+    constexpr int LPR = D / 8, R = 256 / LPR, U = 4;
+    static_assert(kFixKeys % (R * U) == 0, "whole rounds per workgroup");
     const int kh = blockIdx.y, b = blockIdx.z;
     const int rep = P.heads / G.hk, h0 = kh * rep;
     __shared__ float sU[D];
@@ -786,43 +833,52 @@ __global__ __launch_bounds__(256) void k_fix_keys(GradDev G) {
     const int tid = threadIdx.x;
     if (tid < D + 2) {
         float a = 0.f;
-        for (int hh = 0; hh < rep; ++hh) a += G.ws_part[((int64_t)b * P.heads + h0 + hh) * (D + 2) + tid];
+        for (int hh = 0; hh < rep; ++hh) a += part_sum<D>(G, b, h0 + hh, tid);
         if (tid < D) sU[tid] = a;
         else sWC[tid - D] = a;
     }
     __syncthreads();
     if (sWC[1] == 0.f) return;  // no fully-masked row in the group
     const int slot = tid / LPR, c0 = (tid % LPR) * 8;
+    const bool vm = P.vmul.ok();
     float u[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) u[e] = sU[c0 + e];
-    for (int jj = slot; jj < kFixKeys; jj += R) {
-        const int j = blockIdx.x * kFixKeys + jj;
-        const bool ok = j < P.nk && (!P.bias.ok() || bias_class(P.bias.scalar(b, h0, j)) == 0);
-        float dot = 0.f;
-        if (ok) {
-            float v[8], m[8], g[8];
-            load8(P.v.row<T>(b, h0, j) + c0, v);
-            if (P.vmul.ok()) load8(P.vmul.row<T>(b, h0, j) + c0, m);
-            T* dv = G.dv.wrow<T>(b, h0, j) + c0;
-            load8_a8(dv, g);
+    for (int jb = blockIdx.x * kFixKeys + slot; jb < (int)(blockIdx.x + 1) * kFixKeys; jb += R * U) {
+        bool ok[U];
+        float v[U][8], m[U][8], g[U][8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                dot += u[e] * (P.vmul.ok() ? round_to<T>(v[e] * m[e]) : v[e]);
-                g[e] += P.vmul.ok() ? u[e] * m[e] : u[e];
-            }
-            store8_a8(dv, g);
-            if (P.vmul.ok()) {
-                T* dm = G.dvmul.wrow<T>(b, h0, j) + c0;
-                load8_a8(dm, g);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) g[e] += u[e] * v[e];
-                store8_a8(dm, g);
-            }
+        for (int k = 0; k < U; ++k) {
+            const int j = min(jb + k * R, P.nk - 1);
+            ok[k] = jb + k * R < P.nk && (!P.bias.ok() || bias_class(P.bias.scalar(b, h0, j)) == 0);
+            load8(P.v.row<T>(b, h0, j) + c0, v[k]);
+            if (vm) load8(P.vmul.row<T>(b, h0, j) + c0, m[k]);
+            load8_a8(G.dv.wrow<T>(b, h0, j) + c0, g[k]);
         }
 #pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
-        if (ok && c0 == 0 && G.dbias.ok()) *G.dbias.wrow<float>(b, h0, j) += dot - sWC[0];
+        for (int k = 0; k < U; ++k) {
+            const int j = jb + k * R;
+            float dot = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                dot += u[e] * (vm ? round_to<T>(v[k][e] * m[k][e]) : v[k][e]);
+                g[k][e] += vm ? u[e] * m[k][e] : u[e];
+            }
+            if (ok[k]) {
+                store8_a8(G.dv.wrow<T>(b, h0, j) + c0, g[k]);
+                if (vm) {
+                    T* dm = G.dvmul.wrow<T>(b, h0, j) + c0;
+                    float gm[8];
+                    load8_a8(dm, gm);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) gm[e] += u[e] * v[k][e];
+                    store8_a8(dm, gm);
+                }
+            }
+#pragma unroll
+            for (int off = LPR / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+            if (ok[k] && c0 == 0 && G.dbias.ok()) *G.dbias.wrow<float>(b, h0, j) += dot - sWC[0];
+        }
     }
 }
 
@@ -913,7 +969,7 @@ __global__ __launch_bounds__(kSimtRows) void k_fix_keys_b(GradDev G) {
     float dbias = 0.f;
     const int j_first = blockIdx.x * kSimtRows;
     for (int h = h0; h < h0 + rep; ++h) {
-        if (G.ws_part[((int64_t)b * P.heads + h) * (D + 2) + D + 1] == 0.f) continue;
+        if (part_sum<D>(G, b, h, D + 1) == 0.f) continue;
         for (int i0 = 0; i0 < P.nq; i0 += kSimtKT) {
             const int cnt = min(kSimtKT, P.nq - i0);
             if (P.causal && i0 + cnt - 1 < j_first) continue;  // every row precedes these keys
@@ -1075,8 +1131,8 @@ static void launch_simt_bwd_t(const GradDev& G, hipStream_t s, bool pre, bool dq
         if (vec) {
             int lpr = 1;
             while (lpr * 8 < P.dim) lpr <<= 1;
-            const int64_t total = (int64_t)P.batch * P.heads * P.nq;
-            const unsigned blocks = (unsigned)((total * lpr + 255) / 256);
+            const dim3 blocks((unsigned)(((int64_t)P.nq * lpr + 256 * kPreRows - 1) / (256 * kPreRows)),
+                              P.heads, P.batch);
             switch (lpr) {
                 case 1: hipLaunchKernelGGL((k_bwd_pre_vec<T, 1>), dim3(blocks), dim3(256), 0, s, G); break;
                 case 2: hipLaunchKernelGGL((k_bwd_pre_vec<T, 2>), dim3(blocks), dim3(256), 0, s, G); break;
@@ -1125,7 +1181,7 @@ static void launch_mask_fixups_t(const GradDev& G, hipStream_t s) {
     const PassDev& P = G.f;
     {
         ProfScope ps("fix_rows", s);
-        hipLaunchKernelGGL((k_fix_rows<T, D>), dim3(P.heads, P.batch), dim3(kFixThreads), 0, s, G);
+        hipLaunchKernelGGL((k_fix_rows<T, D>), dim3(fix_row_chunks(P.nq), P.heads, P.batch), dim3(256), 0, s, G);
     }
     {
         ProfScope ps("fix_keys", s);
