@@ -940,41 +940,47 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
     const int qi = qw0 + kcol;
     const bool q_ok = qi < P.nq;
 
+    // rows past the end read row 0 and are zeroed: every prologue load goes out before the
+    // first is used (a branch around a load makes its join wait for the loads before it)
+    const int qc = q_ok ? qi : 0;
     frag qf[D / 16], of[D / 16];
+    u32x4_t orows[D / 16];
+    float l = 0.f, dl = 0.f;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
-        u32x4_t qr = {0u, 0u, 0u, 0u}, orr = {0u, 0u, 0u, 0u};
-        if (q_ok) {
-            qr = *reinterpret_cast<const u32x4_t*>(P.q.row<T>(b, h, qi) + c * 16 + 8 * hh);
-            orr = *reinterpret_cast<const u32x4_t*>(G.dout.row<T>(b, h, qi) + c * 16 + 8 * hh);
-        }
+        u32x4_t qr = *reinterpret_cast<const u32x4_t*>(P.q.row<T>(b, h, qc) + c * 16 + 8 * hh);
+        u32x4_t orr = *reinterpret_cast<const u32x4_t*>(G.dout.row<T>(b, h, qc) + c * 16 + 8 * hh);
+        if (!q_ok) qr = orr = u32x4_t{0u, 0u, 0u, 0u};
         qf[c] = __builtin_bit_cast(frag, qr);
         of[c] = __builtin_bit_cast(frag, orr);
     }
-    const int64_t row = ((int64_t)b * P.heads + h) * P.nq + (q_ok ? qi : 0);
+    if (G.fused_pre) {
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+            orows[c] = *reinterpret_cast<const u32x4_t*>(P.out.row<T>(b, h, qc) + c * 16 + 8 * hh);
+        l = *P.lse.row<float>(b, h, qc);
+        if (G.dlse.ok()) dl = *G.dlse.row<float>(b, h, qc);
+    }
+    const int64_t row = ((int64_t)b * P.heads + h) * P.nq + qc;
     float lse_l2, dpi;
     if (G.fused_pre) {
         // the preprocess of this wave's rows: D = rowsum(dO * O) - dlse, lse (+inf for a
         // fully-masked row), also written for the dK/dV kernel that runs next
         float part = 0.f;
-        if (q_ok) {
 #pragma unroll
-            for (int c = 0; c < D / 16; ++c) {
-                const u32x4_t orow = *reinterpret_cast<const u32x4_t*>(P.out.row<T>(b, h, qi) + c * 16 + 8 * hh);
-                const u32x4_t grow = __builtin_bit_cast(u32x4_t, of[c]);
+        for (int c = 0; c < D / 16; ++c) {
+            const u32x4_t grow = __builtin_bit_cast(u32x4_t, of[c]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float o0, o1, g0, g1;
-                    unpack2<T>(orow[e], o0, o1);
-                    unpack2<T>(grow[e], g0, g1);
-                    part += o0 * g0;
-                    part += o1 * g1;
-                }
+            for (int e = 0; e < 4; ++e) {
+                float o0, o1, g0, g1;
+                unpack2<T>(orows[c][e], o0, o1);
+                unpack2<T>(grow[e], g0, g1);
+                part += o0 * g0;
+                part += o1 * g1;
             }
         }
         const float dsum = xhalf_sum(part);
-        const float l = q_ok ? *P.lse.row<float>(b, h, qi) : 0.f;
-        const float dl = (q_ok && G.dlse.ok()) ? *G.dlse.row<float>(b, h, qi) : 0.f;
+        if (!q_ok) l = dl = 0.f;
         const bool normal = l > kMaskedThreshold;
         const float lseb = normal ? l : INFINITY;
         dpi = normal ? dsum - dl : 0.f;

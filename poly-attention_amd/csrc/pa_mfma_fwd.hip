@@ -608,11 +608,13 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
         v.m = -INFINITY;
         v.l = 0.f;
         const int qi = v.qi;
+        // rows past the end read row 0 and are zeroed: no branch around a load (a branch's join
+        // waits for the loads issued before it)
         const T* qrow = P.q.row<T>(b, h, qi < P.nq ? qi : 0);
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) {
-            u32x4_t raw = {0u, 0u, 0u, 0u};
-            if (qi < P.nq) raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
+            u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + c * 16 + 8 * hh);
+            if (qi >= P.nq) raw = u32x4_t{0u, 0u, 0u, 0u};
             v.qf[c] = __builtin_bit_cast(frag, raw);
         }
 #pragma unroll
