@@ -203,10 +203,10 @@ def test_pass_masked_mfma_key_mask_only(causal):
           f"masked mfma key mask only causal={causal}")
 
 
-@param("dtype", (torch.bfloat16, torch.float16))
+@param("dtype,gqa", ((torch.bfloat16, False), (torch.float16, False), (torch.bfloat16, True)))
 @param("causal", (False, True))
 @param("with_bias", (False, True))
-def test_pass_padding_masks_skip_whole_tiles(dtype, causal, with_bias):
+def test_pass_padding_masks_skip_whole_tiles(dtype, gqa, causal, with_bias):
     """Padding masks that cover whole key tiles and whole key blocks: the MFMA kernels pass
     over a tile whose every key term is -inf (forward and dQ: 64-key tiles) and skip a
     workgroup's sweep when all 128 keys of its block are masked (dK/dV), which must give the
@@ -214,9 +214,13 @@ def test_pass_padding_masks_skip_whole_tiles(dtype, causal, with_bias):
     * batch 0: left padding, keys 0-199 masked (causal rows 0-199 fully masked);
     * batch 1: right padding, keys 300-511 masked;
     * batch 2: keys 128-383 masked (dead tiles between live ones) and every fifth key;
-    * batch 3: a key bias of -inf on keys 64-191 instead of a mask (with_bias), else unmasked."""
+    * batch 3: a key bias of -inf on keys 64-191 instead of a mask (with_bias), else unmasked.
+    gqa: 4 query heads over 2 key heads (the dK/dV workgroups sum both query heads of a group;
+    the key bias, at the key heads, is the key term's)."""
     B, H, n, d = 4, 4, 512, 64
-    q, k, v = (randn((B, H, n, d), dtype, s) for s in (71, 72, 73))
+    HK = 2 if gqa else H
+    q = randn((B, H, n, d), dtype, 71)
+    k, v = (randn((B, HK, n, d), dtype, s) for s in (72, 73))
     km = torch.ones(B, n, dtype=torch.bool)
     km[0, :200] = False
     km[1, 300:] = False
@@ -224,10 +228,10 @@ def test_pass_padding_masks_skip_whole_tiles(dtype, causal, with_bias):
     km[2, ::5] = False
     bias = None
     if with_bias:
-        bias = randn((B, H, n), torch.float32, 74)
+        bias = randn((B, HK, n), torch.float32, 74)
         bias[3, :, 64:192] = -float("inf")
     res = run_pass(q, k, v, bias=bias, key_mask=km, causal=causal)
-    check(res, dtype, f"padding masks {dtype} causal={causal} bias={with_bias}")
+    check(res, dtype, f"padding masks {dtype} gqa={gqa} causal={causal} bias={with_bias}")
 
 
 @param("causal", (False, True))
