@@ -329,9 +329,9 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
 
 // ---------------------------------------------------------------------------------------
 // Direct-to-LDS dK / dV / dbias (no value multiplier): the Q and dO tiles of every query
-// tile, with their lse and D rows, travel HBM -> LDS by buffer_load ... lds, three stages
-// deep (tile i+2 in flight while tile i is computed; the query heads of a KV group form one
-// flat tile sequence).  Q and dO stay row-major in LDS and are read both by rows (S = Q K^T,
+// tile, with their lse and D rows, travel HBM -> LDS by buffer_load ... lds, four stages
+// filled and waited for in pairs (tiles i+2 and i+3 in flight while tiles i and i+1 are
+// computed, one barrier per pair; the query heads of a KV group form one flat tile sequence).  Q and dO stay row-major in LDS and are read both by rows (S = Q K^T,
 // dP = dO V^T) and transposed (dV^T += dO^T P, dK^T += Q^T dS, ds_read_b64_tr_b16), under a
 // chunk swizzle that serves both patterns.  The tile's lse and D rows enter as accumulator
 // seeds: S starts at -lse/scale (so P = exp2(scale*log2e*S + bias)) and dP at -D (so
@@ -361,13 +361,13 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
     typedef typename M::frag frag;
     constexpr int BQ = kKvBQ, CPR = D / 8, ELEMS = BQ * D;
     constexpr int NL = BQ * CPR / kBwdThreads;  // chunks per thread and tensor
-    constexpr int NOPS = 2 * NL + 2;            // + lse and D rows
     static_assert(BQ * CPR % kBwdThreads == 0, "tile must split evenly over the threads");
     const PassDev& P = G.f;
-    __shared__ __attribute__((aligned(16))) T sQ[kKvStages * ELEMS];
-    __shared__ __attribute__((aligned(16))) T sO[kKvStages * ELEMS];
-    __shared__ __attribute__((aligned(16))) float sLraw[kKvStages][BQ];
-    __shared__ __attribute__((aligned(16))) float sDraw[kKvStages][BQ];
+    constexpr int NSTG = 4;  // query tiles filled and waited for in pairs
+    __shared__ __attribute__((aligned(16))) T sQ[NSTG * ELEMS];
+    __shared__ __attribute__((aligned(16))) T sO[NSTG * ELEMS];
+    __shared__ __attribute__((aligned(16))) float sLraw[NSTG][BQ];
+    __shared__ __attribute__((aligned(16))) float sDraw[NSTG][BQ];
     __shared__ __attribute__((aligned(16))) float sLw[4][BQ];  // per-wave converted seeds
     __shared__ __attribute__((aligned(16))) float sDw[4][BQ];
 
@@ -514,10 +514,15 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
     int st = 0;
     int q0 = q_start;  // first query of the tile being computed
     for (int idx = 0; idx < total; ++idx, q0 = (q0 + BQ == q_end) ? q_start : q0 + BQ) {
-        if (idx + 1 < total) wait_vmcnt<NOPS>();
-        else wait_vmcnt<0>();
-        lds_barrier();
-        if (idx + 2 < total) issue(st == 0 ? 2 : st - 1);
+        // query tiles in pairs, one workgroup barrier per pair: at an even tile both tiles of
+        // the pair have landed and every wave is done with the previous pair, whose stages
+        // receive the next pair (half the barriers of one per tile: -1.5% on this kernel)
+        if (!(idx & 1)) {
+            wait_vmcnt<0>();
+            lds_barrier();
+            if (idx + 2 < total) issue((st + 2) & 3);
+            if (idx + 3 < total) issue((st + 3) & 3);
+        }
         const T* Qt = sQ + st * ELEMS;
         const T* Ot = sO + st * ELEMS;
         // the tile's seeds: -lse/scale (log2-domain lse with softclamp), -D; read from the
@@ -632,7 +637,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
         accumulate(0, pf0, df0);
         grads(1, s1, dp1, pf1, df1);
         accumulate(1, pf1, df1);
-        st = st == 2 ? 0 : st + 1;
+        st = (st + 1) & 3;
     }
 
     dbias += __shfl_xor(dbias, 32);

@@ -21,8 +21,9 @@
 //
 // Kernels:
 //  * k_mfma_fwd_dma (default): K, V and the key bias travel HBM -> LDS by direct loads,
-//    three stages deep; V^T operands come from transposing LDS reads; without softclamp the
-//    key bias is folded into the score accumulators.
+//    four stages of 64-key tiles filled and waited for in pairs (one barrier per two tiles);
+//    V^T operands come from transposing LDS reads; without softclamp the key bias is folded
+//    into the score accumulators.
 //  * k_mfma_fwd: register-staged loads with a transposing LDS store; the general kernel
 //    (value multiplier, key masks, strided biases, very long rows).
 //
@@ -57,6 +58,7 @@ constexpr float kFwdSumCap = 8192.f;
 #ifndef PA_FWD_SUMCHECK
 #define PA_FWD_SUMCHECK 1
 #endif
+
 
 // Key tile of BN = 32 * KB keys: KB accumulator blocks per wave and tile.
 template <int D, int KB>
@@ -535,7 +537,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
 // only tile t+1's loads are outstanding.  Each wave converts the raw bias of its tile
 // (class filter, log2 domain) into a wave-private LDS row.
 
-constexpr int kFwdStages = 3;
+constexpr int kFwdStages = 4;  // LDS stages of 64-key tiles, filled and waited for in pairs
 
 // chunk swizzles (16-byte chunk index within a row, as a function of the row)
 // K (read as 16-byte fragments, 32 rows per block): for d = 64 the chunk is XORed with a
@@ -570,8 +572,6 @@ template <typename T, int D, int KB, int QB, bool CAUSAL, bool SOFTCLAMP, bool H
 __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(PassDev P) {
     using TL = DmaTile<D, KB>;
     constexpr int BN = TL::BN, NL = TL::NL, BM = kFwdBM * QB;
-    // vector-memory operations per thread and tile: K and V chunks, one bias load
-    constexpr int NOPS = 2 * NL + (HAS_BIAS ? 1 : 0);
     // without softclamp the key bias enters the scores as the MFMA accumulator's initial value
     // (bias / scale, so that scale*log2e*(s + bias/scale) is the log2-domain logit)
     constexpr bool FOLD = HAS_BIAS && !SOFTCLAMP;
@@ -688,11 +688,16 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     // compute loop has a single path
     const int nact = CAUSAL ? min(ntiles, wave_last / BN + 1) : ntiles;
     int st = 0;
+    auto next_st = [](int s) __attribute__((always_inline)) { return (s + 1) & 3; };
+    // tiles in pairs, one workgroup barrier per pair: at an even tile both tiles of the pair
+    // have landed and every wave is done with the previous pair, whose stages receive the
+    // next pair (half the barriers of one per tile: -1% on this kernel)
     auto enter = [&](int t) __attribute__((always_inline)) {
-        if (t + 1 < ntiles) wait_vmcnt<NOPS>();
-        else wait_vmcnt<0>();
+        if (t & 1) return;
+        wait_vmcnt<0>();
         lds_barrier();
-        if (t + 2 < ntiles) issue((t + 2) * BN, st == 0 ? 2 : st - 1);
+        if (t + 2 < ntiles) issue((t + 2) * BN, (st + 2) & 3);
+        if (t + 3 < ntiles) issue((t + 3) * BN, (st + 3) & 3);
     };
     for (int t = 0; t < nact; ++t) {
         const int j0 = t * BN;
@@ -710,7 +715,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
             // a tile whose every key term is -inf (masked keys: padding) adds nothing to any
             // row; a row that has seen only such keys keeps m = -inf and l = 0 either way
             if (!__any(xw != -INFINITY)) {
-                st = st == 2 ? 0 : st + 1;
+                st = next_st(st);
                 continue;
             }
         }
@@ -824,7 +829,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
             recheck(1, lt1, pk1);
             // (D)
             wv[1].pv(vf, pk1);
-            st = st == 2 ? 0 : st + 1;
+            st = next_st(st);
             continue;
         }
 #endif
@@ -877,11 +882,11 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
             else wv[u].l += wv[u].probs(s[u], wv[u].m == -INFINITY ? 0.f : wv[u].m, pk);
             wv[u].pv(vf, pk);
         }
-        st = st == 2 ? 0 : st + 1;
+        st = next_st(st);
     }
     for (int t = nact; t < ntiles; ++t) {
         enter(t);
-        st = st == 2 ? 0 : st + 1;
+        st = next_st(st);
     }
 
 #pragma unroll
