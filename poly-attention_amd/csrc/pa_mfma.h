@@ -241,16 +241,30 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     return (x < rem) ? x * (per + 1) + slot : rem * (per + 1) + (x - rem) * per + slot;
 }
 
+// The unit (batch-major, head-minor) of the j-th of the nu units that XCD x runs.  Where the
+// heads split evenly over the XCDs in runs of whole groups (`group` consecutive heads share
+// their K / V: GQA), each XCD takes heads [x * hpx, (x + 1) * hpx) of every batch row, so that
+// work that differs by batch row (padding masks) is spread over all XCDs; otherwise the XCD's
+// units are consecutive.
+__device__ __forceinline__ int xcd_unit(int x, int j, int nu, int heads, int group) {
+    if (heads % (kNumXcd * group) == 0) {
+        const int hpx = heads / kNumXcd;
+        return (j / hpx) * heads + x * hpx + j % hpx;
+    }
+    return x * nu + j;
+}
+
 // Causal grids (work per block falls with its rank): logical order in which every XCD runs
 // whole (batch, head) units and dispatches the heaviest blocks of all its units first, so the
 // light blocks fill the end of the kernel.  When the XCD ranges do not hold whole units, the
 // order is unit by unit (heaviest first inside each unit).
-__device__ __forceinline__ void heavy_first(int bid, int nblocks, int nblk, int& unit, int& rank) {
+__device__ __forceinline__ void heavy_first(int bid, int nblocks, int nblk, int heads, int group,
+                                            int& unit, int& rank) {
     const int lid = xcd_remap(bid, nblocks);
     const int per = nblocks / kNumXcd;
     if (nblocks % kNumXcd == 0 && per % nblk == 0) {
         const int x = lid / per, k = lid % per, nu = per / nblk;
-        unit = x * nu + k % nu;
+        unit = xcd_unit(x, k % nu, nu, heads, group);
         rank = k / nu;
     } else {
         unit = lid / nblk;
@@ -262,13 +276,21 @@ __device__ __forceinline__ void heavy_first(int bid, int nblocks, int nblk, int&
 #define PA_HEAVY_FIRST 1
 #endif
 
-// (unit, rank) of this workgroup: causal grids in heavy_first order, others unit by unit
+// (unit, rank) of this workgroup: causal grids in heavy_first order, others unit by unit (each
+// unit's blocks consecutive on one XCD).  heads: units per batch row; group: see xcd_unit.
 template <bool CAUSAL>
-__device__ __forceinline__ void block_order(int nblk, int& unit, int& rank) {
+__device__ __forceinline__ void block_order(int nblk, int heads, int group, int& unit, int& rank) {
     if (CAUSAL && PA_HEAVY_FIRST) {
-        heavy_first(blockIdx.x, gridDim.x, nblk, unit, rank);
+        heavy_first(blockIdx.x, gridDim.x, nblk, heads, group, unit, rank);
+        return;
+    }
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int per = gridDim.x / kNumXcd;
+    if (gridDim.x % kNumXcd == 0 && per % nblk == 0) {
+        const int x = lid / per, k = lid % per;
+        unit = xcd_unit(x, k / nblk, per / nblk, heads, group);
+        rank = k % nblk;
     } else {
-        const int lid = xcd_remap(blockIdx.x, gridDim.x);
         unit = lid / nblk;
         rank = lid % nblk;
     }

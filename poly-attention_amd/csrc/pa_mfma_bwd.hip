@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
     const int hh = lane >> 5, kcol = lane & 31;
     const int nkb = (P.nk + kKvBK - 1) / kKvBK;
     int unit, kblk;  // causal: the first key blocks carry the most work
-    block_order<CAUSAL>(nkb, unit, kblk);
+    block_order<CAUSAL>(nkb, G.hk, 1, unit, kblk);
     const int kh = unit % G.hk, b = unit / G.hk;
     const int rep = P.heads / G.hk;
     const int h0 = kh * rep;
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv_d
     const int hh = lane >> 5, kcol = lane & 31;
     const int nkb = (P.nk + kKvBK - 1) / kKvBK;
     int unit, kblk;  // causal: the first key blocks carry the most work
-    block_order<CAUSAL>(nkb, unit, kblk);
+    block_order<CAUSAL>(nkb, G.hk, 1, unit, kblk);
     const int kh = unit % G.hk, b = unit / G.hk;
     const int rep = P.heads / G.hk;
     const int h0 = kh * rep;
@@ -800,7 +800,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
     const int hh = lane >> 5, kcol = lane & 31;
     const int nqb = (P.nq + kDqBM - 1) / kDqBM;
     int unit, rank;
-    block_order<CAUSAL>(nqb, unit, rank);
+    block_order<CAUSAL>(nqb, P.heads, P.k.hdiv, unit, rank);
     const int qblk = CAUSAL ? nqb - 1 - rank : rank;  // heaviest first
     const int h = unit % P.heads, b = unit / P.heads;
     const int qw0 = qblk * kDqBM + w * 32;
@@ -938,7 +938,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
     const int hh = lane >> 5, kcol = lane & 31;
     const int nqb = (P.nq + kDqBM - 1) / kDqBM;
     int unit, rank;
-    block_order<CAUSAL>(nqb, unit, rank);
+    block_order<CAUSAL>(nqb, P.heads, P.k.hdiv, unit, rank);
     const int qblk = CAUSAL ? nqb - 1 - rank : rank;  // heaviest first
     const int h = unit % P.heads, b = unit / P.heads;
     const int qw0 = qblk * kDqBM + w * 32;

@@ -140,8 +140,8 @@ __global__ __launch_bounds__(256) void k_mfma_fwd_f32(PassDev P) {
     const bool causal = P.causal != 0;
     const int nqb = (P.nq + BM - 1) / BM;
     int bh, rank;
-    if (causal) block_order<true>(nqb, bh, rank);
-    else block_order<false>(nqb, bh, rank);
+    if (causal) block_order<true>(nqb, P.heads, P.k.hdiv, bh, rank);
+    else block_order<false>(nqb, P.heads, P.k.hdiv, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
     const int col = lane & 31, hh = lane >> 5;
@@ -247,8 +247,8 @@ __global__ __launch_bounds__(64 * NS) void k_mfma_fwd_f32_split(PassDev P) {
     const bool causal = P.causal != 0;
     const int nqb = (P.nq + 31) / 32;
     int bh, rank;
-    if (causal) block_order<true>(nqb, bh, rank);
-    else block_order<false>(nqb, bh, rank);
+    if (causal) block_order<true>(nqb, P.heads, P.k.hdiv, bh, rank);
+    else block_order<false>(nqb, P.heads, P.k.hdiv, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
     const int col = lane & 31, hh = lane >> 5;
@@ -533,8 +533,8 @@ __global__ __launch_bounds__(256) void k_mfma_bwd_f32_dq(GradDev G) {
     const bool causal = P.causal != 0;
     const int nqb = (P.nq + BM - 1) / BM;
     int bh, rank;
-    if (causal) block_order<true>(nqb, bh, rank);
-    else block_order<false>(nqb, bh, rank);
+    if (causal) block_order<true>(nqb, P.heads, P.k.hdiv, bh, rank);
+    else block_order<false>(nqb, P.heads, P.k.hdiv, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
     const int col = lane & 31, hh = lane >> 5;
@@ -604,8 +604,8 @@ __global__ __launch_bounds__(256) void k_mfma_bwd_f32_dkv(GradDev G) {
     const bool causal = P.causal != 0;
     const int nkb = (P.nk + BK - 1) / BK;
     int unit, kblk;  // causal: the first key blocks carry the most work
-    if (causal) block_order<true>(nkb, unit, kblk);
-    else block_order<false>(nkb, unit, kblk);
+    if (causal) block_order<true>(nkb, G.hk, 1, unit, kblk);
+    else block_order<false>(nkb, G.hk, 1, unit, kblk);
     const int kh = unit % G.hk, b = unit / G.hk;
     const int rep = P.heads / G.hk, h0 = kh * rep;
     const int col = lane & 31, hh = lane >> 5;
@@ -715,8 +715,8 @@ __global__ __launch_bounds__(64 * NS) void k_mfma_bwd_f32_dq_split(GradDev G) {
     const bool causal = P.causal != 0;
     const int nqb = (P.nq + 31) / 32;
     int bh, rank;
-    if (causal) block_order<true>(nqb, bh, rank);
-    else block_order<false>(nqb, bh, rank);
+    if (causal) block_order<true>(nqb, P.heads, P.k.hdiv, bh, rank);
+    else block_order<false>(nqb, P.heads, P.k.hdiv, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
     const int col = lane & 31, hh = lane >> 5;
@@ -803,8 +803,8 @@ __global__ __launch_bounds__(64 * NS) void k_mfma_bwd_f32_dkv_split(GradDev G) {
     const bool causal = P.causal != 0;
     const int nkb = (P.nk + 31) / 32;
     int unit, kblk;
-    if (causal) block_order<true>(nkb, unit, kblk);
-    else block_order<false>(nkb, unit, kblk);
+    if (causal) block_order<true>(nkb, G.hk, 1, unit, kblk);
+    else block_order<false>(nkb, G.hk, 1, unit, kblk);
     const int kh = unit % G.hk, b = unit / G.hk;
     const int rep = P.heads / G.hk, h0 = kh * rep;
     const int col = lane & 31, hh = lane >> 5;

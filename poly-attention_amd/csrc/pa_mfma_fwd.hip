@@ -426,7 +426,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd(PassD
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     int bh, rank;
-    block_order<CAUSAL>(nqb, bh, rank);
+    block_order<CAUSAL>(nqb, P.heads, P.k.hdiv, bh, rank);
     const int qb = CAUSAL ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
 
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int nqb = (P.nq + BM - 1) / BM;
     int bh, rank;
-    block_order<CAUSAL>(nqb, bh, rank);
+    block_order<CAUSAL>(nqb, P.heads, P.k.hdiv, bh, rank);
     const int qb = CAUSAL ? nqb - 1 - rank : rank;
     const int h = bh % P.heads, b = bh / P.heads;
     const int hh = lane >> 5, kcol = lane & 31;

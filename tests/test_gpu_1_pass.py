@@ -234,6 +234,24 @@ def test_pass_padding_masks_skip_whole_tiles(dtype, gqa, causal, with_bias):
     check(res, dtype, f"padding masks {dtype} gqa={gqa} causal={causal} bias={with_bias}")
 
 
+@param("gqa", (False, True))
+def test_pass_padding_masks_units_spread_over_xcds(gqa):
+    """Grids that divide over the 8 XCDs with heads a multiple of 8 (times the GQA group): each
+    XCD then runs some heads of every batch row (instead of whole batch rows), so that padding
+    of some rows spreads over all XCDs.  Left padding on batch 0 (keys 0-639 masked, causal
+    rows 0-639 fully masked), right padding on batch 1 (keys 384- masked): forward and every
+    gradient against the eager result.  gqa: 16 query heads over 8 key heads (group of 2)."""
+    B, n, d = 2, 1024, 64
+    H, HK = (16, 8) if gqa else (8, 8)
+    q = randn((B, H, n, d), torch.bfloat16, 81)
+    k, v = (randn((B, HK, n, d), torch.bfloat16, s) for s in (82, 83))
+    km = torch.ones(B, n, dtype=torch.bool)
+    km[0, :640] = False
+    km[1, 384:] = False
+    res = run_pass(q, k, v, key_mask=km, causal=True)
+    check(res, torch.bfloat16, f"padding masks spread over XCDs gqa={gqa}")
+
+
 @param("causal", (False, True))
 def test_pass_key_masked_forward_with_and_without_workspace(causal):
     """pa_attn_pass_fwd on a key-masked bf16 pass: with its optional workspace the key mask
