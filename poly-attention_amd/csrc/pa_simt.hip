@@ -215,36 +215,35 @@ __device__ __forceinline__ float ordered_sum(const float* p, int n) {
     return a;
 }
 
-// S0 of k_fwd_fixup, one slot's share (key rows slot, slot + R, ...): its key rows four at a
-// time, each round's loads issued unconditionally (rows past the end read the last row and
-// count for nothing) before the first is used -- a load per dependent step took 27 us at 4096
-// keys; eight at a time measured the same.  VM: the values are v * vmul, rounded to T.
-template <typename T, int D, bool VM>
+// S0 of k_fwd_fixup, one slot's share (key rows slot, slot + R, ...): U key rows per round,
+// every load of a round (key term, mask byte, value row) issued before the first is used, rows
+// past the end reading the last row and counting for nothing.  One memory round trip per
+// round: with the key terms loaded first and the value rows behind them (two round trips a
+// round, four rows) the left-padded config-2 pass took 35 us here.  VM: the values are
+// v * vmul, rounded to T.
+template <typename T, int D, bool VM, bool HB, bool HK>
 __device__ __forceinline__ void fixup_s0(const PassDev& P, int b, int h, int slot, int c0,
                                          float (&acc)[8], int& n0, int& n1) {
-    constexpr int R = kFixThreads / (D / 8), kFixU = 4;
+    constexpr int R = kFixThreads / (D / 8), U = VM ? 4 : 8;  // 16 spills at 1024 threads
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    for (int j0 = slot; j0 < P.nk; j0 += R * kFixU) {
-        int cls[kFixU];
-        float v8[kFixU][8], m8[VM ? kFixU : 1][8];
-        // the classes first: a key bias load sits behind a branch, whose join waits for every
-        // load issued before it
+    for (int j0 = slot; j0 < P.nk; j0 += R * U) {
+        float x[U], v8[U][8], m8[VM ? U : 1][8];
+        bool kp[U];
 #pragma unroll
-        for (int u = 0; u < kFixU; ++u) {
-            const int j = j0 + u * R;
-            cls[u] = j >= P.nk ? -1 : P.bias.ok() ? bias_class(P.bias.scalar(b, h, j)) : 0;
-        }
-#pragma unroll
-        for (int u = 0; u < kFixU; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int jc = min(j0 + u * R, P.nk - 1);
+            x[u] = HB ? P.bias.scalar(b, h, jc) : 0.f;
+            kp[u] = HK ? P.km.p[(int64_t)b * P.km.sb + (int64_t)jc * P.km.sn] != 0 : true;
             load8<T>(P.v.row<T>(b, h, jc) + c0, v8[u]);
             if constexpr (VM) load8<T>(P.vmul.row<T>(b, h, jc) + c0, m8[u]);
         }
 #pragma unroll
-        for (int u = 0; u < kFixU; ++u) {
-            if (cls[u] == 1 && P.km.keep(b, j0 + u * R)) ++n1;
-            if (cls[u] != 0) continue;
+        for (int u = 0; u < U; ++u) {
+            if (j0 + u * R >= P.nk) break;
+            const int cls = bias_class(x[u]);
+            if (cls == 1 && kp[u]) ++n1;
+            if (cls != 0) continue;
             ++n0;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -253,6 +252,16 @@ __device__ __forceinline__ void fixup_s0(const PassDev& P, int b, int h, int slo
             }
         }
     }
+}
+
+template <typename T, int D, bool VM>
+__device__ __forceinline__ void fixup_s0_any(const PassDev& P, int b, int h, int slot, int c0,
+                                             float (&acc)[8], int& n0, int& n1) {
+    const bool hb = P.bias.ok(), hk = P.km.p != nullptr;
+    if (hb) hk ? fixup_s0<T, D, VM, true, true>(P, b, h, slot, c0, acc, n0, n1)
+               : fixup_s0<T, D, VM, true, false>(P, b, h, slot, c0, acc, n0, n1);
+    else hk ? fixup_s0<T, D, VM, false, true>(P, b, h, slot, c0, acc, n0, n1)
+            : fixup_s0<T, D, VM, false, false>(P, b, h, slot, c0, acc, n0, n1);
 }
 
 // Finish the rows an MFMA forward left fully masked (their lse holds NaN), one workgroup per
@@ -267,15 +276,24 @@ __global__ __launch_bounds__(kFixThreads) void k_fwd_fixup(PassDev P) {
     const int h = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x;
     bool any = false;
-    for (int i = tid; i < P.nq; i += blockDim.x) any |= isnan(*P.lse.row<float>(b, h, i));
+    {
+        constexpr int RU = 4;  // rows per thread per round, all loads in flight together
+        for (int i0 = tid; i0 < P.nq; i0 += kFixThreads * RU) {
+            float l[RU];
+#pragma unroll
+            for (int u = 0; u < RU; ++u) l[u] = *P.lse.row<float>(b, h, min(i0 + u * kFixThreads, P.nq - 1));
+#pragma unroll
+            for (int u = 0; u < RU; ++u) any |= i0 + u * kFixThreads < P.nq && isnan(l[u]);
+        }
+    }
     if (!__syncthreads_or(any)) return;
 
     // S0 and the counts of bias-class-0 and unmasked bias-class-1 keys
     const int slot = tid / LPR, c0 = (tid % LPR) * 8;
     float acc[8];
     int n0 = 0, n1 = 0;
-    if (P.vmul.ok()) fixup_s0<T, D, true>(P, b, h, slot, c0, acc, n0, n1);
-    else fixup_s0<T, D, false>(P, b, h, slot, c0, acc, n0, n1);
+    if (P.vmul.ok()) fixup_s0_any<T, D, true>(P, b, h, slot, c0, acc, n0, n1);
+    else fixup_s0_any<T, D, false>(P, b, h, slot, c0, acc, n0, n1);
     __shared__ float sS[R][D];
     __shared__ int sN[R][2];
     __shared__ float sT[D];
@@ -289,10 +307,12 @@ __global__ __launch_bounds__(kFixThreads) void k_fwd_fixup(PassDev P) {
     __syncthreads();
     if (tid < D) {
         float a = 0.f;
+#pragma unroll 16  // the LDS reads issued ahead of the (ordered) sums
         for (int r = 0; r < R; ++r) a += sS[r][tid];
         sT[tid] = a;
     } else if (tid < D + 2) {
         int a = 0;
+#pragma unroll 16  // the LDS reads issued ahead of the (ordered) sums
         for (int r = 0; r < R; ++r) a += sN[r][tid - D];
         sCnt[tid - D] = a;
     }
@@ -761,7 +781,14 @@ __global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
     const int i0 = c * kFixRowChunk, i1 = min(P.nq, i0 + kFixRowChunk);
     float* part = G.ws_part + (((int64_t)b * P.heads + h) * fix_row_chunks(P.nq) + c) * (D + 2);
     bool any = false;
-    for (int i = i0 + (int)threadIdx.x; i < i1; i += 256) any |= G.ws_lse[row0 + i] == INFINITY;
+    {
+        static_assert(kFixRowChunk % 256 == 0, "whole rounds per chunk");
+        float l[kFixRowChunk / 256];  // the chunk's rows, all loads in flight together
+#pragma unroll
+        for (int k = 0; k < kFixRowChunk / 256; ++k) l[k] = G.ws_lse[row0 + min(i0 + (int)threadIdx.x + 256 * k, i1 - 1)];
+#pragma unroll
+        for (int k = 0; k < kFixRowChunk / 256; ++k) any |= l[k] == INFINITY;
+    }
     if (!__syncthreads_or(any)) {
         if (threadIdx.x < D + 2) part[threadIdx.x] = 0.f;
         return;
@@ -770,15 +797,20 @@ __global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) u[e] = 0.f;
     for (int ib = i0 + slot; ib < i1; ib += R * U) {
-        float ic[U], dd[U], g8[U][8];
+        float li[U], ic[U], dd[U], g8[U][8];
 #pragma unroll
         for (int k = 0; k < U; ++k) {
+            // every load of the round before the first use (a load behind a lane-dependent
+            // condition would make the branch's join wait for it)
             const int i = min(ib + k * R, i1 - 1);
-            const bool dg = ib + k * R < i1 && degenerate_row(G, row0 + i);
-            ic[k] = dg ? G.ws_invc[row0 + i] : 0.f;
+            li[k] = G.ws_lse[row0 + i];
+            ic[k] = G.ws_invc[row0 + i];
             dd[k] = G.ws_D[row0 + i];
             load8<T>(G.dout.row<T>(b, h, i) + c0, g8[k]);
         }
+#pragma unroll
+        for (int k = 0; k < U; ++k)  // degenerate rows only (see degenerate_row)
+            ic[k] = ib + k * R < i1 && li[k] == INFINITY && ic[k] > 0.f ? ic[k] : 0.f;
 #pragma unroll
         for (int k = 0; k < U; ++k) {
 #pragma unroll
@@ -798,11 +830,13 @@ __global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
     __syncthreads();
     if (threadIdx.x < D) {
         float a = 0.f;
+#pragma unroll 16  // the LDS reads issued ahead of the (ordered) sums
         for (int r = 0; r < R; ++r) a += sU[r][threadIdx.x];
         part[threadIdx.x] = a;
     } else if (threadIdx.x < D + 2) {
         const float* src = threadIdx.x == D ? sW : sC;
         float a = 0.f;
+#pragma unroll 16  // the LDS reads issued ahead of the (ordered) sums
         for (int r = 0; r < R; ++r) a += src[r];
         part[threadIdx.x] = a;
     }
