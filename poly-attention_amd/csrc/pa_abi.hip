@@ -139,6 +139,7 @@ PassDev to_passdev(const pa_pass* p) {
     P.knw = n ? n->k_weight : nullptr;
     P.qeps = n ? n->q_eps : 0.f;
     P.keps = n ? n->k_eps : 0.f;
+    P.live = nullptr;
     return P;
 }
 
@@ -173,8 +174,8 @@ int key_term_stride(const pa_pass& f) { return (f.nk + 3) & ~3; }
 
 size_t elem_bytes(int dtype) { return dtype == PA_F32 ? 4 : 2; }
 
-// forward workspace: the per-key term (and the bias-class counts written with it) of a
-// key-masked 16-bit pass on the MFMA kernels, whose key bias it then is
+// forward workspace: the per-key term of a key-masked 16-bit pass on the MFMA kernels, whose
+// key bias it then is, and the range of keys that can enter a normal row
 size_t fwd_ws_bytes(const pa_pass& f) {
     if (!f.key_mask.ptr || (f.q.dtype != PA_BF16 && f.q.dtype != PA_F16)) return 0;
     if (f.dim != 64 && f.dim != 128) return 0;
@@ -185,8 +186,8 @@ size_t fwd_ws_bytes(const pa_pass& f) {
 }
 
 // [D | lse | 1/c1] per query row; with an epilogue the gradient reaching the pass output;
-// masked passes add the key term (with a key mask), the per-head fully-masked-row sums and
-// the per-key-head bias-class counts
+// masked passes add the key term (with a key mask), the per-head fully-masked-row sums, the
+// per-key-head bias-class counts and the per-key-head range of keys that can enter a normal row
 size_t bwd_ws_bytes(const pa_pass& f) {
     const size_t rows = (size_t)f.batch * f.heads * f.nq;
     size_t n = 3 * align256(rows * sizeof(float));
@@ -195,7 +196,7 @@ size_t bwd_ws_bytes(const pa_pass& f) {
         const size_t kheads = (size_t)f.batch * f.k.heads;
         if (f.key_mask.ptr) n += align256(kheads * key_term_stride(f) * sizeof(float));
         n += align256((size_t)f.batch * f.heads * fix_row_chunks(f.nq) * (f.dim + 2) * sizeof(float));
-        n += align256(kheads * 2 * sizeof(int32_t));
+        n += 2 * align256(kheads * 2 * sizeof(int32_t));
     }
     return n;
 }
@@ -367,11 +368,14 @@ int pa_attn_pass_fwd(const pa_pass* p, void* stream) {
             GradDev G = {};  // the key-term kernel reads f and hk only
             G.f = P;
             G.hk = hk;
-            launch_key_terms(G, kterm, nkp, nullptr, s);  // the key counts serve the backward
+            int32_t* live = reinterpret_cast<int32_t*>(
+                w + align256((size_t)p->batch * hk * nkp * sizeof(float)));
+            launch_key_terms(G, kterm, nkp, nullptr, live, s);  // the counts serve the backward
             PassDev Pm = P;
             Pm.bias = DView{reinterpret_cast<char*>(kterm), (int64_t)hk * nkp, nkp, 1,
                             p->heads / hk, PA_F32};
             Pm.km.p = nullptr;
+            Pm.live = live;
             launch_mfma_fwd(Pm, T, s);
         } else {
             launch_mfma_fwd(P, T, s);
@@ -504,8 +508,10 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
         G.ws_part = reinterpret_cast<float*>(w);
         w += align256((size_t)p->batch * H * fix_row_chunks(p->nq) * (p->dim + 2) * sizeof(float));
         int32_t* kcnt = reinterpret_cast<int32_t*>(w);
+        w += align256((size_t)p->batch * hk * 2 * sizeof(int32_t));
+        int32_t* live = reinterpret_cast<int32_t*>(w);
         G.ws_kcnt = kcnt;
-        launch_key_terms(G, kterm, nkp, kcnt, s);
+        launch_key_terms(G, kterm, nkp, kcnt, live, s);
         launch_simt_bwd(G, T, s, /*pre=*/true, false, false);
         GradDev Gm = G;
         if (kterm) {
@@ -520,6 +526,7 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
         Gm.f.km.p = nullptr;
         Gm.f.qm.p = nullptr;
         Gm.f.flags &= ~PA_FLAG_MAY_DEGENERATE;
+        Gm.f.live = live;
         launch_mfma_bwd(Gm, T, s);
         launch_mask_fixups(G, T, s);
     } else if (mfma_bwd_supported(G, T)) {

@@ -80,6 +80,9 @@ struct PassDev {
     const void* knw;
     float qeps, keps;
     int32_t nflags;
+    // masked passes on the MFMA kernels: per (b, key head) [first, last + 1) of the keys that
+    // can enter a normal row (kept, key bias of class 0), or null
+    const int32_t* live;
 };
 
 struct GradDev {

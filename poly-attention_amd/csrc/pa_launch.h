@@ -25,7 +25,8 @@ void launch_fwd_fixup(const PassDev& P, int dtype, hipStream_t s);
 void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool dq, bool dkv);
 // masked passes on the MFMA backward: per-key-head bias-class counts (and, with kterm, the
 // key mask folded into a per-key term of row stride nkp), then the fully-masked rows' part
-void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, hipStream_t s);
+void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, int32_t* live,
+                      hipStream_t s);
 void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s);
 
 // MFMA kernels (bf16 / f16 / fp32 forward, bf16 / f16 backward; head dim 64 or 128); return

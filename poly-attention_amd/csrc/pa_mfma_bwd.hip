@@ -1065,16 +1065,26 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
     }
 
     const int kend = CAUSAL ? min(P.nk, qblk * kDqBM + kDqBM) : P.nk;
-    const int ntiles = (kend + BN - 1) / BN;
-    const int nact = CAUSAL ? min(ntiles, (qw0 + 31) / BN + 1) : ntiles;
-    if (ntiles > 0) issue(0, 0);
-    if (ntiles > 1) issue(BN, 1);
+    // tiles [tb, te): with the range of keys that can enter a normal row (masked passes), the
+    // tiles outside it are neither loaded nor visited; t counts from tb
+    int tb = 0, te = (kend + BN - 1) / BN;
+    if (HAS_BIAS && P.live) {
+        const int hd = P.bias.hdiv;
+        const int32_t* r = P.live + 2 * ((int64_t)b * (P.heads / hd) + h / hd);
+        const int lo = r[0], hi = r[1];
+        te = min(te, (hi + BN - 1) / BN);
+        tb = min(lo / BN, te);
+    }
+    const int ntiles = te - tb;
+    const int nact = max(0, (CAUSAL ? min(te, (qw0 + 31) / BN + 1) : te) - tb);
+    if (ntiles > 0) issue(tb * BN, 0);
+    if (ntiles > 1) issue((tb + 1) * BN, 1);
     int st = 0;
     auto enter = [&](int t) __attribute__((always_inline)) {
         if (t + 1 < ntiles) wait_vmcnt<NOPS>();
         else wait_vmcnt<0>();
         lds_barrier();
-        if (t + 2 < ntiles) issue((t + 2) * BN, st == 0 ? 2 : st - 1);
+        if (t + 2 < ntiles) issue((tb + t + 2) * BN, st == 0 ? 2 : st - 1);
     };
     // this wave's converted copy of a tile's key terms; true when every one is -inf (masked
     // keys: every probability of the tile is 0)
@@ -1098,7 +1108,7 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 3 : 1) void k_mfma_bwd_dq_dm
                 dead = conv_bias(st);
             }
         }
-        const int j0 = t * BN;
+        const int j0 = (tb + t) * BN;
         const T* Kt = sK + st * ELEMS;
         const T* Vt = sV + st * ELEMS;
         // the two 32-key blocks in a software pipeline (MFMAs of one beside the VALU of the other)

@@ -677,31 +677,42 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
     }
 
     const int kend = CAUSAL ? min(P.nk, qb * BM + BM) : P.nk;
-    const int ntiles = (kend + BN - 1) / BN;
+    // tiles [tb, te): with the range of keys that can enter a normal row (masked passes), the
+    // tiles outside it are neither loaded nor visited
+    int tb = 0, te = (kend + BN - 1) / BN;
+    if (HAS_BIAS && P.live) {
+        const int hd = P.bias.hdiv;
+        const int32_t* r = P.live + 2 * ((int64_t)b * (P.heads / hd) + h / hd);
+        const int lo = r[0], hi = r[1];
+        te = min(te, (hi + BN - 1) / BN);
+        tb = min(lo / BN, te);
+    }
+    const int ntl = te - tb;  // tiles loaded
     const int wave_last = CAUSAL ? (wq0 + 32 * QB - 1) : (1 << 30);
 
-    issue(0, 0);
-    if (ntiles > 1) issue(BN, 1);
+    if (ntl > 0) issue(tb * BN, 0);
+    if (ntl > 1) issue((tb + 1) * BN, 1);
 
-    // tiles [0, nact) hold keys at or below this wave's last query; the remaining tiles of the
-    // workgroup only pass through (loads and barriers), in a loop of their own so that the
-    // compute loop has a single path
-    const int nact = CAUSAL ? min(ntiles, wave_last / BN + 1) : ntiles;
+    // tiles [tb, tb + nact) hold keys at or below this wave's last query; the remaining tiles
+    // of the workgroup only pass through (loads and barriers), in a loop of their own so that
+    // the compute loop has a single path
+    const int nact = max(0, (CAUSAL ? min(te, wave_last / BN + 1) : te) - tb);
     int st = 0;
     auto next_st = [](int s) __attribute__((always_inline)) { return (s + 1) & 3; };
     // tiles in pairs, one workgroup barrier per pair: at an even tile both tiles of the pair
     // have landed and every wave is done with the previous pair, whose stages receive the
-    // next pair (half the barriers of one per tile: -1% on this kernel)
-    auto enter = [&](int t) __attribute__((always_inline)) {
-        if (t & 1) return;
+    // next pair (half the barriers of one per tile: -1% on this kernel).  u: the tile's index
+    // from tb
+    auto enter = [&](int u) __attribute__((always_inline)) {
+        if (u & 1) return;
         wait_vmcnt<0>();
         lds_barrier();
-        if (t + 2 < ntiles) issue((t + 2) * BN, (st + 2) & 3);
-        if (t + 3 < ntiles) issue((t + 3) * BN, (st + 3) & 3);
+        if (u + 2 < ntl) issue((tb + u + 2) * BN, (st + 2) & 3);
+        if (u + 3 < ntl) issue((tb + u + 3) * BN, (st + 3) & 3);
     };
-    for (int t = 0; t < nact; ++t) {
-        const int j0 = t * BN;
-        enter(t);
+    for (int u = 0; u < nact; ++u) {
+        const int j0 = (tb + u) * BN;
+        enter(u);
         const T* K = sK + st * TL::ELEMS;
         const T* V = sV + st * TL::ELEMS;
         if (HAS_BIAS) {
@@ -884,8 +895,8 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
         }
         st = next_st(st);
     }
-    for (int t = nact; t < ntiles; ++t) {
-        enter(t);
+    for (int u = nact; u < ntl; ++u) {
+        enter(u);
         st = next_st(st);
     }
 

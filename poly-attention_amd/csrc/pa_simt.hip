@@ -706,18 +706,21 @@ __global__ __launch_bounds__(kSimtRows) void k_simt_bwd_dkv(GradDev G) {
 // on each bias-class-0 key j.  Part B is a plain loop over the rare (row, key) pairs.
 
 // Per (b, key head): the count of bias-class-0 keys and of unmasked bias-class-1 keys (part
-// B exists only where the latter is nonzero; with kcnt), and (with kterm) the per-key term the
-// MFMA kernels read as their bias, rows of stride nkp.  A workgroup walks a key row in rounds
+// B exists only where the latter is nonzero; with kcnt), (with kterm) the per-key term the
+// MFMA kernels read as their bias, rows of stride nkp, and (with live) the range [first, last
+// + 1) of the keys that are kept and of bias class 0 -- the only keys that enter a normal row;
+// [nk, 0) when there is none.  The MFMA forward and dQ kernels start and end their key loops
+// at the range (padding masks: the masked prefix or suffix is not even loaded).  A workgroup walks a key row in rounds
 // of kKeyTermThreads x kKeyTermPer keys, every load of a round issued before its first use (the
 // key-mask bytes may alias the key-term stores, so a loop mixing them would load one key at
 // a time); at 4096 keys that is one round instead of 16 dependent steps.
 constexpr int kKeyTermThreads = 1024, kKeyTermPer = 4;
 __global__ __launch_bounds__(kKeyTermThreads) void k_key_terms(GradDev G, float* kterm, int nkp,
-                                                               int32_t* kcnt) {
+                                                               int32_t* kcnt, int32_t* live) {
     const PassDev& P = G.f;
     const int kh = blockIdx.x, b = blockIdx.y;
     const int h0 = kh * (P.heads / G.hk);
-    int c0 = 0, c1 = 0;
+    int c0 = 0, c1 = 0, lo = P.nk, hi = 0;
     for (int j0 = 0; j0 < P.nk; j0 += kKeyTermThreads * kKeyTermPer) {
         float x[kKeyTermPer];
         bool kept[kKeyTermPer];
@@ -734,30 +737,48 @@ __global__ __launch_bounds__(kKeyTermThreads) void k_key_terms(GradDev G, float*
             const int cls = bias_class(x[u]);
             c0 += cls == 0;
             c1 += cls == 1 && kept[u];
+            if (cls == 0 && kept[u]) {
+                lo = min(lo, j);
+                hi = j + 1;
+            }
             if (kterm) kterm[((int64_t)b * G.hk + kh) * nkp + j] = kept[u] ? x[u] : -INFINITY;
         }
     }
-    if (!kcnt) return;  // whole workgroup: the forward needs only the key term
+    if (!kcnt && !live) return;  // whole workgroup: nothing to reduce
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         c0 += __shfl_xor(c0, off);
         c1 += __shfl_xor(c1, off);
+        lo = min(lo, __shfl_xor(lo, off));
+        hi = max(hi, __shfl_xor(hi, off));
     }
     __shared__ int s0[kKeyTermThreads / 64], s1[kKeyTermThreads / 64];
+    __shared__ int slo[kKeyTermThreads / 64], shi[kKeyTermThreads / 64];
     const int w = threadIdx.x / 64;
     if (threadIdx.x % 64 == 0) {
         s0[w] = c0;
         s1[w] = c1;
+        slo[w] = lo;
+        shi[w] = hi;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        int t0 = 0, t1 = 0;
+        int t0 = 0, t1 = 0, tlo = P.nk, thi = 0;
         for (int k = 0; k < (int)blockDim.x / 64; ++k) {
             t0 += s0[k];
             t1 += s1[k];
+            tlo = min(tlo, slo[k]);
+            thi = max(thi, shi[k]);
         }
-        kcnt[2 * ((int64_t)b * G.hk + kh)] = t0;
-        kcnt[2 * ((int64_t)b * G.hk + kh) + 1] = t1;
+        const int64_t u = (int64_t)b * G.hk + kh;
+        if (kcnt) {
+            kcnt[2 * u] = t0;
+            kcnt[2 * u + 1] = t1;
+        }
+        if (live) {
+            live[2 * u] = tlo;
+            live[2 * u + 1] = thi;
+        }
     }
 }
 
@@ -1252,10 +1273,11 @@ void launch_epi_bwd(const GradDev& G, void* dO, int hr, int dtype, hipStream_t s
     else launch_epi_bwd_t<bf16>(G, (bf16*)dO, hr, s);
 }
 
-void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, hipStream_t s) {
+void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, int32_t* live,
+                      hipStream_t s) {
     ProfScope ps("key_terms", s);
     hipLaunchKernelGGL(k_key_terms, dim3(G.hk, G.f.batch), dim3(kKeyTermThreads), 0, s, G, kterm,
-                       nkp, kcnt);
+                       nkp, kcnt, live);
 }
 
 void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s) {
