@@ -13,6 +13,7 @@
 #pragma once
 
 #include "pa_common.h"
+#include "pa_order.h"
 
 namespace pa {
 
@@ -231,69 +232,14 @@ __device__ __forceinline__ u32x2_t lds_read_tr(const void* p) {
 // bare v_exp_f32 (2^x; results below 2^-126 flush to 0, which softmax weights tolerate)
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Map the
-// hardware id to a logical id so that every XCD runs a contiguous range of logical ids --
-// consecutive logical ids share a head, so its K/V stay in that XCD's L2.
-constexpr int kNumXcd = 8;
-__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
-    const int per = nblocks / kNumXcd, rem = nblocks % kNumXcd;
-    const int x = bid % kNumXcd, slot = bid / kNumXcd;
-    return (x < rem) ? x * (per + 1) + slot : rem * (per + 1) + (x - rem) * per + slot;
-}
-
-// The unit (batch-major, head-minor) of the j-th of the nu units that XCD x runs.  Where the
-// heads split evenly over the XCDs in runs of whole groups (`group` consecutive heads share
-// their K / V: GQA), each XCD takes heads [x * hpx, (x + 1) * hpx) of every batch row, so that
-// work that differs by batch row (padding masks) is spread over all XCDs; otherwise the XCD's
-// units are consecutive.
-__device__ __forceinline__ int xcd_unit(int x, int j, int nu, int heads, int group) {
-    if (heads % (kNumXcd * group) == 0) {
-        const int hpx = heads / kNumXcd;
-        return (j / hpx) * heads + x * hpx + j % hpx;
-    }
-    return x * nu + j;
-}
-
-// Causal grids (work per block falls with its rank): logical order in which every XCD runs
-// whole (batch, head) units and dispatches the heaviest blocks of all its units first, so the
-// light blocks fill the end of the kernel.  When the XCD ranges do not hold whole units, the
-// order is unit by unit (heaviest first inside each unit).
-__device__ __forceinline__ void heavy_first(int bid, int nblocks, int nblk, int heads, int group,
-                                            int& unit, int& rank) {
-    const int lid = xcd_remap(bid, nblocks);
-    const int per = nblocks / kNumXcd;
-    if (nblocks % kNumXcd == 0 && per % nblk == 0) {
-        const int x = lid / per, k = lid % per, nu = per / nblk;
-        unit = xcd_unit(x, k % nu, nu, heads, group);
-        rank = k / nu;
-    } else {
-        unit = lid / nblk;
-        rank = lid % nblk;
-    }
-}
-
 #ifndef PA_HEAVY_FIRST
 #define PA_HEAVY_FIRST 1
 #endif
 
-// (unit, rank) of this workgroup: causal grids in heavy_first order, others unit by unit (each
-// unit's blocks consecutive on one XCD).  heads: units per batch row; group: see xcd_unit.
+// (unit, rank) of this workgroup (pa_order.h): causal grids heaviest blocks first
 template <bool CAUSAL>
 __device__ __forceinline__ void block_order(int nblk, int heads, int group, int& unit, int& rank) {
-    if (CAUSAL && PA_HEAVY_FIRST) {
-        heavy_first(blockIdx.x, gridDim.x, nblk, heads, group, unit, rank);
-        return;
-    }
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int per = gridDim.x / kNumXcd;
-    if (gridDim.x % kNumXcd == 0 && per % nblk == 0) {
-        const int x = lid / per, k = lid % per;
-        unit = xcd_unit(x, k / nblk, per / nblk, heads, group);
-        rank = k % nblk;
-    } else {
-        unit = lid / nblk;
-        rank = lid % nblk;
-    }
+    block_map(blockIdx.x, gridDim.x, nblk, heads, group, CAUSAL && PA_HEAVY_FIRST, unit, rank);
 }
 
 static inline bool aligned_rows_host(const DView& v, int elems) {
