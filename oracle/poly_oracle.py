@@ -203,13 +203,16 @@ def n_poly_core(q_left: Sequence[Tensor], q_right: Sequence[Tensor], vs_full: Se
 
 def order2_rows(q1: Tensor, q2: Tensor, q3: Tensor, v3: Tensor, rows: Tensor,
                 dout_rows: Optional[Tensor] = None, causal: bool = True,
-                softclamp_value: Optional[float] = None, chunk: int = 1024):
-    """reference_poly_attention (poly_attention.py:48-116, no cache, no masks) for one
-    (batch, head) slice at lengths where the N x N score matrix does not fit: pass 1 runs over
-    every pass-1 row in chunks of ``chunk`` rows (its msg / lse23 feed every pass-2 key), pass 2
-    only for the query rows ``rows``.  q* / v3: [N, d].  Returns (out[rows], msg, lse23) and,
-    with the upstream gradient of those rows, also dq1[rows] (the pass-2 score gradient, which
-    involves only the row itself: dS = P (dP - rowsum(dO * O)), dq1 = scale * dS q2 through the
+                softclamp_value: Optional[float] = None, chunk: int = 1024,
+                key_keep: Optional[Tensor] = None):
+    """reference_poly_attention (poly_attention.py:48-116, no cache) for one (batch, head)
+    slice at lengths where the N x N score matrix does not fit: pass 1 runs over every pass-1
+    row in chunks of ``chunk`` rows (its msg / lse23 feed every pass-2 key), pass 2 only for the
+    query rows ``rows``.  q* / v3: [N, d].  ``key_keep`` ([N] bool): a key mask of both passes,
+    as the context masks (poly_attention.py:75-76, 101-102) and the flash op's key mask
+    (flash_poly_attention.py:109-112) apply it.  Returns (out[rows], msg, lse23) and, with the
+    upstream gradient of those rows, also dq1[rows] (the pass-2 score gradient, which involves
+    only the row itself: dS = P (dP - rowsum(dO * O)), dq1 = scale * dS q2 through the
     softclamp's derivative)."""
     n, d = q1.shape
     scale = d ** -0.5
@@ -225,12 +228,16 @@ def order2_rows(q1: Tensor, q2: Tensor, q3: Tensor, v3: Tensor, rows: Tensor,
         if causal:
             later = torch.arange(kend)[None, :] > torch.arange(i0, i1)[:, None]
             sim = sim.masked_fill(later, mask_value)
+        if key_keep is not None:
+            sim = sim.masked_fill(~key_keep[None, :kend], mask_value)
         lse23[i0:i1] = sim.logsumexp(dim=-1)
         msg[i0:i1] = sim.softmax(dim=-1) @ v3[:kend]
     raw = (q1[rows] @ q2.T) * scale
     sim = softclamp(raw, softclamp_value) if exists(softclamp_value) else raw
     if causal:
         sim = sim.masked_fill(torch.arange(n)[None, :] > rows[:, None], mask_value)
+    if key_keep is not None:
+        sim = sim.masked_fill(~key_keep[None, :], mask_value)
     sim = sim + lse23[None, :]
     attn = sim.softmax(dim=-1)
     out = attn @ msg
@@ -241,6 +248,8 @@ def order2_rows(q1: Tensor, q2: Tensor, q3: Tensor, v3: Tensor, rows: Tensor,
         dsim = dsim * (1 - torch.tanh(raw / softclamp_value) ** 2)
     if causal:
         dsim = dsim.masked_fill(torch.arange(n)[None, :] > rows[:, None], 0.0)
+    if key_keep is not None:
+        dsim = dsim.masked_fill(~key_keep[None, :], 0.0)
     dq1 = (dsim @ q2) * scale
     return out, msg, lse23, dq1
 

@@ -7,6 +7,7 @@ causal flash_poly_attention on (1, 4, N, 64) for N = 8k, 16k, 32k and 64k, forwa
 * Parity: out and dq1 of six query rows of one head (first, last, middle and near the ends)
   against the chunked oracle (oracle.order2_rows: pass 1 over every row in chunks, pass 2 for
   the chosen rows), within the fp16 bound of tests/parity.py.
+* The same in bf16 at N = 16384 with a key-padding mask (left- and right-padded batch rows).
 """
 
 import time
@@ -69,3 +70,38 @@ def test_long_sequences_fp16_causal_memory_and_rows():
     ratio = peaks[LENGTHS[-1]] / peaks[LENGTHS[0]]
     print(f"[long] peak(64k) / peak(8k) = {ratio:.2f}", flush=True)
     assert ratio <= 8 * 1.1
+
+
+def test_long_sequence_padding_masks_bf16_causal_rows():
+    """bf16 causal flash_poly_attention with a key-padding mask (the op's key mask of both
+    passes, flash_poly_attention.py:109-112) at N = 16384, B = 2, 8 heads: batch 0 right-padded
+    (keys from 12000 on masked), batch 1 left-padded (keys below 5000 masked).  The grid takes
+    the order that gives every XCD heads of both batch rows, and the forward and dQ loops run
+    over each row's live key range only.  out and dq1 of six query rows of two heads in each
+    batch row (rows that keep a key) against the chunked oracle with the same mask."""
+    from poly_attention.flash_poly_attention import flash_poly_attention
+
+    d = dev()
+    torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
+    Bm, Hm, n = 2, 8, 16384
+    gen = torch.Generator().manual_seed(7)
+    ts = [torch.randn(Bm, Hm, n, D, generator=gen).to(torch.bfloat16) for _ in range(4)]
+    dout = torch.randn(Bm, Hm, n, D, generator=gen).to(torch.bfloat16)
+    keep = torch.ones(Bm, n, dtype=torch.bool)
+    keep[0, 12000:] = False
+    keep[1, :5000] = False
+    g = [t.to(d).requires_grad_() for t in ts]
+    out = flash_poly_attention(*g, mask=keep.to(d), is_causal=True)
+    out.backward(dout.to(d))
+    torch.cuda.synchronize()
+    row_sets = {0: [0, 1, 777, 11999, 12000, n - 1], 1: [5000, 5001, 8192, 12000, n - 2, n - 1]}
+    for b, rows in row_sets.items():
+        rows = torch.tensor(rows)
+        for h in (0, 5):
+            sl = [t[b, h].float() for t in ts]
+            ref_out, _, _, ref_dq1 = O.order2_rows(*sl, rows, dout_rows=dout[b, h, rows].float(),
+                                                   causal=True, chunk=2048, key_keep=keep[b])
+            what = f"long padded N={n} batch {b} head {h} rows {rows.tolist()}"
+            assert_parity(out[b, h, rows], ref_out, torch.bfloat16, f"{what} out")
+            assert_parity(g[0].grad[b, h, rows], ref_dq1, torch.bfloat16, f"{what} dq1",
+                          grad=True)

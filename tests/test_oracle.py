@@ -65,6 +65,44 @@ def test_order2_rows_equals_full_core_and_its_dq1(causal, softclamp):
     np.testing.assert_allclose(out.numpy(), brute[0, 0, rows.numpy()], rtol=1e-10, atol=1e-10)
 
 
+@param("causal", (False, True))
+def test_order2_rows_with_a_key_mask(causal):
+    """order2_rows with a key mask of both passes: out, msg, lse23 and dq1 of rows that keep
+    a key equal reference_poly_attention with that mask as both context masks (and its
+    autograd); without causality also the brute-force pair softmax over the kept keys alone
+    (q2, q3, v3 restricted to them), and a mask applied to pass 2 only fails that pin."""
+    n, d = 41, 8
+    q1, q2, q3, v3 = (rnd(n, d, seed=60 + s) for s in range(4))
+    keep = torch.ones(n, dtype=torch.bool)
+    keep[:6] = False
+    keep[20:27] = False
+    keep[33] = False
+    rows = torch.tensor([6, 7, 19, 30, 40])  # each keeps at least one key (causal too)
+    dout = rnd(len(rows), d, seed=65)
+    out, msg, lse23, dq1 = O.order2_rows(q1, q2, q3, v3, rows, dout_rows=dout, causal=causal,
+                                         chunk=9, key_keep=keep)
+    q = [t[None, None].clone().requires_grad_() for t in (q1, q2, q3, v3)]
+    km = keep[None]
+    ref, lse_r, msg_r = O.reference_poly_attention(q[0], q[1], q[1], q[2], q[3], causal=causal,
+                                                   context_mask=(km, km))
+    g = torch.zeros_like(ref)
+    g[0, 0, rows] = dout
+    ref.backward(g)
+    torch.testing.assert_close(out, ref[0, 0, rows].detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(msg[keep], msg_r[0, 0, keep].detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(lse23[keep], lse_r[0, 0, keep].detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(dq1, q[0].grad[0, 0, rows], rtol=1e-10, atol=1e-10)
+    if not causal:
+        sub = [t[keep][None, None] for t in (q2, q3, v3)]
+        brute = O.brute_order2(q1[None, None], *sub)
+        np.testing.assert_allclose(out.numpy(), brute[0, 0, rows.numpy()], rtol=1e-10,
+                                   atol=1e-10)
+        wrong, _, _ = O.reference_poly_attention(q1[None, None], q2[None, None], q2[None, None],
+                                                 q3[None, None], v3[None, None],
+                                                 context_mask=(km, None))
+        assert np.abs(wrong[0, 0, rows].numpy() - brute[0, 0, rows.numpy()]).max() > 1e-3
+
+
 def test_order2_brute_force_detects_dropped_bias():
     # planting a mistake in the oracle (no lse bias in pass 2) must break the pin
     q1, q2, q3, v3 = (rnd(1, 2, 6, 8, seed=10 + s) for s in range(4))
