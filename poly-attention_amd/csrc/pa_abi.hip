@@ -512,7 +512,6 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
         int32_t* live = reinterpret_cast<int32_t*>(w);
         G.ws_kcnt = kcnt;
         launch_key_terms(G, kterm, nkp, kcnt, live, s);
-        launch_simt_bwd(G, T, s, /*pre=*/true, false, false);
         GradDev Gm = G;
         if (kterm) {
             DView& kb = Gm.f.bias;
@@ -527,6 +526,11 @@ int pa_attn_pass_bwd(const pa_pass_grad* g, void* stream) {
         Gm.f.qm.p = nullptr;
         Gm.f.flags &= ~PA_FLAG_MAY_DEGENERATE;
         Gm.f.live = live;
+        // the direct-to-LDS dQ kernel does the preprocess of the normal rows where it applies
+        // (fully-masked rows get lse +inf there: no normal entry; k_fix_rows does the rest of
+        // their preprocess from the original masks)
+        Gm.fused_pre = mfma_bwd_fuses_pre(Gm) ? 1 : 0;
+        if (!Gm.fused_pre) launch_simt_bwd(G, T, s, /*pre=*/true, false, false);
         launch_mfma_bwd(Gm, T, s);
         launch_mask_fixups(G, T, s);
     } else if (mfma_bwd_supported(G, T)) {

@@ -787,10 +787,14 @@ __device__ __forceinline__ bool degenerate_row(const GradDev& G, int64_t r) {
 }
 
 // Part A sums over the fully-masked rows, one workgroup per (b, query head, chunk of
-// kFixRowChunk rows): D/8 lanes per row, 16 bytes of dO each; each lane group's rows go four
-// at a time with every load issued first (rows that are not fully masked weigh 0); the row
-// slots are then summed through LDS into the chunk's partial row (fixed order: the sums are
-// deterministic).  A chunk without such a row writes zeros after one scan of its lse.
+// kFixRowChunk rows): D/8 lanes per row, 16 bytes of dO and of O each; each lane group's rows
+// go eight at a time with every load issued first (rows that are not fully masked weigh 0).
+// A fully-masked row is known by its lse entry, which is not finite (+inf from the preprocess
+// kernel, or the dQ kernel's seed of +inf); its preprocess is done here, from the original
+// masks: c1 (its class-1 entries), 1/c1 and D = rowsum(dO * O) - c1 * dlse, written back as
+// lse = +inf, 1/c1, D for the part B kernels.  The row slots are then summed through LDS into
+// the chunk's partial row (fixed order: the sums are deterministic).  A chunk without such a
+// row writes zeros after one scan of its lse.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
     const PassDev& P = G.f;
@@ -808,7 +812,7 @@ __global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
 #pragma unroll
         for (int k = 0; k < kFixRowChunk / 256; ++k) l[k] = G.ws_lse[row0 + min(i0 + (int)threadIdx.x + 256 * k, i1 - 1)];
 #pragma unroll
-        for (int k = 0; k < kFixRowChunk / 256; ++k) any |= l[k] == INFINITY;
+        for (int k = 0; k < kFixRowChunk / 256; ++k) any |= !isfinite(l[k]);
     }
     if (!__syncthreads_or(any)) {
         if (threadIdx.x < D + 2) part[threadIdx.x] = 0.f;
@@ -817,27 +821,54 @@ __global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
     float u[8], wsum = 0.f, cnt = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) u[e] = 0.f;
+    // the key head's class counts (see degenerate_count): c1 of a fully-masked row is the
+    // class-0 count unless the row's query is kept and unmasked class-1 keys exist
+    int kc0 = 0, kc1 = 1;
+    if (G.ws_kcnt) {
+        const int32_t* kc = G.ws_kcnt + 2 * ((int64_t)b * G.hk + h / (P.heads / G.hk));
+        kc0 = kc[0];
+        kc1 = kc[1];
+    }
     for (int ib = i0 + slot; ib < i1; ib += R * U) {
-        float li[U], ic[U], dd[U], g8[U][8];
+        float li[U], dl[U], g8[U][8], o8[U][8];
+        bool qk[U];
 #pragma unroll
         for (int k = 0; k < U; ++k) {
             // every load of the round before the first use (a load behind a lane-dependent
             // condition would make the branch's join wait for it)
             const int i = min(ib + k * R, i1 - 1);
             li[k] = G.ws_lse[row0 + i];
-            ic[k] = G.ws_invc[row0 + i];
-            dd[k] = G.ws_D[row0 + i];
+            dl[k] = G.dlse.ok() ? *G.dlse.row<float>(b, h, i) : 0.f;
+            qk[k] = P.qm.keep(b, i);
             load8<T>(G.dout.row<T>(b, h, i) + c0, g8[k]);
+            load8<T>(P.out.row<T>(b, h, i) + c0, o8[k]);
         }
 #pragma unroll
-        for (int k = 0; k < U; ++k)  // degenerate rows only (see degenerate_row)
-            ic[k] = ib + k * R < i1 && li[k] == INFINITY && ic[k] > 0.f ? ic[k] : 0.f;
-#pragma unroll
         for (int k = 0; k < U; ++k) {
+            // the row's preprocess, for fully-masked rows: whether the preprocess kernel or
+            // the dQ kernel (seed form) ran, such a row's lse entry is not finite
+            float ds = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) u[e] += ic[k] * g8[k][e];
-            wsum += ic[k] * dd[k];
-            cnt += ic[k] > 0.f ? 1.f : 0.f;
+            for (int e = 0; e < 8; ++e) ds += o8[k][e] * g8[k][e];
+#pragma unroll
+            for (int off = LPR / 2; off > 0; off >>= 1) ds += __shfl_xor(ds, off);
+            const int i = ib + k * R;
+            float ic = 0.f, dd = 0.f;
+            if (i < i1 && !isfinite(li[k])) {
+                const float c1 = G.ws_kcnt && (!qk[k] || kc1 == 0) ? (float)kc0
+                                                                 : degenerate_count(G, b, h, i);
+                ic = c1 > 0.f ? 1.f / c1 : 0.f;
+                dd = c1 > 0.f ? ds - c1 * dl[k] : 0.f;
+                if (c0 == 0) {  // the canonical entries the part B kernels read
+                    G.ws_lse[row0 + i] = INFINITY;
+                    G.ws_invc[row0 + i] = ic;
+                    G.ws_D[row0 + i] = dd;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) u[e] += ic * g8[k][e];
+            wsum += ic * dd;
+            cnt += ic > 0.f ? 1.f : 0.f;
         }
     }
     __shared__ float sU[R][D];
