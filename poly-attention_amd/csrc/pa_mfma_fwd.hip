@@ -790,6 +790,9 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb) s[0][kb] = M::run(kf[kb][c], wv[0].qf[c], s[0][kb]);
             wv[0].mask_edges_nk(s[0], j0);
+            // the first tile: O and l are still 0, so the running max is just the tile's (no
+            // attempt against m = -inf that the sum check would send back)
+            if (u == 0) wv[0].m = wv[0].logits(s[0], sBw[w]);
             __builtin_amdgcn_sched_barrier(0);
             // (B)
             u32x4_t pk0[KB][2];
@@ -821,6 +824,7 @@ __global__ __launch_bounds__(kFwdThreads, D == 64 ? 2 : 1) void k_mfma_fwd_dma(P
                     }
             recheck(0, lt0, pk0);
             wv[1].mask_edges_nk(s[1], j0);
+            if (u == 0) wv[1].m = wv[1].logits(s[1], sBw[w]);
             __builtin_amdgcn_sched_barrier(0);
             // (C)
             u32x4_t pk1[KB][2];
