@@ -253,6 +253,22 @@ def test_pass_padding_masks_units_spread_over_xcds(gqa):
 
 
 @param("causal", (False, True))
+def test_pass_padding_masks_ragged_length(causal):
+    """A length that is not a multiple of the 64-key tile (1000) with padding that does not
+    align to tiles: batch 0 left-padded (keys 0-332 masked), batch 1 right-padded (keys from
+    777 on masked), 8 query heads over 4 key heads.  The live key range then starts and ends
+    inside tiles, and its last tile is also the partial last tile of the keys."""
+    B, H, HK, n, d = 2, 8, 4, 1000, 64
+    q = randn((B, H, n, d), torch.bfloat16, 91)
+    k, v = (randn((B, HK, n, d), torch.bfloat16, s) for s in (92, 93))
+    km = torch.ones(B, n, dtype=torch.bool)
+    km[0, :333] = False
+    km[1, 777:] = False
+    res = run_pass(q, k, v, key_mask=km, causal=causal)
+    check(res, torch.bfloat16, f"padding masks ragged n={n} causal={causal}")
+
+
+@param("causal", (False, True))
 def test_pass_key_masked_forward_with_and_without_workspace(causal):
     """pa_attn_pass_fwd on a key-masked bf16 pass: with its optional workspace the key mask
     becomes a per-key term and the direct-to-LDS kernel runs; without it the register-staged
