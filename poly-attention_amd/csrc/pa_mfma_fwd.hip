@@ -984,7 +984,7 @@ __device__ __forceinline__ u32x4_t pack8(const float (&v)[8]) {
 // the others; the chunk sums combine as that kernel's butterfly over its 8 lanes does: chunk
 // pairs first, then (t0 + t1) + (t2 + t3)
 template <typename T>
-__device__ __forceinline__ void norm_q_frags(u32x4_t (&q)[4], const void* weight, float eps, int hh) {
+__device__ __forceinline__ void norm_q_frags(u32x4_t (&q)[4], const u32x4_t (&wf)[4], float eps) {
     constexpr int D = 64;
     float x[D / 16][8], t[D / 16];
 #pragma unroll
@@ -999,10 +999,21 @@ __device__ __forceinline__ void norm_q_frags(u32x4_t (&q)[4], const void* weight
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
         float wq[8], y[8];
-        unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(weight) + c * 16 + 8 * hh), wq);
+        unpack8<T>(wf[c], wq);
         norm_scale(x[c], rs, wq, y);
         q[c] = pack8<T>(y);
     }
+}
+
+// The lane's norm weight fragments of a Q^T operand row (as norm_q_frags takes them), loaded
+// beside the row data; without a norm (w null) a valid row is read instead and not used, so
+// that no load sits behind a branch (a branch's join waits for the loads issued before it)
+template <typename T>
+__device__ __forceinline__ void load_wq_frags(u32x4_t (&wf)[4], const void* w, const T* fallback,
+                                              int hh) {
+    const T* p = w ? static_cast<const T*>(w) : fallback;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) wf[c] = *reinterpret_cast<const u32x4_t*>(p + c * 16 + 8 * hh);
 }
 
 // RMSNorm of a row chunk (8 features) whose row's 8 chunks sit in 8 consecutive lanes, summed
@@ -1137,6 +1148,11 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     }
     float braw = 0.f;  // lane j's key bias (BN = 64 keys, one per lane)
     if (HAS_BIAS) braw = P.bias.scalar(b, h, min(lane, P.nk - 1));
+    // the norm weights, loaded with the rows (see load_wq_frags)
+    u32x4_t wqf[4], wkr;
+    load_wq_frags<T>(wqf, (P.nflags & PA_NORM_Q) ? P.qnw : nullptr, P.q.row<T>(b, h, 0), hh);
+    wkr = *reinterpret_cast<const u32x4_t*>(
+        ((P.nflags & PA_NORM_K) ? static_cast<const T*>(P.knw) : P.k.row<T>(b, h, 0)) + (lane % (D / 8)) * 8);
 #pragma unroll
     for (int u = 0; u < QPW; ++u)
         if (32 * (qb0 + u) + kcol >= P.nq)
@@ -1151,10 +1167,10 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_fwd_short(PassDev P) {
     // optional RMSNorms of the queries and keys
     if (P.nflags & PA_NORM_Q)
 #pragma unroll
-        for (int u = 0; u < QPW; ++u) norm_q_frags<T>(qraw[u], P.qnw, P.qeps, hh);
+        for (int u = 0; u < QPW; ++u) norm_q_frags<T>(qraw[u], wqf, P.qeps);
     if (P.nflags & PA_NORM_K) {
         float wk[8];
-        unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P.knw) + (lane % (D / 8)) * 8), wk);
+        unpack8<T>(wkr, wk);
 #pragma unroll
         for (int i = 0; i < NR; ++i)
 #pragma unroll
@@ -1245,6 +1261,12 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_order2_short(PassDev P1
             vw[r] = *reinterpret_cast<const u32x4_t*>(P1.v.row<T>(b, h, j) + cc * 8);
         }
     }
+    // the norm weights, loaded with the rows (see load_wq_frags)
+    u32x4_t w2f[4], w1f[4], wkr;
+    load_wq_frags<T>(w2f, (P1.nflags & PA_NORM_Q) ? P1.qnw : nullptr, P1.q.row<T>(b, h, 0), hh);
+    load_wq_frags<T>(w1f, (P2.nflags & PA_NORM_Q) ? P2.qnw : nullptr, P2.q.row<T>(b, h, 0), hh);
+    wkr = *reinterpret_cast<const u32x4_t*>(
+        ((P1.nflags & PA_NORM_K) ? static_cast<const T*>(P1.knw) : P1.k.row<T>(b, h, 0)) + cc * 8);
     if (row >= n2)
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) q2r[c] = zero;
@@ -1255,11 +1277,11 @@ __global__ __launch_bounds__(kFwdThreads, 2) void k_mfma_order2_short(PassDev P1
     for (int r = 0; r < 4; ++r)
         if (rg * 4 + r >= P1.nk) kw[r] = vw[r] = zero;
 
-    if (P1.nflags & PA_NORM_Q) norm_q_frags<T>(q2r, P1.qnw, P1.qeps, hh);
-    if (P2.nflags & PA_NORM_Q) norm_q_frags<T>(q1r, P2.qnw, P2.qeps, hh);
+    if (P1.nflags & PA_NORM_Q) norm_q_frags<T>(q2r, w2f, P1.qeps);
+    if (P2.nflags & PA_NORM_Q) norm_q_frags<T>(q1r, w1f, P2.qeps);
     if (P1.nflags & PA_NORM_K) {
         float wk[8];
-        unpack8<T>(*reinterpret_cast<const u32x4_t*>(static_cast<const T*>(P1.knw) + cc * 8), wk);
+        unpack8<T>(wkr, wk);
 #pragma unroll
         for (int r = 0; r < 4; ++r) norm_row_chunk<T>(kw[r], wk, P1.keps);
     }
