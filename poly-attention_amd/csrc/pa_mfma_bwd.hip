@@ -1326,7 +1326,9 @@ bool mfma_bwd_supported(const GradDev& G, int dtype) {
     const PassDev& P = G.f;
     if (dtype == PA_F32) return mfma_bwd_f32_supported(G);
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
-    if (P.dim != 64 && P.dim != 128) return false;
+    if (P.dim != 64 && P.dim != 128 && P.dim != 256) return false;
+    // head dim 256: unmasked passes only (the mask fix-ups hold rows of at most 128)
+    if (P.dim == 256 && (P.km.p || P.qm.p || (P.flags & PA_FLAG_MAY_DEGENERATE))) return false;
     const DView* loads[] = {&P.q, &P.k, &P.v, &G.dout};
     for (const DView* v : loads)
         if (!aligned_rows_host(*v, 8)) return false;
@@ -1377,16 +1379,21 @@ static void launch_dq(const GradDev& G, hipStream_t s) {
     const PassDev& P = G.f;
     dim3 grid(((P.nq + kDqBM - 1) / kDqBM) * P.heads * P.batch);
     ProfScope ps("mfma_bwd_dq", s);
-    if (!V && PA_BWD_DMA && bwd_dq_dma_ok(G))
-        hipLaunchKernelGGL((k_mfma_bwd_dq_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
-    else
-        hipLaunchKernelGGL((k_mfma_bwd_dq<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
+    // head dim 256: the register-staged kernels only (their direct-to-LDS stages would not
+    // fit in LDS)
+    if constexpr (D != 256) {
+        if (!V && PA_BWD_DMA && bwd_dq_dma_ok(G)) {
+            hipLaunchKernelGGL((k_mfma_bwd_dq_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((k_mfma_bwd_dq<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
 }
 
 template <typename T, int D, bool C, bool S, bool V, bool B>
 static void launch_bwd_t(const GradDev& G0, hipStream_t s) {
     const PassDev& P = G0.f;
-    const bool kv_dma = !V && PA_BWD_DMA && bwd_dma_ok(G0);
+    const bool kv_dma = D != 256 && !V && PA_BWD_DMA && bwd_dma_ok(G0);
     GradDev G = G0;
     // the dQ kernel writes the preprocess in the direct-to-LDS dK/dV kernel's seed form
     G.seeds = (G.fused_pre && kv_dma) ? 1 : 0;
@@ -1394,9 +1401,14 @@ static void launch_bwd_t(const GradDev& G0, hipStream_t s) {
     {
         dim3 grid(((P.nk + kKvBK - 1) / kKvBK) * G.hk * P.batch);
         ProfScope ps("mfma_bwd_dkv", s);
-        if (kv_dma)
-            hipLaunchKernelGGL((k_mfma_bwd_dkv_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
-        else
+        bool done = false;
+        if constexpr (D != 256) {  // head dim 256: the register-staged kernel only
+            if (kv_dma) {
+                hipLaunchKernelGGL((k_mfma_bwd_dkv_dma<T, D, C, S, B>), grid, dim3(kBwdThreads), 0, s, G);
+                done = true;
+            }
+        }
+        if (!done)
             hipLaunchKernelGGL((k_mfma_bwd_dkv<T, D, C, S, V, B>), grid, dim3(kBwdThreads), 0, s, G);
     }
     if (!G.fused_pre) launch_dq<T, D, C, S, V, B>(G, s);
@@ -1423,10 +1435,12 @@ void launch_mfma_bwd(const GradDev& G, int dtype, hipStream_t s) {
     }
     if (dtype == PA_BF16) {
         if (G.f.dim == 64) launch_bwd_d<bf16, 64>(G, s);
-        else launch_bwd_d<bf16, 128>(G, s);
+        else if (G.f.dim == 128) launch_bwd_d<bf16, 128>(G, s);
+        else launch_bwd_d<bf16, 256>(G, s);
     } else {
         if (G.f.dim == 64) launch_bwd_d<f16, 64>(G, s);
-        else launch_bwd_d<f16, 128>(G, s);
+        else if (G.f.dim == 128) launch_bwd_d<f16, 128>(G, s);
+        else launch_bwd_d<f16, 256>(G, s);
     }
 }
 

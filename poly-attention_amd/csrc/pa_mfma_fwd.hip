@@ -1354,12 +1354,14 @@ static bool dma_ok(const PassDev& P, int bn) {
 
 // 32-key blocks per key tile (64-key tiles)
 template <int D, bool SOFTCLAMP>
-constexpr int kFwdKB = (D == 64 && !SOFTCLAMP) ? PA_FWD_KB64 : 2;
+constexpr int kFwdKB = (D == 64 && !SOFTCLAMP) ? PA_FWD_KB64 : (D == 256 ? 1 : 2);
 
 bool mfma_fwd_supported(const PassDev& P, int dtype) {
     if (dtype == PA_F32) return mfma_fwd_f32_supported(P);
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
-    if (P.dim != 64 && P.dim != 128) return false;
+    if (P.dim != 64 && P.dim != 128 && P.dim != 256) return false;
+    // head dim 256: unmasked passes only (the mask fix-ups hold rows of at most 128)
+    if (P.dim == 256 && (P.km.p || P.qm.p || (P.flags & PA_FLAG_MAY_DEGENERATE))) return false;
     if (!(P.scale > 0.f)) return false;  // the raw-score running max assumes a positive scale
     if (!aligned_rows_host(P.q, 8) || !aligned_rows_host(P.k, 8) || !aligned_rows_host(P.v, 8)) return false;
     if (P.vmul.ok() && !aligned_rows_host(P.vmul, 8)) return false;
@@ -1391,14 +1393,18 @@ static void launch_t(const PassDev& P, hipStream_t s) {
     const int nqb = (P.nq + kFwdBM - 1) / kFwdBM;
     dim3 grid(nqb * P.heads * P.batch);
     ProfScope ps("mfma_fwd", s);
-    if (!V && dma_ok(P, 32 * KB)) {
-        constexpr int QB = (D == 64) ? PA_FWD_QB64 : 1;
-        const int nqb2 = (P.nq + kFwdBM * QB - 1) / (kFwdBM * QB);
-        hipLaunchKernelGGL((k_mfma_fwd_dma<T, D, KB, QB, C, S, B>), dim3(nqb2 * P.heads * P.batch),
-                           dim3(kFwdThreads), 0, s, P);
-    } else {
-        hipLaunchKernelGGL((k_mfma_fwd<T, D, KB, C, S, V, B>), grid, dim3(kFwdThreads), 0, s, P);
+    // head dim 256: the register-staged kernel only (four direct-to-LDS stages of its tiles
+    // would need 256 KB of LDS)
+    if constexpr (D != 256) {
+        if (!V && dma_ok(P, 32 * KB)) {
+            constexpr int QB = (D == 64) ? PA_FWD_QB64 : 1;
+            const int nqb2 = (P.nq + kFwdBM * QB - 1) / (kFwdBM * QB);
+            hipLaunchKernelGGL((k_mfma_fwd_dma<T, D, KB, QB, C, S, B>), dim3(nqb2 * P.heads * P.batch),
+                               dim3(kFwdThreads), 0, s, P);
+            return;
+        }
     }
+    hipLaunchKernelGGL((k_mfma_fwd<T, D, KB, C, S, V, B>), grid, dim3(kFwdThreads), 0, s, P);
 }
 
 template <typename T, int D, bool C, bool S>
@@ -1422,10 +1428,12 @@ void launch_mfma_fwd(const PassDev& P, int dtype, hipStream_t s) {
     }
     if (dtype == PA_BF16) {
         if (P.dim == 64) launch_d<bf16, 64>(P, s);
-        else launch_d<bf16, 128>(P, s);
+        else if (P.dim == 128) launch_d<bf16, 128>(P, s);
+        else launch_d<bf16, 256>(P, s);
     } else {
         if (P.dim == 64) launch_d<f16, 64>(P, s);
-        else launch_d<f16, 128>(P, s);
+        else if (P.dim == 128) launch_d<f16, 128>(P, s);
+        else launch_d<f16, 256>(P, s);
     }
 }
 

@@ -187,13 +187,15 @@ def _check_pass_inputs(q, k, v, vmul, bias, key_mask, query_mask):
 
 
 def _padded_dim(q: Tensor) -> Optional[int]:
-    """The MFMA head dim (64 or 128) a CUDA pass of another head dim up to 128 is run at, its
-    features zero-padded: the padded features add nothing to any score, and the padded value
-    features are zero (the scale stays the caller's), so out, lse and every gradient are the
-    unpadded pass's.  None when the pass runs as it is."""
+    """The MFMA head dim (64, 128, or 256 for 16-bit passes) a CUDA pass of another head dim
+    up to 256 is run at, its features zero-padded: the padded features add nothing to any
+    score, and the padded value features are zero (the scale stays the caller's), so out, lse
+    and every gradient are the unpadded pass's.  None when the pass runs as it is."""
     d = q.shape[-1]
-    if not q.is_cuda or d in (64, 128) or d > 128:
+    if not q.is_cuda or d in (64, 128, 256) or d > 256:
         return None
+    if d > 128:
+        return 256 if q.dtype in (torch.bfloat16, torch.float16) else None
     return 64 if d < 64 else 128
 
 

@@ -1,0 +1,120 @@
+"""GPU parity of passes at head dims above 128 (libpolyattn through its C ABI) vs the CPU oracle.
+
+The reference's Triton kernel takes any power-of-two head dim (flash_poly_attention.py:12-20,
+340-344).  Here, 16-bit passes of head dim 256 run on the register-staged MFMA kernels
+(k_mfma_fwd, k_mfma_bwd_dq, k_mfma_bwd_dkv at D = 256), and head dims 129..255 are zero-padded
+to 256 by the host layer; masked passes and fp32 passes of these head dims run on the generic
+kernels.  Bound as tests/parity.py states it (fp32 1e-4; bf16 / f16 2e-2 plus one rounding of
+the result's storage type).  The kernel profile shows which kernels ran.
+"""
+
+import pytest
+import torch
+
+import oracle.poly_oracle as O
+from parity import assert_parity
+from test_gpu_1_pass import check, dev, randn, run_pass
+
+pytestmark = pytest.mark.gpu
+param = pytest.mark.parametrize
+
+MFMA = ("mfma_fwd", "mfma_bwd_dq", "mfma_bwd_dkv")
+GENERIC = ("simt_fwd", "simt_bwd_dq", "simt_bwd_dkv")
+
+
+def _profiled(q, k, v, **kw):
+    from poly_attention import _lib
+
+    dev()
+    with _lib.KernelProfile() as prof:
+        res = run_pass(q, k, v, **kw)
+    return res, set(prof.times)
+
+
+@param("dtype", (torch.bfloat16, torch.float16))
+@param("d", (256, 160, 200))
+@param("n", (40, 300))
+@param("causal", (False, True))
+def test_pass_head_dim_256_on_mfma(dtype, d, n, causal):
+    """Forward and gradients at head dim 256 (160 and 200 padded to it): one partial key tile
+    (n = 40) and ten 32-key forward tiles with a ragged end (n = 300, three query blocks)."""
+    q, k, v = (randn((2, 2, n, d), dtype, s) for s in (201, 202, 203))
+    res, ran = _profiled(q, k, v, causal=causal)
+    check(res, dtype, f"head dim {d} {dtype} n={n} causal={causal}")
+    for name in MFMA:
+        assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
+    assert not ran & set(GENERIC), sorted(ran)
+
+
+@param("causal", (False, True))
+@param("softclamp", (None, 10.0))
+def test_pass_head_dim_256_gqa_bias_vmul(causal, softclamp):
+    """A middle level of the chain at head dim 256: 8 query heads over 2 KV heads, key bias, value
+    multiplier (the register-staged kernels' paths), softclamp on and off."""
+    dtype = torch.bfloat16
+    q = randn((1, 8, 150, 256), dtype, 211)
+    k, v, vmul = (randn((1, 2, 150, 256), dtype, s) for s in (212, 213, 214))
+    bias = randn((1, 2, 150), torch.float32, 215, scale=2.0)
+    res, ran = _profiled(q, k, v, vmul=vmul, bias=bias, causal=causal, softclamp=softclamp)
+    check(res, dtype, f"head dim 256 gqa+bias+vmul causal={causal} sc={softclamp}")
+    for name in MFMA:
+        assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
+
+
+@param("dtype", (torch.bfloat16, torch.float32))
+@param("d", (256, 192))
+@param("causal", (False, True))
+def test_pass_head_dim_256_masked_generic(dtype, d, causal):
+    """Key / query masks with fully-masked rows at head dims above 128: the generic kernels."""
+    q, k, v = (randn((2, 2, 24, d), dtype, s) for s in (221, 222, 223))
+    km = torch.ones(2, 24, dtype=torch.bool)
+    km[:, 17:] = False
+    km[1, 0] = False
+    qm = torch.ones(2, 24, dtype=torch.bool)
+    qm[0, 20:] = False
+    res, ran = _profiled(q, k, v, key_mask=km, query_mask=qm, causal=causal)
+    check(res, dtype, f"masked head dim {d} {dtype} causal={causal}")
+    for name in GENERIC:
+        assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
+
+
+def test_pass_head_dim_256_fp32_generic():
+    q, k, v = (randn((1, 2, 70, 256), torch.float32, s) for s in (231, 232, 233))
+    res, ran = _profiled(q, k, v, causal=True)
+    check(res, torch.float32, "head dim 256 fp32")
+    assert "simt_fwd" in ran, sorted(ran)
+
+
+@param("causal", (False, True))
+def test_flash_poly_attention_head_dim_256(causal):
+    """The order-2 chain (flash_poly_attention.py:334-396) at head dim 256 in bf16: both passes
+    and the chain's backward (pass 1's dQ of q2 accumulated into pass 2's dK) on the MFMA
+    kernels, against the fp32 oracle of poly_attention.py:48-116."""
+    from poly_attention import _lib
+    from poly_attention.flash_poly_attention import flash_poly_attention
+
+    d = dev()
+    g = torch.Generator().manual_seed(241)
+    shape = (1, 2, 200, 256)
+    ts = [torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4)]
+    gt = [t.to(d).requires_grad_() for t in ts]
+    ot = [t.float().requires_grad_() for t in ts]
+    with _lib.KernelProfile() as prof:
+        out = flash_poly_attention(*gt, is_causal=causal)
+        dout = torch.randn(out.shape, generator=g).to(torch.bfloat16)
+        out.backward(dout.to(d))
+        torch.cuda.synchronize()
+    ref, _, _ = O.reference_poly_attention(ot[0], ot[1], ot[1], ot[2], ot[3], causal=causal)
+    ref.backward(dout.float())
+    # the oracle in bf16: the reference's own drift at that precision bounds the gradients
+    lt = [t.clone().requires_grad_() for t in ts]
+    lp, _, _ = O.reference_poly_attention(lt[0], lt[1], lt[1], lt[2], lt[3], causal=causal)
+    lp.backward(dout)
+    assert_parity(out, ref, torch.bfloat16, f"chain d=256 causal={causal} out")
+    for i, (a, b, c) in enumerate(zip(gt, ot, lt)):
+        assert_parity(a.grad, b.grad, torch.bfloat16, f"chain d=256 causal={causal} grad {i}",
+                      grad=True, ref_lp=c.grad)
+    ran = set(prof.times)
+    for name in MFMA:
+        assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
+    assert not ran & set(GENERIC), sorted(ran)
