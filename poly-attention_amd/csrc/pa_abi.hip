@@ -158,7 +158,6 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // into the key term, fully-masked rows given lse = +inf and finished by the fix-ups): whether
 // the kernels take that mask-free pass.
 bool mfma_bwd_masked_supported(const GradDev& G, int dtype) {
-    if (G.f.dim > 128) return false;  // the fix-ups hold rows of at most 128
     GradDev Gm = G;
     Gm.f.km.p = nullptr;
     Gm.f.qm.p = nullptr;

@@ -1327,8 +1327,6 @@ bool mfma_bwd_supported(const GradDev& G, int dtype) {
     if (dtype == PA_F32) return mfma_bwd_f32_supported(G);
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
     if (P.dim != 64 && P.dim != 128 && P.dim != 256) return false;
-    // head dim 256: unmasked passes only (the mask fix-ups hold rows of at most 128)
-    if (P.dim == 256 && (P.km.p || P.qm.p || (P.flags & PA_FLAG_MAY_DEGENERATE))) return false;
     const DView* loads[] = {&P.q, &P.k, &P.v, &G.dout};
     for (const DView* v : loads)
         if (!aligned_rows_host(*v, 8)) return false;

@@ -1360,8 +1360,6 @@ bool mfma_fwd_supported(const PassDev& P, int dtype) {
     if (dtype == PA_F32) return mfma_fwd_f32_supported(P);
     if (dtype != PA_BF16 && dtype != PA_F16) return false;
     if (P.dim != 64 && P.dim != 128 && P.dim != 256) return false;
-    // head dim 256: unmasked passes only (the mask fix-ups hold rows of at most 128)
-    if (P.dim == 256 && (P.km.p || P.qm.p || (P.flags & PA_FLAG_MAY_DEGENERATE))) return false;
     if (!(P.scale > 0.f)) return false;  // the raw-score running max assumes a positive scale
     if (!aligned_rows_host(P.q, 8) || !aligned_rows_host(P.k, 8) || !aligned_rows_host(P.v, 8)) return false;
     if (P.vmul.ok() && !aligned_rows_host(P.vmul, 8)) return false;

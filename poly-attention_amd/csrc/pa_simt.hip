@@ -815,7 +815,7 @@ __global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
         for (int k = 0; k < kFixRowChunk / 256; ++k) any |= !isfinite(l[k]);
     }
     if (!__syncthreads_or(any)) {
-        if (threadIdx.x < D + 2) part[threadIdx.x] = 0.f;
+        for (int e = threadIdx.x; e < D + 2; e += 256) part[e] = 0.f;  // D + 2 may exceed 256
         return;
     }
     float u[8], wsum = 0.f, cnt = 0.f;
@@ -880,17 +880,17 @@ __global__ __launch_bounds__(256) void k_fix_rows(GradDev G) {
         sC[slot] = cnt;
     }
     __syncthreads();
-    if (threadIdx.x < D) {
+    for (int e = threadIdx.x; e < D + 2; e += 256) {  // D + 2 may exceed 256
         float a = 0.f;
+        if (e < D) {
 #pragma unroll 16  // the LDS reads issued ahead of the (ordered) sums
-        for (int r = 0; r < R; ++r) a += sU[r][threadIdx.x];
-        part[threadIdx.x] = a;
-    } else if (threadIdx.x < D + 2) {
-        const float* src = threadIdx.x == D ? sW : sC;
-        float a = 0.f;
+            for (int r = 0; r < R; ++r) a += sU[r][e];
+        } else {
+            const float* src = e == D ? sW : sC;
 #pragma unroll 16  // the LDS reads issued ahead of the (ordered) sums
-        for (int r = 0; r < R; ++r) a += src[r];
-        part[threadIdx.x] = a;
+            for (int r = 0; r < R; ++r) a += src[r];
+        }
+        part[e] = a;
     }
 }
 
@@ -917,11 +917,11 @@ __global__ __launch_bounds__(256) void k_fix_keys(GradDev G) {
     __shared__ float sU[D];
     __shared__ float sWC[2];
     const int tid = threadIdx.x;
-    if (tid < D + 2) {
+    for (int e = tid; e < D + 2; e += 256) {  // D + 2 may exceed 256
         float a = 0.f;
-        for (int hh = 0; hh < rep; ++hh) a += part_sum<D>(G, b, h0 + hh, tid);
-        if (tid < D) sU[tid] = a;
-        else sWC[tid - D] = a;
+        for (int hh = 0; hh < rep; ++hh) a += part_sum<D>(G, b, h0 + hh, e);
+        if (e < D) sU[e] = a;
+        else sWC[e - D] = a;
     }
     __syncthreads();
     if (sWC[1] == 0.f) return;  // no fully-masked row in the group
@@ -1311,11 +1311,18 @@ void launch_key_terms(const GradDev& G, float* kterm, int nkp, int32_t* kcnt, in
                        nkp, kcnt, live);
 }
 
+template <typename T>
+static void mask_fixups_d(const GradDev& G, hipStream_t s) {
+    if (G.f.dim == 64) launch_mask_fixups_t<T, 64>(G, s);
+    else if (G.f.dim == 128) launch_mask_fixups_t<T, 128>(G, s);
+    else launch_mask_fixups_t<T, 256>(G, s);
+}
+
+// head dims 64 and 128 (every MFMA dtype) and 256 (16-bit)
 void launch_mask_fixups(const GradDev& G, int dtype, hipStream_t s) {
-    const bool d64 = G.f.dim == 64;
-    if (dtype == PA_F32) d64 ? launch_mask_fixups_t<float, 64>(G, s) : launch_mask_fixups_t<float, 128>(G, s);
-    else if (dtype == PA_F16) d64 ? launch_mask_fixups_t<f16, 64>(G, s) : launch_mask_fixups_t<f16, 128>(G, s);
-    else d64 ? launch_mask_fixups_t<bf16, 64>(G, s) : launch_mask_fixups_t<bf16, 128>(G, s);
+    if (dtype == PA_F32) G.f.dim == 64 ? launch_mask_fixups_t<float, 64>(G, s) : launch_mask_fixups_t<float, 128>(G, s);
+    else if (dtype == PA_F16) mask_fixups_d<f16>(G, s);
+    else mask_fixups_d<bf16>(G, s);
 }
 
 void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s) {
@@ -1323,11 +1330,18 @@ void launch_simt_fwd(const PassDev& P, int dtype, hipStream_t s) {
     else if (dtype == PA_F16) simt_fwd_d<f16>(P, s);
     else simt_fwd_d<bf16>(P, s);
 }
+template <typename T>
+static void fwd_fixup_d(const PassDev& P, hipStream_t s) {
+    if (P.dim == 64) launch_fwd_fixup_t<T, 64>(P, s);
+    else if (P.dim == 128) launch_fwd_fixup_t<T, 128>(P, s);
+    else launch_fwd_fixup_t<T, 256>(P, s);
+}
+
+// head dims 64 and 128 (every MFMA dtype) and 256 (16-bit)
 void launch_fwd_fixup(const PassDev& P, int dtype, hipStream_t s) {
-    const bool d64 = P.dim == 64;
-    if (dtype == PA_F32) d64 ? launch_fwd_fixup_t<float, 64>(P, s) : launch_fwd_fixup_t<float, 128>(P, s);
-    else if (dtype == PA_F16) d64 ? launch_fwd_fixup_t<f16, 64>(P, s) : launch_fwd_fixup_t<f16, 128>(P, s);
-    else d64 ? launch_fwd_fixup_t<bf16, 64>(P, s) : launch_fwd_fixup_t<bf16, 128>(P, s);
+    if (dtype == PA_F32) P.dim == 64 ? launch_fwd_fixup_t<float, 64>(P, s) : launch_fwd_fixup_t<float, 128>(P, s);
+    else if (dtype == PA_F16) fwd_fixup_d<f16>(P, s);
+    else fwd_fixup_d<bf16>(P, s);
 }
 void launch_simt_bwd(const GradDev& G, int dtype, hipStream_t s, bool pre, bool dq, bool dkv) {
     if (dtype == PA_F32) simt_bwd_d<float>(G, s, pre, dq, dkv);

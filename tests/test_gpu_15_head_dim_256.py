@@ -3,7 +3,8 @@
 The reference's Triton kernel takes any power-of-two head dim (flash_poly_attention.py:12-20,
 340-344).  Here, 16-bit passes of head dim 256 run on the register-staged MFMA kernels
 (k_mfma_fwd, k_mfma_bwd_dq, k_mfma_bwd_dkv at D = 256), and head dims 129..255 are zero-padded
-to 256 by the host layer; masked passes and fp32 passes of these head dims run on the generic
+to 256 by the host layer, masked passes included (the key mask folded into the key term, the
+fully-masked rows finished by the fix-ups); fp32 passes of these head dims run on the generic
 kernels.  Bound as tests/parity.py states it (fp32 1e-4; bf16 / f16 2e-2 plus one rounding of
 the result's storage type).  The kernel profile shows which kernels ran.
 """
@@ -61,11 +62,13 @@ def test_pass_head_dim_256_gqa_bias_vmul(causal, softclamp):
         assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
 
 
-@param("dtype", (torch.bfloat16, torch.float32))
+@param("dtype", (torch.bfloat16, torch.float16, torch.float32))
 @param("d", (256, 192))
 @param("causal", (False, True))
-def test_pass_head_dim_256_masked_generic(dtype, d, causal):
-    """Key / query masks with fully-masked rows at head dims above 128: the generic kernels."""
+def test_pass_head_dim_256_masked(dtype, d, causal):
+    """Key / query masks with fully-masked rows at head dims above 128: 16-bit passes on the
+    register-staged MFMA kernels with the key mask folded into the key term and the fix-ups
+    finishing the fully-masked rows; fp32 passes on the generic kernels."""
     q, k, v = (randn((2, 2, 24, d), dtype, s) for s in (221, 222, 223))
     km = torch.ones(2, 24, dtype=torch.bool)
     km[:, 17:] = False
@@ -74,8 +77,47 @@ def test_pass_head_dim_256_masked_generic(dtype, d, causal):
     qm[0, 20:] = False
     res, ran = _profiled(q, k, v, key_mask=km, query_mask=qm, causal=causal)
     check(res, dtype, f"masked head dim {d} {dtype} causal={causal}")
-    for name in GENERIC:
+    if dtype == torch.float32:
+        for name in GENERIC:
+            assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
+    else:
+        for name in MFMA + ("fwd_fixup", "key_terms", "fix_rows", "fix_keys"):
+            assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
+        assert not ran & set(GENERIC), sorted(ran)
+
+
+@param("n", (150, 256))
+@param("causal", (False, True))
+@param("gqa", (False, True))
+def test_pass_head_dim_256_masked_bias_classes(n, causal, gqa):
+    """The masked cases of the head-dim-64/128 test at head dim 256 in bf16: leading keys
+    masked (causal rows 0-2 fully masked), batch 1's keys 3-5 biased to -finfo.max (bias class
+    1: fully-masked rows with unmasked class-1 keys, finished by the part B fix-ups), a -inf
+    bias entry, query-masked rows; gqa: 4 query heads over 2 key heads with a value
+    multiplier."""
+    dtype, d = torch.bfloat16, 256
+    B, H, HK = 2, 4, (2 if gqa else 4)
+    q = randn((B, H, n, d), dtype, 251)
+    k, v = (randn((B, HK, n, d), dtype, s) for s in (252, 253))
+    vmul = randn((B, HK, n, d), dtype, 254) if gqa else None
+    bias = torch.log(torch.arange(1, n + 1).float())[None, None].repeat(B, HK, 1)
+    bias = bias + randn((B, HK, n), torch.float32, 255)
+    fmax = torch.finfo(torch.float32).max
+    km = torch.ones(B, n, dtype=torch.bool)
+    qm = torch.ones(B, n, dtype=torch.bool)
+    km[:, :3] = False
+    km[0, n // 2:n // 2 + 20] = False
+    bias[1, :, 3:6] = -fmax
+    bias[0, 0, 10] = -float("inf")
+    qm[0, -7:] = False
+    if not causal:
+        km[1, 6:] = False
+    res, ran = _profiled(q, k, v, vmul=vmul, bias=bias, key_mask=km, query_mask=qm,
+                         causal=causal)
+    check(res, dtype, f"masked head dim 256 n={n} causal={causal} gqa={gqa}")
+    for name in MFMA + ("fix_rows", "fix_keys", "fix_part_b"):
         assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
+    assert not ran & set(GENERIC), sorted(ran)
 
 
 def test_pass_head_dim_256_fp32_generic():
