@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import oracle.poly_oracle as O
-from parity import assert_parity
+from parity import assert_drift, assert_parity
 from test_gpu_1_pass import check, dev, randn, run_pass
 
 pytestmark = pytest.mark.gpu
@@ -160,3 +160,80 @@ def test_flash_poly_attention_head_dim_256(causal):
     for name in MFMA:
         assert name in ran, f"{name} did not run (kernels: {sorted(ran)})"
     assert not ran & set(GENERIC), sorted(ran)
+
+
+@param("masked", (False, True))
+def test_module_head_dim_256_bf16_training(masked):
+    """PolyAttention (poly_attention.py:120-365) at dim_head = 256 trained in bf16: forward and
+    backward through the fused projections, q/k norms, both passes on the head-dim-256 MFMA
+    kernels (with a key-padding mask: the key term and fix-ups) and the output projection.  As in
+    the config-2 module test, each result is held to the drift of the reference's own bf16
+    arithmetic (tests/parity.py, assert_drift)."""
+    from poly_attention import PolyAttention
+
+    d = dev()
+    B, N, DIM, H, DH = 2, 160, 512, 4, 256
+    cfg = dict(heads=H, dim_head=DH, causal=True)
+    torch.manual_seed(3)
+    m = PolyAttention(dim=DIM, **cfg).to(d, torch.bfloat16)
+    x = torch.randn(B, N, DIM, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    dout = torch.randn(B, N, DIM, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    mask = None
+    if masked:  # right-padded batch row 1, left-padded batch row 0
+        mask = torch.ones(B, N, dtype=torch.bool)
+        mask[1, 120:] = False
+        mask[0, :17] = False
+
+    xg = x.to(d).requires_grad_()
+    out = m(xg, mask=mask.to(d) if masked else None)
+    out.backward(dout.to(d))
+    torch.cuda.synchronize()
+
+    sd = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    p32 = {k: v.float().requires_grad_(v.is_floating_point()) for k, v in sd.items()}
+    x32 = x.float().requires_grad_()
+    ref = O.order2_forward(p32, cfg, x32, mask=mask)
+    ref.backward(dout.float())
+    p16 = {k: v.clone().requires_grad_(v.is_floating_point()) for k, v in sd.items()}
+    x16 = x.clone().requires_grad_()
+    lp = O.order2_forward(p16, cfg, x16, mask=mask)
+    lp.backward(dout)
+
+    what = f"module dim_head=256 bf16 masked={masked}"
+    assert_drift(out, ref, lp, f"{what} out")
+    assert_drift(xg.grad, x32.grad, x16.grad, f"{what} dx")
+    for name, p in m.named_parameters():
+        assert p.grad is not None and p32[name].grad is not None, name
+        assert_drift(p.grad, p32[name].grad, p16[name].grad, f"{what} d{name}")
+
+
+@param("order", (2, 3))
+def test_cache_stepwise_head_dim_256_bf16(order):
+    """Prefill at dim_head = 256 in bf16 (the MFMA passes) with return_cache, then single-token
+    steps through the decode kernel: the concatenated outputs against the oracle's parallel
+    causal forward (reference tests:103-179), 2 KV heads under 4 query heads; held to the drift
+    of the reference's own bf16 arithmetic, as the module test above."""
+    from poly_attention import NPolyAttention, Order2PolyAttention
+
+    d = dev()
+    torch.manual_seed(13)
+    cfg = dict(heads=4, kv_heads=2, dim_head=256, causal=True)
+    if order == 2:
+        m = Order2PolyAttention(dim=128, **cfg)
+        fwd = O.order2_forward
+    else:
+        m = NPolyAttention(dim=128, order=order, **cfg)
+        fwd = O.npoly_forward
+        cfg = dict(cfg, order=order)
+    m = m.to(d, torch.bfloat16)
+    x = torch.randn(2, 70, 128).to(torch.bfloat16)
+    sd = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    ref = fwd({k: v.float() for k, v in sd.items()}, cfg, x.float())
+    lp = fwd(sd, cfg, x)  # the reference's own bf16 arithmetic: the drift bound
+    with torch.no_grad():
+        out0, cache = m(x[:, :64].to(d), return_cache=True)
+        outs = [out0]
+        for i in range(64, 70):
+            o, cache = m(x[:, i:i + 1].to(d), cache=cache, return_cache=True)
+            outs.append(o)
+    assert_drift(torch.cat(outs, dim=1), ref, lp, f"stepwise dim_head=256 order={order} bf16")
