@@ -207,7 +207,10 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dkv(G
             kv_store<T, D>(st, sQ, sO, sQt, sOt, sL, sD);
             __syncthreads();
             if (PREFETCH && t + 1 < ntiles) kv_load<T, D>(qs, q0 + kKvBQ, st);
-#pragma unroll
+            // head dim 256, not causal: the two query halves one after the other (unrolled, the
+            // scheduler kept both halves' temporaries live: 479 against 106 spilled registers,
+            // 3.75 against 1.80 ms per launch at N = 2048); causal, unrolled was faster
+#pragma unroll(D == 256 && !CAUSAL ? 1 : 2)
             for (int qb = 0; qb < 2; ++qb) {
                 const int qbase = q0 + qb * 32;
                 if (CAUSAL && qbase + 31 < kw0) continue;  // every query precedes every key
@@ -836,20 +839,19 @@ __global__ __launch_bounds__(kBwdThreads, D == 64 ? 2 : 1) void k_mfma_bwd_dq(Gr
     const int kend = CAUSAL ? min(P.nk, qblk * kDqBM + kDqBM) : P.nk;
     const int ntiles = (kend + kDqBN - 1) / kDqBN;
     const KeyRows<T> ks = key_rows<T>(P, b, h);
-    // head dim 256: the next tile is loaded just before it is stored, as in k_mfma_bwd_dkv
-    // (2.00 against 3.17 ms per launch at N = 4096)
-    constexpr bool PREFETCH = D < 256;
     DqStage<D> st;
-    if (PREFETCH) dq_load<T, D, HAS_VMUL, HAS_BIAS>(ks, 0, st);
+    dq_load<T, D, HAS_VMUL, HAS_BIAS>(ks, 0, st);
     for (int t = 0; t < ntiles; ++t) {
         const int j0 = t * kDqBN;
-        if (!PREFETCH) dq_load<T, D, HAS_VMUL, HAS_BIAS>(ks, j0, st);
         dq_store<T, D>(st, sK, sV, sKt, sB);
         __syncthreads();
-        if (PREFETCH && t + 1 < ntiles) dq_load<T, D, HAS_VMUL, HAS_BIAS>(ks, j0 + kDqBN, st);
+        if (t + 1 < ntiles) dq_load<T, D, HAS_VMUL, HAS_BIAS>(ks, j0 + kDqBN, st);
         if (!(CAUSAL && j0 > qw0 + 31)) {
             const bool diag = CAUSAL && (j0 + kDqBN - 1 > qw0);
-#pragma unroll
+            // head dim 256: the two key blocks one after the other (unrolled, the register file
+            // spilled up to 200 registers; rolled, none: 1.39 against 2.02 ms per launch at
+            // N = 4096, causal)
+#pragma unroll(D == 256 ? 1 : 2)
             for (int kb = 0; kb < 2; ++kb) {
                 f32x16_t s = zero16(), dp = zero16();
 #pragma unroll
