@@ -1,7 +1,7 @@
 """GPU parity of passes at head dims above 128 (libpolyattn through its C ABI) vs the CPU oracle.
 
-The reference's Triton kernel takes any power-of-two head dim (flash_poly_attention.py:12-20,
-340-344).  Here, 16-bit passes of head dim 256 run on the register-staged MFMA kernels
+The reference's Triton kernels take the head dim as BLOCK_DMODEL = dim (flash_poly_attention.py:
+357,375,420,440; autotuned per value, :12-20), any power of two.  Here, 16-bit passes of head dim 256 run on the register-staged MFMA kernels
 (k_mfma_fwd, k_mfma_bwd_dq, k_mfma_bwd_dkv at D = 256), and head dims 129..255 are zero-padded
 to 256 by the host layer, masked passes included (the key mask folded into the key term, the
 fully-masked rows finished by the fix-ups); fp32 passes of these head dims run on the generic
